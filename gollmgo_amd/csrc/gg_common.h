@@ -1,0 +1,198 @@
+// gg_common.h — shared definitions of the gfx950 verify-path library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+
+#include "../../include/gg_verify.h"
+
+#define GG_API extern "C" __attribute__((visibility("default")))
+
+namespace gg {
+
+// ---- error reporting (per calling thread, like gollmgo_backend_last_error) ----
+void set_error(const std::string& msg);
+void clear_error();
+gg_status_t fail(gg_status_t st, const std::string& msg);
+gg_status_t check_hip(hipError_t e, const char* what);
+
+// ---- KV cache handle ----
+struct KV {
+    int num_layers = 0;
+    int num_blocks = 0;
+    int block_size = 0;
+    int num_kv_heads = 0;
+    int head_dim = 0;
+    gg_dtype_t dtype = GG_DTYPE_BF16;
+    gg_scale_mode_t scale_mode = GG_SCALE_NONE;
+    int device = 0;
+    size_t elem_bytes = 2;
+    size_t layer_bytes = 0;       // bytes of one layer's K (or V) pool
+    size_t scale_layer_elems = 0; // scales per layer per pool
+    uint8_t* k_pool = nullptr;    // [layers][layer_bytes]
+    uint8_t* v_pool = nullptr;
+    void* k_scales = nullptr;     // PER_HEAD: float[layers][Hkv]; PER_BLOCK: u16[layers][blocks][Hkv]
+    void* v_scales = nullptr;
+    float* block_amax = nullptr;  // PER_BLOCK staging: float[blocks][Hkv][2], kept at zero between calls
+};
+
+__host__ __device__ inline size_t dtype_bytes(gg_dtype_t t) {
+    switch (t) {
+        case GG_DTYPE_F32: return 4;
+        case GG_DTYPE_F16: return 2;
+        case GG_DTYPE_BF16: return 2;
+        case GG_DTYPE_FP8_E4M3: return 1;
+        case GG_DTYPE_INT8: return 1;
+    }
+    return 0;
+}
+
+__host__ __device__ inline bool is_float_io(gg_dtype_t t) {
+    return t == GG_DTYPE_F32 || t == GG_DTYPE_F16 || t == GG_DTYPE_BF16;
+}
+
+// ---- launchers (defined in the .hip files) ----
+gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg_dtype_t src,
+                             const int32_t* slots, int n_rows, hipStream_t s);
+
+struct AttnArgs {
+    const KV* kv;
+    int layer;
+    const void* q;
+    gg_dtype_t q_dtype;
+    void* out;
+    gg_dtype_t out_dtype;
+    const int32_t* ctx_lens;
+    const int32_t* row_counts;
+    const int32_t* block_tables;
+    int max_blocks;
+    int num_seqs;
+    int rows;
+    int num_q_heads;
+    float scale;
+    int kv_bs;         // block size of the pool
+    int partition;     // resolved partition length (tokens)
+    int max_parts;
+    float* ws_ml;      // [seqs][rows][Hq][max_parts][2]
+    float* ws_acc;     // [seqs][rows][Hq][max_parts][D]
+};
+int attn_resolve_partition(const KV* kv, int num_seqs, int rows, int num_q_heads,
+                           int max_blocks, int partition_tokens);
+size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
+                            int max_blocks, int partition);
+gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s);
+
+size_t greedy_workspace_bytes(int num_seqs, int max_drafts, int vocab);
+gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs, int max_drafts,
+                                 int vocab, const int32_t* drafts, const int32_t* n_drafts,
+                                 int32_t* out_acc, int32_t* out_tok, void* ws, hipStream_t s);
+
+size_t rejection_workspace_bytes(int num_seqs, int max_drafts, int vocab);
+gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const float* q, int num_seqs,
+                                    int max_drafts, int vocab, const int32_t* drafts,
+                                    const int32_t* n_drafts, const float* uniforms, float temperature,
+                                    float top_p, int32_t* out_acc, int32_t* out_tok, void* ws,
+                                    hipStream_t s);
+
+gg_status_t launch_ngram_draft(const int32_t* hist, int stride, const int32_t* hist_len, int num_seqs,
+                               int n, int max_drafts, int32_t* out_drafts, int32_t* out_n,
+                               hipStream_t s);
+
+}  // namespace gg
+
+// The opaque handle of the C ABI is the KV description itself.
+struct gg_kv : public gg::KV {};
+
+// ---- device helpers shared by the kernels ----
+#ifdef __HIPCC__
+namespace gg {
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Load element i of a float-like array of type dt as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, gg_dtype_t dt, size_t i) {
+    switch (dt) {
+        case GG_DTYPE_F32: return ((const float*)p)[i];
+        case GG_DTYPE_F16: return f16_bits_to_f32(((const uint16_t*)p)[i]);
+        case GG_DTYPE_BF16: return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+        default: return 0.f;
+    }
+}
+__device__ __forceinline__ void store_from_f32(void* p, gg_dtype_t dt, size_t i, float v) {
+    switch (dt) {
+        case GG_DTYPE_F32: ((float*)p)[i] = v; break;
+        case GG_DTYPE_F16: ((uint16_t*)p)[i] = f32_to_f16_bits(v); break;
+        case GG_DTYPE_BF16: ((uint16_t*)p)[i] = f32_to_bf16_bits(v); break;
+        default: break;
+    }
+}
+
+// OCP FP8 E4M3 ("fn") decode: bias 7, no infinities, S.1111.111 = NaN.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint8_t b) {
+    uint32_t s = (uint32_t)(b & 0x80) << 24;
+    uint32_t e = (b >> 3) & 0xF;
+    uint32_t m = b & 0x7;
+    if ((b & 0x7F) == 0x7F) return __uint_as_float(0x7fc00000u | s);
+    if (e == 0) {
+        float v = (float)m * 0.001953125f;  // m * 2^-9
+        return s ? -v : v;
+    }
+    return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// fp32 -> E4M3 with round-to-nearest-even and saturation to +-448 (the
+// __NV_SATFINITE convention of kernels/gollmgo_model.cu:254). NaN -> 0x7F|sign.
+__device__ __forceinline__ uint8_t f32_to_fp8e4m3_sat(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint8_t)(sign | 0x7F);
+    if (a >= 0x43E00000u) return (uint8_t)(sign | 0x7E);  // >= 448 (incl. inf) saturates
+    int e = (int)(a >> 23) - 127;
+    if (e < -6) {
+        // Subnormal range: value = k * 2^-9, k in [0,8]; RNE on k.
+        float af = __uint_as_float(a);
+        float k = af * 512.0f;  // exact scaling
+        float r = __builtin_rintf(k);  // ties-to-even
+        uint32_t ki = (uint32_t)r;
+        return (uint8_t)(sign | ki);  // ki == 8 encodes the smallest normal (e=1,m=0)
+    }
+    // Normal: keep 3 mantissa bits, RNE on the remaining 20.
+    uint32_t mant = a & 0x7fffffu;
+    uint32_t keep = mant >> 20;
+    uint32_t rest = mant & 0xfffffu;
+    uint32_t half = 0x80000u;
+    uint32_t biased = (uint32_t)(e + 7);
+    uint32_t code = (biased << 3) | keep;
+    if (rest > half || (rest == half && (keep & 1))) code += 1;
+    if (code > 0x7E) code = 0x7E;
+    return (uint8_t)(sign | code);
+}
+
+// Symmetric int8: round-half-even, clamp to +-127 (kernels/gollmgo_model.cu:258-268).
+__device__ __forceinline__ int8_t f32_to_i8_sat(float f) {
+    float r = __builtin_rintf(f);
+    if (!(r == r)) r = 0.f;
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    return (int8_t)(int)r;
+}
+
+}  // namespace gg
+#endif

@@ -1,0 +1,65 @@
+// gg_fixed_exp.h — the exponential and fixed-point weights used by rejection acceptance.
+//
+// Decisions must be bit-identical wherever the acceptance rule is evaluated, so
+// the library does not call a platform exp: exp is computed with Cody–Waite range
+// reduction (x = k*ln2 + r, ln2 split into a short high part and a low part) and
+// the degree-7 Taylor polynomial of e^r on |r| <= ln2/2, every step an explicit
+// fmaf, a correctly rounded IEEE operation on every conforming host and on AMD
+// GPUs. Weights are w = floor(e * 2^35) as exact integers, so sums and prefix sums
+// do not depend on summation order; vocabularies up to 2^18 keep every sum
+// below 2^53, so conversions to double are exact too.
+#pragma once
+
+#ifdef __HIPCC__
+#define GG_HD __host__ __device__ __forceinline__
+#else
+#define GG_HD static inline
+#endif
+
+#define GG_FIX_SCALE 34359738368.0f /* 2^35 */
+
+GG_HD float gg_expf_fixed(float x) {
+    if (!(x >= -80.0f)) return 0.0f;  // e^-80 < 2^-115: weight 0; also catches NaN
+    if (x > 0.0f) x = 0.0f;           // callers pass x <= 0
+    const float kf = __builtin_floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
+    float r = __builtin_fmaf(kf, -0.693145751953125f, x);
+    r = __builtin_fmaf(kf, -1.42860682030941723212e-6f, r);
+    float p = 1.98412698412698412698e-4f;               // 1/5040
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f); // 1/720
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-3f); // 1/120
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-2f); // 1/24
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-1f); // 1/6
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int k = (int)kf;  // in [-116, 0]
+    union {
+        unsigned int u;
+        float f;
+    } s;
+    s.u = (unsigned int)(k + 127) << 23;
+    return p * s.f;
+}
+
+// Fixed-point weight of logit l given the row max m and 1/T (all finite).
+GG_HD unsigned long long gg_weight(float l, float m, float inv_t) {
+    const float x = (l - m) * inv_t;
+    const float e = gg_expf_fixed(x);
+    return (unsigned long long)__builtin_floorf(e * GG_FIX_SCALE);
+}
+
+// Monotone order key of a finite logit (larger logit -> larger key; -0 == +0).
+GG_HD unsigned int gg_order_key(float l) {
+    union {
+        float f;
+        unsigned int u;
+    } v;
+    v.f = (l == 0.0f) ? 0.0f : l;
+    return (v.u & 0x80000000u) ? ~v.u : (v.u | 0x80000000u);
+}
+
+// Coarse nucleus bin: 1/64-nat slices of (m - l)/T, monotone non-increasing in l.
+GG_HD int gg_coarse_bin(float l, float m, float inv_t) {
+    const float y = -((l - m) * inv_t) * 64.0f;
+    return y >= 2047.0f ? 2047 : (int)y;
+}

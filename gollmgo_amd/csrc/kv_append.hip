@@ -1,0 +1,237 @@
+// kv_append.hip — draft-KV append into the paged cache (quantise-on-write).
+//
+// Replaces paged_kv_write_{f16,bf16} (kernels/gollmgo_paged_attn.cu:14-35,126-146)
+// as called per layer from run_layer (kernels/gollmgo_model.cu:610-625). The
+// reference copies 2-byte rows to cache[slot][Hkv][D]; here rows land in the
+// block layouts K[blk][Hkv][bs][D] and V[blk][Hkv][D][bs] and are quantised to
+// FP8-E4M3 (per-head fp32 scale) or INT8 (per-block fp16 scale) when the pool
+// stores them. Quantisation follows the reference's weight conventions:
+// q = cvt(x * (1/scale)) with E4M3 satfinite / int8 RNE clamped to +-127
+// (kernels/gollmgo_model.cu:248-268).
+#include "gg_common.h"
+
+namespace gg {
+namespace {
+
+__device__ __forceinline__ size_t k_index(int blk, int h, int off, int d, int Hkv, int bs, int D) {
+    return (((size_t)blk * Hkv + h) * bs + off) * D + d;
+}
+__device__ __forceinline__ size_t v_index(int blk, int h, int off, int d, int Hkv, int bs, int D) {
+    return (((size_t)blk * Hkv + h) * D + d) * bs + off;
+}
+
+struct AppendArgs {
+    uint8_t* kc;
+    uint8_t* vc;
+    const void* k;
+    const void* v;
+    gg_dtype_t src;
+    const int32_t* slots;
+    int n_rows;
+    int Hkv, D, bs;
+    long long num_slots;  // num_blocks * bs: larger slots are skipped
+    gg_dtype_t dst;
+    const float* k_scale;  // PER_HEAD scales [Hkv]
+    const float* v_scale;
+    const float* k_inv;    // PER_HEAD inverse scales [Hkv]
+    const float* v_inv;
+    uint16_t* k_bscale;    // PER_BLOCK fp16 scales [blocks][Hkv]
+    uint16_t* v_bscale;
+    float* amax;           // PER_BLOCK staging [blocks][Hkv][2]
+};
+
+// Plain / per-head-scaled append: grid (n_rows), one thread per (head, dim) element.
+__global__ void __launch_bounds__(256) append_direct_kernel(AppendArgs a) {
+    const int r = blockIdx.x;
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int blk = slot / a.bs, off = slot % a.bs;
+    const int n = a.Hkv * a.D;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int h = i / a.D, d = i % a.D;
+        const size_t src_i = (size_t)r * n + i;
+        float kx = load_as_f32(a.k, a.src, src_i);
+        float vx = load_as_f32(a.v, a.src, src_i);
+        size_t ki = k_index(blk, h, off, d, a.Hkv, a.bs, a.D);
+        size_t vi = v_index(blk, h, off, d, a.Hkv, a.bs, a.D);
+        switch (a.dst) {
+            case GG_DTYPE_F32:
+                ((float*)a.kc)[ki] = kx;
+                ((float*)a.vc)[vi] = vx;
+                break;
+            case GG_DTYPE_F16:
+                ((uint16_t*)a.kc)[ki] = f32_to_f16_bits(kx);
+                ((uint16_t*)a.vc)[vi] = f32_to_f16_bits(vx);
+                break;
+            case GG_DTYPE_BF16:
+                ((uint16_t*)a.kc)[ki] = f32_to_bf16_bits(kx);
+                ((uint16_t*)a.vc)[vi] = f32_to_bf16_bits(vx);
+                break;
+            case GG_DTYPE_FP8_E4M3:
+                a.kc[ki] = f32_to_fp8e4m3_sat(kx * a.k_inv[h]);
+                a.vc[vi] = f32_to_fp8e4m3_sat(vx * a.v_inv[h]);
+                break;
+            default:
+                break;
+        }
+    }
+}
+
+// ---- PER_BLOCK int8: three passes (amax, quantise/requantise, publish) ----
+
+__device__ __forceinline__ float warp_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Pass A: per (row, head) amax of K and V, folded into the block's staging slot.
+// Non-negative floats order like their bit patterns, so atomicMax on the bits is exact.
+__global__ void __launch_bounds__(64) append_amax_kernel(AppendArgs a) {
+    const int r = blockIdx.x, h = blockIdx.y;
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int blk = slot / a.bs;
+    float mk = 0.f, mv = 0.f;
+    for (int d = threadIdx.x; d < a.D; d += 64) {
+        size_t i = ((size_t)r * a.Hkv + h) * a.D + d;
+        float kx = fabsf(load_as_f32(a.k, a.src, i));
+        float vx = fabsf(load_as_f32(a.v, a.src, i));
+        mk = fmaxf(mk, kx == kx ? kx : 0.f);
+        mv = fmaxf(mv, vx == vx ? vx : 0.f);
+    }
+    mk = warp_max(mk);
+    mv = warp_max(mv);
+    if (threadIdx.x == 0) {
+        unsigned int* p = (unsigned int*)(a.amax + ((size_t)blk * a.Hkv + h) * 2);
+        atomicMax(p, __float_as_uint(fminf(mk, 3.0e38f)));
+        atomicMax(p + 1, __float_as_uint(fminf(mv, 3.0e38f)));
+    }
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_rne_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// The leader of row r is the first row of the run of adjacent rows in the same block.
+__device__ __forceinline__ int find_leader(const int32_t* slots, int r, int bs) {
+    const int blk = slots[r] / bs;
+    int l = r;
+    while (l > 0) {
+        int s = slots[l - 1];
+        if (s < 0 || s / bs != blk) break;  // out-of-range slots never match a valid block
+        --l;
+    }
+    return l;
+}
+
+struct BlockScale {
+    float old_s, new_s, inv_new;
+};
+
+__device__ __forceinline__ BlockScale block_scale(const AppendArgs& a, int blk, int h, int which,
+                                                  bool fresh) {
+    const uint16_t* sc = which == 0 ? a.k_bscale : a.v_bscale;
+    float old_s = fresh ? 0.f : f16_bits_to_f32(sc[(size_t)blk * a.Hkv + h]);
+    float am = a.amax[((size_t)blk * a.Hkv + h) * 2 + which];
+    float cand = f16_bits_to_f32(f32_to_f16_rne_bits(am / 127.0f));
+    BlockScale b;
+    b.old_s = old_s;
+    b.new_s = fmaxf(old_s, cand);
+    b.inv_new = b.new_s > 0.f ? 1.0f / b.new_s : 0.f;
+    return b;
+}
+
+// Pass B: quantise every new row with its block's new scale; the leader row also
+// re-quantises the tokens that were already in the block when the scale grew.
+__global__ void __launch_bounds__(256) append_int8_block_kernel(AppendArgs a) {
+    const int r = blockIdx.x;
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int blk = slot / a.bs, off = slot % a.bs;
+    const int lead = find_leader(a.slots, r, a.bs);
+    const int lead_off = a.slots[lead] % a.bs;
+    const bool fresh = lead_off == 0;
+    int8_t* kc = (int8_t*)a.kc;
+    int8_t* vc = (int8_t*)a.vc;
+    const int n = a.Hkv * a.D;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int h = i / a.D, d = i % a.D;
+        BlockScale ks = block_scale(a, blk, h, 0, fresh);
+        BlockScale vs = block_scale(a, blk, h, 1, fresh);
+        const size_t src_i = (size_t)r * n + i;
+        kc[k_index(blk, h, off, d, a.Hkv, a.bs, a.D)] = f32_to_i8_sat(load_as_f32(a.k, a.src, src_i) * ks.inv_new);
+        vc[v_index(blk, h, off, d, a.Hkv, a.bs, a.D)] = f32_to_i8_sat(load_as_f32(a.v, a.src, src_i) * vs.inv_new);
+        if (r == lead && lead_off > 0) {
+            for (int t = 0; t < lead_off; ++t) {
+                if (ks.new_s != ks.old_s) {
+                    size_t ki = k_index(blk, h, t, d, a.Hkv, a.bs, a.D);
+                    kc[ki] = f32_to_i8_sat(((float)kc[ki] * ks.old_s) * ks.inv_new);
+                }
+                if (vs.new_s != vs.old_s) {
+                    size_t vi = v_index(blk, h, t, d, a.Hkv, a.bs, a.D);
+                    vc[vi] = f32_to_i8_sat(((float)vc[vi] * vs.old_s) * vs.inv_new);
+                }
+            }
+        }
+    }
+}
+
+// Pass C: leaders publish the new block scales and clear the staging slots.
+__global__ void __launch_bounds__(64) append_int8_publish_kernel(AppendArgs a) {
+    const int r = blockIdx.x;
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int lead = find_leader(a.slots, r, a.bs);
+    if (lead != r) return;
+    const int blk = slot / a.bs;
+    const bool fresh = (slot % a.bs) == 0;
+    for (int h = threadIdx.x; h < a.Hkv; h += blockDim.x) {
+        BlockScale ks = block_scale(a, blk, h, 0, fresh);
+        BlockScale vs = block_scale(a, blk, h, 1, fresh);
+        a.k_bscale[(size_t)blk * a.Hkv + h] = f32_to_f16_rne_bits(ks.new_s);
+        a.v_bscale[(size_t)blk * a.Hkv + h] = f32_to_f16_rne_bits(vs.new_s);
+        a.amax[((size_t)blk * a.Hkv + h) * 2 + 0] = 0.f;
+        a.amax[((size_t)blk * a.Hkv + h) * 2 + 1] = 0.f;
+    }
+}
+
+}  // namespace
+
+gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg_dtype_t src,
+                             const int32_t* slots, int n_rows, hipStream_t s) {
+    if (n_rows == 0) return GG_OK;
+    AppendArgs a{};
+    a.kc = kv->k_pool + (size_t)layer * kv->layer_bytes;
+    a.vc = kv->v_pool + (size_t)layer * kv->layer_bytes;
+    a.k = k;
+    a.v = v;
+    a.src = src;
+    a.slots = slots;
+    a.n_rows = n_rows;
+    a.Hkv = kv->num_kv_heads;
+    a.D = kv->head_dim;
+    a.bs = kv->block_size;
+    a.num_slots = (long long)kv->num_blocks * kv->block_size;
+    a.dst = kv->dtype;
+    if (kv->scale_mode == GG_SCALE_PER_HEAD) {
+        const float* ks = (const float*)kv->k_scales + (size_t)layer * 2 * kv->num_kv_heads;
+        const float* vs = (const float*)kv->v_scales + (size_t)layer * 2 * kv->num_kv_heads;
+        a.k_scale = ks;
+        a.k_inv = ks + kv->num_kv_heads;
+        a.v_scale = vs;
+        a.v_inv = vs + kv->num_kv_heads;
+    }
+    if (kv->scale_mode == GG_SCALE_PER_BLOCK) {
+        a.k_bscale = (uint16_t*)kv->k_scales + (size_t)layer * kv->scale_layer_elems;
+        a.v_bscale = (uint16_t*)kv->v_scales + (size_t)layer * kv->scale_layer_elems;
+        a.amax = kv->block_amax;
+        append_amax_kernel<<<dim3(n_rows, kv->num_kv_heads), 64, 0, s>>>(a);
+        append_int8_block_kernel<<<n_rows, 256, 0, s>>>(a);
+        append_int8_publish_kernel<<<n_rows, 64, 0, s>>>(a);
+    } else {
+        append_direct_kernel<<<n_rows, 256, 0, s>>>(a);
+    }
+    return check_hip(hipGetLastError(), "kv_append launch");
+}
+
+}  // namespace gg

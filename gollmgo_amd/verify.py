@@ -1,0 +1,224 @@
+"""Host-side mirror of the verify path over torch device tensors.
+
+Thin plumbing around the C ABI (include/gg_verify.h): torch provides device
+memory and the current HIP stream; every computation runs in the HIP kernels
+of libgg_verify.so. Names follow the reference's domain:
+
+  KVCache            ~ CUDAKVCache (internal/backend/cuda/kvcache_bridge.go:16-91)
+  KVCache.append     ~ CUDAKVCache.Write / gollmgo_kvcache_write
+  KVCache.attention  ~ gollmgo_kvcache_attention, for k+1 verify rows per sequence
+  accept_greedy      ~ Verify + argmax as emitSpeculative drives them
+                       (internal/engine/speculative.go:68-84, serving.go:514-566)
+  accept_rejection   ~ speculative sampling with Sampler's temperature/top-p rules
+  ngram_draft        ~ NGramDrafter.Draft (internal/engine/speculative.go:24-62)
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import torch
+
+from ._lib import DType, ScaleMode, check, lib
+
+_TORCH_TO_DT = {torch.float32: DType.F32, torch.float16: DType.F16, torch.bfloat16: DType.BF16}
+
+
+def dtype_of(t: torch.Tensor) -> DType:
+    try:
+        return _TORCH_TO_DT[t.dtype]
+    except KeyError as e:
+        raise TypeError(f"unsupported tensor dtype {t.dtype}") from e
+
+
+def _stream(stream: Optional[torch.cuda.Stream]) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None) -> int:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.data_ptr()
+
+
+class _DeviceBuffer:
+    """Exposes raw device memory to torch through __cuda_array_interface__."""
+
+    def __init__(self, ptr: int, nbytes: int):
+        self.__cuda_array_interface__ = {
+            "shape": (nbytes,), "typestr": "|u1", "data": (ptr, False), "version": 3, "strides": None,
+        }
+
+
+def device_bytes(ptr: int, nbytes: int) -> torch.Tensor:
+    """A uint8 torch view of `nbytes` of device memory at `ptr` (no copy)."""
+    return torch.as_tensor(_DeviceBuffer(ptr, nbytes), device="cuda")
+
+
+class KVCache:
+    """Paged K/V pools for all layers (K[blk][Hkv][bs][D], V[blk][Hkv][D][bs])."""
+
+    def __init__(self, num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
+                 head_dim: int, dtype: DType):
+        self.num_layers, self.num_blocks, self.block_size = num_layers, num_blocks, block_size
+        self.num_kv_heads, self.head_dim, self.dtype = num_kv_heads, head_dim, DType(dtype)
+        self.scale_mode = {DType.FP8_E4M3: ScaleMode.PER_HEAD, DType.INT8: ScaleMode.PER_BLOCK}.get(
+            self.dtype, ScaleMode.NONE)
+        torch.cuda.init()
+        h = C.c_void_p()
+        check(lib().gg_kv_create(num_layers, num_blocks, block_size, num_kv_heads, head_dim,
+                                 int(self.dtype), int(self.scale_mode), C.byref(h)), "gg_kv_create")
+        self.handle = h
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            torch.cuda.synchronize()
+            check(lib().gg_kv_destroy(self.handle), "gg_kv_destroy")
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def layer_bytes(self) -> int:
+        return lib().gg_kv_layer_bytes(self.handle)
+
+    def k_pool(self, layer: int) -> torch.Tensor:
+        return device_bytes(lib().gg_kv_k_layer_ptr(self.handle, layer), self.layer_bytes)
+
+    def v_pool(self, layer: int) -> torch.Tensor:
+        return device_bytes(lib().gg_kv_v_layer_ptr(self.handle, layer), self.layer_bytes)
+
+    def scales(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """(k, v) scales: PER_HEAD fp32 [Hkv]; PER_BLOCK fp16 [blocks, Hkv]."""
+        if self.scale_mode == ScaleMode.PER_HEAD:
+            n, dt = self.num_kv_heads * 4, torch.float32
+        elif self.scale_mode == ScaleMode.PER_BLOCK:
+            n, dt = self.num_blocks * self.num_kv_heads * 2, torch.float16
+        else:
+            raise ValueError("pool has no scales")
+        k = device_bytes(lib().gg_kv_k_scale_ptr(self.handle, layer), n).view(dt)
+        v = device_bytes(lib().gg_kv_v_scale_ptr(self.handle, layer), n).view(dt)
+        if self.scale_mode == ScaleMode.PER_BLOCK:
+            k, v = k.view(self.num_blocks, self.num_kv_heads), v.view(self.num_blocks, self.num_kv_heads)
+        return k, v
+
+    def set_head_scales(self, layer: int, k_scales, v_scales) -> None:
+        ks = (C.c_float * self.num_kv_heads)(*[float(x) for x in k_scales])
+        vs = (C.c_float * self.num_kv_heads)(*[float(x) for x in v_scales])
+        check(lib().gg_kv_set_head_scales(self.handle, layer, ks, vs), "gg_kv_set_head_scales")
+
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+               stream: Optional[torch.cuda.Stream] = None) -> None:
+        n = int(slot_mapping.numel())
+        if k.shape != v.shape or k.numel() != n * self.num_kv_heads * self.head_dim:
+            raise ValueError("k/v must be [n_rows, num_kv_heads, head_dim] matching slot_mapping")
+        check(lib().gg_kv_append(self.handle, layer, _dev(k, "k"), _dev(v, "v", k.dtype), int(dtype_of(k)),
+                                 _dev(slot_mapping, "slot_mapping", torch.int32), n, _stream(stream)),
+              "gg_kv_append")
+
+    def attention_workspace(self, num_seqs: int, rows_per_seq: int, num_q_heads: int,
+                            max_blocks_per_seq: int, partition_tokens: int = 0) -> torch.Tensor:
+        n = lib().gg_verify_attention_workspace_size(self.handle, num_seqs, rows_per_seq, num_q_heads,
+                                                     max_blocks_per_seq, partition_tokens)
+        return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
+
+    def attention(self, layer: int, q: torch.Tensor, out: torch.Tensor, ctx_lens: torch.Tensor,
+                  block_tables: torch.Tensor, scale: float, row_counts: Optional[torch.Tensor] = None,
+                  partition_tokens: int = 0, workspace: Optional[torch.Tensor] = None,
+                  stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """q, out: [num_seqs, rows_per_seq, num_q_heads, head_dim]."""
+        if q.dim() != 4 or q.shape[-1] != self.head_dim or out.shape != q.shape:
+            raise ValueError("q/out must be [num_seqs, rows_per_seq, num_q_heads, head_dim]")
+        B, R, Hq, _ = q.shape
+        if block_tables.dim() != 2 or block_tables.shape[0] != B:
+            raise ValueError("block_tables must be [num_seqs, max_blocks_per_seq]")
+        mb = block_tables.shape[1]
+        if workspace is None:
+            workspace = self.attention_workspace(B, R, Hq, mb, partition_tokens)
+        rc = _dev(row_counts, "row_counts", torch.int32) if row_counts is not None else None
+        check(lib().gg_verify_attention(
+            self.handle, layer, _dev(q, "q"), int(dtype_of(q)), _dev(out, "out"), int(dtype_of(out)),
+            _dev(ctx_lens, "ctx_lens", torch.int32), rc, _dev(block_tables, "block_tables", torch.int32),
+            mb, B, R, Hq, float(scale), partition_tokens, workspace.data_ptr(), workspace.numel(),
+            _stream(stream)), "gg_verify_attention")
+        return out
+
+
+def greedy_workspace(num_seqs: int, max_drafts: int, vocab: int) -> torch.Tensor:
+    n = lib().gg_accept_greedy_workspace_size(num_seqs, max_drafts, vocab)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
+
+
+def rejection_workspace(num_seqs: int, max_drafts: int, vocab: int) -> torch.Tensor:
+    n = lib().gg_accept_rejection_workspace_size(num_seqs, max_drafts, vocab)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
+
+
+def accept_greedy(logits: torch.Tensor, drafts: torch.Tensor, n_drafts: torch.Tensor,
+                  workspace: Optional[torch.Tensor] = None, out: Optional[tuple] = None,
+                  stream: Optional[torch.cuda.Stream] = None):
+    """logits [B, K+1, V]; drafts [B, K] int32; n_drafts [B] int32 -> (accepted [B], token [B])."""
+    B, R, V = logits.shape
+    K = R - 1
+    if drafts.shape != (B, K) and not (K == 0 and drafts.numel() == 0):
+        raise ValueError("drafts must be [num_seqs, max_drafts]")
+    if workspace is None:
+        workspace = greedy_workspace(B, K, V)
+    acc, tok = out if out is not None else (torch.empty(B, dtype=torch.int32, device="cuda"),
+                                            torch.empty(B, dtype=torch.int32, device="cuda"))
+    check(lib().gg_accept_greedy(
+        _dev(logits, "logits"), int(dtype_of(logits)), B, K, V,
+        drafts.data_ptr() if drafts.numel() else None, _dev(n_drafts, "n_drafts", torch.int32),
+        _dev(acc, "accepted", torch.int32), _dev(tok, "token", torch.int32), workspace.data_ptr(),
+        workspace.numel(), _stream(stream)), "gg_accept_greedy")
+    return acc, tok
+
+
+def accept_rejection(target_logits: torch.Tensor, drafts: torch.Tensor, n_drafts: torch.Tensor,
+                     uniforms: torch.Tensor, temperature: float, top_p: float = 1.0,
+                     draft_probs: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                     out: Optional[tuple] = None, stream: Optional[torch.cuda.Stream] = None):
+    """target_logits [B, K+1, V]; draft_probs [B, K, V] fp32 or None (one-hot drafter);
+    uniforms [B, K+1] fp32 -> (accepted [B], token [B])."""
+    B, R, V = target_logits.shape
+    K = R - 1
+    if uniforms.shape != (B, R):
+        raise ValueError("uniforms must be [num_seqs, max_drafts + 1]")
+    if draft_probs is not None and draft_probs.shape != (B, K, V):
+        raise ValueError("draft_probs must be [num_seqs, max_drafts, vocab]")
+    if workspace is None:
+        workspace = rejection_workspace(B, K, V)
+    acc, tok = out if out is not None else (torch.empty(B, dtype=torch.int32, device="cuda"),
+                                            torch.empty(B, dtype=torch.int32, device="cuda"))
+    dp = _dev(draft_probs, "draft_probs", torch.float32) if draft_probs is not None else None
+    check(lib().gg_accept_rejection(
+        _dev(target_logits, "target_logits"), int(dtype_of(target_logits)), dp, B, K, V,
+        drafts.data_ptr() if drafts.numel() else None, _dev(n_drafts, "n_drafts", torch.int32),
+        _dev(uniforms, "uniforms", torch.float32), float(temperature), float(top_p),
+        _dev(acc, "accepted", torch.int32), _dev(tok, "token", torch.int32), workspace.data_ptr(),
+        workspace.numel(), _stream(stream)), "gg_accept_rejection")
+    return acc, tok
+
+
+def ngram_draft(history: torch.Tensor, hist_len: torch.Tensor, n: int, max_drafts: int,
+                out: Optional[tuple] = None, stream: Optional[torch.cuda.Stream] = None):
+    """history [B, stride] int32, hist_len [B] int32 -> (drafts [B, K'], n_out [B]),
+    K' = max_drafts after NewNGramDrafter's normalisation (< 1 -> 4)."""
+    B, stride = history.shape
+    K = max_drafts if max_drafts >= 1 else 4
+    d, nn = out if out is not None else (torch.zeros(B, K, dtype=torch.int32, device="cuda"),
+                                         torch.empty(B, dtype=torch.int32, device="cuda"))
+    check(lib().gg_ngram_draft(_dev(history, "history", torch.int32), stride,
+                               _dev(hist_len, "hist_len", torch.int32), B, n, max_drafts,
+                               _dev(d, "drafts", torch.int32), _dev(nn, "n_out", torch.int32),
+                               _stream(stream)), "gg_ngram_draft")
+    return d, nn

@@ -1,0 +1,223 @@
+/*
+ * gg_verify.h — C ABI of the MI355X (gfx950) speculative-decoding verify path.
+ *
+ * This is the drop-in boundary a cgo `internal/backend/rocm` runner binds to.
+ * It keeps the conventions of the reference's C ABI:
+ *   - status codes mirror gollmgo_status_t (kernels/gollmgo_backend.h:21-27);
+ *   - a human-readable last-error string mirrors gollmgo_backend_last_error
+ *     (kernels/gollmgo_backend.h:43-44, backend.cu:20-31), kept per calling thread;
+ *   - opaque handles (gollmgo_kvcache_t, kernels/gollmgo_kvcache.h:16);
+ *   - NULL/invalid arguments return GG_ERR_INVALID, never abort; destroy(NULL) is OK.
+ *
+ * Differences from the reference, on purpose:
+ *   - every compute entry point takes DEVICE pointers and a hipStream_t (passed as
+ *     void*; NULL = the null stream) and is asynchronous. The reference copies host
+ *     buffers and synchronises on every call (gollmgo_kvcache.cu:65-159).
+ *   - no entry point allocates device memory. Scratch comes in as a caller-owned
+ *     workspace whose size is returned by the matching *_workspace_size() call.
+ *   - handles are not thread-safe: one engine thread drives one handle, as the
+ *     reference's single engine goroutine does (internal/engine/serving.go:160).
+ *
+ * KV layout in HBM (per layer, per K or V pool), chosen for 16-byte loads:
+ *   K: [num_blocks][num_kv_heads][block_size][head_dim]   (token-major inside a block)
+ *   V: [num_blocks][num_kv_heads][head_dim][block_size]   (dim-major inside a block)
+ * A reference slot index (internal/kvcache/block_table.go:39) still addresses a
+ * token: slot = physical_block * block_size + offset.
+ */
+#ifndef GG_VERIFY_H
+#define GG_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Mirrors gollmgo_status_t (kernels/gollmgo_backend.h:21-27). */
+typedef enum {
+    GG_OK = 0,
+    GG_ERR_HIP = 1,      /* GOLLMGO_ERR_CUDA */
+    GG_ERR_OOM = 2,
+    GG_ERR_INVALID = 3,
+    GG_ERR_INTERNAL = 4,
+} gg_status_t;
+
+/* Element types. FP8 is OCP E4M3 ("e4m3fn": no inf, NaN = S.1111.111). */
+typedef enum {
+    GG_DTYPE_F32 = 0,
+    GG_DTYPE_F16 = 1,
+    GG_DTYPE_BF16 = 2,
+    GG_DTYPE_FP8_E4M3 = 3,
+    GG_DTYPE_INT8 = 4,
+} gg_dtype_t;
+
+/* How a quantised KV pool is scaled (dequant: x = q * scale).
+ *   PER_HEAD : one fp32 scale per (layer, kv head) for K and one for V, set by
+ *              gg_kv_set_head_scales (the reference's amax/448 convention,
+ *              kernels/gollmgo_model.cu:415-427, applied per head).
+ *   PER_BLOCK: one fp16 scale per (layer, block, kv head) for K and for V,
+ *              maintained by gg_kv_append as the running amax/127 of the block
+ *              (int8 convention of kernels/gollmgo_model.cu:430-441). */
+typedef enum {
+    GG_SCALE_NONE = 0,
+    GG_SCALE_PER_HEAD = 1,
+    GG_SCALE_PER_BLOCK = 2,
+} gg_scale_mode_t;
+
+typedef struct gg_kv* gg_kv_t;
+
+/* Last error message of the calling thread ("" if none). */
+const char* gg_last_error(void);
+
+/* Library version string and the gfx target it was built for. */
+const char* gg_version(void);
+
+/* Select the HIP device used by later calls on this thread.
+ * Replaces gollmgo_backend_create's device selection (gollmgo_backend.h:30). */
+gg_status_t gg_set_device(int device_id);
+
+/* Block until all work queued on `stream` has finished. */
+gg_status_t gg_sync(void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged KV cache.
+ * Replaces gollmgo_kvcache_create / _k_layer_ptr / _v_layer_ptr / _destroy
+ * (kernels/gollmgo_kvcache.h:26-35,66). The reference takes num_slots and stores
+ * 2-byte elements only (gollmgo_kvcache.cu:39-40); here the pool is sized in
+ * blocks and the element type and scale mode are chosen at creation.
+ * ------------------------------------------------------------------------- */
+gg_status_t gg_kv_create(int num_layers, int num_blocks, int block_size,
+                         int num_kv_heads, int head_dim, gg_dtype_t dtype,
+                         gg_scale_mode_t scale_mode, gg_kv_t* out);
+gg_status_t gg_kv_destroy(gg_kv_t kv);
+
+/* Device pointers to one layer's pools (NULL on bad arguments). */
+void* gg_kv_k_layer_ptr(gg_kv_t kv, int layer);
+void* gg_kv_v_layer_ptr(gg_kv_t kv, int layer);
+/* PER_HEAD: float[num_kv_heads]; PER_BLOCK: uint16 (fp16 bits)[num_blocks][num_kv_heads]. */
+void* gg_kv_k_scale_ptr(gg_kv_t kv, int layer);
+void* gg_kv_v_scale_ptr(gg_kv_t kv, int layer);
+/* Bytes of one layer's K (or V) pool. */
+size_t gg_kv_layer_bytes(gg_kv_t kv);
+
+/* PER_HEAD only: upload host arrays k_scales[num_kv_heads], v_scales[num_kv_heads]
+ * (synchronous). Scales must be finite and > 0. */
+gg_status_t gg_kv_set_head_scales(gg_kv_t kv, int layer, const float* k_scales,
+                                  const float* v_scales);
+
+/* Draft-KV append: write n_rows new K/V rows of one layer into their slots,
+ * quantising on write for FP8/INT8 pools.
+ * Replaces gollmgo_kvcache_write (kernels/gollmgo_kvcache.h:41-45) and the
+ * paged_kv_write_{f16,bf16} kernels (kernels/gollmgo_paged_attn.cu:14-35,126-146).
+ *   k, v         : device [n_rows][num_kv_heads][head_dim] of src_dtype (F32/F16/BF16)
+ *   slot_mapping : device int32[n_rows]; slot = block*block_size + offset; a
+ *                  negative slot skips the row.
+ * PER_BLOCK pools: rows that land in the same block in one call must be adjacent
+ * in slot_mapping with increasing offsets (as BlockTable.Append produces them,
+ * internal/kvcache/block_table.go:24-42). Such a block's scale becomes
+ * max(old scale, amax(new rows)/127) rounded to fp16; rows already in the block
+ * are re-quantised to the new scale. Appends never target a block whose refcount
+ * is above one (the kvcache package only shares full blocks). */
+gg_status_t gg_kv_append(gg_kv_t kv, int layer, const void* k, const void* v,
+                         gg_dtype_t src_dtype, const int32_t* slot_mapping,
+                         int n_rows, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Multi-query paged attention over the k+1 verify rows (split-K "v2").
+ * Replaces gollmgo_kvcache_attention (kernels/gollmgo_kvcache.h:55-63) and the
+ * paged_attention_v1/v2 kernels (kernels/gollmgo_paged_attn.cu:38-119,234-384),
+ * generalised from one query per sequence to rows_per_seq causal query rows.
+ *   q           : device [num_seqs][rows_per_seq][num_q_heads][head_dim], q_dtype
+ *                 F32/F16/BF16
+ *   out         : device, same shape, out_dtype F32/F16/BF16
+ *   ctx_lens    : device int32[num_seqs], keys in the cache for each sequence
+ *                 INCLUDING its appended verify rows (Batch.SeqContextLens,
+ *                 internal/backend/runner.go:43-44)
+ *   row_counts  : device int32[num_seqs] or NULL (= rows_per_seq for all). Row j
+ *                 of sequence b sits at position ctx_lens[b]-row_counts[b]+j and
+ *                 attends to keys [0, that position] (causal rule of
+ *                 naive_attention, kernels/gollmgo_ops.cu:178). Rows j >=
+ *                 row_counts[b] are not written.
+ *   block_tables: device int32[num_seqs][max_blocks_per_seq] of physical blocks
+ *   scale       : softmax scale (1/sqrt(head_dim) in the reference)
+ *   partition_tokens: split-K partition length, a multiple of 64 (0 = auto).
+ * workspace must hold gg_verify_attention_workspace_size(...) bytes (may be 0). */
+size_t gg_verify_attention_workspace_size(gg_kv_t kv, int num_seqs, int rows_per_seq,
+                                          int num_q_heads, int max_blocks_per_seq,
+                                          int partition_tokens);
+gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
+                                void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                const int32_t* row_counts, const int32_t* block_tables,
+                                int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                int num_q_heads, float scale, int partition_tokens,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Greedy acceptance.
+ * Replaces Verify + argmax (internal/engine/speculative.go:68-84,
+ * internal/engine/sampling.go:75-85) as driven by emitSpeculative
+ * (internal/engine/serving.go:514-566) with a greedy sampler.
+ *   logits   : device [num_seqs][max_drafts+1][vocab] of F32/F16/BF16; row j scores
+ *              the token after position j (row 0 = current token).
+ *   drafts   : device int32[num_seqs][max_drafts]
+ *   n_drafts : device int32[num_seqs], each in [0, max_drafts]
+ * Outputs per sequence: out_accepted = longest prefix j with argmax(row j) ==
+ * drafts[j]; out_token = argmax(row out_accepted) (the corrected token, or the bonus
+ * token when every draft was accepted). argmax returns the first index of the
+ * maximum, skips NaN, and returns 0 when element 0 is NaN (sequential `>` scan).
+ * workspace: gg_accept_greedy_workspace_size bytes. */
+size_t gg_accept_greedy_workspace_size(int num_seqs, int max_drafts, int vocab);
+gg_status_t gg_accept_greedy(const void* logits, gg_dtype_t logits_dtype, int num_seqs,
+                             int max_drafts, int vocab, const int32_t* drafts,
+                             const int32_t* n_drafts, int32_t* out_accepted,
+                             int32_t* out_token, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Rejection-sampling acceptance (speculative sampling, Leviathan et al. 2023,
+ * Alg. 1) with the reference sampler's temperature and top-p rules
+ * (internal/engine/sampling.go:40-72,112-192). Not present in the reference.
+ *   target_logits: device [num_seqs][max_drafts+1][vocab], F32/F16/BF16
+ *   draft_probs  : device float[num_seqs][max_drafts][vocab], or NULL for a
+ *                  deterministic drafter (n-gram), i.e. q = one-hot(draft)
+ *   uniforms     : device float[num_seqs][max_drafts+1] in [0,1): element j < n
+ *                  decides draft j; element max_drafts drives the final draw
+ *   temperature  : > 0 (<= 1e-9 falls back to gg_accept_greedy semantics, as
+ *                  Sampler.Sample does at sampling.go:54-56)
+ *   top_p        : (0,1) enables the nucleus filter; otherwise disabled
+ * Probabilities are fixed-point: w_i = floor(exp_gg((l_i - max) * (1/T)) * 2^40)
+ * with the library's own exp (identical on host and device), so every sum and
+ * prefix sum is an exact integer and decisions are bit-reproducible. Nucleus
+ * order is (logit desc, index asc). Draft j is accepted iff
+ * u_j * q_j(x_j) * Zp < w(x_j) (doubles); on the first rejection the token is drawn
+ * from max(0, w - floor(q*Zp)); if all drafts pass, the bonus is drawn from row n.
+ * A draw picks the first index whose inclusive prefix sum exceeds floor(u*total).
+ * workspace: gg_accept_rejection_workspace_size bytes. */
+size_t gg_accept_rejection_workspace_size(int num_seqs, int max_drafts, int vocab);
+gg_status_t gg_accept_rejection(const void* target_logits, gg_dtype_t logits_dtype,
+                                const float* draft_probs, int num_seqs, int max_drafts,
+                                int vocab, const int32_t* drafts, const int32_t* n_drafts,
+                                const float* uniforms, float temperature, float top_p,
+                                int32_t* out_accepted, int32_t* out_token, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * n-gram draft lookup on the device.
+ * Replaces NGramDrafter.Draft (internal/engine/speculative.go:12-62): the table
+ * maps each (n-1)-gram of the history to the token that followed its LATEST
+ * occurrence; drafting chains up to max_drafts lookups of the running suffix.
+ *   history  : device int32[num_seqs][hist_stride]
+ *   hist_len : device int32[num_seqs]
+ *   n        : n-gram size; values < 2 become 2 (NewNGramDrafter), must be <= 9
+ *   max_drafts: values < 1 become 4 (NewNGramDrafter)
+ *   out_drafts: device int32[num_seqs][max_drafts]; out_n: device int32[num_seqs] */
+gg_status_t gg_ngram_draft(const int32_t* history, int hist_stride, const int32_t* hist_len,
+                           int num_seqs, int n, int max_drafts, int32_t* out_drafts,
+                           int32_t* out_n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GG_VERIFY_H */

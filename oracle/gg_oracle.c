@@ -1,0 +1,632 @@
+/*
+ * gg_oracle.c — CPU oracle of the speculative-decoding verify path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker / the timed
+ * CPU baseline; the product path never calls it.
+ *
+ * Each function restates the reference behaviour it cites, with plain loops and no
+ * cleverness, so that it can be checked by reading. The reference (Go + CUDA) cannot
+ * be built in this image (no Go toolchain, no nvcc), so nothing here is compiled
+ * from it.
+ *
+ * Parity pins (see tests/test_oracle.py):
+ *   ora_argmax / ora_verify / ora_ngram_draft / softmax / top-p / categorical:
+ *       the reference's Go known-answer tests (speculative_test.go, sampling_test.go)
+ *       plus brute force on tiny inputs.
+ *   ora_fp8_encode: exhaustive nearest-value search, cross-checked against
+ *       torch.float8_e4m3fn casts.
+ *   ora_attention: torch scaled_dot_product_attention in float64 with an explicit
+ *       causal mask, closed forms (one key -> V, equal keys -> mean of V).
+ *   ora_expf_fixed: error bound against libm exp (<= 2 ulp on the domain used).
+ *   ora_accept_rejection: invariants (one-hot q with p==q -> always accept; q==p ->
+ *       accept; distribution of the output token over many uniforms equals p).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ floats */
+
+float ora_bf16_decode(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float ora_f16_decode(uint16_t h) {
+    int s = (h >> 15) & 1, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    float v;
+    if (e == 0) v = ldexpf((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexpf((float)(m | 0x400), e - 25);
+    return s ? -v : v;
+}
+
+/* Round a float to the nearest fp16 value (ties to even), returned as float. */
+float ora_f16_round(float x) {
+    if (isnan(x) || isinf(x) || x == 0.f) return x;
+    int e;
+    float f = frexpf(x, &e); /* x = f * 2^e, |f| in [0.5, 1) */
+    float r;
+    if (e - 1 < -14) r = ldexpf(nearbyintf(ldexpf(x, 24)), -24); /* subnormal step 2^-24 */
+    else r = ldexpf(nearbyintf(ldexpf(f, 11)), e - 11);
+    if (fabsf(r) > 65504.f) r = copysignf(INFINITY, x);
+    return r;
+}
+
+/* OCP E4M3 (fn): bias 7, S.1111.111 = NaN, max finite 448. */
+float ora_fp8_decode(uint8_t b) {
+    int s = b >> 7, e = (b >> 3) & 0xf, m = b & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) v = ldexpf((float)m, -9);
+    else v = ldexpf((float)(8 + m), e - 10);
+    return s ? -v : v;
+}
+
+/* Nearest finite E4M3 value, ties to the even code (last mantissa bit 0),
+ * saturating at +-448 (the __NV_SATFINITE rule of kernels/gollmgo_model.cu:254):
+ * an exhaustive search over the 127 non-negative finite codes. */
+uint8_t ora_fp8_encode(float x) {
+    if (isnan(x)) return (uint8_t)(signbit(x) ? 0xFF : 0x7F);
+    uint8_t sign = signbit(x) ? 0x80 : 0;
+    double a = fabs((double)x);
+    int best = 0;
+    double best_d = INFINITY;
+    for (int c = 0; c <= 0x7E; ++c) {
+        double v = ora_fp8_decode((uint8_t)c);
+        double d = fabs(v - a);
+        if (d < best_d || (d == best_d && (c & 1) == 0)) {
+            best_d = d;
+            best = c;
+        }
+    }
+    return (uint8_t)(sign | best);
+}
+
+/* Symmetric int8: round half to even, clamp to +-127 (kernels/gollmgo_model.cu:258-268). */
+int8_t ora_int8_encode(float x) {
+    if (isnan(x)) return 0;
+    float r = nearbyintf(x); /* default rounding mode: to nearest, ties to even */
+    if (r > 127.f) r = 127.f;
+    if (r < -127.f) r = -127.f;
+    return (int8_t)r;
+}
+
+/* ------------------------------------------------------------ Go sampler */
+
+/* sampling.go:75-85: first index of the maximum, scanning with `>`. */
+int ora_argmax(const float* x, int n) {
+    int best = 0;
+    float bv = x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] > bv) {
+            bv = x[i];
+            best = i;
+        }
+    }
+    return best;
+}
+
+/* speculative.go:68-84 exactly: rows[nrows][V]. corrected = -1 when every draft is
+ * accepted and no extra row is given. */
+void ora_verify(const int32_t* drafts, int nd, const float* rows, int nrows, int V, int* accepted,
+                int* corrected) {
+    for (int i = 0; i < nd; ++i) {
+        if (i >= nrows) break;
+        int c = ora_argmax(rows + (size_t)i * V, V);
+        if (c != drafts[i]) {
+            *accepted = i;
+            *corrected = c;
+            return;
+        }
+    }
+    *accepted = nd;
+    *corrected = nrows > nd ? ora_argmax(rows + (size_t)nd * V, V) : -1;
+}
+
+/* emitSpeculative (serving.go:514-566) with a greedy sampler: Verify over the K
+ * draft rows, then the corrected token, or the bonus = argmax of row n. */
+void ora_accept_greedy(const float* logits, int B, int K, int V, const int32_t* drafts,
+                       const int32_t* n_drafts, int32_t* out_acc, int32_t* out_tok) {
+    for (int b = 0; b < B; ++b) {
+        int n = n_drafts[b];
+        if (n < 0) n = 0;
+        if (n > K) n = K;
+        const float* rows = logits + (size_t)b * (K + 1) * V;
+        int acc, cor;
+        ora_verify(drafts + (size_t)b * K, n, rows, n, V, &acc, &cor);
+        out_acc[b] = acc;
+        out_tok[b] = acc < n ? cor : ora_argmax(rows + (size_t)n * V, V);
+    }
+}
+
+/* softmax (sampling.go:112-136) in float64, -inf -> 0. */
+void ora_softmax_f64(const double* in, int n, double* out) {
+    double mx = in[0];
+    for (int i = 1; i < n; ++i)
+        if (in[i] > mx) mx = in[i];
+    double sum = 0;
+    for (int i = 0; i < n; ++i) {
+        if (isinf(in[i]) && in[i] < 0) out[i] = 0;
+        else {
+            out[i] = exp(in[i] - mx);
+            sum += out[i];
+        }
+    }
+    if (sum > 0)
+        for (int i = 0; i < n; ++i) out[i] /= sum;
+}
+
+typedef struct {
+    int idx;
+    double v;
+} ora_iv;
+
+static int cmp_desc_stable(const void* a, const void* b) {
+    const ora_iv* x = (const ora_iv*)a;
+    const ora_iv* y = (const ora_iv*)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->idx - y->idx;
+}
+
+/* topPFilter (sampling.go:139-173) with ties broken by lower index first (the
+ * reference's sort.Slice leaves tie order unspecified). */
+void ora_top_p_filter_f64(const double* probs, int n, double p, double* out) {
+    ora_iv* it = (ora_iv*)malloc(sizeof(ora_iv) * (size_t)n);
+    for (int i = 0; i < n; ++i) {
+        it[i].idx = i;
+        it[i].v = probs[i];
+        out[i] = 0;
+    }
+    qsort(it, (size_t)n, sizeof(ora_iv), cmp_desc_stable);
+    double cum = 0;
+    for (int k = 0; k < n; ++k) {
+        if (cum >= p && cum > 0) break;
+        out[it[k].idx] = it[k].v;
+        cum += it[k].v;
+    }
+    double s = 0;
+    for (int i = 0; i < n; ++i) s += out[i];
+    if (s > 0)
+        for (int i = 0; i < n; ++i) out[i] /= s;
+    free(it);
+}
+
+/* categoricalSample (sampling.go:176-192) with the uniform supplied. */
+int ora_categorical_f64(const double* probs, int n, double u) {
+    double cum = 0;
+    for (int i = 0; i < n; ++i) {
+        cum += probs[i];
+        if (u < cum) return i;
+    }
+    for (int i = n - 1; i >= 0; --i)
+        if (probs[i] > 0) return i;
+    return 0;
+}
+
+/* ------------------------------------------------------------ n-gram drafter */
+
+/* NGramDrafter.Draft (speculative.go:12-62) with an explicit hash map whose
+ * entries are overwritten in history order, so the latest occurrence wins. */
+typedef struct {
+    int32_t key[8];
+    int32_t val;
+    int used;
+} ora_slot;
+
+static uint64_t key_hash(const int32_t* k, int kl) {
+    uint64_t h = 1469598103934665603ull;
+    for (int i = 0; i < kl; ++i) {
+        h ^= (uint32_t)k[i];
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+int ora_ngram_draft(const int32_t* hist, int len, int n, int max_drafts, int32_t* out) {
+    if (n < 2) n = 2;
+    if (max_drafts < 1) max_drafts = 4;
+    if (n > 9) return -1;
+    if (len < n) return 0;
+    const int kl = n - 1;
+    size_t cap = 16;
+    while (cap < (size_t)len * 2 + 16) cap <<= 1;
+    ora_slot* tab = (ora_slot*)calloc(cap, sizeof(ora_slot));
+    for (int i = 0; i <= len - n; ++i) {
+        uint64_t h = key_hash(hist + i, kl) & (cap - 1);
+        while (tab[h].used && memcmp(tab[h].key, hist + i, sizeof(int32_t) * kl) != 0) h = (h + 1) & (cap - 1);
+        tab[h].used = 1;
+        memcpy(tab[h].key, hist + i, sizeof(int32_t) * kl);
+        tab[h].val = hist[i + kl];
+    }
+    int32_t suffix[8];
+    memcpy(suffix, hist + len - kl, sizeof(int32_t) * kl);
+    int cnt = 0;
+    while (cnt < max_drafts) {
+        uint64_t h = key_hash(suffix, kl) & (cap - 1);
+        int found = 0;
+        while (tab[h].used) {
+            if (memcmp(tab[h].key, suffix, sizeof(int32_t) * kl) == 0) {
+                found = 1;
+                break;
+            }
+            h = (h + 1) & (cap - 1);
+        }
+        if (!found) break;
+        int32_t next = tab[h].val;
+        out[cnt++] = next;
+        memmove(suffix, suffix + 1, sizeof(int32_t) * (kl - 1));
+        suffix[kl - 1] = next;
+    }
+    free(tab);
+    return cnt;
+}
+
+/* ------------------------------------------------- fixed-point acceptance */
+
+/* The acceptance rule's exponential: Cody-Waite reduction with ln2 = hi + lo and
+ * the degree-7 Taylor polynomial of e^r, every step an fmaf (correctly rounded). */
+float ora_expf_fixed(float x) {
+    if (!(x >= -80.0f)) return 0.0f;
+    if (x > 0.0f) x = 0.0f;
+    float kf = floorf(fmaf(x, 1.44269504088896341f, 0.5f));
+    float r = fmaf(kf, -0.693145751953125f, x);
+    r = fmaf(kf, -1.42860682030941723212e-6f, r);
+    float p = 1.98412698412698412698e-4f;
+    p = fmaf(p, r, 1.38888888888888888889e-3f);
+    p = fmaf(p, r, 8.33333333333333333333e-3f);
+    p = fmaf(p, r, 4.16666666666666666667e-2f);
+    p = fmaf(p, r, 1.66666666666666666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return p * ldexpf(1.0f, (int)kf);
+}
+
+uint64_t ora_weight(float l, float m, float inv_t) {
+    float x = (l - m) * inv_t;
+    float e = ora_expf_fixed(x);
+    return (uint64_t)floorf(e * 34359738368.0f); /* 2^35 */
+}
+
+typedef struct {
+    int idx;
+    float l;
+} ora_il;
+
+static int cmp_logit_desc(const void* a, const void* b) {
+    const ora_il* x = (const ora_il*)a;
+    const ora_il* y = (const ora_il*)b;
+    if (x->l > y->l) return -1;
+    if (x->l < y->l) return 1;
+    return x->idx - y->idx;
+}
+
+/* Nucleus-filtered fixed-point weights of one row: w_out[i] (0 outside), returns Zp. */
+static uint64_t row_weights(const float* row, int V, float inv_t, float top_p, uint64_t* w_out, ora_il* scratch) {
+    float m = -INFINITY;
+    for (int i = 0; i < V; ++i)
+        if (isfinite(row[i]) && row[i] > m) m = row[i];
+    if (!isfinite(m)) {
+        memset(w_out, 0, sizeof(uint64_t) * (size_t)V);
+        return 0;
+    }
+    uint64_t z = 0;
+    int nf = 0;
+    for (int i = 0; i < V; ++i) {
+        w_out[i] = isfinite(row[i]) ? ora_weight(row[i], m, inv_t) : 0;
+        z += w_out[i];
+        if (isfinite(row[i])) {
+            scratch[nf].idx = i;
+            scratch[nf].l = row[i] == 0.0f ? 0.0f : row[i];
+            ++nf;
+        }
+    }
+    if (!(top_p > 0.f && top_p < 1.f) || z == 0) return z;
+    /* topPFilter: walk in (logit desc, index asc) order; keep while the mass before
+     * the item is below p (cumulative >= p && cumulative > 0 stops the walk). */
+    uint64_t tp = (uint64_t)ceil((double)top_p * (double)z);
+    qsort(scratch, (size_t)nf, sizeof(ora_il), cmp_logit_desc);
+    uint64_t cum = 0;
+    int k = 0;
+    for (; k < nf; ++k) {
+        if (cum >= tp && cum > 0) break;
+        cum += w_out[scratch[k].idx];
+    }
+    for (; k < nf; ++k) w_out[scratch[k].idx] = 0;
+    return cum;
+}
+
+/* Speculative sampling (Leviathan et al. 2023, Alg. 1) over fixed-point weights:
+ *   accept draft j iff u_j * q_j(x_j) * Zp_j < w_j(x_j)   (doubles, left to right)
+ *   first rejection at row a: draw from r_i = max(0, w_i - floor(q_i * Zp_a));
+ *     if every r_i is 0, draw from w of row a itself;
+ *   all accepted: draw from w of row n;
+ *   draw(u, r): t = floor(u * sum r); first i with inclusive prefix > t; else the
+ *     last i with r_i > 0; else 0.
+ * logits [B][K+1][V] (fp32 values), dprobs [B][K][V] or NULL (one-hot q),
+ * uniforms [B][K+1] (element K drives the final draw). */
+void ora_accept_rejection(const float* logits, int B, int K, int V, const float* dprobs,
+                          const int32_t* drafts, const int32_t* n_drafts, const float* uniforms,
+                          float temperature, float top_p, int32_t* out_acc, int32_t* out_tok) {
+    const float inv_t = 1.0f / temperature;
+    uint64_t* w = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    uint64_t* r = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    ora_il* scratch = (ora_il*)malloc(sizeof(ora_il) * (size_t)V);
+    for (int b = 0; b < B; ++b) {
+        int n = n_drafts[b];
+        if (n < 0) n = 0;
+        if (n > K) n = K;
+        const float* lg = logits + (size_t)b * (K + 1) * V;
+        int a = n;
+        uint64_t zp = 0;
+        for (int j = 0; j < n; ++j) {
+            zp = row_weights(lg + (size_t)j * V, V, inv_t, top_p, w, scratch);
+            int x = drafts[(size_t)b * K + j];
+            int ok = 0;
+            if (x >= 0 && x < V) {
+                double q = dprobs ? (double)dprobs[((size_t)b * K + j) * V + x] : 1.0;
+                double u = (double)uniforms[(size_t)b * (K + 1) + j];
+                ok = u * q * (double)zp < (double)w[x];
+            }
+            if (!ok) {
+                a = j;
+                break;
+            }
+        }
+        zp = row_weights(lg + (size_t)a * V, V, inv_t, top_p, w, scratch);
+        uint64_t tot = 0;
+        int residual = a < n;
+        if (residual) {
+            int xr = drafts[(size_t)b * K + a];
+            for (int i = 0; i < V; ++i) {
+                uint64_t qf;
+                if (dprobs) {
+                    float qi = dprobs[((size_t)b * K + a) * V + i];
+                    qf = qi < 0.f ? 0 : (uint64_t)((double)qi * (double)zp);
+                } else {
+                    qf = i == xr ? zp : 0;
+                }
+                r[i] = w[i] > qf ? w[i] - qf : 0;
+                tot += r[i];
+            }
+        }
+        if (!residual || tot == 0) {
+            tot = 0;
+            for (int i = 0; i < V; ++i) {
+                r[i] = w[i];
+                tot += r[i];
+            }
+        }
+        int tok = 0;
+        if (tot > 0) {
+            double u = (double)uniforms[(size_t)b * (K + 1) + K];
+            uint64_t t = (uint64_t)(u * (double)tot);
+            uint64_t c = 0;
+            int found = -1;
+            for (int i = 0; i < V; ++i) {
+                c += r[i];
+                if (c > t) {
+                    found = i;
+                    break;
+                }
+            }
+            if (found < 0)
+                for (int i = V - 1; i >= 0; --i)
+                    if (r[i] > 0) {
+                        found = i;
+                        break;
+                    }
+            tok = found < 0 ? 0 : found;
+        }
+        out_acc[b] = a;
+        out_tok[b] = tok;
+    }
+    free(w);
+    free(r);
+    free(scratch);
+}
+
+/* ------------------------------------------------------------- KV cache */
+
+/* Pool element access for the block layouts
+ *   K[blk][Hkv][bs][D], V[blk][Hkv][D][bs]; dtype codes as gg_dtype_t
+ *   (0 f32, 1 f16, 2 bf16, 3 fp8-e4m3, 4 int8). */
+static size_t k_off(int blk, int h, int o, int d, int H, int bs, int D) {
+    return (((size_t)blk * H + h) * bs + o) * D + d;
+}
+static size_t v_off(int blk, int h, int o, int d, int H, int bs, int D) {
+    return (((size_t)blk * H + h) * D + d) * bs + o;
+}
+static float raw_elem(const uint8_t* p, int dt, size_t i) {
+    switch (dt) {
+        case 0: {
+            float f;
+            memcpy(&f, p + 4 * i, 4);
+            return f;
+        }
+        case 1: {
+            uint16_t h;
+            memcpy(&h, p + 2 * i, 2);
+            return ora_f16_decode(h);
+        }
+        case 2: {
+            uint16_t h;
+            memcpy(&h, p + 2 * i, 2);
+            return ora_bf16_decode(h);
+        }
+        case 3: return ora_fp8_decode(p[i]);
+        case 4: return (float)(int8_t)p[i];
+    }
+    return 0.f;
+}
+
+/* Quantised append for 1-byte pools (the float pools are written with numpy casts
+ * by the Python side). Mirrors the rules stated in gg_verify.h:
+ *   fp8 (dt 3): q = E4M3_sat(x * inv_scale[h]) with inv_scale = 1/scale (fp32);
+ *   int8 (dt 4): per block b and head h, new scale = max(old, fp16(amax(new rows)/127))
+ *     where old = 0 if the block's first new row sits at offset 0; existing tokens are
+ *     re-quantised as int8(q_old * old * (1/new)) when the scale changes.
+ * rows: k,v [n][H][D] fp32; f16 scales are held as float values here. */
+void ora_kv_append_q(uint8_t* kc, uint8_t* vc, int dt, int H, int D, int bs, const float* k,
+                     const float* v, const int32_t* slots, int n, const float* k_inv,
+                     const float* v_inv, float* k_bscale, float* v_bscale) {
+    if (dt == 3) {
+        for (int r = 0; r < n; ++r) {
+            if (slots[r] < 0) continue;
+            int blk = slots[r] / bs, o = slots[r] % bs;
+            for (int h = 0; h < H; ++h)
+                for (int d = 0; d < D; ++d) {
+                    size_t s = ((size_t)r * H + h) * D + d;
+                    kc[k_off(blk, h, o, d, H, bs, D)] = ora_fp8_encode(k[s] * k_inv[h]);
+                    vc[v_off(blk, h, o, d, H, bs, D)] = ora_fp8_encode(v[s] * v_inv[h]);
+                }
+        }
+        return;
+    }
+    /* int8 per block: process runs of adjacent rows in the same block. */
+    int r = 0;
+    while (r < n) {
+        if (slots[r] < 0) {
+            ++r;
+            continue;
+        }
+        int blk = slots[r] / bs;
+        int e = r;
+        while (e < n && slots[e] >= 0 && slots[e] / bs == blk) ++e;
+        int lead_off = slots[r] % bs;
+        for (int h = 0; h < H; ++h) {
+            for (int which = 0; which < 2; ++which) {
+                const float* src = which ? v : k;
+                uint8_t* pool = which ? vc : kc;
+                float* sc = which ? v_bscale : k_bscale;
+                float am = 0.f;
+                for (int rr = r; rr < e; ++rr)
+                    for (int d = 0; d < D; ++d) {
+                        float a = fabsf(src[((size_t)rr * H + h) * D + d]);
+                        if (a == a && a > am) am = a;
+                    }
+                float old_s = lead_off == 0 ? 0.f : sc[(size_t)blk * H + h];
+                float cand = ora_f16_round(am / 127.0f);
+                float new_s = cand > old_s ? cand : old_s;
+                float inv = new_s > 0.f ? 1.0f / new_s : 0.f;
+                if (new_s != old_s)
+                    for (int o = 0; o < lead_off; ++o)
+                        for (int d = 0; d < D; ++d) {
+                            size_t i = which ? v_off(blk, h, o, d, H, bs, D) : k_off(blk, h, o, d, H, bs, D);
+                            pool[i] = (uint8_t)ora_int8_encode(((float)(int8_t)pool[i] * old_s) * inv);
+                        }
+                for (int rr = r; rr < e; ++rr) {
+                    int o = slots[rr] % bs;
+                    for (int d = 0; d < D; ++d) {
+                        size_t i = which ? v_off(blk, h, o, d, H, bs, D) : k_off(blk, h, o, d, H, bs, D);
+                        pool[i] = (uint8_t)ora_int8_encode(src[((size_t)rr * H + h) * D + d] * inv);
+                    }
+                }
+                sc[(size_t)blk * H + h] = new_s;
+            }
+        }
+        r = e;
+    }
+}
+
+/* Textbook softmax attention in float64 for the verify rows
+ * (kernels/gollmgo_paged_attn.cu:38-119 per row; causal rule of
+ * kernels/gollmgo_ops.cu:178 across the R rows of a sequence).
+ *   q [B][R][Hq][D] fp32 values; out [B][R][Hq][D] fp32.
+ *   kc/vc pools of dtype dt; k_scale/v_scale: per-head [H] (dt 3) or per-block
+ *   [blocks][H] (dt 4) as floats, NULL otherwise.
+ *   row_counts may be NULL (all R). Rows j >= row_counts[b] are left untouched. */
+void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t* vc, int dt, int H,
+                   int D, int bs, const float* k_scale, const float* v_scale, const int32_t* ctx_lens,
+                   const int32_t* row_counts, const int32_t* block_tables, int max_blocks, int B, int R,
+                   int Hq, float scale, int threads) {
+    const int G = Hq / H;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#else
+    (void)threads;
+#endif
+    for (int b = 0; b < B; ++b) {
+        const int ctx = ctx_lens[b];
+        const int nr = row_counts ? row_counts[b] : R;
+        double* sc = (double*)malloc(sizeof(double) * (size_t)(ctx > 0 ? ctx : 1));
+        double* acc = (double*)malloc(sizeof(double) * (size_t)D);
+        for (int j = 0; j < nr; ++j) {
+            const int pos = ctx - nr + j;
+            for (int hq = 0; hq < Hq; ++hq) {
+                const int h = hq / G;
+                const float* qv = q + (((size_t)b * R + j) * Hq + hq) * D;
+                double mx = -INFINITY;
+                for (int t = 0; t <= pos; ++t) {
+                    int blk = block_tables[(size_t)b * max_blocks + t / bs], o = t % bs;
+                    double ks = dt == 3 ? k_scale[h] : dt == 4 ? k_scale[(size_t)blk * H + h] : 1.0;
+                    double dot = 0;
+                    for (int d = 0; d < D; ++d)
+                        dot += (double)qv[d] * (double)raw_elem(kc, dt, k_off(blk, h, o, d, H, bs, D));
+                    sc[t] = dot * ks * (double)scale;
+                    if (sc[t] > mx) mx = sc[t];
+                }
+                double sum = 0;
+                for (int t = 0; t <= pos; ++t) {
+                    sc[t] = exp(sc[t] - mx);
+                    sum += sc[t];
+                }
+                for (int d = 0; d < D; ++d) acc[d] = 0;
+                for (int t = 0; t <= pos; ++t) {
+                    int blk = block_tables[(size_t)b * max_blocks + t / bs], o = t % bs;
+                    double vs = dt == 3 ? v_scale[h] : dt == 4 ? v_scale[(size_t)blk * H + h] : 1.0;
+                    double p = sc[t] / sum * vs;
+                    for (int d = 0; d < D; ++d)
+                        acc[d] += p * (double)raw_elem(vc, dt, v_off(blk, h, o, d, H, bs, D));
+                }
+                float* ov = out + (((size_t)b * R + j) * Hq + hq) * D;
+                for (int d = 0; d < D; ++d) ov[d] = (float)acc[d];
+            }
+        }
+        free(sc);
+        free(acc);
+    }
+}
+
+/* ------------------------------------------------------- array helpers */
+
+void ora_fp8_encode_n(const float* x, uint8_t* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = ora_fp8_encode(x[i]);
+}
+void ora_fp8_decode_n(const uint8_t* x, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = ora_fp8_decode(x[i]);
+}
+void ora_int8_encode_n(const float* x, int8_t* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = ora_int8_encode(x[i]);
+}
+void ora_f16_round_n(const float* x, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = ora_f16_round(x[i]);
+}
+void ora_expf_fixed_n(const float* x, float* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = ora_expf_fixed(x[i]);
+}
+/* Greedy/rejection/n-gram over a batch, timed as the CPU baseline. */
+void ora_ngram_draft_batch(const int32_t* hist, int stride, const int32_t* lens, int B, int n, int K,
+                           int32_t* out, int32_t* out_n, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#else
+    (void)threads;
+#endif
+    for (int b = 0; b < B; ++b) {
+        int c = ora_ngram_draft(hist + (size_t)b * stride, lens[b], n, K, out + (size_t)b * (K < 1 ? 4 : K));
+        out_n[b] = c < 0 ? 0 : c;
+    }
+}

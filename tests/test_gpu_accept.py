@@ -1,0 +1,154 @@
+"""GPU parity: greedy and rejection acceptance, bit-exact against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+import gollmgo_amd.verify as gv
+from helpers import say
+from oracle import oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+TD = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def logits_case(B, K, V, dt, seed, sd=2.0, match_rate=0.6):
+    """Logits ~ N(0, sd) in dtype dt; drafts copy the row argmax with probability match_rate
+    so accepted lengths spread over [0, K]."""
+    rng = np.random.default_rng(seed)
+    lg = torch.from_numpy(rng.normal(0, sd, (B, K + 1, V)).astype(np.float32)).to(TD[dt])
+    host = lg.float().numpy()
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    for b in range(B):
+        for j in range(K):
+            if rng.random() < match_rate:
+                drafts[b, j] = ora.argmax(host[b, j])
+    n = rng.integers(0, K + 1, B).astype(np.int32)
+    return lg, host, drafts, n
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", [(4, 4, 32000), (32, 4, 128256), (8, 8, 128256), (3, 0, 1000), (5, 2, 4099)])
+def test_greedy_matches_oracle(gpu, dt, shape):
+    B, K, V = shape
+    say(f"greedy dt={dt} shape={shape}")
+    lg, host, drafts, n = logits_case(B, K, V, dt, seed=B * 7 + K + V % 97)
+    acc, tok = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
+    torch.cuda.synchronize()
+    ea, et = ora.accept_greedy(host, drafts, n)
+    assert np.array_equal(acc.cpu().numpy(), ea)
+    assert np.array_equal(tok.cpu().numpy(), et)
+
+
+def test_greedy_ties_nan_and_negative_zero(gpu):
+    say("greedy ties/nan")
+    V = 9000
+    rows = np.zeros((6, 2, V), np.float32)
+    rows[0, 0, [5, 4000, 8999]] = 3.0                 # tie across segments -> 5
+    rows[1, 0, 0] = np.nan; rows[1, 0, 7] = 9          # NaN at index 0 -> 0
+    rows[2, 0, :] = np.nan; rows[2, 0, 8000] = 1       # NaN elsewhere never wins -> 8000
+    rows[3, 0, :] = -np.inf                            # all -inf -> 0
+    rows[4, 0, 10] = -0.0                              # -0 == +0 -> first index 0
+    rows[5, 0, :] = -1; rows[5, 0, 4097] = 2; rows[5, 0, 4096] = 2  # segment boundary tie -> 4096
+    drafts = np.array([[5], [0], [8000], [0], [0], [4096]], np.int32)
+    n = np.ones(6, np.int32)
+    for dt in ("f32", "bf16", "f16"):
+        lg = torch.from_numpy(rows).to(TD[dt])
+        acc, tok = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
+        torch.cuda.synchronize()
+        ea, et = ora.accept_greedy(lg.float().numpy(), drafts, n)
+        assert np.array_equal(acc.cpu().numpy(), ea), dt
+        assert np.array_equal(tok.cpu().numpy(), et), dt
+        assert acc.cpu().tolist() == [1, 1, 1, 1, 1, 1]
+
+
+def test_greedy_unaligned_rows(gpu):
+    """Odd vocab (rows not 16-byte aligned) takes the scalar path."""
+    say("greedy unaligned")
+    lg, host, drafts, n = logits_case(7, 3, 5001, "bf16", seed=99)
+    acc, tok = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
+    torch.cuda.synchronize()
+    ea, et = ora.accept_greedy(host, drafts, n)
+    assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
+
+
+def rejection_case(B, K, V, dt, seed, with_q, sd=2.0):
+    rng = np.random.default_rng(seed)
+    lg, host, drafts, n = logits_case(B, K, V, dt, seed, sd=sd, match_rate=0.8)
+    q = None
+    if with_q:
+        # Draft distributions: a sharpened copy of the target row, so acceptances are frequent.
+        qn = torch.softmax(torch.from_numpy(host[:, :K] * 1.5), dim=-1).numpy().astype(np.float32)
+        q = np.ascontiguousarray(qn)
+        for b in range(B):
+            for j in range(K):
+                if rng.random() < 0.7:
+                    drafts[b, j] = int(np.argmax(q[b, j]))
+    u = rng.random((B, K + 1)).astype(np.float32)
+    return lg, host, drafts, n, q, u
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("with_q", [False, True])
+@pytest.mark.parametrize("top_p", [1.0, 0.95, 0.5])
+def test_rejection_matches_oracle(gpu, dt, with_q, top_p):
+    B, K, V = 6, 5, 128256
+    say(f"rejection dt={dt} q={with_q} top_p={top_p}")
+    lg, host, drafts, n, q, u = rejection_case(B, K, V, dt, seed=int(top_p * 100) + with_q, with_q=with_q)
+    acc, tok = gv.accept_rejection(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(),
+                                   torch.from_numpy(u).cuda(), 0.8, top_p,
+                                   draft_probs=torch.from_numpy(q).cuda() if q is not None else None)
+    torch.cuda.synchronize()
+    ea, et = ora.accept_rejection(host, drafts, n, u, 0.8, top_p, q)
+    print("  accepted", acc.cpu().tolist(), "of", n.tolist())
+    assert np.array_equal(acc.cpu().numpy(), ea)
+    assert np.array_equal(tok.cpu().numpy(), et)
+
+
+def test_rejection_ties_in_nucleus(gpu):
+    """Heavily tied bf16 logits: the nucleus boundary cuts through a tie group."""
+    say("rejection tied nucleus")
+    rng = np.random.default_rng(21)
+    B, K, V = 8, 2, 20000
+    vals = rng.integers(-3, 3, (B, K + 1, V)).astype(np.float32)
+    lg = torch.from_numpy(vals).to(torch.bfloat16)
+    host = lg.float().numpy()
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    n = np.full(B, K, np.int32)
+    u = rng.random((B, K + 1)).astype(np.float32)
+    for top_p in (0.3, 0.77, 0.999):
+        acc, tok = gv.accept_rejection(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(),
+                                       torch.from_numpy(u).cuda(), 1.0, top_p)
+        torch.cuda.synchronize()
+        ea, et = ora.accept_rejection(host, drafts, n, u, 1.0, top_p)
+        assert np.array_equal(acc.cpu().numpy(), ea), top_p
+        assert np.array_equal(tok.cpu().numpy(), et), top_p
+
+
+def test_rejection_small_temperature_is_greedy(gpu):
+    say("rejection T->0")
+    lg, host, drafts, n = logits_case(5, 3, 3000, "f32", seed=5)
+    u = np.full((5, 4), 0.5, np.float32)
+    acc, tok = gv.accept_rejection(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(),
+                                   torch.from_numpy(u).cuda(), 1e-12)
+    torch.cuda.synchronize()
+    ea, et = ora.accept_greedy(host, drafts, n)
+    assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
+
+
+def test_rejection_invalid_and_nonfinite(gpu):
+    say("rejection invalid drafts / non-finite logits")
+    rng = np.random.default_rng(8)
+    B, K, V = 4, 2, 5000
+    host = rng.normal(0, 1, (B, K + 1, V)).astype(np.float32)
+    host[0, 0, :] = -np.inf                    # no finite logit in a row
+    host[1, :, 17] = np.nan
+    host[2, :, 3] = np.inf
+    drafts = np.array([[1, 2], [17, 3], [V + 5, 1], [-1, 0]], np.int32)
+    n = np.array([2, 2, 2, 1], np.int32)
+    u = rng.random((B, K + 1)).astype(np.float32)
+    acc, tok = gv.accept_rejection(torch.from_numpy(host).cuda(), torch.from_numpy(drafts).cuda(),
+                                   torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda(), 0.7, 0.9)
+    torch.cuda.synchronize()
+    ea, et = ora.accept_rejection(host, drafts, n, u, 0.7, 0.9)
+    assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)

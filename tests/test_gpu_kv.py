@@ -1,0 +1,270 @@
+"""GPU parity: draft-KV append (bit-exact) and verify attention
+against the CPU oracle, through the C ABI."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gollmgo_amd._lib import DType
+from gollmgo_amd.verify import KVCache
+from gollmgo_amd.workloads import CONFIGS, build_layout, scaled
+from helpers import PoolMirror, TOL, append_rows, glibc_rand_uniform, per_head_amax_scales, rel_err_per_vector, say
+from oracle import oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"f32": DType.F32, "f16": DType.F16, "bf16": DType.BF16, "fp8": DType.FP8_E4M3, "int8": DType.INT8}
+
+
+def make_cache(dt, H, D, bs, nb, layers=1):
+    return KVCache(layers, nb, bs, H, D, DTYPES[dt])
+
+
+# ------------------------------------------------------------------ append
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "fp8", "int8"])
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+def test_append_bit_exact(gpu, dt, src):
+    say(f"append dt={dt} src={src}")
+    H, D, bs, nb = 4, 128, 16, 40
+    kv = make_cache(dt, H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    rng = np.random.default_rng(1)
+    if dt == "fp8":
+        ks = np.array([0.01, 0.02, 0.005, 0.03], np.float32)
+        vs = np.array([0.02, 0.01, 0.04, 0.015], np.float32)
+        kv.set_head_scales(0, ks, vs)
+        mirror.set_head_scales(ks, vs)
+    perm = rng.permutation(nb)
+    # Three calls: whole blocks, then partial runs, then single rows into partly filled blocks
+    # (int8: later rows grow the block scale and re-quantise earlier rows).
+    slots1 = np.concatenate([perm[b] * bs + np.arange(bs) for b in range(6)]).astype(np.int32)
+    slots2 = np.concatenate([perm[6] * bs + np.arange(5), perm[7] * bs + np.arange(9), [-1]]).astype(np.int32)
+    slots3 = np.array([perm[6] * bs + 5, perm[6] * bs + 6, perm[7] * bs + 9, perm[8] * bs], np.int32)
+    for i, (slots, sd) in enumerate([(slots1, 1.0), (slots2, 2.0), (slots3, 8.0)]):
+        k = rng.normal(0, sd, (len(slots), H, D)).astype(np.float32)
+        v = rng.normal(0, sd, (len(slots), H, D)).astype(np.float32)
+        append_rows(kv, mirror, k, v, slots, src)
+        mirror.compare_with_device()
+    kv.close()
+
+
+# ------------------------------------------------------------------ attention
+
+def run_attention_case(dt, B, R, Hq, H, D, bs, ctx, partition=0, src="f32", seed=0, q_dt="f32",
+                       row_counts=None, kv_sd=1.0):
+    rng = np.random.default_rng(seed)
+    keys = np.asarray(ctx, np.int32) + R
+    nbs = [(int(k) + bs - 1) // bs for k in keys]
+    max_blocks = max(nbs)
+    nb = sum(nbs) + 4
+    perm = rng.permutation(nb)
+    bt = np.zeros((B, max_blocks), np.int32)
+    p = 0
+    for b in range(B):
+        bt[b, :nbs[b]] = perm[p:p + nbs[b]]
+        p += nbs[b]
+    kv = make_cache(dt, H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    slots = np.concatenate([bt[b, np.arange(keys[b]) // bs] * bs + np.arange(keys[b]) % bs for b in range(B)]).astype(np.int32)
+    kk = rng.normal(0, kv_sd, (len(slots), H, D)).astype(np.float32)
+    vv = rng.normal(0, kv_sd, (len(slots), H, D)).astype(np.float32)
+    if dt == "fp8":
+        ks, vs = per_head_amax_scales(kk), per_head_amax_scales(vv)
+        kv.set_head_scales(0, ks, vs)
+        mirror.set_head_scales(ks, vs)
+    append_rows(kv, mirror, kk, vv, slots, src)
+    mirror.sync_from_device()
+    q = rng.normal(0, 1, (B, R, Hq, D)).astype(np.float32)
+    qt = torch.from_numpy(q).to({"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[q_dt]).cuda()
+    qh = qt.float().cpu().numpy()
+    out = torch.zeros(B, R, Hq, D, dtype=torch.float32, device="cuda")
+    rc_t = torch.from_numpy(np.asarray(row_counts, np.int32)).cuda() if row_counts is not None else None
+    if row_counts is not None:
+        keys = np.asarray(ctx, np.int32) + np.asarray(row_counts, np.int32)
+    scale = 1.0 / math.sqrt(D)
+    kv.attention(0, qt, out, torch.from_numpy(keys).cuda(), torch.from_numpy(bt).cuda(), scale,
+                 row_counts=rc_t, partition_tokens=partition)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ksc, vsc = mirror.scales_for_oracle()
+    ref = ora.attention(qh, mirror.kc, mirror.vc, dt, H, D, bs, keys, bt, scale, ksc, vsc,
+                        row_counts=row_counts)
+    if row_counts is not None:
+        mask = np.arange(R)[None, :] < np.asarray(row_counts)[:, None]
+        got, ref = got[mask], ref[mask]
+    kv.close()
+    return rel_err_per_vector(got, ref)
+
+
+MFMA_SHAPES = [
+    # (B, R, Hq, H, ctx) with D=128, bs=16 -> MFMA path (G*R <= 64)
+    (3, 5, 24, 8, [40, 700, 1500]),          # 3B geometry, 1 row tile
+    (4, 6, 32, 8, [100, 1030, 2047, 64]),    # 8B geometry, 2 row tiles
+    (2, 9, 32, 8, [5000, 777]),              # config-4 geometry, 3 row tiles
+    (2, 16, 16, 4, [300, 129]),              # 4 row tiles
+    (2, 1, 8, 8, [31, 65]),                  # decode-only (R=1)
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "fp8", "int8"])
+@pytest.mark.parametrize("shape", range(len(MFMA_SHAPES)))
+def test_attention_mfma_path(gpu, dt, shape):
+    B, R, Hq, H, ctx = MFMA_SHAPES[shape]
+    for part in (0, 256):
+        say(f"attention mfma dt={dt} shape={MFMA_SHAPES[shape]} partition={part}")
+        err = run_attention_case(dt, B, R, Hq, H, 128, 16, ctx, partition=part, src="bf16", q_dt="bf16", seed=shape)
+        print(f"  rel err {err:.2e}")
+        assert err <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "fp8", "int8"])
+def test_attention_generic_path(gpu, dt):
+    # head_dim 64 (config 1 geometry), head_dim 16 with block size 4, and G*R > 64 rows.
+    for (B, R, Hq, H, D, bs, ctx) in [(4, 5, 8, 2, 64, 16, [64, 128, 192, 256]),
+                                      (2, 3, 4, 4, 16, 4, [8, 30]),
+                                      (2, 5, 32, 2, 128, 16, [600, 90])]:
+        for part in (0, 64):
+            say(f"attention generic dt={dt} shape={(B, R, Hq, H, D, bs, ctx)} partition={part}")
+            err = run_attention_case(dt, B, R, Hq, H, D, bs, ctx, partition=part, seed=D)
+            print(f"  rel err {err:.2e}")
+            assert err <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp8"])
+def test_attention_ragged_rows(gpu, dt):
+    """Sequences with fewer drafts than max (row_counts) only write their own rows."""
+    say(f"attention ragged dt={dt}")
+    err = run_attention_case(dt, 3, 6, 32, 8, 128, 16, [300, 1000, 17], row_counts=[6, 1, 3], src="bf16",
+                             q_dt="bf16", seed=7)
+    assert err <= TOL[dt]
+
+
+def test_attention_reference_paged_vs_naive_inputs(gpu):
+    """The reference's test_paged_vs_naive inputs (srand(42), 9 tokens, 4 heads, D=16,
+    block size 4, identity slots; kernels/gollmgo_paged_attn_test.cu:39-217), fp16 pool."""
+    say("attention reference paged_vs_naive inputs")
+    T, Hq, H, D, bs = 9, 4, 4, 16, 4
+    u = glibc_rand_uniform(42, T * Hq * D + 2 * T * H * D)
+    q_all = u[:T * Hq * D].reshape(T, Hq, D)
+    k = u[T * Hq * D:T * Hq * D + T * H * D].reshape(T, H, D)
+    v = u[T * Hq * D + T * H * D:].reshape(T, H, D)
+    kv = make_cache("f16", H, D, bs, 3)
+    mirror = PoolMirror(kv)
+    append_rows(kv, mirror, k, v, np.arange(T, dtype=np.int32), "f16")
+    q = ora.round_f16(q_all[T - 1:T]).reshape(1, 1, Hq, D)
+    out = torch.zeros(1, 1, Hq, D, dtype=torch.float32, device="cuda")
+    bt = np.array([[0, 1, 2]], np.int32)
+    kv.attention(0, torch.from_numpy(q).half().cuda(), out, torch.tensor([T], dtype=torch.int32, device="cuda"),
+                 torch.from_numpy(bt).cuda(), 1.0 / math.sqrt(D))
+    torch.cuda.synchronize()
+    ref = ora.attention(q, mirror.kc, mirror.vc, "f16", H, D, bs, np.array([T], np.int32), bt, 1 / math.sqrt(D))
+    assert rel_err_per_vector(out.cpu().numpy(), ref) <= 2e-3
+    # The reference's own bar: |paged - naive| <= 0.05 absolute.
+    assert np.abs(out.cpu().numpy() - ref).max() <= 0.05
+    kv.close()
+
+
+V2_SWEEP = [(256, 4, 4, 64), (2048, 8, 8, 64), (4096, 8, 2, 64), (4096, 16, 8, 128), (8192, 8, 8, 64)]
+
+
+@pytest.mark.parametrize("case", V2_SWEEP)
+@pytest.mark.parametrize("R", [1, 5])
+def test_attention_reference_v2_sweep_inputs(gpu, case, R):
+    """The reference's v2 parity sweep shapes and inputs (srand(4242+seq+7H+KV),
+    256-token partitions; kernels/gollmgo_paged_attn_test.cu:361-510), fp16 pool,
+    extended to R verify rows."""
+    S, Hq, H, D = case
+    say(f"attention reference v2 sweep {case} R={R}")
+    seed = 4242 + S + Hq * 7 + H
+    n = R * Hq * D + 2 * S * H * D
+    u = glibc_rand_uniform(seed, n)
+    q = ora.round_f16(u[:R * Hq * D]).reshape(1, R, Hq, D)
+    k = u[R * Hq * D:R * Hq * D + S * H * D].reshape(S, H, D)
+    v = u[R * Hq * D + S * H * D:].reshape(S, H, D)
+    bs = 16
+    nb = (S + bs - 1) // bs
+    kv = make_cache("f16", H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    append_rows(kv, mirror, k, v, np.arange(S, dtype=np.int32), "f16")
+    bt = np.arange(nb, dtype=np.int32)[None]
+    out = torch.zeros(1, R, Hq, D, dtype=torch.float32, device="cuda")
+    keys = np.array([S], np.int32)
+    kv.attention(0, torch.from_numpy(q).half().cuda(), out, torch.from_numpy(keys).cuda(), torch.from_numpy(bt).cuda(),
+                 1 / math.sqrt(D), partition_tokens=256)
+    torch.cuda.synchronize()
+    ref = ora.attention(q, mirror.kc, mirror.vc, "f16", H, D, bs, keys, bt, 1 / math.sqrt(D))
+    assert rel_err_per_vector(out.cpu().numpy(), ref) <= 2e-3
+    assert np.abs(out.cpu().numpy() - ref).max() <= 0.1  # the reference's v2-vs-v1 bar
+    kv.close()
+
+
+@pytest.mark.parametrize("out_dt", ["bf16", "f16"])
+def test_attention_low_precision_output(gpu, out_dt):
+    """bf16/f16 outputs equal the fp32 output rounded once."""
+    say(f"attention output dtype {out_dt}")
+    rng = np.random.default_rng(3)
+    B, R, Hq, H, D, bs = 2, 5, 24, 8, 128, 16
+    ctx = [900, 40]
+    keys = np.asarray(ctx, np.int32) + R
+    nbs = [(int(k) + bs - 1) // bs for k in keys]
+    bt = np.zeros((B, max(nbs)), np.int32)
+    bt[0, :nbs[0]] = np.arange(nbs[0])
+    bt[1, :nbs[1]] = nbs[0] + np.arange(nbs[1])
+    kv = make_cache("bf16", H, D, bs, sum(nbs))
+    slots = np.concatenate([bt[b, np.arange(keys[b]) // bs] * bs + np.arange(keys[b]) % bs for b in range(B)])
+    kv.append(0, torch.randn(len(slots), H, D, dtype=torch.bfloat16, device="cuda"),
+              torch.randn(len(slots), H, D, dtype=torch.bfloat16, device="cuda"),
+              torch.from_numpy(slots.astype(np.int32)).cuda())
+    q = torch.randn(B, R, Hq, D, dtype=torch.bfloat16, device="cuda")
+    o32 = torch.zeros(B, R, Hq, D, dtype=torch.float32, device="cuda")
+    olo = torch.zeros(B, R, Hq, D, dtype={"bf16": torch.bfloat16, "f16": torch.float16}[out_dt], device="cuda")
+    args = (torch.from_numpy(keys).cuda(), torch.from_numpy(bt).cuda(), 1 / math.sqrt(D))
+    kv.attention(0, q, o32, *args)
+    kv.attention(0, q, olo, *args)
+    torch.cuda.synchronize()
+    assert torch.equal(o32.to(olo.dtype), olo)
+    kv.close()
+
+
+def test_attention_config_layouts(gpu):
+    """Configs 2-5 geometry and layouts (shared prefixes, shuffled pools), scaled down
+    to oracle-friendly sizes."""
+    for cid, kw in [(2, dict(num_seqs=4, ctx=("uniform", 512, 1200), pool_blocks=4096)),
+                    (3, dict(num_seqs=4, ctx=("uniform", 1024, 1600))),
+                    (4, dict(num_seqs=2, ctx=("uniform", 2000, 3000))),
+                    (5, dict(num_seqs=4, ctx=("uniform", 256, 700)))]:
+        cfg = scaled(CONFIGS[cid], **kw)
+        say(f"attention config {cid} scaled {kw}")
+        lay = build_layout(cfg)
+        kv = make_cache(cfg.kv_dtype, cfg.num_kv_heads, cfg.head_dim, cfg.block_size, lay.num_blocks)
+        mirror = PoolMirror(kv)
+        rng = np.random.default_rng(cid)
+        H, D = cfg.num_kv_heads, cfg.head_dim
+        kk = rng.normal(0, 1, (len(lay.fill_slots), H, D)).astype(np.float32)
+        vv = rng.normal(0, 1, (len(lay.fill_slots), H, D)).astype(np.float32)
+        if cfg.kv_dtype == "fp8":
+            ks, vs = per_head_amax_scales(kk), per_head_amax_scales(vv)
+            kv.set_head_scales(0, ks, vs)
+            mirror.set_head_scales(ks, vs)
+        append_rows(kv, mirror, kk, vv, lay.fill_slots, "bf16")
+        # The verify step's own append, then attention.
+        R = cfg.rows
+        ka = rng.normal(0, 1, (len(lay.append_slots), H, D)).astype(np.float32)
+        va = rng.normal(0, 1, (len(lay.append_slots), H, D)).astype(np.float32)
+        append_rows(kv, mirror, ka, va, lay.append_slots, "bf16")
+        mirror.compare_with_device()
+        mirror.sync_from_device()
+        q = torch.randn(cfg.num_seqs, R, cfg.num_q_heads, D, dtype=torch.bfloat16, device="cuda")
+        out = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+        kv.attention(0, q, out, torch.from_numpy(lay.keys).cuda(), torch.from_numpy(lay.block_tables).cuda(),
+                     1 / math.sqrt(D), partition_tokens=cfg.partition)
+        torch.cuda.synchronize()
+        ksc, vsc = mirror.scales_for_oracle()
+        ref = ora.attention(q.float().cpu().numpy(), mirror.kc, mirror.vc, cfg.kv_dtype, H, D, cfg.block_size,
+                            lay.keys, lay.block_tables, 1 / math.sqrt(D), ksc, vsc)
+        err = rel_err_per_vector(out.cpu().numpy(), ref)
+        print(f"  config {cid}: rel err {err:.2e}")
+        assert err <= TOL[cfg.kv_dtype]
+        kv.close()

@@ -1,0 +1,380 @@
+"""Pins of the CPU oracle: the reference's own known-answer tests, library
+routines (torch SDPA in float64, torch float8 casts, numpy float16 casts, libm exp),
+closed forms and invariants. CPU only."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+
+# ---------------------------------------------------------------- reference KATs
+
+def test_ngram_reference_cases(ora, golden):
+    for c in golden["ngram_draft"]:
+        assert ora.ngram_draft(c["history"], c["n"], c["k"]) == c["expect"]
+
+
+def test_verify_reference_cases(ora, golden):
+    for c in golden["verify"]:
+        # Rows may differ in length (Go slices); -inf padding leaves every argmax unchanged.
+        width = max((len(r) for r in c["rows"]), default=0)
+        rows = [list(r) + [-math.inf] * (width - len(r)) for r in c["rows"]]
+        acc, cor = ora.verify(c["drafts"], rows)
+        assert acc == c["expect_accepted"]
+        if c["expect_corrected"] is not None:
+            assert cor == c["expect_corrected"]
+
+
+def test_verify_rows_of_different_length(ora):
+    # The reference's all-accepted case uses rows of lengths 11/21/31; pad with -inf so
+    # the argmax of each row is unchanged and check the same answer.
+    rows = [[0.0] * 10 + [5.0], [0.0] * 20 + [5.0], [0.0] * 30 + [5.0]]
+    padded = [r + [-math.inf] * (31 - len(r)) for r in rows]
+    assert ora.verify([10, 20, 30], padded)[0] == 3
+
+
+def test_argmax_reference_cases(ora, golden):
+    for c in golden["argmax"]:
+        assert ora.argmax(c["logits"]) == c["expect"]
+    for c in golden["greedy_sample"]:
+        assert ora.argmax(c["logits"]) == c["expect"]
+
+
+def test_argmax_ties_and_nan(ora):
+    assert ora.argmax([1, 3, 3, 2]) == 1
+    assert ora.argmax([float("nan"), 5, 6]) == 0          # NaN at 0 never loses
+    assert ora.argmax([1, float("nan"), 0.5, 2]) == 3      # NaN elsewhere never wins
+    assert ora.argmax([-0.0, 0.0]) == 0                     # equal values: first index
+
+
+def test_top_p_reference_case(ora, golden):
+    for c in golden["top_p"]:
+        out = ora.top_p_filter_f64(c["probs"], c["p"])
+        for i in c["kept"]:
+            assert out[i] > 0
+        assert abs(out.sum() - c["sum"]) < c["tol"]
+
+
+def test_softmax_reference_cases(ora, golden):
+    for c in golden["softmax"]:
+        x = [float(v) for v in c["logits"]]
+        p = ora.softmax_f64(x)
+        assert abs(p.sum() - c["sum"]) < c["tol"]
+        if c.get("increasing"):
+            assert p[0] < p[1] < p[2]
+        if "zero_at" in c:
+            assert p[c["zero_at"]] == 0
+
+
+def test_categorical_closed_form(ora):
+    p = [0.1, 0.2, 0.3, 0.4]
+    assert ora.categorical_f64(p, 0.0) == 0
+    assert ora.categorical_f64(p, 0.0999) == 0
+    assert ora.categorical_f64(p, 0.1001) == 1
+    assert ora.categorical_f64(p, 0.61) == 3
+    assert ora.categorical_f64(p, 1.5) == 3               # fallback: last non-zero
+    assert ora.categorical_f64([0.5, 0.5, 0.0], 2.0) == 1
+
+
+# ---------------------------------------------------------------- n-gram brute force
+
+def _draft_literal(hist, n, k):
+    """A line-by-line Python restatement of speculative.go:24-62 (dict = Go map)."""
+    if n < 2:
+        n = 2
+    if k < 1:
+        k = 4
+    if len(hist) < n:
+        return []
+    kl = n - 1
+    table = {}
+    for i in range(0, len(hist) - n + 1):
+        table[tuple(hist[i:i + kl])] = hist[i + kl]
+    out = []
+    suffix = list(hist[len(hist) - kl:])
+    while len(out) < k:
+        nxt = table.get(tuple(suffix))
+        if nxt is None:
+            break
+        out.append(nxt)
+        suffix = suffix[1:] + [nxt]
+    return out
+
+
+@pytest.mark.parametrize("n", [2, 3, 4, 9])
+def test_ngram_brute_force(ora, n):
+    rng = np.random.default_rng(n)
+    for trial in range(200):
+        L = int(rng.integers(0, 60))
+        hist = rng.integers(0, 5, size=L).tolist()
+        k = int(rng.integers(0, 7))
+        assert ora.ngram_draft(hist, n, k) == _draft_literal(hist, n, k), (hist, n, k)
+
+
+def test_ngram_rejects_large_n(ora):
+    with pytest.raises(ValueError):
+        ora.ngram_draft([1, 2, 3] * 5, 10, 4)
+
+
+# ---------------------------------------------------------------- number formats
+
+def test_fp8_encode_matches_torch():
+    from oracle import oracle as ora
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.normal(0, 1, 20000), rng.normal(0, 100, 20000), rng.uniform(-448, 448, 20000),
+                        rng.uniform(-0.02, 0.02, 20000)]).astype(np.float32)
+    # Exact ties between representable values, both signs.
+    codes = np.arange(0, 0x7E, dtype=np.uint8)
+    vals = ora.fp8_decode(codes)
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    x = np.concatenate([x, mids, -mids, vals, -vals])
+    # torch's cast turns |x| >= 464 into NaN; the reference convention saturates (checked below).
+    x = x[np.abs(x) <= 448]
+    ours = ora.fp8_encode(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, ref)
+
+
+def test_fp8_saturates_and_decodes():
+    from oracle import oracle as ora
+    assert ora.fp8_encode(np.array([1e6, -1e6, 448.0, 460.0, np.inf], np.float32)).tolist() == [0x7E, 0xFE, 0x7E, 0x7E, 0x7E]
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    ours = ora.fp8_decode(codes)
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ours[ok], ref[ok])
+
+
+def test_int8_rne_and_clamp(ora):
+    x = np.array([2.5, 3.5, -2.5, -3.5, 0.49, 126.6, 200, -200, np.nan], np.float32)
+    assert ora.int8_encode(x).tolist() == [2, 4, -2, -4, 0, 127, 127, -127, 0]
+
+
+def test_f16_round_matches_numpy(ora):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.normal(0, 1, 5000), rng.normal(0, 1e-5, 5000), rng.normal(0, 1e4, 5000)]).astype(np.float32)
+    assert np.array_equal(ora.f16_round_c(x), x.astype(np.float16).astype(np.float32))
+
+
+def test_bf16_helpers_match_torch(ora):
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 3, 10000).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ora.round_bf16(x), ref)
+
+
+# ---------------------------------------------------------------- fixed-point exp
+
+def test_expf_fixed_accuracy(ora):
+    x = np.linspace(-80, 0, 400001).astype(np.float32)
+    ours = ora.expf_fixed(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    rel = np.abs(ours - ref) / ref
+    assert rel.max() < 4e-7  # ~3 ulp of fp32
+    assert ora.expf_fixed(np.array([0.0, -100.0, np.nan], np.float32)).tolist()[:2] == [1.0, 0.0]
+
+
+def test_weight_closed_forms(ora):
+    assert ora.weight(1.0, 1.0, 1.25) == 2 ** 35
+    assert ora.weight(-200.0, 0.0, 1.0) == 0
+    ws = [ora.weight(float(l), 0.0, 1.25) for l in np.linspace(-10, 0, 200)]
+    assert all(a <= b for a, b in zip(ws, ws[1:]))
+
+
+# ---------------------------------------------------------------- rejection acceptance
+
+def _softmax_fixed_rows(ora, logits, T):
+    inv_t = np.float32(1.0) / np.float32(T)
+    out = []
+    for row in logits:
+        m = float(np.max(row))
+        out.append(np.array([ora.weight(float(l), m, float(inv_t)) for l in row], dtype=np.float64))
+    return out
+
+
+def test_rejection_one_hot_q_accepts_iff_u_below_p(ora):
+    rng = np.random.default_rng(3)
+    V, K, B = 7, 1, 400
+    logits = rng.normal(0, 1, (B, K + 1, V)).astype(np.float32)
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    u = rng.random((B, K + 1)).astype(np.float32)
+    acc, tok = ora.accept_rejection(logits, drafts, np.full(B, K, np.int32), u, 0.8)
+    for b in range(B):
+        w = _softmax_fixed_rows(ora, logits[b, :1], 0.8)[0]
+        p = w[drafts[b, 0]] / w.sum()
+        assert acc[b] == (1 if u[b, 0] < p else 0)
+        if acc[b] == 0:
+            assert tok[b] != drafts[b, 0]  # the residual excludes the rejected draft
+
+
+def test_rejection_q_equal_p_always_accepts(ora):
+    rng = np.random.default_rng(4)
+    V, K, B = 50, 3, 64
+    logits = rng.normal(0, 2, (B, K + 1, V)).astype(np.float32)
+    # q = p - tiny: then p/q >= 1 and every draft is accepted.
+    q = np.zeros((B, K, V), np.float32)
+    for b in range(B):
+        for j, w in enumerate(_softmax_fixed_rows(ora, logits[b, :K], 1.0)):
+            q[b, j] = (w / w.sum() * (1 - 1e-6)).astype(np.float32)
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    u = (rng.random((B, K + 1)) * 0.999).astype(np.float32)
+    acc, _ = ora.accept_rejection(logits, drafts, np.full(B, K, np.int32), u, 1.0, draft_probs=q)
+    assert (acc == K).all()
+
+
+def test_rejection_output_distribution_is_target(ora):
+    """Leviathan et al.: the first emitted token is distributed as p whatever q is."""
+    rng = np.random.default_rng(5)
+    V, N = 5, 40000
+    base = np.array([1.0, 0.2, -0.5, 0.7, -1.0], np.float32)
+    logits = np.broadcast_to(base, (N, 2, V)).copy()
+    q = np.array([0.05, 0.5, 0.3, 0.1, 0.05], np.float32)
+    dp = np.broadcast_to(q, (N, 1, V)).copy()
+    drafts = rng.choice(V, size=(N, 1), p=q / q.sum()).astype(np.int32)
+    u = rng.random((N, 2)).astype(np.float32)
+    acc, tok = ora.accept_rejection(logits, drafts, np.ones(N, np.int32), u, 1.0, draft_probs=dp)
+    first = np.where(acc == 1, drafts[:, 0], tok)
+    w = _softmax_fixed_rows(ora, base[None], 1.0)[0]
+    p = w / w.sum()
+    freq = np.bincount(first, minlength=V) / N
+    assert np.abs(freq - p).max() < 0.01
+
+
+def test_rejection_top_p_matches_go_rule(ora):
+    """The integer nucleus equals topPFilter's float64 nucleus on generic rows."""
+    rng = np.random.default_rng(6)
+    V = 300
+    for trial in range(20):
+        row = rng.normal(0, 2, V).astype(np.float32)
+        T, top_p = 0.8, 0.9
+        # Float64 Go rule.
+        scaled = row.astype(np.float64) * (1.0 / T)
+        go_keep = ora.top_p_filter_f64(ora.softmax_f64(scaled), top_p) > 0
+        # Integer rule, observed through the bonus draw: a token outside the nucleus is never drawn.
+        w = _softmax_fixed_rows(ora, row[None], T)[0]
+        order = sorted(range(V), key=lambda i: (-row[i], i))
+        tp = math.ceil(top_p * w.sum())
+        cum, keep = 0, np.zeros(V, bool)
+        for i in order:
+            if cum >= tp and cum > 0:
+                break
+            keep[i] = True
+            cum += w[i]
+        assert np.array_equal(keep, go_keep)
+        # And the oracle's draws only land in the nucleus.
+        N = 200
+        logits = np.broadcast_to(row, (N, 1, V)).copy()
+        u = rng.random((N, 1)).astype(np.float32)
+        _, tok = ora.accept_rejection(logits, np.zeros((N, 0), np.int32), np.zeros(N, np.int32), u, T, top_p)
+        assert keep[tok].all()
+
+
+# ---------------------------------------------------------------- attention
+
+def _bf16_pool_case(ora, B=3, R=4, Hq=8, H=2, D=32, bs=4, ctx=(5, 17, 30), seed=0):
+    rng = np.random.default_rng(seed)
+    maxb = max((c + R + bs - 1) // bs for c in ctx)
+    nblk = B * maxb + 3
+    perm = rng.permutation(nblk)
+    bt = perm[:B * maxb].reshape(B, maxb).astype(np.int32)
+    keys = np.array([c + R for c in ctx], np.int32)
+    kvals = ora.round_bf16(rng.normal(0, 1, (nblk, H, bs, D)).astype(np.float32))
+    vvals = ora.round_bf16(rng.normal(0, 1, (nblk, H, D, bs)).astype(np.float32))
+    kc = ora.bf16_bits(kvals).view(np.uint8).copy()
+    vc = ora.bf16_bits(vvals).view(np.uint8).copy()
+    q = rng.normal(0, 1, (B, R, Hq, D)).astype(np.float32)
+    return q, kc, vc, kvals, vvals, keys, bt
+
+
+def test_attention_matches_torch_sdpa(ora):
+    B, R, Hq, H, D, bs = 3, 4, 8, 2, 32, 4
+    q, kc, vc, kvals, vvals, keys, bt = _bf16_pool_case(ora, B, R, Hq, H, D, bs)
+    scale = 1 / math.sqrt(D)
+    out = ora.attention(q, kc, vc, "bf16", H, D, bs, keys, bt, scale)
+    G = Hq // H
+    for b in range(B):
+        n = int(keys[b])
+        t = np.arange(n)
+        blk = bt[b, t // bs]
+        k = kvals[blk, :, t % bs, :].transpose(1, 0, 2)               # [H, n, D]
+        v = vvals[blk, :, :, t % bs].transpose(1, 0, 2)               # [H, n, D]
+        k = np.repeat(k, G, axis=0)
+        v = np.repeat(v, G, axis=0)
+        qq = q[b].transpose(1, 0, 2)                                  # [Hq, R, D]
+        pos = n - R + np.arange(R)
+        mask = t[None, :] <= pos[:, None]                             # [R, n]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(qq).double(), torch.from_numpy(k).double(), torch.from_numpy(v).double(),
+            attn_mask=torch.from_numpy(mask), scale=scale).numpy()    # [Hq, R, D]
+        np.testing.assert_allclose(out[b].transpose(1, 0, 2), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_closed_forms(ora):
+    # One visible key -> output equals that key's V; identical keys -> mean of visible V.
+    B, R, Hq, H, D, bs = 1, 2, 2, 1, 16, 4
+    rng = np.random.default_rng(9)
+    bt = np.array([[0, 1]], np.int32)
+    kvals = np.ones((2, H, bs, D), np.float32)
+    vvals = ora.round_bf16(rng.normal(0, 1, (2, H, D, bs)).astype(np.float32))
+    kc, vc = ora.bf16_bits(kvals).view(np.uint8).copy(), ora.bf16_bits(vvals).view(np.uint8).copy()
+    q = rng.normal(0, 1, (B, R, Hq, D)).astype(np.float32)
+    keys = np.array([R], np.int32)  # row 0 sees key 0 only; row 1 sees keys 0,1
+    out = ora.attention(q, kc, vc, "bf16", H, D, bs, keys, bt, 0.25)
+    np.testing.assert_allclose(out[0, 0, 0], vvals[0, 0, :, 0], rtol=1e-6)
+    np.testing.assert_allclose(out[0, 1, 1], (vvals[0, 0, :, 0] + vvals[0, 0, :, 1]) / 2, rtol=1e-6)
+
+
+def test_attention_block_permutation_invariance(ora):
+    q, kc, vc, kvals, vvals, keys, bt = _bf16_pool_case(ora, seed=11)
+    H, D, bs = 2, 32, 4
+    out = ora.attention(q, kc, vc, "bf16", H, D, bs, keys, bt, 0.2)
+    # Move every block to a new physical index, rewrite the tables accordingly.
+    nblk = kvals.shape[0]
+    perm = np.random.default_rng(12).permutation(nblk)
+    k2, v2 = np.empty_like(kvals), np.empty_like(vvals)
+    k2[perm], v2[perm] = kvals, vvals
+    out2 = ora.attention(q, ora.bf16_bits(k2).view(np.uint8).copy(), ora.bf16_bits(v2).view(np.uint8).copy(),
+                         "bf16", H, D, bs, keys, perm[bt].astype(np.int32), 0.2)
+    np.testing.assert_array_equal(out, out2)
+
+
+def test_kv_append_fp8_matches_encoder(ora):
+    H, D, bs, nblk = 2, 8, 4, 3
+    rng = np.random.default_rng(13)
+    k = rng.normal(0, 3, (5, H, D)).astype(np.float32)
+    v = rng.normal(0, 3, (5, H, D)).astype(np.float32)
+    slots = np.array([0, 1, 5, 11, -1], np.int32)
+    kc = np.zeros(nblk * H * bs * D, np.uint8)
+    vc = np.zeros(nblk * H * bs * D, np.uint8)
+    kinv = np.array([1 / 0.5, 1 / 0.25], np.float32)
+    ora.kv_append_q(kc, vc, "fp8", H, D, bs, k, v, slots, k_inv=kinv, v_inv=kinv)
+    K = kc.reshape(nblk, H, bs, D)
+    V = vc.reshape(nblk, H, D, bs)
+    for r, s in enumerate(slots[:4]):
+        blk, o = divmod(int(s), bs)
+        for h in range(H):
+            assert np.array_equal(K[blk, h, o], ora.fp8_encode(k[r, h] * kinv[h]))
+            assert np.array_equal(V[blk, h, :, o], ora.fp8_encode(v[r, h] * kinv[h]))
+
+
+def test_kv_append_int8_block_scales(ora):
+    H, D, bs, nblk = 1, 4, 4, 2
+    k = np.array([[[1, -2, 3, 4]], [[0.5, 0.5, 0.5, 0.5]], [[10, 0, 0, 0]]], np.float32)
+    kc = np.zeros(nblk * H * bs * D, np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros(nblk * H, np.float32)
+    vs = np.zeros(nblk * H, np.float32)
+    ora.kv_append_q(kc, vc, "int8", H, D, bs, k[:2], k[:2], np.array([0, 1], np.int32), k_bscale=ks, v_bscale=vs)
+    s0 = ora.f16_round_c(np.array([4 / 127], np.float32))[0]
+    assert ks[0] == s0
+    K = kc.view(np.int8).reshape(nblk, H, bs, D)
+    assert K[0, 0, 0].tolist() == ora.int8_encode(k[0, 0] * np.float32(1 / s0)).tolist()
+    # A larger row grows the scale and re-quantises the rows already in the block.
+    old = K[0, 0, :2].copy()
+    ora.kv_append_q(kc, vc, "int8", H, D, bs, k[2:], k[2:], np.array([2], np.int32), k_bscale=ks, v_bscale=vs)
+    s1 = ora.f16_round_c(np.array([10 / 127], np.float32))[0]
+    assert ks[0] == s1
+    want = ora.int8_encode((old.astype(np.float32) * s0) * np.float32(1 / s1))
+    assert np.array_equal(K[0, 0, :2], want)
