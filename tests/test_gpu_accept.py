@@ -46,7 +46,7 @@ def test_greedy_ties_nan_and_negative_zero(gpu):
     rows = np.zeros((6, 2, V), np.float32)
     rows[0, 0, [5, 4000, 8999]] = 3.0                 # tie across segments -> 5
     rows[1, 0, 0] = np.nan; rows[1, 0, 7] = 9          # NaN at index 0 -> 0
-    rows[2, 0, :] = np.nan; rows[2, 0, 8000] = 1       # NaN elsewhere never wins -> 8000
+    rows[2, 0, :] = np.nan; rows[2, 0, 0] = -5; rows[2, 0, 8000] = 1  # NaN elsewhere never wins -> 8000
     rows[3, 0, :] = -np.inf                            # all -inf -> 0
     rows[4, 0, 10] = -0.0                              # -0 == +0 -> first index 0
     rows[5, 0, :] = -1; rows[5, 0, 4097] = 2; rows[5, 0, 4096] = 2  # segment boundary tie -> 4096
