@@ -1,0 +1,298 @@
+#!/usr/bin/env python3
+"""Spec-verify benchmark of the gfx950 verify path (one GPU).
+
+One step = one verify pass of a batch: for each of L layers, draft-KV append of the
+B*(k+1) verify rows followed by multi-query paged attention over the whole context;
+then one acceptance over the full-vocabulary logits. Inputs are synthetic, seeded,
+and resident in HBM before the timed region starts.
+
+value = verified tokens/s = B*(k+1) / (L*(t_append + t_attn) + t_accept), taken from
+the wall clock of the timed steps (the same formula the measurement plan uses).
+The roofline object describes the attention call (the dominant kernel); its
+duration is the HIP-event average over every attention call in the timed region.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, help="workload config id (default 3 = 8B fp8)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seqs", type=int, default=8, help="sequences in the CPU baseline sample")
+    ap.add_argument("--partition", type=int, default=-1, help="override split-K partition tokens")
+    ap.add_argument("--layers", type=int, default=0, help="override layer count (0 = config)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of known size (for PMC byte calibration)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import gollmgo_amd.verify as gv
+    from gollmgo_amd._lib import DType
+    from gollmgo_amd.workloads import CONFIGS, build_layout, scaled
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    torch.cuda.set_device(0)
+    dev = "cuda"
+
+    if args.copy_calibration:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n}))
+        return
+
+    cfg = CONFIGS[args.config]
+    if args.layers:
+        cfg = scaled(cfg, layers=args.layers)
+    if args.partition >= 0:
+        cfg = scaled(cfg, partition=args.partition)
+    B, R, K = cfg.num_seqs, cfg.rows, cfg.max_drafts
+    Hq, H, D, bs, V, L = cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size, cfg.vocab, cfg.layers
+    kv_dt = {"bf16": DType.BF16, "f16": DType.F16, "fp8": DType.FP8_E4M3, "int8": DType.INT8, "f32": DType.F32}[cfg.kv_dtype]
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+    t_setup = time.time()
+    lay = build_layout(cfg)
+    kv = gv.KVCache(L, lay.num_blocks, bs, H, D, kv_dt)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(cfg.seed)
+    fill_slots = torch.from_numpy(lay.fill_slots).to(dev)
+    append_slots = torch.from_numpy(lay.append_slots).to(dev)
+    n_fill = len(lay.fill_slots)
+    chunk = 1 << 16
+    for layer in range(L):
+        if cfg.kv_dtype == "fp8":
+            # Per-head amax/448 scales over this layer's context (the reference's fp8 convention).
+            kmax = torch.zeros(H, device=dev)
+            vmax = torch.zeros(H, device=dev)
+            for s in range(0, n_fill, chunk):
+                m = min(chunk, n_fill - s)
+                torch.manual_seed(cfg.seed * 1000 + layer * 100 + s // chunk)
+                kx = torch.randn(m, H, D, device=dev, dtype=torch.bfloat16)
+                vx = torch.randn(m, H, D, device=dev, dtype=torch.bfloat16)
+                kmax = torch.maximum(kmax, kx.float().abs().amax(dim=(0, 2)))
+                vmax = torch.maximum(vmax, vx.float().abs().amax(dim=(0, 2)))
+            kv.set_head_scales(layer, (kmax / 448).clamp_min(1e-8).tolist(), (vmax / 448).clamp_min(1e-8).tolist())
+        for s in range(0, n_fill, chunk):
+            m = min(chunk, n_fill - s)
+            torch.manual_seed(cfg.seed * 1000 + layer * 100 + s // chunk)
+            kx = torch.randn(m, H, D, device=dev, dtype=torch.bfloat16)
+            vx = torch.randn(m, H, D, device=dev, dtype=torch.bfloat16)
+            kv.append(layer, kx, vx, fill_slots[s:s + m])
+    torch.cuda.synchronize()
+
+    q = torch.randn(L, B, R, Hq, D, device=dev, dtype=tdt[cfg.q_dtype], generator=gen)
+    out = torch.empty(B, R, Hq, D, device=dev, dtype=torch.bfloat16)
+    k_new = torch.randn(L, B * R, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    v_new = torch.randn(L, B * R, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    keys = torch.from_numpy(lay.keys).to(dev)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    ws_attn = kv.attention_workspace(B, R, Hq, bt.shape[1], cfg.partition)
+
+    # Acceptance inputs: target logits, draft distributions (a sharpened copy of the
+    # target row) and drafts that mostly follow the draft distribution's mode.
+    logits = (torch.randn(B, R, V, device=dev, generator=gen) * 2.0).to(tdt[cfg.logits_dtype])
+    draft_probs = torch.softmax(logits[:, :K].float() * 1.5, dim=-1).contiguous() if cfg.draft_probs else None
+    drafts = torch.randint(0, V, (B, K), device=dev, dtype=torch.int32, generator=gen)
+    base = draft_probs if draft_probs is not None else logits[:, :K].float()
+    mode = base.argmax(dim=-1).to(torch.int32)
+    pick = torch.rand(B, K, device=dev, generator=gen) < 0.8
+    drafts = torch.where(pick, mode, drafts).contiguous()
+    n_drafts = torch.full((B,), K, device=dev, dtype=torch.int32)
+    uniforms = torch.rand(B, R, device=dev, generator=gen)
+    acc_out = (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int32, device=dev))
+    if cfg.accept == "rejection":
+        ws_acc = gv.rejection_workspace(B, K, V)
+    else:
+        ws_acc = gv.greedy_workspace(B, K, V)
+    torch.cuda.synchronize()
+    setup_s = time.time() - t_setup
+
+    scale = 1.0 / math.sqrt(D)
+    ev = {name: [] for name in ("append", "attn", "accept")}
+
+    def step(record: bool):
+        for layer in range(L):
+            if record:
+                e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                e0.record()
+            kv.append(layer, k_new[layer], v_new[layer], append_slots)
+            if record:
+                e1.record()
+            kv.attention(layer, q[layer], out, keys, bt, scale, partition_tokens=cfg.partition, workspace=ws_attn)
+            if record:
+                e2.record()
+                ev["append"].append((e0, e1))
+                ev["attn"].append((e1, e2))
+        if record:
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record()
+        if cfg.accept == "rejection":
+            gv.accept_rejection(logits, drafts, n_drafts, uniforms, cfg.temperature, cfg.top_p,
+                                draft_probs=draft_probs, workspace=ws_acc, out=acc_out)
+        else:
+            gv.accept_greedy(logits, drafts, n_drafts, workspace=ws_acc, out=acc_out)
+        if record:
+            a1.record()
+            ev["accept"].append((a0, a1))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    # Timed region, wall clock (no per-kernel events inside).
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(False)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # Same steps again with HIP events around every call (per-kernel durations).
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+
+    def avg_us(name):
+        xs = [s.elapsed_time(e) * 1000.0 for s, e in ev[name]]
+        xs.sort()
+        return sum(xs) / len(xs), xs[len(xs) // 2]
+
+    t_app, t_app_med = avg_us("append")
+    t_attn, t_attn_med = avg_us("attn")
+    t_acc, t_acc_med = avg_us("accept")
+    ms_per_step = wall * 1000.0 / args.steps
+    tokens = B * R
+    value = tokens / (ms_per_step / 1000.0)
+    kernel_formula_tps = tokens / ((L * (t_app + t_attn) + t_acc) * 1e-6)
+    accepted = acc_out[0].cpu()
+    accepted_tps = float((accepted + 1).sum()) / (ms_per_step / 1000.0)
+
+    # Algorithmic bytes of one attention call (one layer): K+V once per sequence, Q in, out, scales, tables.
+    eb = {"bf16": 2, "f16": 2, "fp8": 1, "int8": 1, "f32": 4}[cfg.kv_dtype]
+    keys_np = lay.keys.astype(np.int64)
+    kv_bytes = int(keys_np.sum()) * H * D * eb * 2
+    q_bytes = B * R * Hq * D * q.element_size()
+    o_bytes = B * R * Hq * D * out.element_size()
+    blocks_used = int(((keys_np + bs - 1) // bs).sum())
+    scale_bytes = H * 4 * 2 if cfg.kv_dtype == "fp8" else (blocks_used * H * 2 * 2 if cfg.kv_dtype == "int8" else 0)
+    attn_bytes = kv_bytes + q_bytes + o_bytes + scale_bytes + blocks_used * 4
+    achieved = attn_bytes / (t_attn * 1e-6) / 1e9
+    lb = logits.element_size()
+    acc_bytes = B * R * V * lb + (B * K * V * 4 if draft_probs is not None else 0)
+
+    result = {
+        "metric": "spec-verify tokens/s at Llama-3.1-8B shape, FP8 KV; achieved HBM GB/s",
+        "value": round(value, 1),
+        "unit": "verified tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp8": "fp8-e4m3 KV, f16 MFMA, fp32 softmax", "bf16": "bf16", "int8": "int8 KV, f16 MFMA",
+                  "f16": "f16", "f32": "f32"}[cfg.kv_dtype],
+        "data": "synthetic (seeded N(0,1) K/V/Q, N(0,2) logits), random-permuted paged pool",
+        "config": {
+            "workload": f"config {args.config}: {cfg.name} verify step",
+            "batch": B, "draft_k": K, "rows_per_seq": R, "q_heads": Hq, "kv_heads": H, "head_dim": D,
+            "block_size": bs, "ctx": list(cfg.ctx), "mean_keys": float(keys_np.mean()), "kv_dtype": cfg.kv_dtype,
+            "layers": L, "vocab": V, "accept": cfg.accept, "temperature": cfg.temperature, "top_p": cfg.top_p,
+            "draft_probs": cfg.draft_probs, "partition_tokens": cfg.partition or "auto",
+            "shared_prefix_frac": cfg.shared_prefix_frac,
+        },
+        "kernels_us": {"append_avg": round(t_app, 2), "attention_avg": round(t_attn, 2),
+                       "attention_median": round(t_attn_med, 2), "accept_avg": round(t_acc, 2)},
+        "tokens_per_s_from_kernel_times": round(kernel_formula_tps, 1),
+        "accepted_tokens_per_s": round(accepted_tps, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gg_verify_attention (attn_mfma_kernel + attn_combine_kernel)",
+                     "algorithmic_bytes_per_launch": attn_bytes},
+        "accept_roofline": {"achieved": round(acc_bytes / (t_acc * 1e-6) / 1e9, 1), "unit": "GB/s",
+                            "algorithmic_bytes_per_launch": acc_bytes},
+        "setup_s": round(setup_s, 1),
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts,
+                                              uniforms, scale)
+    kv.close()
+    print(json.dumps(result))
+
+
+def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, uniforms, scale):
+    """The CPU oracle (a C port of the reference's host logic and of its attention
+    semantics) timed on this host on a bounded sample of the same workload:
+    attention of layer 0 for the first S sequences, scaled by L layers, plus the
+    acceptance of the same S sequences."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as ora
+
+    S = min(args.cpu_seqs, cfg.num_seqs)
+    threads = min(os.cpu_count() or 1, 16)
+    kc = kv.k_pool(0).cpu().numpy()
+    vc = kv.v_pool(0).cpu().numpy()
+    ks = vs = None
+    if cfg.kv_dtype == "fp8":
+        k_s, v_s = kv.scales(0)
+        ks, vs = k_s.cpu().numpy()[:cfg.num_kv_heads], v_s.cpu().numpy()[:cfg.num_kv_heads]
+    elif cfg.kv_dtype == "int8":
+        k_s, v_s = kv.scales(0)
+        ks, vs = k_s.float().cpu().numpy().reshape(-1), v_s.float().cpu().numpy().reshape(-1)
+    qh = q[0, :S].float().cpu().numpy()
+    t0 = time.perf_counter()
+    ora.attention(qh, kc, vc, cfg.kv_dtype, cfg.num_kv_heads, cfg.head_dim, cfg.block_size, lay.keys[:S],
+                  lay.block_tables[:S], scale, ks, vs, threads=threads)
+    t_attn = time.perf_counter() - t0
+    lg = logits[:S].float().cpu().numpy()
+    dp = draft_probs[:S].cpu().numpy() if draft_probs is not None else None
+    dr = drafts[:S].cpu().numpy()
+    nd = n_drafts[:S].cpu().numpy()
+    un = uniforms[:S].cpu().numpy()
+    t0 = time.perf_counter()
+    if cfg.accept == "rejection":
+        ora.accept_rejection(lg, dr, nd, un, cfg.temperature, cfg.top_p, dp)
+    else:
+        ora.accept_greedy(lg, dr, nd)
+    t_acc = time.perf_counter() - t0
+    step_s = cfg.layers * t_attn + t_acc
+    return {"value": round(S * cfg.rows / step_s, 2), "unit": "verified tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{S} of {cfg.num_seqs} sequences: layer-0 attention ({t_attn:.2f} s, fp64, OpenMP over "
+                      f"sequences) x {cfg.layers} layers + {cfg.accept} acceptance ({t_acc:.2f} s, 1 thread)",
+            "attention_s_per_layer": round(t_attn, 3), "accept_s": round(t_acc, 3)}
+
+
+if __name__ == "__main__":
+    main()
