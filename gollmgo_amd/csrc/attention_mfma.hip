@@ -7,7 +7,7 @@
 // a bandwidth-bound decode into MFMA-friendly tiles. The four waves stream
 // disjoint chunks and merge their (max, sum, P.V) states through LDS at the end.
 //
-// Per chunk and row tile, with lane = 16*g4 + c:
+// Per chunk (64 tokens for 1-byte pools, 32 for 2-byte pools) and row tile, lane = 16*g4 + c:
 //   S^T = K . Q^T   v_mfma_f32_16x16x32_{bf16,f16}: A = K (16 tokens x 32 dims),
 //                   B = Q^T. Token m = 4q+i of tile s is (block q, offset 4s+i), so
 //                   the output gives lane (g4, c) row c and block g4's offsets 4s..4s+3.
@@ -20,7 +20,7 @@
 //
 // Pool types: BF16 (bf16 MFMA; P split into bf16 hi+lo for two MFMAs so the
 // probabilities keep ~16 bits), F16 (f16 MFMA), FP8-E4M3 and INT8 (decoded in
-// registers to exact f16 values: E4M3 bits shifted into an f16 at 2^-8 scale, int8
+// registers to exact f16 values: E4M3 by the gfx950 pk_f16_fp8 conversion, int8
 // via the 0x6400 magic; the per-head / per-block scales are applied to the fp32
 // scores and to P, never to the operands).
 #include "gg_common.h"
@@ -72,15 +72,12 @@ __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c, bool bf16) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Two E4M3 bytes (bits 0-7 and 16-23 of x) -> two f16 equal to value * 2^-8 (exact).
-__device__ __forceinline__ uint32_t e4m3x2_to_f16x2(uint32_t x) {
-    return ((x & 0x00800080u) << 8) | ((x & 0x007F007Fu) << 7);
-}
-// Four E4M3 bytes -> four f16 (value * 2^-8), as two dwords.
+// Four E4M3 bytes -> four f16 (exact: every E4M3 value, subnormals included, is an
+// f16 value), two hardware conversions (v_cvt_scalef32_pk_f16_fp8, scale 1).
 __device__ __forceinline__ uint2 e4m3x4_to_f16x4(uint32_t w) {
-    uint32_t lo = (w & 0xFFu) | ((w & 0xFF00u) << 8);
-    uint32_t hi = ((w >> 16) & 0xFFu) | ((w >> 8) & 0xFF0000u);
-    return make_uint2(e4m3x2_to_f16x2(lo), e4m3x2_to_f16x2(hi));
+    const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+    const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+    return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
 }
 // Four int8 -> four f16 (exact): (0x6400 | (b ^ 0x80)) is 1024 + b + 128.
 __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t w) {
@@ -141,13 +138,46 @@ __device__ __forceinline__ uint4 mask_halves8(uint4 v, int nvalid, int first) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Chunk geometry. A chunk is kTok consecutive tokens (kTok/16 blocks). 1-byte pools use
+// 64-token chunks, 2-byte pools 32-token chunks, so that in both cases a lane moves
+// 256 bytes per chunk: K rows of kTok/16 tiles (32 dims each) and one 16-byte run
+// of V offsets for each of the eight dim tiles.
+//
+// S tile s, M index m = 4q + i (q = m/4) holds token (block bq(q), offset ob(q) + 4s + i):
+//   64-token chunks: bq(q) = q,    ob(q) = 0       (tiles s = 0..3)
+//   32-token chunks: bq(q) = q/2,  ob(q) = 8*(q%2) (tiles s = 0..1)
+// The MFMA output gives lane (g4, c16) row c16 and tokens (bq(g4), ob(g4) + 4s + i), so the
+// lane's P values are the consecutive offsets ob(g4) .. ob(g4) + 4*NS - 1 of one block,
+// which is exactly the A operand of P.V (k = 8*g4 + i' -> offset ob(g4) + 8*pv + i') and
+// one contiguous run of the dim-major V block.
+template <int kEB>
+struct Geo {
+    static constexpr int kTok = kEB == 1 ? 64 : 32;
+    static constexpr int kNS = kTok / 16;                 // S tiles (and blocks) per chunk
+    static constexpr int kNPV = kNS / 2;                  // P.V MFMAs per dim tile
+    static constexpr int kKVec = 32 * kEB / 16;           // 16-byte loads per lane per K tile
+    static constexpr int kVBytes = 8 * kNPV * kEB;        // V bytes per lane per dim tile (16)
+    __device__ static __forceinline__ int bq(int q) { return kTok == 64 ? q : (q >> 1); }
+    __device__ static __forceinline__ int ob(int q) { return kTok == 64 ? 0 : 8 * (q & 1); }
+};
+
+template <int kEB>
+struct ChunkRegs {
+    using G = Geo<kEB>;
+    uint4 k[G::kNS][G::kKVec];
+    uint4 v[8];
+};
+
 template <gg_dtype_t DT, int NT>
 __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
     attn_mfma_kernel(AttnArgs a, KVView kv) {
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
     constexpr int kEB = T::kEB;
-    constexpr int kRows = NT * 16;
+    using Geom = Geo<kEB>;
+    using Regs = ChunkRegs<kEB>;
+    constexpr int kTok = Geom::kTok;
+    constexpr int kNS = Geom::kNS;
 
     const int part = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -170,39 +200,81 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
 
     const int t0 = part * P;
     const int t_end = min(t0 + P, ctx);
-    const int nchunks = (t_end - t0 + kChunk - 1) / kChunk;
+    const int nchunks = (t_end - t0 + kTok - 1) / kTok;
     const int first_masked = ctx - nrows;  // tokens >= this are causally masked for some row
 
     // Score multiplier (log2 domain) and P.V multiplier per pool type.
     float sscale = a.scale * kLog2e;
     float vfold = 1.f;
     if constexpr (DT == GG_DTYPE_FP8_E4M3) {
-        sscale *= kv.k_head_scale[kvh] * 256.f;
-        vfold = kv.v_head_scale[kvh] * 256.f;
+        sscale *= kv.k_head_scale[kvh];
+        vfold = kv.v_head_scale[kvh];
     }
 
     // ---- Q operands: B[k = 8*g4+i][n = c16] <- Q[row rt*16+c16][32*g4 + 8*mm + i] ----
+    // All loads are issued unconditionally (invalid rows read row 0 and are zeroed).
     uint4 qop[NT][4];
     int row_pos[NT];  // last visible key position of the lane's S row (c16)
+    {
+        size_t qb[NT];
+        bool qvalid[NT];
 #pragma unroll
-    for (int rt = 0; rt < NT; ++rt) {
-        const int r = rt * 16 + c16;
-        const bool valid = r < nvalid_rows;
-        const int j = valid ? r / G : 0;
-        const int g = valid ? r % G : 0;
-        row_pos[rt] = valid ? first_masked + j : ctx - 1;
-        const size_t qb = (((size_t)b * R + j) * Hq + (size_t)kvh * G + g) * kD + 32 * g4;
+        for (int rt = 0; rt < NT; ++rt) {
+            const int r = rt * 16 + c16;
+            qvalid[rt] = r < nvalid_rows;
+            const int j = qvalid[rt] ? r / G : 0;
+            const int g = qvalid[rt] ? r % G : 0;
+            row_pos[rt] = qvalid[rt] ? first_masked + j : ctx - 1;
+            qb[rt] = (((size_t)b * R + j) * Hq + (size_t)kvh * G + g) * kD + 32 * g4;
+        }
+        if (a.q_dtype == GG_DTYPE_F32) {
+            float4 raw[NT][4][2];
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            float f[8];
+            for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) f[i] = valid ? load_as_f32(a.q, a.q_dtype, qb + 8 * mm + i) : 0.f;
-            if constexpr (kIsBf16)
-                qop[rt][mm] = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
-                                         pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
-            else
-                qop[rt][mm] = make_uint4(pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]),
-                                         pack_f16x2(f[4], f[5]), pack_f16x2(f[6], f[7]));
+                for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        raw[rt][mm][h] = ((const float4*)((const float*)a.q + qb[rt] + 8 * mm))[h];
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) {
+                    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                    const float4 x = qvalid[rt] ? raw[rt][mm][0] : z4, y = qvalid[rt] ? raw[rt][mm][1] : z4;
+                    if constexpr (kIsBf16)
+                        qop[rt][mm] = make_uint4(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w),
+                                                 pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w));
+                    else
+                        qop[rt][mm] = make_uint4(pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w),
+                                                 pack_f16x2(y.x, y.y), pack_f16x2(y.z, y.w));
+                }
+        } else {
+            const bool src_bf16 = a.q_dtype == GG_DTYPE_BF16;
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm)
+                    qop[rt][mm] = *(const uint4*)((const uint16_t*)a.q + qb[rt] + 8 * mm);
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) {
+                    if (!qvalid[rt]) qop[rt][mm] = zero4();
+                    // Convert when the Q type differs from the MFMA operand type.
+                    if (src_bf16 != kIsBf16) {
+                        const uint32_t w[4] = {qop[rt][mm].x, qop[rt][mm].y, qop[rt][mm].z, qop[rt][mm].w};
+                        uint32_t o4[4];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const uint16_t lo = (uint16_t)w[k], hi = (uint16_t)(w[k] >> 16);
+                            const float flo = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                            const float fhi = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                            o4[k] = kIsBf16 ? pack_bf16x2(flo, fhi) : pack_f16x2(flo, fhi);
+                        }
+                        qop[rt][mm] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+                    }
+                }
         }
     }
 
@@ -217,56 +289,67 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
     }
 
     const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
-    const size_t head_stride_k = (size_t)kBS * kD;  // elements per (block, head) tile
+    const size_t head_stride = (size_t)kBS * kD;  // elements per (block, head) tile
 
-    for (int ch = wave; ch < nchunks; ch += kWaves) {
-        const int tc = t0 + ch * kChunk;
-        // K rows: lane supplies token (block c16/4, offset 4s + c16%4) for tile s.
-        const int tk = tc + 16 * (c16 >> 2);
-        int blk_k = tk < ctx ? bt[tk >> 4] : -1;
-        if (blk_k >= kv.num_blocks) blk_k = -1;
-        // V columns / P rows: lane owns block g4 of the chunk.
-        const int tv = tc + 16 * g4;
-        int blk_v = tv < ctx ? bt[tv >> 4] : -1;
-        if (blk_v >= kv.num_blocks) blk_v = -1;
-        const int nvalid_v = ctx - tv;
+    // The kNS physical blocks of chunk ch, read with wave-uniform (scalar) loads so that
+    // waiting for them never waits on the vector loads of K/V in flight. -1 = no block
+    // (past the keys, past the partition, or an out-of-range table entry).
+    struct Blocks {
+        int q[kNS];
+    };
+    auto chunk_blocks = [&](int ch) -> Blocks {
+        Blocks r;
+#pragma unroll
+        for (int qb = 0; qb < kNS; ++qb) {
+            const int t = t0 + ch * kTok + 16 * qb;
+            int blk = (ch < nchunks && t < ctx) ? bt[t >> 4] : -1;
+            blk = __builtin_amdgcn_readfirstlane(blk);
+            r.q[qb] = (blk >= kv.num_blocks) ? -1 : blk;
+        }
+        return r;
+    };
+    auto pick = [](const Blocks& bl, int i) -> int {
+        if constexpr (kNS == 4) return i == 0 ? bl.q[0] : i == 1 ? bl.q[1] : i == 2 ? bl.q[2] : bl.q[3];
+        else return i == 0 ? bl.q[0] : bl.q[1];
+    };
+    // K rows: lane supplies M index c16 of every tile. Loads are unconditional (missing
+    // blocks read block 0); such tokens are always masked in S.
+    const int kq = c16 >> 2;
+    auto load_k = [&](const Blocks& bl, Regs& rg) {
+        const int blk = pick(bl, Geom::bq(kq));
+        const uint8_t* base = kv.kc + (((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * head_stride + 32 * g4) * kEB;
+#pragma unroll
+        for (int s = 0; s < kNS; ++s) {
+            const int off = Geom::ob(kq) + 4 * s + (c16 & 3);
+#pragma unroll
+            for (int v = 0; v < Geom::kKVec; ++v) rg.k[s][v] = *(const uint4*)(base + (size_t)off * kD * kEB + 16 * v);
+        }
+    };
+    // V: lane owns block bq(g4), dim dt*16 + c16, offsets ob(g4) .. ob(g4)+16/kEB-1 (zeroed
+    // later when the block is missing or partly past the keys).
+    auto load_v = [&](const Blocks& bl, Regs& rg) {
+        const int blk = pick(bl, Geom::bq(g4));
+        const uint8_t* base = kv.vc + ((((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * kD) * kBS + Geom::ob(g4)) * kEB;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int d = dt * 16 + c16;
+            rg.v[dt] = *(const uint4*)(base + (size_t)d * kBS * kEB);
+        }
+    };
 
-        // ---- loads ----
-        constexpr int kKVec = 32 * kEB / 16;  // 16-byte loads per lane per K tile
-        uint4 kraw[4][kKVec];
-        {
-            const uint8_t* kbase = kv.kc + (((size_t)(blk_k < 0 ? 0 : blk_k) * kv.Hkv + kvh) * head_stride_k +
-                                            32 * g4) * kEB;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int off = 4 * s + (c16 & 3);
-#pragma unroll
-                for (int v = 0; v < kKVec; ++v)
-                    kraw[s][v] = blk_k >= 0 ? *(const uint4*)(kbase + (size_t)off * kD * kEB + 16 * v) : zero4();
-            }
-        }
-        constexpr int kVVec = 16 * kEB / 16;  // 16-byte loads per lane per V dim-tile
-        uint4 vraw[8][kVVec];
-        {
-            const uint8_t* vbase = kv.vc + (((size_t)(blk_v < 0 ? 0 : blk_v) * kv.Hkv + kvh) * kD) * kBS * kEB;
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const int d = dt * 16 + c16;
-#pragma unroll
-                for (int v = 0; v < kVVec; ++v)
-                    vraw[dt][v] = blk_v >= 0 ? *(const uint4*)(vbase + (size_t)d * kBS * kEB + 16 * v) : zero4();
-            }
-        }
-        if (blk_v >= 0 && nvalid_v < kBS) {
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                if constexpr (kEB == 1) vraw[dt][0] = mask_bytes16(vraw[dt][0], nvalid_v);
-                else {
-                    vraw[dt][0] = mask_halves8(vraw[dt][0], nvalid_v, 0);
-                    vraw[dt][1] = mask_halves8(vraw[dt][1], nvalid_v, 8);
-                }
-            }
-        }
+    Regs cur;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    Blocks bl_cur = chunk_blocks(wave_u);
+    load_k(bl_cur, cur);
+    load_v(bl_cur, cur);
+
+    for (int ch = wave_u; ch < nchunks; ch += kWaves) {
+        const int blk_v = pick(bl_cur, Geom::bq(g4));
+        const Blocks bl_next = chunk_blocks(ch + kWaves);
+        const int tc = t0 + ch * kTok;
+        const int tlane = tc + 16 * Geom::bq(g4) + Geom::ob(g4);  // first token of the lane's P run
+        // Valid offsets of the lane's V block (offsets counted from the block start).
+        const int nvalid_v = blk_v < 0 ? 0 : ctx - (tc + 16 * Geom::bq(g4));
 
         float kblk_scale = 1.f, vblk_scale = 1.f;
         if constexpr (DT == GG_DTYPE_INT8) {
@@ -276,46 +359,45 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
             }
         }
 
-        // K operands per (tile s, dim group mm)
-        uint4 kop[4][4];
+        // ---- S^T = K . Q^T for kTok tokens x all row tiles; each K tile decoded once ----
+        f32x4 sacc[NT][kNS];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < kNS; ++s) {
+            uint4 kop[4];
 #pragma unroll
             for (int mm = 0; mm < 4; ++mm) {
                 if constexpr (kEB == 2) {
-                    kop[s][mm] = kraw[s][mm];
+                    kop[mm] = cur.k[s][mm];
                 } else {
-                    const uint4 r = kraw[s][mm >> 1];
-                    const uint32_t w0 = (mm & 1) ? r.z : r.x;
-                    const uint32_t w1 = (mm & 1) ? r.w : r.y;
-                    kop[s][mm] = bytes8_to_f16x8<DT>(w0, w1);
+                    const uint4 r = cur.k[s][mm >> 1];
+                    kop[mm] = (mm & 1) ? bytes8_to_f16x8<DT>(r.z, r.w) : bytes8_to_f16x8<DT>(r.x, r.y);
                 }
             }
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt) {
+                sacc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) sacc[rt][s] = mfma(kop[mm], qop[rt][mm], sacc[rt][s], kIsBf16);
+            }
         }
+        // Next chunk's K rows stream in while this chunk finishes.
+        load_k(bl_next, cur);
 
-        const bool need_mask = tc + kChunk - 1 >= first_masked;
+        // ---- online softmax; P packed as MFMA A operands ----
+        const bool need_mask = tc + kTok - 1 >= first_masked;
+        const float mult = DT == GG_DTYPE_INT8 ? sscale * kblk_scale : sscale;
+        constexpr int kNP = 4 * kNS;  // P values per lane per row tile
+        uint4 pop[NT][Geom::kNPV][kIsBf16 ? 2 : 1];
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
-            // ---- scores for 64 tokens x 16 rows ----
-            f32x4 sacc[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                sacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int mm = 0; mm < 4; ++mm) sacc[s] = mfma(kop[s][mm], qop[rt][mm], sacc[s], kIsBf16);
-            }
-            float sc[16];
+            float sc[kNP];
             float cmax = -INFINITY;
-            const float mult = DT == GG_DTYPE_INT8 ? sscale * kblk_scale : sscale;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < kNS; ++s) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = sacc[s][i] * mult;
-                    if (need_mask) {
-                        const int t = tv + 4 * s + i;
-                        v = t <= row_pos[rt] ? v : -INFINITY;
-                    }
+                    float v = sacc[rt][s][i] * mult;
+                    if (need_mask) v = (tlane + 4 * s + i) <= row_pos[rt] ? v : -INFINITY;
                     sc[4 * s + i] = v;
                     cmax = fmaxf(cmax, v);
                 }
@@ -327,25 +409,27 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
             m_run[rt] = m_new;
             float psum = 0.f;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
+            for (int k = 0; k < kNP; ++k) {
                 sc[k] = __builtin_amdgcn_exp2f(sc[k] - m_new);
                 psum += sc[k];
             }
             l_run[rt] = l_run[rt] * alpha + psum;
-            // Rescale O rows (4*g4 + i) with their rows' alpha.
+            // Rescale O rows (4*g4 + i) by their rows' alpha; skipped by the whole wave
+            // when no row max moved (the common case once the running max has settled).
+            if (__any(alpha != 1.f)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float al = __shfl(alpha, 4 * g4 + i);
+                for (int i = 0; i < 4; ++i) {
+                    const float al = __shfl(alpha, 4 * g4 + i);
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt) o[rt][dt][i] *= al;
+                    for (int dt = 0; dt < 8; ++dt) o[rt][dt][i] *= al;
+                }
             }
-            // ---- O += P . V ----
             if constexpr (DT == GG_DTYPE_INT8) {
 #pragma unroll
-                for (int k = 0; k < 16; ++k) sc[k] *= vblk_scale;
+                for (int k = 0; k < kNP; ++k) sc[k] *= vblk_scale;
             }
 #pragma unroll
-            for (int pv = 0; pv < 2; ++pv) {
+            for (int pv = 0; pv < Geom::kNPV; ++pv) {
                 const float* pp = sc + 8 * pv;
                 if constexpr (kIsBf16) {
                     float hi[8], lo[8];
@@ -354,32 +438,46 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
                         hi[k] = bf16_bits_to_f32(f32_to_bf16_bits(pp[k]));
                         lo[k] = pp[k] - hi[k];
                     }
-                    const uint4 ph = make_uint4(pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3]),
+                    pop[rt][pv][0] = make_uint4(pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3]),
                                                 pack_bf16x2(hi[4], hi[5]), pack_bf16x2(hi[6], hi[7]));
-                    const uint4 pl = make_uint4(pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]),
-                                                pack_bf16x2(lo[4], lo[5]), pack_bf16x2(lo[6], lo[7]));
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt) {
-                        o[rt][dt] = mfma(ph, vraw[dt][pv], o[rt][dt], true);
-                        o[rt][dt] = mfma(pl, vraw[dt][pv], o[rt][dt], true);
-                    }
+                    pop[rt][pv][kIsBf16 ? 1 : 0] = make_uint4(pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]),
+                                                              pack_bf16x2(lo[4], lo[5]), pack_bf16x2(lo[6], lo[7]));
                 } else {
-                    const uint4 ph = make_uint4(pack_f16x2(pp[0], pp[1]), pack_f16x2(pp[2], pp[3]),
+                    pop[rt][pv][0] = make_uint4(pack_f16x2(pp[0], pp[1]), pack_f16x2(pp[2], pp[3]),
                                                 pack_f16x2(pp[4], pp[5]), pack_f16x2(pp[6], pp[7]));
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt) {
-                        uint4 vop;
-                        if constexpr (kEB == 2) {
-                            vop = vraw[dt][pv];
-                        } else {
-                            const uint4 r = vraw[dt][0];
-                            vop = pv ? bytes8_to_f16x8<DT>(r.z, r.w) : bytes8_to_f16x8<DT>(r.x, r.y);
-                        }
-                        o[rt][dt] = mfma(ph, vop, o[rt][dt], false);
-                    }
                 }
             }
         }
+
+        // ---- O += P . V; each V dim tile decoded once for all row tiles ----
+        if (nvalid_v < kBS) {
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                if constexpr (kEB == 1) cur.v[dt] = mask_bytes16(cur.v[dt], nvalid_v);
+                else cur.v[dt] = mask_halves8(cur.v[dt], nvalid_v, Geom::ob(g4));
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+            for (int pv = 0; pv < Geom::kNPV; ++pv) {
+                uint4 vop;
+                if constexpr (kEB == 2) {
+                    vop = cur.v[dt];
+                } else {
+                    const uint4 r = cur.v[dt];
+                    vop = pv ? bytes8_to_f16x8<DT>(r.z, r.w) : bytes8_to_f16x8<DT>(r.x, r.y);
+                }
+#pragma unroll
+                for (int rt = 0; rt < NT; ++rt) {
+                    o[rt][dt] = mfma(pop[rt][pv][0], vop, o[rt][dt], kIsBf16);
+                    if constexpr (kIsBf16) o[rt][dt] = mfma(pop[rt][pv][1], vop, o[rt][dt], true);
+                }
+            }
+        }
+        // Next chunk's V columns.
+        load_v(bl_next, cur);
+        bl_cur = bl_next;
     }
 
     // ---- merge the four waves' states through LDS ----
