@@ -16,10 +16,14 @@
 //     2048-bin histogram of (max-l)/T in 1/64-nat slices followed by three
 //     11/11/10-bit radix levels on the order key (LDS u64 atomics: exact), and a
 //     9+9-bit index select when the boundary value is tied and cut.
-//   kernel 2 (decide), one block per sequence: walks the drafts
-//     (accept iff u*q(x)*Zp < w(x)), then draws the corrected token from
-//     max(0, w - floor(q*Zp)) or the bonus token from row n with a block-wide
-//     exclusive scan over the row.
+//     Without top-p the same statistics come from two segmented launches (segment
+//     max, then segment sums of w) over (row, 8192-logit segment) blocks.
+//   draw sums, one block per (sequence, segment): walks the drafts (accept iff
+//     u*q(x)*Zp < w(x)), then sums the final row's segment of max(0, w -
+//     floor(q*Zp)) (first rejection) or of w (bonus, row n);
+//   draw find, one block per sequence: locates floor(u*total) among the segment sums,
+//     then inside that one segment.
+// The draft distributions are read only at drafted tokens and on the final row.
 #pragma clang fp contract(off)
 
 #include "gg_common.h"
@@ -319,118 +323,421 @@ __global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
 }
 
 // Block-wide inclusive scan of u64 (1024 threads), returns inclusive value.
-__device__ u64 block_scan_u64(u64 v, u64* red, u64* total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    u64 incl = v;
-    for (int o = 1; o < 64; o <<= 1) {
-        u64 t = shfl_up_u64(incl, o);
-        if (lane >= o) incl += t;
-    }
+// ---------------------------------------------------------------------------
+// Segmented path. A row of V logits is cut into segments of kSegElems; every
+// (row, segment) pair is one 256-thread block, so a launch has thousands of blocks.
+// All cross-segment combinations are max of floats or sums of integers: exact and
+// order-free, so the result is the same bit pattern whatever the schedule.
+
+constexpr int kSegThreads = 256;
+constexpr int kSegElems = 8192;  // 32 logits per thread
+
+struct SegOut {
+    u64 sum_res;     // residual weights of the segment (final row)
+    u64 sum_plain;   // nucleus weights of the segment (final row)
+    int last_res;    // last index with a non-zero residual weight (-1: none)
+    int last_plain;
+};
+
+struct SeqDecision {
+    int accepted;
+    int row;         // row of the final draw
+    int residual;    // 1: draw from max(0, w - floor(q*Zp)), 0: from w
+};
+
+__device__ __forceinline__ float seg_block_max(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     __syncthreads();
-    if (lane == 63) red[w] = incl;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    u64 before = 0, tot = 0;
-    for (int i = 0; i < kWaves; ++i) {
-        if (i < w) before += red[i];
-        tot += red[i];
-    }
-    *total = tot;
-    return before + incl;
+    float t = red[0];
+    for (int i = 1; i < kSegThreads / 64; ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+__device__ __forceinline__ u64 seg_block_sum(u64 v, u64* red) {
+    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_u64(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    u64 t = 0;
+    for (int i = 0; i < kSegThreads / 64; ++i) t += red[i];
+    return t;
+}
+__device__ __forceinline__ int seg_block_maxi(int v, int* red) {
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int t = red[0];
+    for (int i = 1; i < kSegThreads / 64; ++i) t = max(t, red[i]);
+    return t;
 }
 
+// The 32 logits a thread owns in a segment: elements base + 8*threadIdx + {0..7} of each
+// of the four 2048-element quarters (16-byte loads; scalar fallback for odd rows).
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kThreads) rejection_decide_kernel(
-    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V,
-    const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
-    const float* __restrict__ uniforms, float inv_t, const RowStats* __restrict__ stats,
-    int32_t* __restrict__ out_acc, int32_t* __restrict__ out_tok) {
-    const int b = blockIdx.x;
+__device__ __forceinline__ void load_seg(const void* row, int V, int seg, bool vec_ok, float (&x)[32],
+                                         int (&idx)[32]) {
+    const int base = seg * kSegElems;
+#pragma unroll
+    for (int qtr = 0; qtr < 4; ++qtr) {
+        const int e0 = base + qtr * 2048 + 8 * threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) idx[qtr * 8 + k] = e0 + k;
+        if (vec_ok && e0 + 8 <= V) {
+            if constexpr (DT == GG_DTYPE_F32) {
+                const float4 a = *(const float4*)((const float*)row + e0);
+                const float4 b = *(const float4*)((const float*)row + e0 + 4);
+                x[qtr * 8 + 0] = a.x; x[qtr * 8 + 1] = a.y; x[qtr * 8 + 2] = a.z; x[qtr * 8 + 3] = a.w;
+                x[qtr * 8 + 4] = b.x; x[qtr * 8 + 5] = b.y; x[qtr * 8 + 6] = b.z; x[qtr * 8 + 7] = b.w;
+            } else {
+                const uint4 r = *(const uint4*)((const uint16_t*)row + e0);
+                const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint16_t h = (uint16_t)(w[k >> 1] >> ((k & 1) * 16));
+                    x[qtr * 8 + k] = DT == GG_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[qtr * 8 + k] = (e0 + k < V) ? ld<DT>(row, e0 + k) : NAN;
+        }
+    }
+}
+
+// A: per (row, segment) max over finite logits.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) seg_max_kernel(const void* __restrict__ logits, int K, int V,
+                                                              int nseg, int vec_ok,
+                                                              const int32_t* __restrict__ n_drafts,
+                                                              float* __restrict__ seg_max) {
+    const int seg = blockIdx.x, row = blockIdx.y;
     const int R = K + 1;
+    const int b = row / R, j = row % R;
     int n = n_drafts[b];
     n = n < 0 ? 0 : (n > K ? K : n);
-    __shared__ u64 red64[kWaves];
-    __shared__ int redi[kWaves];
-    __shared__ int s_found;
+    if (j > n) return;
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    float x[32];
+    int idx[32];
+    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+        if (finite_f(x[k])) m = fmaxf(m, x[k]);
+    __shared__ float red[kSegThreads / 64];
+    m = seg_block_max(m, red);
+    if (threadIdx.x == 0) seg_max[(size_t)row * nseg + seg] = m;
+}
 
-    // Sequential acceptance walk (uniform across the block).
-    int a = n;
+__device__ __forceinline__ float row_max_from_segs(const float* seg_max, int row, int nseg) {
+    float m = -INFINITY;
+    for (int s = 0; s < nseg; ++s) m = fmaxf(m, seg_max[(size_t)row * nseg + s]);
+    return m;
+}
+
+// B: per (row, segment) sum of fixed-point weights.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) seg_z_kernel(const void* __restrict__ logits, int K, int V,
+                                                            int nseg, int vec_ok, float inv_t,
+                                                            const int32_t* __restrict__ n_drafts,
+                                                            const float* __restrict__ seg_max,
+                                                            u64* __restrict__ seg_z) {
+    const int seg = blockIdx.x, row = blockIdx.y;
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    int n = n_drafts[b];
+    n = n < 0 ? 0 : (n > K ? K : n);
+    if (j > n) return;
+    __shared__ float s_m;
+    __shared__ u64 red[kSegThreads / 64];
+    if (threadIdx.x == 0) s_m = row_max_from_segs(seg_max, row, nseg);
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    float x[32];
+    int idx[32];
+    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
+    __syncthreads();
+    const float m = s_m;
+    u64 z = 0;
+    if (finite_f(m)) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k)
+            if (finite_f(x[k])) z += gg_weight(x[k], m, inv_t);
+    }
+    z = seg_block_sum(z, red);
+    if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
+}
+
+// Per-row statistics seen by the decision: max, nucleus mass and nucleus boundary.
+struct RowView {
+    float m;
+    u64 zp;
+    unsigned int lam;
+    int idx_cut;
+};
+
+__device__ __forceinline__ RowView row_view(int row, int nseg, int use_topp, const RowStats* stats,
+                                            const float* seg_max, const u64* seg_z) {
+    RowView v;
+    if (use_topp) {
+        const RowStats& st = stats[row];
+        v.m = st.m;
+        v.zp = st.zp;
+        v.lam = st.lam;
+        v.idx_cut = st.idx_cut;
+    } else {
+        v.m = row_max_from_segs(seg_max, row, nseg);
+        u64 z = 0;
+        for (int s = 0; s < nseg; ++s) z += seg_z[(size_t)row * nseg + s];
+        v.zp = z;
+        v.lam = 0;
+        v.idx_cut = 0x7fffffff;
+    }
+    return v;
+}
+
+// Acceptance walk of one sequence (identical in every block that evaluates it).
+template <gg_dtype_t DT>
+__device__ SeqDecision decide_seq(const void* logits, const float* dprobs, int K, int V, int b, int n,
+                                  const int32_t* drafts, const float* uniforms, float inv_t, int nseg,
+                                  int use_topp, const RowStats* stats, const float* seg_max,
+                                  const u64* seg_z) {
+    const int R = K + 1;
+    SeqDecision d{n, n, 0};
     for (int j = 0; j < n; ++j) {
-        const RowStats& st = stats[(size_t)b * R + j];
+        const int row = b * R + j;
+        const RowView rv = row_view(row, nseg, use_topp, stats, seg_max, seg_z);
         const int x = drafts[(size_t)b * K + j];
-        double q = 1.0;
-        if (dprobs) q = (x >= 0 && x < V) ? (double)dprobs[((size_t)b * K + j) * V + x] : 0.0;
-        const double u = (double)uniforms[(size_t)b * R + j];
-        const bool ok = (x >= 0 && x < V) && (u * q * (double)st.zp < (double)st.wx);
+        bool ok = false;
+        if (x >= 0 && x < V && finite_f(rv.m)) {
+            const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+            Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
+            const u64 wx = nu.weight(ld<DT>(lp, x), x);
+            const double q = dprobs ? (double)dprobs[((size_t)b * K + j) * V + x] : 1.0;
+            const double u = (double)uniforms[(size_t)b * R + j];
+            ok = u * q * (double)rv.zp < (double)wx;
+        }
         if (!ok) {
-            a = j;
+            d.accepted = j;
+            d.row = j;
+            d.residual = 1;
             break;
         }
     }
-    const bool residual = a < n;
-    const int f = a;  // row of the final draw
-    const RowStats st = stats[(size_t)b * R + f];
-    const void* lp = (const uint8_t*)logits + (size_t)((size_t)b * R + f) * V * dtype_bytes(DT);
-    Nucleus nu{st.m, inv_t, st.lam, st.idx_cut};
-    const float* qrow = (residual && dprobs) ? dprobs + ((size_t)b * K + f) * V : nullptr;
-    const int xr = residual ? drafts[(size_t)b * K + f] : -1;
-    const double zp_d = (double)st.zp;
+    return d;
+}
 
-    auto r_at = [&](int i, bool use_res) -> u64 {
-        if (!finite_f(st.m)) return 0ull;
+// D: per (sequence, segment): decide, then the segment's residual and plain weight
+// sums on the final row (and the last non-zero index of each).
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) seg_draw_sums_kernel(
+    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
+    float inv_t, int use_topp, const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
+    const float* __restrict__ uniforms, const RowStats* __restrict__ stats,
+    const float* __restrict__ seg_max, const u64* __restrict__ seg_z, SeqDecision* __restrict__ dec,
+    SegOut* __restrict__ seg_out) {
+    const int seg = blockIdx.x, b = blockIdx.y;
+    const int R = K + 1;
+    int n = n_drafts[b];
+    n = n < 0 ? 0 : (n > K ? K : n);
+    __shared__ SeqDecision s_d;
+    __shared__ RowView s_rv;
+    __shared__ u64 red[kSegThreads / 64];
+    __shared__ int redi[kSegThreads / 64];
+    if (threadIdx.x == 0) {
+        s_d = decide_seq<DT>(logits, dprobs, K, V, b, n, drafts, uniforms, inv_t, nseg, use_topp, stats,
+                             seg_max, seg_z);
+        s_rv = row_view(b * R + s_d.row, nseg, use_topp, stats, seg_max, seg_z);
+        if (seg == 0) dec[b] = s_d;
+    }
+    __syncthreads();
+    const SeqDecision d = s_d;
+    const RowView rv = s_rv;
+    const int row = b * R + d.row;
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    float x[32];
+    int idx[32];
+    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
+    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
+    const float* qrow = (d.residual && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
+    const int xr = d.residual ? drafts[(size_t)b * K + d.row] : -1;
+    const double zp_d = (double)rv.zp;
+    u64 s_res = 0, s_pl = 0;
+    int l_res = -1, l_pl = -1;
+    const bool row_ok = finite_f(rv.m);
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const int i = idx[k];
+        if (i >= V || !row_ok) continue;
+        const u64 w = nu.weight(x[k], i);
+        u64 r = w;
+        if (d.residual) {
+            u64 qf;
+            if (qrow) {
+                const float qi = qrow[i];
+                qf = (u64)(qi < 0.f ? 0.0 : (double)qi * zp_d);
+            } else {
+                qf = (i == xr) ? rv.zp : 0ull;
+            }
+            r = w > qf ? w - qf : 0ull;
+        }
+        s_res += r;
+        s_pl += w;
+        if (r) l_res = max(l_res, i);
+        if (w) l_pl = max(l_pl, i);
+    }
+    s_res = seg_block_sum(s_res, red);
+    s_pl = seg_block_sum(s_pl, red);
+    l_res = seg_block_maxi(l_res, redi);
+    l_pl = seg_block_maxi(l_pl, redi);
+    if (threadIdx.x == 0) seg_out[(size_t)b * nseg + seg] = SegOut{s_res, s_pl, l_res, l_pl};
+}
+
+// E: per sequence: pick the segment holding floor(u * total), then the element inside it.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
+    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, float inv_t,
+    int use_topp, const int32_t* __restrict__ drafts, const float* __restrict__ uniforms,
+    const RowStats* __restrict__ stats, const float* __restrict__ seg_max, const u64* __restrict__ seg_z,
+    const SeqDecision* __restrict__ dec, const SegOut* __restrict__ seg_out, int32_t* __restrict__ out_acc,
+    int32_t* __restrict__ out_tok) {
+    const int b = blockIdx.x;
+    const int R = K + 1;
+    __shared__ int s_seg, s_use_res, s_found;
+    __shared__ u64 s_t;
+    __shared__ u64 s_scan[kSegThreads];
+    const SeqDecision d = dec[b];
+    if (threadIdx.x == 0) {
+        u64 tot_res = 0, tot_pl = 0;
+        int last_res = -1, last_pl = -1;
+        for (int s = 0; s < nseg; ++s) {
+            const SegOut o = seg_out[(size_t)b * nseg + s];
+            tot_res += o.sum_res;
+            tot_pl += o.sum_plain;
+            last_res = max(last_res, o.last_res);
+            last_pl = max(last_pl, o.last_plain);
+        }
+        // A vanished residual falls back to the target row itself.
+        const int use_res = (d.residual && tot_res > 0) ? 1 : 0;
+        const u64 tot = use_res ? tot_res : tot_pl;
+        const int last = use_res ? last_res : last_pl;
+        s_use_res = use_res;
+        s_seg = -1;
+        s_found = -1;
+        int token = 0;
+        if (tot > 0) {
+            const double u = (double)uniforms[(size_t)b * R + K];
+            const u64 t = (u64)(u * (double)tot);
+            u64 c = 0;
+            for (int s = 0; s < nseg; ++s) {
+                const SegOut o = seg_out[(size_t)b * nseg + s];
+                const u64 v = use_res ? o.sum_res : o.sum_plain;
+                if (c + v > t) {
+                    s_seg = s;
+                    s_t = t - c;
+                    break;
+                }
+                c += v;
+            }
+            token = last >= 0 ? last : 0;  // used when no segment crosses (u >= 1)
+        }
+        s_found = token;
+        out_acc[b] = d.accepted;
+    }
+    __syncthreads();
+    if (s_seg < 0) {
+        if (threadIdx.x == 0) out_tok[b] = s_found;
+        return;
+    }
+    // Scan the chosen segment: thread k owns 32 consecutive elements [32k, 32k+32).
+    const int row = b * R + d.row;
+    const RowView rv = row_view(row, nseg, use_topp, stats, seg_max, seg_z);
+    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    const float* qrow = (s_use_res && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
+    const int xr = s_use_res ? drafts[(size_t)b * K + d.row] : -1;
+    const double zp_d = (double)rv.zp;
+    auto r_at = [&](int i) -> u64 {
+        if (i >= V) return 0ull;
         const u64 w = nu.weight(ld<DT>(lp, i), i);
-        if (!use_res) return w;
+        if (!s_use_res) return w;
         u64 qf;
-        if (qrow) qf = (u64)(qrow[i] < 0.f ? 0.0 : (double)qrow[i] * zp_d);
-        else qf = (i == xr) ? st.zp : 0ull;
+        if (qrow) {
+            const float qi = qrow[i];
+            qf = (u64)(qi < 0.f ? 0.0 : (double)qi * zp_d);
+        } else {
+            qf = (i == xr) ? rv.zp : 0ull;
+        }
         return w > qf ? w - qf : 0ull;
     };
-
-    bool use_res = residual;
-    u64 tot = 0;
-    int last_nz = -1;
-    for (int pass = 0; pass < 2; ++pass) {
-        u64 s = 0;
-        int lnz = -1;
-        for (int i = threadIdx.x; i < V; i += kThreads) {
-            const u64 r = r_at(i, use_res);
-            s += r;
-            if (r) lnz = i;
-        }
-        tot = block_sum_u64(s, red64);
-        last_nz = block_max_i(lnz, redi);
-        if (tot > 0 || !use_res) break;
-        use_res = false;  // residual vanished: draw from the target row itself
-    }
-    int token = 0;
-    if (tot > 0) {
-        const double u = (double)uniforms[(size_t)b * R + K];
-        const u64 t = (u64)(u * (double)tot);
-        if (threadIdx.x == 0) s_found = -1;
-        u64 carry = 0;
-        for (int base = 0; base < V; base += kThreads) {
-            const int i = base + threadIdx.x;
-            const u64 r = i < V ? r_at(i, use_res) : 0ull;
-            u64 tile_total;
-            const u64 incl = block_scan_u64(r, red64, &tile_total) + carry;
-            const bool hit = r > 0 && incl > t && (incl - r) <= t;
-            __syncthreads();
-            if (hit) s_found = i;
-            __syncthreads();
-            if (s_found >= 0) break;
-            carry += tile_total;
-        }
-        token = s_found >= 0 ? s_found : (last_nz >= 0 ? last_nz : 0);
-    }
+    const int e0 = s_seg * kSegElems + 32 * threadIdx.x;
+    u64 mine = 0;
+    for (int k = 0; k < 32; ++k) mine += r_at(e0 + k);
+    s_scan[threadIdx.x] = mine;
+    __syncthreads();
     if (threadIdx.x == 0) {
-        out_acc[b] = a;
-        out_tok[b] = token;
+        // Exclusive prefix of the per-thread sums (256 entries, serial: cheap).
+        u64 c = 0;
+        for (int k = 0; k < kSegThreads; ++k) {
+            const u64 v = s_scan[k];
+            s_scan[k] = c;
+            c += v;
+        }
     }
+    __syncthreads();
+    const u64 t = s_t;
+    const u64 before = s_scan[threadIdx.x];
+    if (before <= t && before + mine > t) {
+        u64 c = before;
+        for (int k = 0; k < 32; ++k) {
+            c += r_at(e0 + k);
+            if (c > t) {
+                s_found = e0 + k;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) out_tok[b] = s_found;
 }
 
 }  // namespace
 
+static int rej_nseg(int vocab) { return (vocab + kSegElems - 1) / kSegElems; }
+
+struct RejWs {
+    RowStats* stats;
+    float* seg_max;
+    u64* seg_z;
+    SeqDecision* dec;
+    SegOut* seg_out;
+    size_t bytes;
+};
+
+static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab) {
+    const size_t rows = (size_t)num_seqs * (max_drafts + 1);
+    const int nseg = rej_nseg(vocab);
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    size_t off = 0;
+    RejWs w{};
+    uint8_t* p = (uint8_t*)base;
+    w.stats = (RowStats*)(p + off);
+    off += al(rows * sizeof(RowStats));
+    w.seg_max = (float*)(p + off);
+    off += al(rows * nseg * sizeof(float));
+    w.seg_z = (u64*)(p + off);
+    off += al(rows * nseg * sizeof(u64));
+    w.dec = (SeqDecision*)(p + off);
+    off += al((size_t)num_seqs * sizeof(SeqDecision));
+    w.seg_out = (SegOut*)(p + off);
+    off += al((size_t)num_seqs * nseg * sizeof(SegOut));
+    w.bytes = off;
+    return w;
+}
+
 size_t rejection_workspace_bytes(int num_seqs, int max_drafts, int vocab) {
-    size_t own = (size_t)num_seqs * (max_drafts + 1) * sizeof(RowStats);
+    size_t own = rej_layout(nullptr, num_seqs, max_drafts, vocab).bytes;
     size_t g = greedy_workspace_bytes(num_seqs, max_drafts, vocab);
     return own > g ? own : g;
 }
@@ -442,14 +749,28 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                     hipStream_t s) {
     const float inv_t = 1.0f / temperature;
     const int use_topp = (top_p > 0.f && top_p < 1.f) ? 1 : 0;
-    RowStats* st = (RowStats*)ws;
+    const RejWs w = rej_layout(ws, num_seqs, max_drafts, vocab);
     const int rows = num_seqs * (max_drafts + 1);
-#define GG_REJ(DTV)                                                                                  \
-    rejection_row_stats_kernel<DTV><<<rows, kThreads, 0, s>>>(logits, max_drafts, vocab, drafts,     \
-                                                              n_drafts, inv_t, top_p, use_topp, st); \
-    rejection_decide_kernel<DTV><<<num_seqs, kThreads, 0, s>>>(logits, q, max_drafts, vocab, drafts, \
-                                                               n_drafts, uniforms, inv_t, st,        \
-                                                               out_acc, out_tok);
+    const int nseg = rej_nseg(vocab);
+    const int K = max_drafts;
+    const size_t eb = dtype_bytes(dt);
+    const int vec_ok = ((vocab * eb) % 16 == 0) && (((uintptr_t)logits) % 16 == 0);
+#define GG_REJ(DTV)                                                                                        \
+    if (use_topp) {                                                                                        \
+        rejection_row_stats_kernel<DTV><<<rows, kThreads, 0, s>>>(logits, K, vocab, drafts, n_drafts,      \
+                                                                  inv_t, top_p, use_topp, w.stats);        \
+    } else {                                                                                               \
+        seg_max_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,       \
+                                                                     n_drafts, w.seg_max);                 \
+        seg_z_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, inv_t,  \
+                                                                   n_drafts, w.seg_max, w.seg_z);          \
+    }                                                                                                      \
+    seg_draw_sums_kernel<DTV><<<dim3(nseg, num_seqs), kSegThreads, 0, s>>>(                                \
+        logits, q, K, vocab, nseg, vec_ok, inv_t, use_topp, drafts, n_drafts, uniforms, w.stats,           \
+        w.seg_max, w.seg_z, w.dec, w.seg_out);                                                             \
+    seg_draw_find_kernel<DTV><<<num_seqs, kSegThreads, 0, s>>>(logits, q, K, vocab, nseg, inv_t, use_topp, \
+                                                               drafts, uniforms, w.stats, w.seg_max,       \
+                                                               w.seg_z, w.dec, w.seg_out, out_acc, out_tok);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_REJ(GG_DTYPE_BF16) break;

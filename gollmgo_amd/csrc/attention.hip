@@ -153,10 +153,11 @@ int attn_resolve_partition(const KV* kv, int num_seqs, int rows, int num_q_heads
                            int partition_tokens) {
     if (partition_tokens > 0) return partition_tokens;
     (void)num_seqs;
-    (void)rows;
-    (void)num_q_heads;
-    (void)max_blocks;
-    return attn_mfma_supported(kv, rows, num_q_heads) ? kMfmaAutoPartition : 512;
+    if (!attn_mfma_supported(kv, rows, num_q_heads)) return 512;
+    // Longer partitions amortise each workgroup's pipeline start (Q, block ids, first
+    // chunk) and its partial write; short contexts keep more workgroups in flight.
+    const long long max_keys = (long long)max_blocks * kv->block_size;
+    return max_keys >= 4096 ? 2 * kMfmaAutoPartition : kMfmaAutoPartition;
 }
 
 size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
