@@ -173,9 +173,12 @@ size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_head
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s) {
     const KV* kv = a.kv;
     KVView view = make_kv_view(kv, a.layer);
-    if (attn_mfma_supported(kv, a.rows, a.num_q_heads) && a.partition % 64 == 0) {
+    if (a.streamk || (attn_mfma_supported(kv, a.rows, a.num_q_heads) && a.partition % 64 == 0 &&
+                      a.partition <= kMfmaMaxPartition)) {
+        // Stream-K launches its own combine over its record layout.
         gg_status_t st = launch_attn_mfma(a, view, s);
         if (st != GG_OK) return st;
+        if (a.streamk) return check_hip(hipGetLastError(), "verify_attention launch");
     } else {
         const int DC = (kv->head_dim + 63) / 64;
         dim3 grid(a.max_parts, a.num_q_heads, a.num_seqs * a.rows);

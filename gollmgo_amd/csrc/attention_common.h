@@ -5,6 +5,8 @@
 namespace gg {
 
 constexpr int kMfmaAutoPartition = 1024;
+constexpr int kMfmaMaxPartition = 16384;  // longest explicit partition on the MFMA path
+constexpr int kStreamKMinChunks = 16;     // least chunks per stream-K workgroup
 
 // One layer of the paged pools, with dequantisation folded in.
 struct KVView {

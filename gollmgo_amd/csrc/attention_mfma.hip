@@ -11,7 +11,7 @@
 //   S^T = K . Q^T   v_mfma_f32_16x16x32_{bf16,f16}: A = K (16 tokens x 32 dims),
 //                   B = Q^T. Token m = 4q+i of tile s is (block q, offset 4s+i), so
 //                   the output gives lane (g4, c) row c and block g4's offsets 4s..4s+3.
-//   P = softmax     online, per row, base-2 exponent; row max via xor-shuffles 16/32.
+//   P = softmax     online, per row, base-2 exponent; row max via the row-swap permutes.
 //   O += P . V      A = P (row c, k = 8*g4+i -> block g4 offset 8*pv+i),
 //                   B = V from the dim-major V block: one 16-byte load gives a lane
 //                   all 16 offsets of one dim.
@@ -112,6 +112,17 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
 
+// Max over lanes l, l^16, l^32, l^48 (the four 16-lane rows of the wave) with the gfx950
+// row-swap permutes, which stay in the VALU instead of going through the LDS crossbar.
+__device__ __forceinline__ float max_over_rows(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Zero the 1-byte elements at offsets >= nvalid of a 16-offset run.
 __device__ __forceinline__ uint4 mask_bytes16(uint4 v, int nvalid) {
     uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -168,9 +179,12 @@ struct ChunkRegs {
     uint4 v[8];
 };
 
+// One piece of work: tokens [t0, t_end) of sequence b against kv head kvh. The result
+// goes to the output (part < 0 && rec < 0), to partition slot `part` of the fixed
+// partition grid, or to stream-K record `rec`. Must be reached by the whole workgroup.
 template <gg_dtype_t DT, int NT>
-__global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
-    attn_mfma_kernel(AttnArgs a, KVView kv) {
+__device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, int b, int kvh, int t0,
+                                           int t_end, int part, int rec) {
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
     constexpr int kEB = T::kEB;
@@ -179,27 +193,20 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
     constexpr int kTok = Geom::kTok;
     constexpr int kNS = Geom::kNS;
 
-    const int part = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
     const int ctx = seq_keys(a, b, kBS);
-    const int P = a.partition;
-    const int nparts = (ctx + P - 1) / P;
-    if (part >= nparts) return;
     const int R = a.rows;
     const int nrows = a.row_counts ? a.row_counts[b] : R;
     if (nrows <= 0 || nrows > ctx) return;
     const int Hq = a.num_q_heads;
     const int G = Hq / kv.Hkv;
     const int nvalid_rows = G * nrows;
+    const bool final_out = part < 0 && rec < 0;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int c16 = lane & 15;
     const int g4 = lane >> 4;
 
-    const int t0 = part * P;
-    const int t_end = min(t0 + P, ctx);
     const int nchunks = (t_end - t0 + kTok - 1) / kTok;
     const int first_masked = ctx - nrows;  // tokens >= this are causally masked for some row
 
@@ -212,10 +219,13 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
     }
 
     // ---- Q operands: B[k = 8*g4+i][n = c16] <- Q[row rt*16+c16][32*g4 + 8*mm + i] ----
-    // All loads are issued unconditionally (invalid rows read row 0 and are zeroed).
-    uint4 qop[NT][4];
+    // Staged once per piece in LDS (wave w converts dim group mm = w for every row tile)
+    // and read back per chunk one mm at a time, so only NT operands are live in the loop.
+    // Loads are issued unconditionally (invalid rows read row 0 and are zeroed).
+    __shared__ uint4 s_q[NT][4][64];  // [rt][mm][lane]
     int row_pos[NT];  // last visible key position of the lane's S row (c16)
     {
+        const int mm = wave;
         size_t qb[NT];
         bool qvalid[NT];
 #pragma unroll
@@ -225,57 +235,50 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
             const int j = qvalid[rt] ? r / G : 0;
             const int g = qvalid[rt] ? r % G : 0;
             row_pos[rt] = qvalid[rt] ? first_masked + j : ctx - 1;
-            qb[rt] = (((size_t)b * R + j) * Hq + (size_t)kvh * G + g) * kD + 32 * g4;
+            qb[rt] = (((size_t)b * R + j) * Hq + (size_t)kvh * G + g) * kD + 32 * g4 + 8 * mm;
         }
+        // One uniform dtype branch around all row tiles, so their loads issue together.
+        uint4 op[NT];
         if (a.q_dtype == GG_DTYPE_F32) {
-            float4 raw[NT][4][2];
+            float4 raw[NT][2];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-                for (int mm = 0; mm < 4; ++mm)
+                for (int h = 0; h < 2; ++h) raw[rt][h] = ((const float4*)((const float*)a.q + qb[rt]))[h];
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                        raw[rt][mm][h] = ((const float4*)((const float*)a.q + qb[rt] + 8 * mm))[h];
-#pragma unroll
-            for (int rt = 0; rt < NT; ++rt)
-#pragma unroll
-                for (int mm = 0; mm < 4; ++mm) {
-                    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-                    const float4 x = qvalid[rt] ? raw[rt][mm][0] : z4, y = qvalid[rt] ? raw[rt][mm][1] : z4;
-                    if constexpr (kIsBf16)
-                        qop[rt][mm] = make_uint4(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w),
-                                                 pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w));
-                    else
-                        qop[rt][mm] = make_uint4(pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w),
-                                                 pack_f16x2(y.x, y.y), pack_f16x2(y.z, y.w));
-                }
+            for (int rt = 0; rt < NT; ++rt) {
+                const float4 x = raw[rt][0], y = raw[rt][1];
+                if constexpr (kIsBf16)
+                    op[rt] = make_uint4(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w), pack_bf16x2(y.x, y.y),
+                                        pack_bf16x2(y.z, y.w));
+                else
+                    op[rt] = make_uint4(pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w), pack_f16x2(y.x, y.y),
+                                        pack_f16x2(y.z, y.w));
+            }
         } else {
             const bool src_bf16 = a.q_dtype == GG_DTYPE_BF16;
 #pragma unroll
-            for (int rt = 0; rt < NT; ++rt)
+            for (int rt = 0; rt < NT; ++rt) op[rt] = *(const uint4*)((const uint16_t*)a.q + qb[rt]);
+            // Convert when the Q type differs from the MFMA operand type.
+            if (src_bf16 != kIsBf16) {
 #pragma unroll
-                for (int mm = 0; mm < 4; ++mm)
-                    qop[rt][mm] = *(const uint4*)((const uint16_t*)a.q + qb[rt] + 8 * mm);
+                for (int rt = 0; rt < NT; ++rt) {
+                    const uint32_t w[4] = {op[rt].x, op[rt].y, op[rt].z, op[rt].w};
+                    uint32_t o4[4];
 #pragma unroll
-            for (int rt = 0; rt < NT; ++rt)
-#pragma unroll
-                for (int mm = 0; mm < 4; ++mm) {
-                    if (!qvalid[rt]) qop[rt][mm] = zero4();
-                    // Convert when the Q type differs from the MFMA operand type.
-                    if (src_bf16 != kIsBf16) {
-                        const uint32_t w[4] = {qop[rt][mm].x, qop[rt][mm].y, qop[rt][mm].z, qop[rt][mm].w};
-                        uint32_t o4[4];
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const uint16_t lo = (uint16_t)w[k], hi = (uint16_t)(w[k] >> 16);
-                            const float flo = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-                            const float fhi = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-                            o4[k] = kIsBf16 ? pack_bf16x2(flo, fhi) : pack_f16x2(flo, fhi);
-                        }
-                        qop[rt][mm] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+                    for (int k = 0; k < 4; ++k) {
+                        const uint16_t lo = (uint16_t)w[k], hi = (uint16_t)(w[k] >> 16);
+                        const float flo = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                        const float fhi = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                        o4[k] = kIsBf16 ? pack_bf16x2(flo, fhi) : pack_f16x2(flo, fhi);
                     }
+                    op[rt] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
                 }
+            }
         }
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) s_q[rt][mm][lane] = qvalid[rt] ? op[rt] : zero4();
+        __syncthreads();
     }
 
     f32x4 o[NT][8];
@@ -339,13 +342,16 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
 
     Regs cur;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // Block ids run two chunks ahead and are requested after the softmax: the LDS
+    // reads of Q at the top of the next chunk wait on every outstanding scalar load,
+    // and by then these have had the whole P.V stage to arrive.
     Blocks bl_cur = chunk_blocks(wave_u);
+    Blocks bl_next = chunk_blocks(wave_u + kWaves);
     load_k(bl_cur, cur);
     load_v(bl_cur, cur);
 
     for (int ch = wave_u; ch < nchunks; ch += kWaves) {
         const int blk_v = pick(bl_cur, Geom::bq(g4));
-        const Blocks bl_next = chunk_blocks(ch + kWaves);
         const int tc = t0 + ch * kTok;
         const int tlane = tc + 16 * Geom::bq(g4) + Geom::ob(g4);  // first token of the lane's P run
         // Valid offsets of the lane's V block (offsets counted from the block start).
@@ -360,24 +366,33 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
         }
 
         // ---- S^T = K . Q^T for kTok tokens x all row tiles; each K tile decoded once ----
+        // The Q index is opaque to the optimiser so that the LDS reads stay in the loop
+        // instead of being hoisted into registers for the whole piece.
+        // (Non-volatile and without a memory clobber, the asm leaves the block-table
+        // loads free to stay scalar; the chunk index input keeps it inside the loop.)
+        int qlane;
+        asm("" : "=v"(qlane) : "0"(lane), "s"(ch));
         f32x4 sacc[NT][kNS];
 #pragma unroll
-        for (int s = 0; s < kNS; ++s) {
-            uint4 kop[4];
+        for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-            for (int mm = 0; mm < 4; ++mm) {
+            for (int s = 0; s < kNS; ++s) sacc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            uint4 qop[NT];
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt) qop[rt] = s_q[rt][mm][qlane];
+#pragma unroll
+            for (int s = 0; s < kNS; ++s) {
+                uint4 kop;
                 if constexpr (kEB == 2) {
-                    kop[mm] = cur.k[s][mm];
+                    kop = cur.k[s][mm];
                 } else {
                     const uint4 r = cur.k[s][mm >> 1];
-                    kop[mm] = (mm & 1) ? bytes8_to_f16x8<DT>(r.z, r.w) : bytes8_to_f16x8<DT>(r.x, r.y);
+                    kop = (mm & 1) ? bytes8_to_f16x8<DT>(r.z, r.w) : bytes8_to_f16x8<DT>(r.x, r.y);
                 }
-            }
 #pragma unroll
-            for (int rt = 0; rt < NT; ++rt) {
-                sacc[rt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int mm = 0; mm < 4; ++mm) sacc[rt][s] = mfma(kop[mm], qop[rt][mm], sacc[rt][s], kIsBf16);
+                for (int rt = 0; rt < NT; ++rt) sacc[rt][s] = mfma(kop, qop[rt], sacc[rt][s], kIsBf16);
             }
         }
         // Next chunk's K rows stream in while this chunk finishes.
@@ -402,8 +417,7 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
                     cmax = fmaxf(cmax, v);
                 }
             }
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+            cmax = max_over_rows(cmax);
             const float m_new = fmaxf(m_run[rt], cmax);
             const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
             m_run[rt] = m_new;
@@ -449,6 +463,8 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
             }
         }
 
+        const Blocks bl_after = chunk_blocks(ch + 2 * kWaves);
+
         // ---- O += P . V; each V dim tile decoded once for all row tiles ----
         if (nvalid_v < kBS) {
 #pragma unroll
@@ -478,6 +494,7 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
         // Next chunk's V columns.
         load_v(bl_next, cur);
         bl_cur = bl_next;
+        bl_next = bl_after;
     }
 
     // ---- merge the four waves' states through LDS ----
@@ -528,11 +545,12 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
             const int j = r / G, g = r % G;
             const size_t z = zbase + j;
             const int h = kvh * G + g;
-            if (nparts == 1) {
+            if (final_out) {
                 const float val = L > 0.f ? acc * vfold / L : 0.f;
                 store_from_f32(a.out, a.out_dtype, (z * Hq + h) * kD + d, val);
             } else {
-                const size_t pidx = (z * Hq + h) * a.max_parts + part;
+                const size_t pidx = rec >= 0 ? (size_t)rec * (size_t)(G * R) + (size_t)r
+                                             : (z * Hq + h) * a.max_parts + part;
                 a.ws_acc[pidx * kD + d] = acc * vfold;
                 if (d == 0) {
                     a.ws_ml[pidx * 2 + 0] = mx > -1e29f ? mx * kLn2 : -1e30f;
@@ -544,8 +562,121 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1))
     }
 }
 
+// Fixed partition grid: workgroup (part, kvh, b) takes tokens [part*P, (part+1)*P).
+template <gg_dtype_t DT, int NT>
+__global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1)) attn_mfma_kernel(AttnArgs a, KVView kv) {
+    const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int ctx = seq_keys(a, b, kBS);
+    const int P = a.partition;
+    const int nparts = (ctx + P - 1) / P;
+    if (part >= nparts) return;
+    attn_piece<DT, NT>(a, kv, b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1);
+}
+
+// Chunks of work of sequence b (0 when it has nothing to compute).
+__device__ __forceinline__ int seq_chunks(const AttnArgs& a, int b, int tok) {
+    const int ctx = seq_keys(a, b, kBS);
+    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    if (nrows <= 0 || nrows > ctx) return 0;
+    return (ctx + tok - 1) / tok;
+}
+
+// Stream-K: the (sequence, kv head) items are laid end to end in chunk units; the grid
+// of gridDim.x workgroups splits that total evenly (at least sk_min_chunks each). A
+// workgroup's range is cut at item boundaries into pieces; a piece that is a whole item
+// writes the output, any other piece writes record (workgroup + item), and
+// attn_streamk_combine_kernel merges the records of split items.
+template <gg_dtype_t DT, int NT>
+__global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1)) attn_mfma_streamk_kernel(AttnArgs a, KVView kv) {
+    constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
+    const int w = blockIdx.x;
+    const int Hkv = kv.Hkv;
+    __shared__ long long s_scan[256];
+    __shared__ long long s_total;
+    __shared__ int s_b0;
+    __shared__ long long s_base0;
+    // Per-thread slice of sequences, its work, and an exclusive scan over threads.
+    const int B = a.num_seqs;
+    const int per_t = (B + 255) / 256;
+    const int b_lo = min(B, (int)threadIdx.x * per_t), b_hi = min(B, b_lo + per_t);
+    long long mine = 0;
+    for (int bb = b_lo; bb < b_hi; ++bb) mine += (long long)Hkv * seq_chunks(a, bb, kTok);
+    s_scan[threadIdx.x] = mine;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long c = 0;
+        for (int t = 0; t < 256; ++t) {
+            const long long v = s_scan[t];
+            s_scan[t] = c;
+            c += v;
+        }
+        s_total = c;
+        s_b0 = B;
+        s_base0 = c;
+    }
+    __syncthreads();
+    const long long C = s_total;
+    const long long per = max((C + gridDim.x - 1) / gridDim.x, (long long)a.sk_min_chunks);
+    const long long g0 = (long long)w * per;
+    if (g0 >= C) return;
+    const long long g1 = min(g0 + per, C);
+    // The thread whose slice holds chunk g0 finds the sequence.
+    {
+        long long gb = s_scan[threadIdx.x];
+        if (gb <= g0 && g0 < gb + mine) {
+            for (int bb = b_lo; bb < b_hi; ++bb) {
+                const long long wk = (long long)Hkv * seq_chunks(a, bb, kTok);
+                if (g0 < gb + wk) {
+                    s_b0 = bb;
+                    s_base0 = gb;
+                    break;
+                }
+                gb += wk;
+            }
+        }
+    }
+    __syncthreads();
+    // Loop state is wave-uniform 32-bit (chunk totals stay far below 2^31) and kept in
+    // scalar registers so that nothing but the piece itself holds vector registers.
+    int b = __builtin_amdgcn_readfirstlane(s_b0);
+    int gb = __builtin_amdgcn_readfirstlane((int)s_base0);  // chunk index where sequence b starts
+    int g = __builtin_amdgcn_readfirstlane((int)g0);
+    const int ge = __builtin_amdgcn_readfirstlane((int)g1);
+    while (g < ge && b < B) {
+        const int nch = __builtin_amdgcn_readfirstlane(seq_chunks(a, b, kTok));
+        const int wk = Hkv * nch;
+        if (nch == 0 || g >= gb + wk) {
+            gb += wk;
+            ++b;
+            continue;
+        }
+        const int off = g - gb;
+        const int kvh = off / nch;
+        const int c0 = off % nch;
+        const int c1 = min(nch, c0 + (ge - g));
+        const int item = b * Hkv + kvh;
+        const bool whole = c0 == 0 && c1 == nch;
+        const int ctx = __builtin_amdgcn_readfirstlane(seq_keys(a, b, kBS));
+        attn_piece<DT, NT>(a, kv, b, kvh, c0 * kTok, min(c1 * kTok, ctx), -1, whole ? -1 : w + item);
+        g = __builtin_amdgcn_readfirstlane(g + (c1 - c0));
+        b = __builtin_amdgcn_readfirstlane(b);
+        gb = __builtin_amdgcn_readfirstlane(gb);
+    }
+}
+
 template <gg_dtype_t DT>
 gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s) {
+    if (a.streamk) {
+        const int grid = a.sk_grid_per_occ * (nt <= 2 ? 2 : 1);
+        switch (nt) {
+            case 1: attn_mfma_streamk_kernel<DT, 1><<<grid, 256, 0, s>>>(a, kv); break;
+            case 2: attn_mfma_streamk_kernel<DT, 2><<<grid, 256, 0, s>>>(a, kv); break;
+            case 3: attn_mfma_streamk_kernel<DT, 3><<<grid, 256, 0, s>>>(a, kv); break;
+            case 4: attn_mfma_streamk_kernel<DT, 4><<<grid, 256, 0, s>>>(a, kv); break;
+            default: return fail(GG_ERR_INVALID, "attention: too many rows per kv head for the MFMA path");
+        }
+        return GG_OK;
+    }
     dim3 grid(a.max_parts, kv.Hkv, a.num_seqs);
     switch (nt) {
         case 1: attn_mfma_kernel<DT, 1><<<grid, 256, 0, s>>>(a, kv); break;
@@ -557,18 +688,89 @@ gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s
     return GG_OK;
 }
 
+// Merge the stream-K records of one (sequence, row, query head) whose item was split.
+__global__ void __launch_bounds__(128) attn_streamk_combine_kernel(AttnArgs a, int Hkv, int tok, int grid) {
+    const int h = blockIdx.x;
+    const int z = blockIdx.y;
+    const int b = z / a.rows, j = z % a.rows;
+    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    if (j >= nrows) return;
+    const int nch = seq_chunks(a, b, tok);
+    if (nch == 0) return;
+    // Chunks before sequence b and in total (same arithmetic as the producer).
+    __shared__ long long s_red[128];
+    long long before = 0, total = 0;
+    for (int bb = threadIdx.x; bb < a.num_seqs; bb += 128) {
+        const long long wk = (long long)Hkv * seq_chunks(a, bb, tok);
+        total += wk;
+        if (bb < b) before += wk;
+    }
+    s_red[threadIdx.x] = before;
+    __syncthreads();
+    for (int o = 64; o > 0; o >>= 1) {
+        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        __syncthreads();
+    }
+    before = s_red[0];
+    __syncthreads();
+    s_red[threadIdx.x] = total;
+    __syncthreads();
+    for (int o = 64; o > 0; o >>= 1) {
+        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        __syncthreads();
+    }
+    total = s_red[0];
+    const long long per = max((total + grid - 1) / grid, (long long)a.sk_min_chunks);
+    const int G = a.num_q_heads / Hkv;
+    const int kvh = h / G;
+    const long long gi0 = before + (long long)kvh * nch, gi1 = gi0 + nch;
+    const long long w0 = gi0 / per, w1 = (gi1 - 1) / per;
+    if (w0 == w1) return;  // one piece: the producer wrote the output
+    const int item = b * Hkv + kvh;
+    const int RW = G * a.rows;
+    const int r = j * G + (h % G);
+    float M = -1e30f;
+    for (long long w = w0; w <= w1; ++w) M = fmaxf(M, a.ws_ml[((w + item) * RW + r) * 2]);
+    float L = 0.f, accd = 0.f;
+    const int d = threadIdx.x;  // kD == 128 == blockDim.x
+    for (long long w = w0; w <= w1; ++w) {
+        const size_t p = (size_t)((w + item) * RW + r);
+        const float f = __expf(a.ws_ml[p * 2] - M);
+        L += f * a.ws_ml[p * 2 + 1];
+        accd += f * a.ws_acc[p * kD + d];
+    }
+    const size_t obase = ((size_t)z * a.num_q_heads + h) * kD;
+    store_from_f32(a.out, a.out_dtype, obase + d, L > 0.f ? accd / L : 0.f);
+}
+
 }  // namespace
 
 gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s) {
     const int G = a.num_q_heads / kv.Hkv;
     const int nt = (G * a.rows + 15) / 16;
+    gg_status_t st;
     switch (kv.dt) {
-        case GG_DTYPE_BF16: return launch_dt<GG_DTYPE_BF16>(a, kv, nt, s);
-        case GG_DTYPE_F16: return launch_dt<GG_DTYPE_F16>(a, kv, nt, s);
-        case GG_DTYPE_FP8_E4M3: return launch_dt<GG_DTYPE_FP8_E4M3>(a, kv, nt, s);
-        case GG_DTYPE_INT8: return launch_dt<GG_DTYPE_INT8>(a, kv, nt, s);
+        case GG_DTYPE_BF16: st = launch_dt<GG_DTYPE_BF16>(a, kv, nt, s); break;
+        case GG_DTYPE_F16: st = launch_dt<GG_DTYPE_F16>(a, kv, nt, s); break;
+        case GG_DTYPE_FP8_E4M3: st = launch_dt<GG_DTYPE_FP8_E4M3>(a, kv, nt, s); break;
+        case GG_DTYPE_INT8: st = launch_dt<GG_DTYPE_INT8>(a, kv, nt, s); break;
         default: return fail(GG_ERR_INVALID, "attention: pool dtype not on the MFMA path");
     }
+    if (st != GG_OK || !a.streamk) return st;
+    const int tok = (kv.dt == GG_DTYPE_FP8_E4M3 || kv.dt == GG_DTYPE_INT8) ? 64 : 32;
+    const int grid = a.sk_grid_per_occ * (nt <= 2 ? 2 : 1);
+    attn_streamk_combine_kernel<<<dim3(a.num_q_heads, a.num_seqs * a.rows), 128, 0, s>>>(a, kv.Hkv, tok, grid);
+    return GG_OK;
+}
+
+size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, int grid_per_occ) {
+    const int G = num_q_heads / kv->num_kv_heads;
+    const int nt = (G * rows + 15) / 16;
+    const size_t grid = (size_t)grid_per_occ * (nt <= 2 ? 2 : 1);
+    const size_t records = grid + (size_t)num_seqs * kv->num_kv_heads;
+    const size_t rw = (size_t)G * rows;
+    size_t n_ml = ((records * rw * 2 + 63) / 64) * 64;
+    return (n_ml + records * rw * kD) * sizeof(float);
 }
 
 }  // namespace gg

@@ -4,6 +4,7 @@
 // kernels/gollmgo_backend.cu:20-31, kernels/gollmgo_kvcache.cu:23-63): status codes,
 // a last-error string, NULL/invalid -> GG_ERR_INVALID, destroy(NULL) -> OK.
 #include "gg_common.h"
+#include "attention_common.h"
 
 #include <cmath>
 #include <cstring>
@@ -197,6 +198,25 @@ GG_API gg_status_t gg_kv_append(gg_kv_t kv, int layer, const void* k, const void
 
 // ---------------------------------------------------------------- attention
 
+namespace gg {
+int device_cu_count() {
+    static int cache[64] = {0};
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
+    if (cache[d] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || n <= 0) n = 256;
+        cache[d] = n;
+    }
+    return cache[d];
+}
+}  // namespace gg
+
+// Automatic partitioning on the MFMA path uses the stream-K schedule.
+static bool use_streamk(gg_kv_t kv, int rows, int hq, int partition_tokens) {
+    return partition_tokens == 0 && attn_mfma_supported(kv, rows, hq);
+}
+
 static bool attn_shape_ok(gg_kv_t kv, int num_seqs, int rows, int hq, int max_blocks) {
     return kv && num_seqs > 0 && rows > 0 && hq > 0 && max_blocks > 0 && hq % kv->num_kv_heads == 0 &&
            (long long)max_blocks * kv->block_size <= (1LL << 30);
@@ -207,6 +227,8 @@ GG_API size_t gg_verify_attention_workspace_size(gg_kv_t kv, int num_seqs, int r
                                                  int partition_tokens) {
     if (!attn_shape_ok(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq)) return 0;
     if (partition_tokens < 0 || partition_tokens % 64 != 0) return 0;
+    if (use_streamk(kv, rows_per_seq, num_q_heads, partition_tokens))
+        return attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, device_cu_count());
     int p = attn_resolve_partition(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq,
                                    partition_tokens);
     return attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, p);
@@ -247,12 +269,24 @@ GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_
     a.partition = attn_resolve_partition(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq,
                                          partition_tokens);
     a.max_parts = (max_blocks_per_seq * kv->block_size + a.partition - 1) / a.partition;
-    size_t need = attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq,
-                                       a.partition);
+    a.streamk = use_streamk(kv, rows_per_seq, num_q_heads, partition_tokens) ? 1 : 0;
+    a.sk_grid_per_occ = device_cu_count();
+    a.sk_min_chunks = kStreamKMinChunks;
+    size_t need, n_ml;
+    if (a.streamk) {
+        need = attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, a.sk_grid_per_occ);
+        const int G = num_q_heads / kv->num_kv_heads;
+        const int nt = (G * rows_per_seq + 15) / 16;
+        const size_t records =
+            (size_t)a.sk_grid_per_occ * (nt <= 2 ? 2 : 1) + (size_t)num_seqs * kv->num_kv_heads;
+        n_ml = records * (size_t)G * rows_per_seq * 2;
+    } else {
+        need = attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, a.partition);
+        n_ml = (size_t)num_seqs * rows_per_seq * num_q_heads * a.max_parts * 2;
+    }
     GG_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                  "gg_verify_attention: workspace too small");
     if (need) {
-        size_t n_ml = (size_t)num_seqs * rows_per_seq * num_q_heads * a.max_parts * 2;
         a.ws_ml = (float*)workspace;
         a.ws_acc = (float*)workspace + ((n_ml + 63) / 64) * 64;
     }

@@ -75,9 +75,15 @@ struct AttnArgs {
     int kv_bs;         // block size of the pool
     int partition;     // resolved partition length (tokens)
     int max_parts;
-    float* ws_ml;      // [seqs][rows][Hq][max_parts][2]
-    float* ws_acc;     // [seqs][rows][Hq][max_parts][D]
+    float* ws_ml;      // partition grid: [seqs][rows][Hq][max_parts][2]; stream-K: [records][G*R][2]
+    float* ws_acc;     // partition grid: [seqs][rows][Hq][max_parts][D]; stream-K: [records][G*R][D]
+    int streamk;       // 1: stream-K schedule (MFMA path, automatic partitioning)
+    int sk_grid_per_occ;  // workgroups per unit of occupancy (the device's CU count)
+    int sk_min_chunks;    // least chunks a stream-K workgroup takes
 };
+size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
+                                    int grid_per_occ);
+int device_cu_count();
 int attn_resolve_partition(const KV* kv, int num_seqs, int rows, int num_q_heads,
                            int max_blocks, int partition_tokens);
 size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
