@@ -33,6 +33,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;
 constexpr int kBS = 16;
@@ -103,6 +105,16 @@ __device__ __forceinline__ uint4 bytes8_to_f16x8(uint32_t w0, uint32_t w1) {
     return make_uint4(a.x, a.y, b.x, b.y);
 }
 
+// Hardware round-to-nearest-even pair conversions (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32)
+// for probabilities, which are finite and non-negative.
+__device__ __forceinline__ uint32_t cvt_pk_f16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
 }
@@ -172,11 +184,17 @@ struct Geo {
     __device__ static __forceinline__ int ob(int q) { return kTok == 64 ? 0 : 8 * (q & 1); }
 };
 
+// Workgroups (of four waves) per CU for a row-tile count: two while the registers of
+// one wave fit half the file, else one. Shared by the launch bounds and the stream-K
+// grid, which launches exactly one resident wave of workgroups.
+__host__ __device__ constexpr int attn_occupancy(int nt) { return nt <= 2 ? 2 : 1; }
+
 template <int kEB>
 struct ChunkRegs {
     using G = Geo<kEB>;
     uint4 k[G::kNS][G::kKVec];
     uint4 v[8];
+    float ksc, vsc;  // INT8 pools: scales of the lane's V block, fetched with its V
 };
 
 // One piece of work: tokens [t0, t_end) of sequence b against kv head kvh. The result
@@ -332,6 +350,12 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     // later when the block is missing or partly past the keys).
     auto load_v = [&](const Blocks& bl, Regs& rg) {
         const int blk = pick(bl, Geom::bq(g4));
+        if constexpr (DT == GG_DTYPE_INT8) {
+            // Scales first: the softmax that needs them then waits for nothing behind them.
+            const size_t si = (size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh;
+            rg.ksc = f16_bits_to_f32(kv.k_blk_scale[si]);
+            rg.vsc = f16_bits_to_f32(kv.v_blk_scale[si]);
+        }
         const uint8_t* base = kv.vc + ((((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * kD) * kBS + Geom::ob(g4)) * kEB;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
@@ -357,13 +381,9 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         // Valid offsets of the lane's V block (offsets counted from the block start).
         const int nvalid_v = blk_v < 0 ? 0 : ctx - (tc + 16 * Geom::bq(g4));
 
-        float kblk_scale = 1.f, vblk_scale = 1.f;
-        if constexpr (DT == GG_DTYPE_INT8) {
-            if (blk_v >= 0) {
-                kblk_scale = f16_bits_to_f32(kv.k_blk_scale[(size_t)blk_v * kv.Hkv + kvh]);
-                vblk_scale = f16_bits_to_f32(kv.v_blk_scale[(size_t)blk_v * kv.Hkv + kvh]);
-            }
-        }
+        // (A missing block reads block 0's scales; its tokens are masked either way.)
+        const float kblk_scale = DT == GG_DTYPE_INT8 ? cur.ksc : 1.f;
+        const float vblk_scale = DT == GG_DTYPE_INT8 ? cur.vsc : 1.f;
 
         // ---- S^T = K . Q^T for kTok tokens x all row tiles; each K tile decoded once ----
         // The Q index is opaque to the optimiser so that the LDS reads stay in the loop
@@ -405,26 +425,29 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         uint4 pop[NT][Geom::kNPV][kIsBf16 ? 2 : 1];
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
+            // The multiplier is positive, so the scaled maximum is the maximum of the raw
+            // scores times the lane's multiplier (rounding is monotonic); the scale then
+            // folds into the exponent's FMA.
             float sc[kNP];
             float cmax = -INFINITY;
 #pragma unroll
             for (int s = 0; s < kNS; ++s) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = sacc[rt][s][i] * mult;
+                    float v = sacc[rt][s][i];
                     if (need_mask) v = (tlane + 4 * s + i) <= row_pos[rt] ? v : -INFINITY;
                     sc[4 * s + i] = v;
                     cmax = fmaxf(cmax, v);
                 }
             }
-            cmax = max_over_rows(cmax);
+            cmax = max_over_rows(cmax * mult);
             const float m_new = fmaxf(m_run[rt], cmax);
             const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
             m_run[rt] = m_new;
             float psum = 0.f;
 #pragma unroll
             for (int k = 0; k < kNP; ++k) {
-                sc[k] = __builtin_amdgcn_exp2f(sc[k] - m_new);
+                sc[k] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[k], mult, -m_new));
                 psum += sc[k];
             }
             l_run[rt] = l_run[rt] * alpha + psum;
@@ -446,19 +469,19 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             for (int pv = 0; pv < Geom::kNPV; ++pv) {
                 const float* pp = sc + 8 * pv;
                 if constexpr (kIsBf16) {
-                    float hi[8], lo[8];
+                    // P = hi + lo, both bf16, so the probabilities keep ~16 bits.
+                    uint32_t hw[4], lw[4];
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        hi[k] = bf16_bits_to_f32(f32_to_bf16_bits(pp[k]));
-                        lo[k] = pp[k] - hi[k];
+                    for (int k = 0; k < 4; ++k) {
+                        hw[k] = cvt_pk_bf16(pp[2 * k], pp[2 * k + 1]);
+                        const float h0 = __uint_as_float(hw[k] << 16), h1 = __uint_as_float(hw[k] & 0xffff0000u);
+                        lw[k] = cvt_pk_bf16(pp[2 * k] - h0, pp[2 * k + 1] - h1);
                     }
-                    pop[rt][pv][0] = make_uint4(pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3]),
-                                                pack_bf16x2(hi[4], hi[5]), pack_bf16x2(hi[6], hi[7]));
-                    pop[rt][pv][kIsBf16 ? 1 : 0] = make_uint4(pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]),
-                                                              pack_bf16x2(lo[4], lo[5]), pack_bf16x2(lo[6], lo[7]));
+                    pop[rt][pv][0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                    pop[rt][pv][kIsBf16 ? 1 : 0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
                 } else {
-                    pop[rt][pv][0] = make_uint4(pack_f16x2(pp[0], pp[1]), pack_f16x2(pp[2], pp[3]),
-                                                pack_f16x2(pp[4], pp[5]), pack_f16x2(pp[6], pp[7]));
+                    pop[rt][pv][0] = make_uint4(cvt_pk_f16(pp[0], pp[1]), cvt_pk_f16(pp[2], pp[3]),
+                                                cvt_pk_f16(pp[4], pp[5]), cvt_pk_f16(pp[6], pp[7]));
                 }
             }
         }
@@ -564,7 +587,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 
 // Fixed partition grid: workgroup (part, kvh, b) takes tokens [part*P, (part+1)*P).
 template <gg_dtype_t DT, int NT>
-__global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1)) attn_mfma_kernel(AttnArgs a, KVView kv) {
+__global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(AttnArgs a, KVView kv) {
     const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int ctx = seq_keys(a, b, kBS);
     const int P = a.partition;
@@ -587,7 +610,7 @@ __device__ __forceinline__ int seq_chunks(const AttnArgs& a, int b, int tok) {
 // writes the output, any other piece writes record (workgroup + item), and
 // attn_streamk_combine_kernel merges the records of split items.
 template <gg_dtype_t DT, int NT>
-__global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1)) attn_mfma_streamk_kernel(AttnArgs a, KVView kv) {
+__global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_kernel(AttnArgs a, KVView kv) {
     constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
     const int w = blockIdx.x;
     const int Hkv = kv.Hkv;
@@ -667,7 +690,7 @@ __global__ void __launch_bounds__(256, (NT <= 2 ? 2 : 1)) attn_mfma_streamk_kern
 template <gg_dtype_t DT>
 gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s) {
     if (a.streamk) {
-        const int grid = a.sk_grid_per_occ * (nt <= 2 ? 2 : 1);
+        const int grid = a.sk_grid_per_occ * attn_occupancy(nt);
         switch (nt) {
             case 1: attn_mfma_streamk_kernel<DT, 1><<<grid, 256, 0, s>>>(a, kv); break;
             case 2: attn_mfma_streamk_kernel<DT, 2><<<grid, 256, 0, s>>>(a, kv); break;
@@ -688,59 +711,66 @@ gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s
     return GG_OK;
 }
 
-// Merge the stream-K records of one (sequence, row, query head) whose item was split.
+// Merge the stream-K records of one (sequence, kv head) item that was split over
+// several workgroups. Workgroup (item, y) takes rows 4y .. 4y+3 of the item; each thread
+// one row and four dims, merged in one online pass whose record loads are independent.
 __global__ void __launch_bounds__(128) attn_streamk_combine_kernel(AttnArgs a, int Hkv, int tok, int grid) {
-    const int h = blockIdx.x;
-    const int z = blockIdx.y;
-    const int b = z / a.rows, j = z % a.rows;
+    const int item = blockIdx.x;
+    const int b = item / Hkv, kvh = item % Hkv;
+    const int G = a.num_q_heads / Hkv;
     const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
-    if (j >= nrows) return;
+    const int r = blockIdx.y * 4 + (threadIdx.x >> 5);
+    const int d4 = threadIdx.x & 31;
     const int nch = seq_chunks(a, b, tok);
-    if (nch == 0) return;
+    if (nch == 0 || (int)blockIdx.y * 4 >= G * nrows) return;
     // Chunks before sequence b and in total (same arithmetic as the producer).
-    __shared__ long long s_red[128];
+    __shared__ long long s_before[128], s_total[128];
     long long before = 0, total = 0;
     for (int bb = threadIdx.x; bb < a.num_seqs; bb += 128) {
         const long long wk = (long long)Hkv * seq_chunks(a, bb, tok);
         total += wk;
         if (bb < b) before += wk;
     }
-    s_red[threadIdx.x] = before;
+    s_before[threadIdx.x] = before;
+    s_total[threadIdx.x] = total;
     __syncthreads();
     for (int o = 64; o > 0; o >>= 1) {
-        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        if (threadIdx.x < o) {
+            s_before[threadIdx.x] += s_before[threadIdx.x + o];
+            s_total[threadIdx.x] += s_total[threadIdx.x + o];
+        }
         __syncthreads();
     }
-    before = s_red[0];
-    __syncthreads();
-    s_red[threadIdx.x] = total;
-    __syncthreads();
-    for (int o = 64; o > 0; o >>= 1) {
-        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
-        __syncthreads();
-    }
-    total = s_red[0];
+    before = s_before[0];
+    total = s_total[0];
     const long long per = max((total + grid - 1) / grid, (long long)a.sk_min_chunks);
-    const int G = a.num_q_heads / Hkv;
-    const int kvh = h / G;
     const long long gi0 = before + (long long)kvh * nch, gi1 = gi0 + nch;
-    const long long w0 = gi0 / per, w1 = (gi1 - 1) / per;
-    if (w0 == w1) return;  // one piece: the producer wrote the output
-    const int item = b * Hkv + kvh;
+    const int w0 = (int)(gi0 / per), w1 = (int)((gi1 - 1) / per);
+    if (w0 == w1 || r >= G * nrows) return;  // one piece: the producer wrote the output
     const int RW = G * a.rows;
-    const int r = j * G + (h % G);
-    float M = -1e30f;
-    for (long long w = w0; w <= w1; ++w) M = fmaxf(M, a.ws_ml[((w + item) * RW + r) * 2]);
-    float L = 0.f, accd = 0.f;
-    const int d = threadIdx.x;  // kD == 128 == blockDim.x
-    for (long long w = w0; w <= w1; ++w) {
-        const size_t p = (size_t)((w + item) * RW + r);
-        const float f = __expf(a.ws_ml[p * 2] - M);
-        L += f * a.ws_ml[p * 2 + 1];
-        accd += f * a.ws_acc[p * kD + d];
+    float M = -1e30f, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int w = w0; w <= w1; ++w) {
+        const size_t p = (size_t)(w + item) * RW + r;
+        const float2 ml = *(const float2*)(a.ws_ml + p * 2);
+        const float4 v = ((const float4*)(a.ws_acc + p * kD))[d4];
+        const float mn = fmaxf(M, ml.x);
+        const float fo = __expf(M - mn), fn = __expf(ml.x - mn);
+        M = mn;
+        L = L * fo + ml.y * fn;
+        acc.x = acc.x * fo + v.x * fn;
+        acc.y = acc.y * fo + v.y * fn;
+        acc.z = acc.z * fo + v.z * fn;
+        acc.w = acc.w * fo + v.w * fn;
     }
-    const size_t obase = ((size_t)z * a.num_q_heads + h) * kD;
-    store_from_f32(a.out, a.out_dtype, obase + d, L > 0.f ? accd / L : 0.f);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int j = r / G, g = r % G;
+    const size_t obase = (((size_t)b * a.rows + j) * a.num_q_heads + (size_t)kvh * G + g) * kD + 4 * d4;
+    store_from_f32(a.out, a.out_dtype, obase + 0, acc.x * inv);
+    store_from_f32(a.out, a.out_dtype, obase + 1, acc.y * inv);
+    store_from_f32(a.out, a.out_dtype, obase + 2, acc.z * inv);
+    store_from_f32(a.out, a.out_dtype, obase + 3, acc.w * inv);
 }
 
 }  // namespace
@@ -758,15 +788,15 @@ gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s)
     }
     if (st != GG_OK || !a.streamk) return st;
     const int tok = (kv.dt == GG_DTYPE_FP8_E4M3 || kv.dt == GG_DTYPE_INT8) ? 64 : 32;
-    const int grid = a.sk_grid_per_occ * (nt <= 2 ? 2 : 1);
-    attn_streamk_combine_kernel<<<dim3(a.num_q_heads, a.num_seqs * a.rows), 128, 0, s>>>(a, kv.Hkv, tok, grid);
+    const int grid = a.sk_grid_per_occ * attn_occupancy(nt);
+    attn_streamk_combine_kernel<<<dim3(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4), 128, 0, s>>>(a, kv.Hkv, tok, grid);
     return GG_OK;
 }
 
 size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, int grid_per_occ) {
     const int G = num_q_heads / kv->num_kv_heads;
     const int nt = (G * rows + 15) / 16;
-    const size_t grid = (size_t)grid_per_occ * (nt <= 2 ? 2 : 1);
+    const size_t grid = (size_t)grid_per_occ * attn_occupancy(nt);
     const size_t records = grid + (size_t)num_seqs * kv->num_kv_heads;
     const size_t rw = (size_t)G * rows;
     size_t n_ml = ((records * rw * 2 + 63) / 64) * 64;
