@@ -149,15 +149,20 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a, int D) {
 
 }  // namespace
 
-int attn_resolve_partition(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
-                           int partition_tokens) {
-    if (partition_tokens > 0) return partition_tokens;
-    (void)num_seqs;
-    if (!attn_mfma_supported(kv, rows, num_q_heads)) return 512;
-    // Longer partitions amortise each workgroup's pipeline start (Q, block ids, first
-    // chunk) and its partial write; short contexts keep more workgroups in flight.
+AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
+                   int partition_tokens) {
+    if (partition_tokens > 0) return {false, partition_tokens};
+    if (!attn_mfma_supported(kv, rows, num_q_heads)) return {false, 512};
+    // Measured on MI355X: while the (sequence, kv head) items alone fill every resident
+    // workgroup slot, one workgroup per item (no split, no merge) is fastest; with fewer
+    // items than slots, or keys beyond one MFMA piece, stream-K balances the work.
+    const int G = num_q_heads / kv->num_kv_heads;
+    const int nt = (G * rows + 15) / 16;
     const long long max_keys = (long long)max_blocks * kv->block_size;
-    return max_keys >= 4096 ? 2 * kMfmaAutoPartition : kMfmaAutoPartition;
+    const long long items = (long long)num_seqs * kv->num_kv_heads;
+    const long long slots = (long long)device_cu_count() * attn_occupancy(nt);
+    if (items >= slots && max_keys <= kMfmaMaxPartition) return {false, (int)((max_keys + 63) / 64 * 64)};
+    return {true, 0};
 }
 
 size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,

@@ -86,6 +86,19 @@ inline bool attn_mfma_supported(const KV* kv, int rows, int num_q_heads) {
             kv->dtype == GG_DTYPE_FP8_E4M3 || kv->dtype == GG_DTYPE_INT8);
 }
 
+// MFMA kernel workgroups (of four waves) per CU for a row-tile count: two while one
+// wave's registers fit half the file, else one. Shared by the launch bounds, the stream-K
+// grid (one resident wave of workgroups) and the schedule choice.
+__host__ __device__ constexpr int attn_occupancy(int nt) { return nt <= 2 ? 2 : 1; }
+
+// How one verify_attention call is scheduled.
+struct AttnPlan {
+    bool streamk;   // stream-K over a fixed grid (MFMA path only)
+    int partition;  // otherwise: tokens per workgroup of the partition grid
+};
+AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
+                   int partition_tokens);
+
 gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s);
 
 }  // namespace gg

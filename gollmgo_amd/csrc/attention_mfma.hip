@@ -184,11 +184,6 @@ struct Geo {
     __device__ static __forceinline__ int ob(int q) { return kTok == 64 ? 0 : 8 * (q & 1); }
 };
 
-// Workgroups (of four waves) per CU for a row-tile count: two while the registers of
-// one wave fit half the file, else one. Shared by the launch bounds and the stream-K
-// grid, which launches exactly one resident wave of workgroups.
-__host__ __device__ constexpr int attn_occupancy(int nt) { return nt <= 2 ? 2 : 1; }
-
 template <int kEB>
 struct ChunkRegs {
     using G = Geo<kEB>;
@@ -690,7 +685,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
 template <gg_dtype_t DT>
 gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s) {
     if (a.streamk) {
-        const int grid = a.sk_grid_per_occ * attn_occupancy(nt);
+        const int grid = a.sk_grid;
         switch (nt) {
             case 1: attn_mfma_streamk_kernel<DT, 1><<<grid, 256, 0, s>>>(a, kv); break;
             case 2: attn_mfma_streamk_kernel<DT, 2><<<grid, 256, 0, s>>>(a, kv); break;
@@ -788,19 +783,24 @@ gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s)
     }
     if (st != GG_OK || !a.streamk) return st;
     const int tok = (kv.dt == GG_DTYPE_FP8_E4M3 || kv.dt == GG_DTYPE_INT8) ? 64 : 32;
-    const int grid = a.sk_grid_per_occ * attn_occupancy(nt);
+    const int grid = a.sk_grid;
     attn_streamk_combine_kernel<<<dim3(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4), 128, 0, s>>>(a, kv.Hkv, tok, grid);
     return GG_OK;
 }
 
-size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, int grid_per_occ) {
+int attn_streamk_grid(const KV* kv, int rows, int num_q_heads) {
     const int G = num_q_heads / kv->num_kv_heads;
     const int nt = (G * rows + 15) / 16;
-    const size_t grid = (size_t)grid_per_occ * attn_occupancy(nt);
-    const size_t records = grid + (size_t)num_seqs * kv->num_kv_heads;
-    const size_t rw = (size_t)G * rows;
-    size_t n_ml = ((records * rw * 2 + 63) / 64) * 64;
-    return (n_ml + records * rw * kD) * sizeof(float);
+    // One resident wave of workgroups: each CU holds attn_occupancy(nt) of them.
+    return device_cu_count() * attn_occupancy(nt);
+}
+
+size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, size_t* ml_elems) {
+    const size_t records = (size_t)attn_streamk_grid(kv, rows, num_q_heads) + (size_t)num_seqs * kv->num_kv_heads;
+    const size_t rw = (size_t)(num_q_heads / kv->num_kv_heads) * rows;
+    const size_t n_ml = records * rw * 2;
+    if (ml_elems) *ml_elems = n_ml;
+    return (((n_ml + 63) / 64) * 64 + records * rw * kD) * sizeof(float);
 }
 
 }  // namespace gg

@@ -212,11 +212,6 @@ int device_cu_count() {
 }
 }  // namespace gg
 
-// Automatic partitioning on the MFMA path uses the stream-K schedule.
-static bool use_streamk(gg_kv_t kv, int rows, int hq, int partition_tokens) {
-    return partition_tokens == 0 && attn_mfma_supported(kv, rows, hq);
-}
-
 static bool attn_shape_ok(gg_kv_t kv, int num_seqs, int rows, int hq, int max_blocks) {
     return kv && num_seqs > 0 && rows > 0 && hq > 0 && max_blocks > 0 && hq % kv->num_kv_heads == 0 &&
            (long long)max_blocks * kv->block_size <= (1LL << 30);
@@ -227,11 +222,9 @@ GG_API size_t gg_verify_attention_workspace_size(gg_kv_t kv, int num_seqs, int r
                                                  int partition_tokens) {
     if (!attn_shape_ok(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq)) return 0;
     if (partition_tokens < 0 || partition_tokens % 64 != 0) return 0;
-    if (use_streamk(kv, rows_per_seq, num_q_heads, partition_tokens))
-        return attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, device_cu_count());
-    int p = attn_resolve_partition(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq,
-                                   partition_tokens);
-    return attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, p);
+    const AttnPlan plan = attn_plan(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, partition_tokens);
+    if (plan.streamk) return attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, nullptr);
+    return attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, plan.partition);
 }
 
 GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
@@ -266,20 +259,15 @@ GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_
     a.num_q_heads = num_q_heads;
     a.scale = scale;
     a.kv_bs = kv->block_size;
-    a.partition = attn_resolve_partition(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq,
-                                         partition_tokens);
+    const AttnPlan plan = attn_plan(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, partition_tokens);
+    a.streamk = plan.streamk ? 1 : 0;
+    a.partition = plan.streamk ? kMfmaAutoPartition : plan.partition;
     a.max_parts = (max_blocks_per_seq * kv->block_size + a.partition - 1) / a.partition;
-    a.streamk = use_streamk(kv, rows_per_seq, num_q_heads, partition_tokens) ? 1 : 0;
-    a.sk_grid_per_occ = device_cu_count();
     a.sk_min_chunks = kStreamKMinChunks;
     size_t need, n_ml;
     if (a.streamk) {
-        need = attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, a.sk_grid_per_occ);
-        const int G = num_q_heads / kv->num_kv_heads;
-        const int nt = (G * rows_per_seq + 15) / 16;
-        const size_t records =
-            (size_t)a.sk_grid_per_occ * (nt <= 2 ? 2 : 1) + (size_t)num_seqs * kv->num_kv_heads;
-        n_ml = records * (size_t)G * rows_per_seq * 2;
+        a.sk_grid = attn_streamk_grid(kv, rows_per_seq, num_q_heads);
+        need = attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, &n_ml);
     } else {
         need = attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, a.partition);
         n_ml = (size_t)num_seqs * rows_per_seq * num_q_heads * a.max_parts * 2;

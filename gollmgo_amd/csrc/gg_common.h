@@ -78,14 +78,16 @@ struct AttnArgs {
     float* ws_ml;      // partition grid: [seqs][rows][Hq][max_parts][2]; stream-K: [records][G*R][2]
     float* ws_acc;     // partition grid: [seqs][rows][Hq][max_parts][D]; stream-K: [records][G*R][D]
     int streamk;       // 1: stream-K schedule (MFMA path, automatic partitioning)
-    int sk_grid_per_occ;  // workgroups per unit of occupancy (the device's CU count)
+    int sk_grid;       // stream-K workgroups (attn_streamk_grid)
     int sk_min_chunks;    // least chunks a stream-K workgroup takes
 };
+// Stream-K launch: workgroups for a shape on the current device, and the workspace it
+// needs (grid + num_seqs * Hkv partial records of G*rows rows; ml_elems receives the
+// float count of the (max, sum) part, which the P.V part follows 64-float aligned).
+int attn_streamk_grid(const KV* kv, int rows, int num_q_heads);
 size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
-                                    int grid_per_occ);
+                                    size_t* ml_elems);
 int device_cu_count();
-int attn_resolve_partition(const KV* kv, int num_seqs, int rows, int num_q_heads,
-                           int max_blocks, int partition_tokens);
 size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
                             int max_blocks, int partition);
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s);
