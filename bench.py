@@ -9,7 +9,8 @@ and resident in HBM before the timed region starts.
 value = verified tokens/s = B*(k+1) / (L*(t_append + t_attn) + t_accept), taken from
 the wall clock of the timed steps (the same formula the measurement plan uses).
 The roofline object describes the attention call (the dominant kernel); its
-duration is the HIP-event average over every attention call in the timed region.
+duration is the HIP-event average over every attention call in the timed region, and
+its traffic comes from the committed rocprofv3 PMC summary of the same workload.
 """
 from __future__ import annotations
 
@@ -34,7 +35,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, help="workload config id (default 3 = 8B fp8)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seqs", type=int, default=8, help="sequences in the CPU baseline sample")
+    ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU baseline sample")
     ap.add_argument("--partition", type=int, default=-1, help="override split-K partition tokens")
     ap.add_argument("--layers", type=int, default=0, help="override layer count (0 = config)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -168,16 +169,13 @@ def main():
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
-    # Timed region, wall clock (no per-kernel events inside).
+    # Timed region: wall clock for `value`, HIP events (on the stream the library launches
+    # on, torch's current stream) around every call for the per-kernel durations.
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(False)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    # Same steps again with HIP events around every call (per-kernel durations).
     for _ in range(args.steps):
         step(True)
     torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
 
     def avg_us(name):
         xs = [s.elapsed_time(e) * 1000.0 for s, e in ev[name]]
@@ -204,6 +202,17 @@ def main():
     scale_bytes = H * 4 * 2 if cfg.kv_dtype == "fp8" else (blocks_used * H * 2 * 2 if cfg.kv_dtype == "int8" else 0)
     attn_bytes = kv_bytes + q_bytes + o_bytes + scale_bytes + blocks_used * 4
     achieved = attn_bytes / (t_attn * 1e-6) / 1e9
+    # One gg_verify_attention call: a single-piece plan (no workspace) is one launch of the
+    # MFMA kernel; otherwise stream-K (or an explicit partition grid) plus its merge.
+    from gollmgo_amd._lib import lib as _gglib
+    ws_need = _gglib().gg_verify_attention_workspace_size(kv.handle, B, R, Hq, bt.shape[1], cfg.partition)
+    if ws_need == 0:
+        attn_kernels = "attn_mfma_kernel (one workgroup per sequence x kv head)"
+    elif cfg.partition:
+        attn_kernels = "attn_mfma_kernel + attn_combine_kernel (partition grid)"
+    else:
+        attn_kernels = "attn_mfma_streamk_kernel + attn_streamk_combine_kernel"
+    traffic, traffic_src = pmc_traffic(args.config)
     lb = logits.element_size()
     acc_bytes = B * R * V * lb + (B * K * V * 4 if draft_probs is not None else 0)
 
@@ -234,9 +243,9 @@ def main():
         "tokens_per_s_from_kernel_times": round(kernel_formula_tps, 1),
         "accepted_tokens_per_s": round(accepted_tps, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gg_verify_attention (attn_mfma_kernel + attn_combine_kernel)",
-                     "algorithmic_bytes_per_launch": attn_bytes},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": attn_kernels, "algorithmic_bytes_per_launch": attn_bytes,
+                     "traffic_source": traffic_src},
         "accept_roofline": {"achieved": round(acc_bytes / (t_acc * 1e-6) / 1e9, 1), "unit": "GB/s",
                             "algorithmic_bytes_per_launch": acc_bytes},
         "setup_s": round(setup_s, 1),
@@ -247,6 +256,20 @@ def main():
                                               uniforms, scale)
     kv.close()
     print(json.dumps(result))
+
+
+def pmc_traffic(config_id: int):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary of this
+    workload (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the copy-kernel
+    calibration recorded there), or None when no summary exists for it."""
+    import re
+    path = ROOT / "profiles" / f"attention_config{config_id}_pmc.md"
+    if not path.exists():
+        return None, None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", path.read_text(), re.M)
+    if not m:
+        return None, None
+    return int(m.group(1)), str(path.relative_to(ROOT))
 
 
 def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, uniforms, scale):
