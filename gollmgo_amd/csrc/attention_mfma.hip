@@ -235,7 +235,11 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     // Staged once per piece in LDS (wave w converts dim group mm = w for every row tile)
     // and read back per chunk one mm at a time, so only NT operands are live in the loop.
     // Loads are issued unconditionally (invalid rows read row 0 and are zeroed).
-    __shared__ uint4 s_q[NT][4][64];  // [rt][mm][lane]
+    // BF16 pools take Q as bf16 hi + lo (two S MFMAs) unless Q already is bf16, so f32
+    // and f16 queries keep ~16 bits instead of bf16's 8.
+    __shared__ uint4 s_q[NT][4][64];                   // [rt][mm][lane]
+    __shared__ uint4 s_qlo[kIsBf16 ? NT : 1][4][64];  // low parts (BF16 pools)
+    const bool qsplit = kIsBf16 && a.q_dtype != GG_DTYPE_BF16;
     int row_pos[NT];  // last visible key position of the lane's S row (c16)
     {
         const int mm = wave;
@@ -252,6 +256,25 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         }
         // One uniform dtype branch around all row tiles, so their loads issue together.
         uint4 op[NT];
+        // Eight values -> MFMA operand (and, for a split, the operand of the remainder).
+        auto pack8 = [&](const float* f, uint4& hi, uint4& lo) {
+            if constexpr (kIsBf16) {
+                uint32_t h[4], l[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    h[k] = pack_bf16x2(f[2 * k], f[2 * k + 1]);
+                    l[k] = pack_bf16x2(f[2 * k] - __uint_as_float(h[k] << 16),
+                                       f[2 * k + 1] - __uint_as_float(h[k] & 0xffff0000u));
+                }
+                hi = make_uint4(h[0], h[1], h[2], h[3]);
+                lo = make_uint4(l[0], l[1], l[2], l[3]);
+            } else {
+                hi = make_uint4(pack_f16x2(f[0], f[1]), pack_f16x2(f[2], f[3]), pack_f16x2(f[4], f[5]),
+                                pack_f16x2(f[6], f[7]));
+                lo = zero4();
+            }
+        };
+        uint4 opl[NT];
         if (a.q_dtype == GG_DTYPE_F32) {
             float4 raw[NT][2];
 #pragma unroll
@@ -260,37 +283,38 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
                 for (int h = 0; h < 2; ++h) raw[rt][h] = ((const float4*)((const float*)a.q + qb[rt]))[h];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt) {
-                const float4 x = raw[rt][0], y = raw[rt][1];
-                if constexpr (kIsBf16)
-                    op[rt] = make_uint4(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w), pack_bf16x2(y.x, y.y),
-                                        pack_bf16x2(y.z, y.w));
-                else
-                    op[rt] = make_uint4(pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w), pack_f16x2(y.x, y.y),
-                                        pack_f16x2(y.z, y.w));
+                const float f[8] = {raw[rt][0].x, raw[rt][0].y, raw[rt][0].z, raw[rt][0].w,
+                                    raw[rt][1].x, raw[rt][1].y, raw[rt][1].z, raw[rt][1].w};
+                pack8(f, op[rt], opl[rt]);
             }
         } else {
             const bool src_bf16 = a.q_dtype == GG_DTYPE_BF16;
 #pragma unroll
-            for (int rt = 0; rt < NT; ++rt) op[rt] = *(const uint4*)((const uint16_t*)a.q + qb[rt]);
+            for (int rt = 0; rt < NT; ++rt) {
+                op[rt] = *(const uint4*)((const uint16_t*)a.q + qb[rt]);
+                opl[rt] = zero4();
+            }
             // Convert when the Q type differs from the MFMA operand type.
             if (src_bf16 != kIsBf16) {
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) {
                     const uint32_t w[4] = {op[rt].x, op[rt].y, op[rt].z, op[rt].w};
-                    uint32_t o4[4];
+                    float f[8];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const uint16_t lo = (uint16_t)w[k], hi = (uint16_t)(w[k] >> 16);
-                        const float flo = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-                        const float fhi = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-                        o4[k] = kIsBf16 ? pack_bf16x2(flo, fhi) : pack_f16x2(flo, fhi);
+                        f[2 * k] = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                        f[2 * k + 1] = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
                     }
-                    op[rt] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+                    pack8(f, op[rt], opl[rt]);
                 }
             }
         }
 #pragma unroll
-        for (int rt = 0; rt < NT; ++rt) s_q[rt][mm][lane] = qvalid[rt] ? op[rt] : zero4();
+        for (int rt = 0; rt < NT; ++rt) {
+            s_q[rt][mm][lane] = qvalid[rt] ? op[rt] : zero4();
+            if constexpr (kIsBf16) s_qlo[rt][mm][lane] = qvalid[rt] ? opl[rt] : zero4();
+        }
         __syncthreads();
     }
 
@@ -409,12 +433,26 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) sacc[rt][s] = mfma(kop, qop[rt], sacc[rt][s], kIsBf16);
             }
+            if constexpr (kIsBf16) {
+                if (qsplit) {
+#pragma unroll
+                    for (int rt = 0; rt < NT; ++rt) qop[rt] = s_qlo[rt][mm][qlane];
+#pragma unroll
+                    for (int s = 0; s < kNS; ++s)
+#pragma unroll
+                        for (int rt = 0; rt < NT; ++rt) sacc[rt][s] = mfma(cur.k[s][mm], qop[rt], sacc[rt][s], true);
+                }
+            }
         }
         // Next chunk's K rows stream in while this chunk finishes.
         load_k(bl_next, cur);
 
         // ---- online softmax; P packed as MFMA A operands ----
-        const bool need_mask = tc + kTok - 1 >= first_masked;
+        // Masked scores: causal (keys past the row's position, which covers keys past the
+        // context) and every key of a missing block (its K was read from block 0). A
+        // lane's scores all come from its V block, so a missing block masks whole lanes.
+        const bool blk_missing = blk_v < 0;
+        const bool need_mask = tc + kTok - 1 >= first_masked || __any(blk_missing);
         const float mult = DT == GG_DTYPE_INT8 ? sscale * kblk_scale : sscale;
         constexpr int kNP = 4 * kNS;  // P values per lane per row tile
         uint4 pop[NT][Geom::kNPV][kIsBf16 ? 2 : 1];
@@ -430,7 +468,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float v = sacc[rt][s][i];
-                    if (need_mask) v = (tlane + 4 * s + i) <= row_pos[rt] ? v : -INFINITY;
+                    if (need_mask) v = (!blk_missing && (tlane + 4 * s + i) <= row_pos[rt]) ? v : -INFINITY;
                     sc[4 * s + i] = v;
                     cmax = fmaxf(cmax, v);
                 }

@@ -141,7 +141,9 @@ gg_status_t gg_kv_append(gg_kv_t kv, int layer, const void* k, const void* v,
  *                 row_counts[b] are not written.
  *   block_tables: device int32[num_seqs][max_blocks_per_seq] of physical blocks
  *   scale       : softmax scale (1/sqrt(head_dim) in the reference)
- *   partition_tokens: split-K partition length, a multiple of 64 (0 = auto).
+ *   partition_tokens: split-K partition length, a multiple of 64. 0 = automatic:
+ *                 one workgroup per (sequence, kv head) when those items fill the
+ *                 device, else a stream-K split over a fixed grid (same results).
  * workspace must hold gg_verify_attention_workspace_size(...) bytes (may be 0). */
 size_t gg_verify_attention_workspace_size(gg_kv_t kv, int num_seqs, int rows_per_seq,
                                           int num_q_heads, int max_blocks_per_seq,
@@ -186,7 +188,7 @@ gg_status_t gg_accept_greedy(const void* logits, gg_dtype_t logits_dtype, int nu
  *   temperature  : > 0 (<= 1e-9 falls back to gg_accept_greedy semantics, as
  *                  Sampler.Sample does at sampling.go:54-56)
  *   top_p        : (0,1) enables the nucleus filter; otherwise disabled
- * Probabilities are fixed-point: w_i = floor(exp_gg((l_i - max) * (1/T)) * 2^40)
+ * Probabilities are fixed-point: w_i = floor(exp_gg((l_i - max) * (1/T)) * 2^35)
  * with the library's own exp (identical on host and device), so every sum and
  * prefix sum is an exact integer and decisions are bit-reproducible. Nucleus
  * order is (logit desc, index asc). Draft j is accepted iff

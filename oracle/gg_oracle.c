@@ -545,11 +545,15 @@ void ora_kv_append_q(uint8_t* kc, uint8_t* vc, int dt, int H, int D, int bs, con
  *   q [B][R][Hq][D] fp32 values; out [B][R][Hq][D] fp32.
  *   kc/vc pools of dtype dt; k_scale/v_scale: per-head [H] (dt 3) or per-block
  *   [blocks][H] (dt 4) as floats, NULL otherwise.
- *   row_counts may be NULL (all R). Rows j >= row_counts[b] are left untouched. */
+ *   row_counts may be NULL (all R). Rows j >= row_counts[b] are left untouched.
+ *   Boundary semantics of gg_verify_attention (no reference counterpart: the
+ *   reference trusts its slot tables): ctx_lens are clamped to [0, max_blocks*bs];
+ *   a sequence with no rows or with more rows than keys is left untouched; keys whose
+ *   block id is outside [0, num_blocks) take no part in the softmax. */
 void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t* vc, int dt, int H,
                    int D, int bs, const float* k_scale, const float* v_scale, const int32_t* ctx_lens,
                    const int32_t* row_counts, const int32_t* block_tables, int max_blocks, int B, int R,
-                   int Hq, float scale, int threads) {
+                   int Hq, float scale, int threads, int num_blocks) {
     const int G = Hq / H;
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
@@ -558,8 +562,11 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
     (void)threads;
 #endif
     for (int b = 0; b < B; ++b) {
-        const int ctx = ctx_lens[b];
+        int ctx = ctx_lens[b];
+        if (ctx < 0) ctx = 0;
+        if (ctx > max_blocks * bs) ctx = max_blocks * bs;
         const int nr = row_counts ? row_counts[b] : R;
+        if (nr <= 0 || nr > ctx) continue;
         double* sc = (double*)malloc(sizeof(double) * (size_t)(ctx > 0 ? ctx : 1));
         double* acc = (double*)malloc(sizeof(double) * (size_t)D);
         for (int j = 0; j < nr; ++j) {
@@ -570,6 +577,10 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
                 double mx = -INFINITY;
                 for (int t = 0; t <= pos; ++t) {
                     int blk = block_tables[(size_t)b * max_blocks + t / bs], o = t % bs;
+                    if (blk < 0 || blk >= num_blocks) {
+                        sc[t] = -INFINITY;
+                        continue;
+                    }
                     double ks = dt == 3 ? k_scale[h] : dt == 4 ? k_scale[(size_t)blk * H + h] : 1.0;
                     double dot = 0;
                     for (int d = 0; d < D; ++d)
@@ -579,14 +590,15 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
                 }
                 double sum = 0;
                 for (int t = 0; t <= pos; ++t) {
-                    sc[t] = exp(sc[t] - mx);
+                    sc[t] = mx == -INFINITY ? 0.0 : exp(sc[t] - mx);
                     sum += sc[t];
                 }
                 for (int d = 0; d < D; ++d) acc[d] = 0;
                 for (int t = 0; t <= pos; ++t) {
                     int blk = block_tables[(size_t)b * max_blocks + t / bs], o = t % bs;
+                    if (blk < 0 || blk >= num_blocks) continue;
                     double vs = dt == 3 ? v_scale[h] : dt == 4 ? v_scale[(size_t)blk * H + h] : 1.0;
-                    double p = sc[t] / sum * vs;
+                    double p = sum > 0 ? sc[t] / sum * vs : 0.0;
                     for (int d = 0; d < D; ++d)
                         acc[d] += p * (double)raw_elem(vc, dt, v_off(blk, h, o, d, H, bs, D));
                 }

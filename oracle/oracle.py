@@ -217,7 +217,8 @@ def kv_append_q(kc: np.ndarray, vc: np.ndarray, dt: str, H: int, D: int, bs: int
 def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, dt: str, H: int, D: int, bs: int,
               ctx_lens: np.ndarray, block_tables: np.ndarray, scale: float, k_scale=None, v_scale=None,
               row_counts=None, threads: int = 0) -> np.ndarray:
-    """fp64 textbook attention; q [B,R,Hq,D] fp32 values; pools as raw bytes."""
+    """fp64 textbook attention; q [B,R,Hq,D] fp32 values; pools as raw bytes (one
+    layer, all blocks: the block count is taken from their size)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     B, R, Hq, Dq = q.shape
     assert Dq == D
@@ -227,9 +228,13 @@ def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, dt: str, H: int, D:
     rc = np.ascontiguousarray(row_counts, dtype=np.int32) if row_counts is not None else None
     ks = np.ascontiguousarray(k_scale, dtype=np.float32) if k_scale is not None else None
     vs = np.ascontiguousarray(v_scale, dtype=np.float32) if v_scale is not None else None
+    kc = np.ascontiguousarray(kc)
+    vc = np.ascontiguousarray(vc)
+    eb = {"f32": 4, "f16": 2, "bf16": 2, "fp8": 1, "int8": 1}[dt]
+    num_blocks = kc.nbytes // (H * bs * D * eb)
     f = lib().ora_attention
-    f.argtypes = [C.c_void_p] * 4 + [C.c_int] * 4 + [C.c_void_p] * 5 + [C.c_int] * 4 + [C.c_float, C.c_int]
-    f(_p(q), _p(out), _p(np.ascontiguousarray(kc)), _p(np.ascontiguousarray(vc)), DT_CODE[dt], H, D, bs,
+    f.argtypes = [C.c_void_p] * 4 + [C.c_int] * 4 + [C.c_void_p] * 5 + [C.c_int] * 4 + [C.c_float, C.c_int, C.c_int]
+    f(_p(q), _p(out), _p(kc), _p(vc), DT_CODE[dt], H, D, bs,
       _p(ks) if ks is not None else None, _p(vs) if vs is not None else None, _p(cl),
-      _p(rc) if rc is not None else None, _p(bt), bt.shape[1], B, R, Hq, float(scale), threads)
+      _p(rc) if rc is not None else None, _p(bt), bt.shape[1], B, R, Hq, float(scale), threads, int(num_blocks))
     return out

@@ -268,3 +268,131 @@ def test_attention_config_layouts(gpu):
         print(f"  config {cid}: rel err {err:.2e}")
         assert err <= TOL[cfg.kv_dtype]
         kv.close()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp8", "int8", "f32"])
+def test_attention_boundary_cases(gpu, dt):
+    """Context of one key, a sequence with no rows, one with more rows than keys, key
+    blocks with out-of-range ids (skipped), and a context beyond the table width
+    (clamped): the ABI's boundary rules, checked against the oracle's. bf16/fp8/int8
+    take the MFMA path (Hq=32, Hkv=8, D=128, R=6), f32 the generic path."""
+    say(f"attention boundary cases dt={dt}")
+    B, R, Hq, H, D, bs = 6, 6, 32, 8, 128, 16
+    nb = 24
+    rng = np.random.default_rng(31)
+    perm = rng.permutation(nb)
+    max_blocks = 4
+    bt = np.zeros((B, max_blocks), np.int32)
+    ctx = np.array([1, 40, 3, 50, 64, 30], np.int32)   # keys incl. the verify rows
+    rows = np.array([1, 0, 6, 6, 6, 6], np.int32)       # seq 1: no rows; seq 2: 6 rows > 3 keys
+    fill = []
+    p = 0
+    for b in range(B):
+        nblk = (int(min(ctx[b], max_blocks * bs)) + bs - 1) // bs
+        bt[b, :nblk] = perm[p:p + nblk]
+        p += nblk
+        fill += [bt[b, t // bs] * bs + t % bs for t in range(min(int(ctx[b]), max_blocks * bs))]
+    bt[3, 1] = -1          # a skipped block in the middle of sequence 3
+    bt[4, 2] = nb + 100    # an id past the pool in sequence 4
+    ctx[5] = 10 ** 6       # beyond the table: clamped to max_blocks * bs
+    bt[5, :] = perm[p:p + max_blocks]
+    fill += [bt[5, t // bs] * bs + t % bs for t in range(max_blocks * bs)]
+    slots = np.unique(np.array(fill, np.int32))
+    kv = make_cache(dt, H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    kk = rng.normal(0, 1, (len(slots), H, D)).astype(np.float32)
+    vv = rng.normal(0, 1, (len(slots), H, D)).astype(np.float32)
+    if dt == "fp8":
+        ks, vs = per_head_amax_scales(kk), per_head_amax_scales(vv)
+        kv.set_head_scales(0, ks, vs)
+        mirror.set_head_scales(ks, vs)
+    append_rows(kv, mirror, kk, vv, slots, "f32")
+    mirror.sync_from_device()
+    q = torch.randn(B, R, Hq, D, dtype=torch.float32, generator=torch.Generator().manual_seed(3)).cuda()
+    sentinel = 7.0
+    out = torch.full((B, R, Hq, D), sentinel, dtype=torch.float32, device="cuda")
+    kv.attention(0, q, out, torch.from_numpy(ctx).cuda(), torch.from_numpy(bt).cuda(), 1 / math.sqrt(D),
+                 row_counts=torch.from_numpy(rows).cuda())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ksc, vsc = mirror.scales_for_oracle()
+    ref = ora.attention(q.cpu().numpy(), mirror.kc, mirror.vc, dt, H, D, bs, ctx, bt, 1 / math.sqrt(D), ksc, vsc,
+                        row_counts=rows)
+    # Untouched: rows past each sequence's row count, the row-less sequence, the sequence
+    # with more rows than keys.
+    for b in range(B):
+        n = 0 if b in (1, 2) else rows[b]
+        assert (got[b, n:] == sentinel).all(), f"seq {b}: rows >= {n} written"
+    written = [(b, j) for b in range(B) for j in range(R) if b not in (1, 2) and j < rows[b]]
+    g = np.stack([got[b, j] for b, j in written])
+    r = np.stack([ref[b, j] for b, j in written])
+    err = rel_err_per_vector(g, r)
+    print(f"  boundary {dt}: rel err {err:.2e}")
+    assert err <= TOL[dt]
+    kv.close()
+
+
+def _full_config_case(cid):
+    """A config at its real shape, one layer, pools filled on the GPU; returns the
+    pieces the full-size checks need."""
+    cfg = scaled(CONFIGS[cid], layers=1)
+    lay = build_layout(cfg)
+    H, D, bs = cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    kv = make_cache(cfg.kv_dtype, H, D, bs, lay.num_blocks)
+    gen = torch.Generator(device="cuda").manual_seed(cfg.seed)
+    if cfg.kv_dtype == "fp8":
+        # Values ~N(0,1): scales from a fixed amax of 4.5 (saturating the rare tail).
+        kv.set_head_scales(0, [4.5 / 448] * H, [4.5 / 448] * H)
+    # The context, then the step's own rows, in separate calls (INT8 pools need a block's
+    # rows adjacent within one call).
+    for part in (lay.fill_slots, lay.append_slots):
+        slots = torch.from_numpy(part).cuda()
+        for s in range(0, len(slots), 1 << 16):
+            m = min(1 << 16, len(slots) - s)
+            kx = torch.randn(m, H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+            vx = torch.randn(m, H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+            kv.append(0, kx, vx, slots[s:s + m])
+    q = torch.randn(cfg.num_seqs, cfg.rows, cfg.num_q_heads, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    keys = torch.from_numpy(lay.keys).cuda()
+    bt = torch.from_numpy(lay.block_tables).cuda()
+    torch.cuda.synchronize()
+    return cfg, lay, kv, q, keys, bt
+
+
+@pytest.mark.parametrize("cid,explicit", [(2, 1024), (3, 1024), (4, 512), (5, 2048)])
+def test_attention_full_size_configs(gpu, cid, explicit):
+    """Configs 2-5 at their real sizes. Size-independent property over every sequence:
+    the automatic schedule (stream-K for configs 2 and 4, one workgroup per item for 3
+    and 5) equals an explicit partition grid to 1e-3 (the schedules round P to the MFMA
+    type against different running maxima). Then the two shortest sequences against the
+    fp64 oracle at the north-star tolerance."""
+    say(f"attention full-size config {cid}")
+    cfg, lay, kv, q, keys, bt = _full_config_case(cid)
+    D = cfg.head_dim
+    scale = 1 / math.sqrt(D)
+    outs = {}
+    for p in (0, explicit):
+        ws = kv.attention_workspace(cfg.num_seqs, cfg.rows, cfg.num_q_heads, bt.shape[1], p)
+        o = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+        kv.attention(0, q, o, keys, bt, scale, partition_tokens=p, workspace=ws)
+        torch.cuda.synchronize()
+        outs[p] = o.cpu().numpy()
+    agree = rel_err_per_vector(outs[0], outs[explicit])
+    print(f"  config {cid}: auto vs partition {explicit}: rel diff {agree:.2e}")
+    assert agree <= 1e-3
+    idx = np.argsort(lay.keys)[:2]
+    k_s = v_s = None
+    if cfg.kv_dtype == "fp8":
+        a, b = kv.scales(0)
+        k_s, v_s = a.cpu().numpy()[:cfg.num_kv_heads], b.cpu().numpy()[:cfg.num_kv_heads]
+    elif cfg.kv_dtype == "int8":
+        a, b = kv.scales(0)
+        k_s, v_s = a.float().cpu().numpy().reshape(-1), b.float().cpu().numpy().reshape(-1)
+    say(f"  oracle on sequences {idx.tolist()} (keys {lay.keys[idx].tolist()})")
+    ref = ora.attention(q[idx].float().cpu().numpy(), kv.k_pool(0).cpu().numpy(), kv.v_pool(0).cpu().numpy(),
+                        cfg.kv_dtype, cfg.num_kv_heads, D, cfg.block_size, lay.keys[idx], lay.block_tables[idx],
+                        scale, k_s, v_s, threads=8)
+    err = rel_err_per_vector(outs[0][idx], ref)
+    print(f"  config {cid}: oracle rel err {err:.2e}")
+    assert err <= TOL[cfg.kv_dtype]
+    kv.close()

@@ -340,6 +340,34 @@ def test_attention_block_permutation_invariance(ora):
     np.testing.assert_array_equal(out, out2)
 
 
+def test_attention_boundary_semantics(ora):
+    """gg_verify_attention's boundary rules, pinned by equivalences: a key block whose
+    id is out of range (negative or >= the pool's blocks) counts exactly as if it were
+    removed from the table; context lengths beyond the table clamp to its width; a
+    sequence with no rows or more rows than keys is left untouched."""
+    H, D, bs, nblk, R = 2, 8, 4, 6, 3
+    rng = np.random.default_rng(21)
+    kc = rng.normal(0, 1, (nblk, H, bs, D)).astype(np.float32)
+    vc = rng.normal(0, 1, (nblk, H, D, bs)).astype(np.float32)
+    q = rng.normal(0, 1, (1, R, 4, D)).astype(np.float32)
+    args = (kc.view(np.uint8).reshape(-1), vc.view(np.uint8).reshape(-1), "f32", H, D, bs)
+    ref = ora.attention(q, *args, np.array([10], np.int32), np.array([[0, 2, 3]], np.int32), 0.3)
+    assert np.abs(ref).sum() > 0
+    for bad in (-1, nblk, 10 ** 6):
+        got = ora.attention(q, *args, np.array([14], np.int32), np.array([[0, bad, 2, 3]], np.int32), 0.3)
+        np.testing.assert_array_equal(got, ref)
+    # ctx beyond the table width: clamped (3 blocks -> 12 keys).
+    a = ora.attention(q, *args, np.array([99], np.int32), np.array([[4, 5, 1]], np.int32), 0.3)
+    b = ora.attention(q, *args, np.array([12], np.int32), np.array([[4, 5, 1]], np.int32), 0.3)
+    np.testing.assert_array_equal(a, b)
+    # More rows than keys, or no rows: untouched (zeros).
+    z = ora.attention(q, *args, np.array([2], np.int32), np.array([[0, 1]], np.int32), 0.3)
+    assert not z.any()
+    z = ora.attention(q, *args, np.array([9], np.int32), np.array([[0, 1, 2]], np.int32), 0.3,
+                      row_counts=np.array([0], np.int32))
+    assert not z.any()
+
+
 def test_kv_append_fp8_matches_encoder(ora):
     H, D, bs, nblk = 2, 8, 4, 3
     rng = np.random.default_rng(13)
