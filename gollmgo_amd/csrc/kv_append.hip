@@ -77,6 +77,83 @@ __global__ void __launch_bounds__(256) append_direct_kernel(AppendArgs a) {
     }
 }
 
+// Vectorised plain / per-head-scaled append for head_dim % 8 == 0: one thread per eight
+// consecutive elements of one (row, head), all source loads issued together, the
+// element types fixed at compile time. Same roundings as append_direct_kernel.
+template <gg_dtype_t SRC>
+__device__ __forceinline__ void load8(const void* p, size_t i, float* x) {
+    if constexpr (SRC == GG_DTYPE_F32) {
+        const float4 a = ((const float4*)((const float*)p + i))[0];
+        const float4 b = ((const float4*)((const float*)p + i))[1];
+        x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    } else {
+        const uint4 w = *(const uint4*)((const uint16_t*)p + i);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint16_t lo = (uint16_t)u[k], hi = (uint16_t)(u[k] >> 16);
+            x[2 * k] = SRC == GG_DTYPE_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+            x[2 * k + 1] = SRC == GG_DTYPE_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+    }
+}
+
+template <gg_dtype_t SRC, gg_dtype_t DST>
+__global__ void __launch_bounds__(256) append_vec_kernel(AppendArgs a) {
+    const int groups = a.Hkv * a.D / 8;  // eight-element groups per row
+    const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long long)a.n_rows * groups) return;
+    const int r = (int)(gid / groups), g = (int)(gid % groups);
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int blk = slot / a.bs, off = slot % a.bs;
+    const int i0 = g * 8, h = i0 / a.D, d0 = i0 % a.D;
+    const size_t src_i = (size_t)r * a.Hkv * a.D + i0;
+    float kx[8], vx[8];
+    load8<SRC>(a.k, src_i, kx);
+    load8<SRC>(a.v, src_i, vx);
+    const size_t ki = k_index(blk, h, off, d0, a.Hkv, a.bs, a.D);  // 8 contiguous elements
+    const size_t vi = v_index(blk, h, off, d0, a.Hkv, a.bs, a.D);  // stride bs per element
+    if constexpr (DST == GG_DTYPE_F32) {
+        float4* kp = (float4*)((float*)a.kc + ki);
+        kp[0] = make_float4(kx[0], kx[1], kx[2], kx[3]);
+        kp[1] = make_float4(kx[4], kx[5], kx[6], kx[7]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ((float*)a.vc)[vi + (size_t)j * a.bs] = vx[j];
+    } else if constexpr (DST == GG_DTYPE_F16 || DST == GG_DTYPE_BF16) {
+        uint16_t kb[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            kb[j] = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(kx[j]) : f32_to_f16_bits(kx[j]);
+            const uint16_t vb = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(vx[j]) : f32_to_f16_bits(vx[j]);
+            ((uint16_t*)a.vc)[vi + (size_t)j * a.bs] = vb;
+        }
+        *(uint4*)((uint16_t*)a.kc + ki) = make_uint4(kb[0] | ((uint32_t)kb[1] << 16), kb[2] | ((uint32_t)kb[3] << 16),
+                                                     kb[4] | ((uint32_t)kb[5] << 16), kb[6] | ((uint32_t)kb[7] << 16));
+    } else {  // FP8-E4M3, per-head scales
+        const float kinv = a.k_inv[h], vinv = a.v_inv[h];
+        uint32_t kw[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            kw[j >> 2] |= (uint32_t)f32_to_fp8e4m3_sat(kx[j] * kinv) << (8 * (j & 3));
+            a.vc[vi + (size_t)j * a.bs] = f32_to_fp8e4m3_sat(vx[j] * vinv);
+        }
+        *(uint2*)(a.kc + ki) = make_uint2(kw[0], kw[1]);
+    }
+}
+
+template <gg_dtype_t SRC>
+void launch_vec(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
+    const long long threads = (long long)a.n_rows * (a.Hkv * a.D / 8);
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    switch (dst) {
+        case GG_DTYPE_F32: append_vec_kernel<SRC, GG_DTYPE_F32><<<grid, 256, 0, s>>>(a); break;
+        case GG_DTYPE_F16: append_vec_kernel<SRC, GG_DTYPE_F16><<<grid, 256, 0, s>>>(a); break;
+        case GG_DTYPE_BF16: append_vec_kernel<SRC, GG_DTYPE_BF16><<<grid, 256, 0, s>>>(a); break;
+        default: append_vec_kernel<SRC, GG_DTYPE_FP8_E4M3><<<grid, 256, 0, s>>>(a); break;
+    }
+}
+
 // ---- PER_BLOCK int8: three passes (amax, quantise/requantise, publish) ----
 
 __device__ __forceinline__ float warp_max(float v) {
@@ -228,6 +305,12 @@ gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg
         append_amax_kernel<<<dim3(n_rows, kv->num_kv_heads), 64, 0, s>>>(a);
         append_int8_block_kernel<<<n_rows, 256, 0, s>>>(a);
         append_int8_publish_kernel<<<n_rows, 64, 0, s>>>(a);
+    } else if (a.D % 8 == 0 && a.dst != GG_DTYPE_INT8 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0) {
+        switch (src) {
+            case GG_DTYPE_F32: launch_vec<GG_DTYPE_F32>(a, a.dst, s); break;
+            case GG_DTYPE_F16: launch_vec<GG_DTYPE_F16>(a, a.dst, s); break;
+            default: launch_vec<GG_DTYPE_BF16>(a, a.dst, s); break;
+        }
     } else {
         append_direct_kernel<<<n_rows, 256, 0, s>>>(a);
     }
