@@ -139,9 +139,21 @@ def main():
     setup_s = time.time() - t_setup
 
     scale = 1.0 / math.sqrt(D)
-    ev = {name: [] for name in ("append", "attn", "accept")}
+    ev = {name: [] for name in ("append", "attn", "accept", "plan")}
+
+    # The attention schedule depends only on the context lengths, shared by all layers of
+    # a step: computed once per step (gg_verify_attention_plan), used by every layer.
+    use_plan = cfg.partition == 0
 
     def step(record: bool):
+        if use_plan:
+            if record:
+                p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                p0.record()
+            kv.attention_plan(keys, R, Hq, bt.shape[1], ws_attn)
+            if record:
+                p1.record()
+                ev["plan"].append((p0, p1))
         for layer in range(L):
             if record:
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
@@ -149,7 +161,8 @@ def main():
             kv.append(layer, k_new[layer], v_new[layer], append_slots)
             if record:
                 e1.record()
-            kv.attention(layer, q[layer], out, keys, bt, scale, partition_tokens=cfg.partition, workspace=ws_attn)
+            kv.attention(layer, q[layer], out, keys, bt, scale, partition_tokens=cfg.partition, workspace=ws_attn,
+                         planned=use_plan)
             if record:
                 e2.record()
                 ev["append"].append((e0, e1))
@@ -179,16 +192,19 @@ def main():
 
     def avg_us(name):
         xs = [s.elapsed_time(e) * 1000.0 for s, e in ev[name]]
+        if not xs:
+            return 0.0, 0.0
         xs.sort()
         return sum(xs) / len(xs), xs[len(xs) // 2]
 
     t_app, t_app_med = avg_us("append")
     t_attn, t_attn_med = avg_us("attn")
     t_acc, t_acc_med = avg_us("accept")
+    t_plan, _ = avg_us("plan")
     ms_per_step = wall * 1000.0 / args.steps
     tokens = B * R
     value = tokens / (ms_per_step / 1000.0)
-    kernel_formula_tps = tokens / ((L * (t_app + t_attn) + t_acc) * 1e-6)
+    kernel_formula_tps = tokens / ((L * (t_app + t_attn) + t_acc + t_plan) * 1e-6)
     accepted = acc_out[0].cpu()
     accepted_tps = float((accepted + 1).sum()) / (ms_per_step / 1000.0)
 
@@ -211,7 +227,7 @@ def main():
     elif cfg.partition:
         attn_kernels = "attn_mfma_kernel + attn_combine_kernel (partition grid)"
     else:
-        attn_kernels = "attn_mfma_streamk_kernel + attn_streamk_combine_kernel"
+        attn_kernels = "gg_verify_attention_planned: the library's automatic schedule (LPT pieces or stream-K) + merge"
     traffic, traffic_src = pmc_traffic(args.config)
     lb = logits.element_size()
     acc_bytes = B * R * V * lb + (B * K * V * 4 if draft_probs is not None else 0)
@@ -239,7 +255,8 @@ def main():
             "shared_prefix_frac": cfg.shared_prefix_frac,
         },
         "kernels_us": {"append_avg": round(t_app, 2), "attention_avg": round(t_attn, 2),
-                       "attention_median": round(t_attn_med, 2), "accept_avg": round(t_acc, 2)},
+                       "attention_median": round(t_attn_med, 2), "accept_avg": round(t_acc, 2),
+                       "attention_plan_per_step": round(t_plan, 2)},
         "tokens_per_s_from_kernel_times": round(kernel_formula_tps, 1),
         "accepted_tokens_per_s": round(accepted_tps, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

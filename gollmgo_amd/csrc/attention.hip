@@ -151,18 +151,22 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a, int D) {
 
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens) {
-    if (partition_tokens > 0) return {false, partition_tokens};
-    if (!attn_mfma_supported(kv, rows, num_q_heads)) return {false, 512};
+    if (partition_tokens > 0) return {ATTN_SCHED_GRID, partition_tokens};
+    if (!attn_mfma_supported(kv, rows, num_q_heads)) return {ATTN_SCHED_GRID, 512};
     // Measured on MI355X: while the (sequence, kv head) items alone fill every resident
-    // workgroup slot, one workgroup per item (no split, no merge) is fastest; with fewer
-    // items than slots, or keys beyond one MFMA piece, stream-K balances the work.
+    // workgroup slot, longest-first pieces (LPT: items longer than the mean slot load cut
+    // in equal pieces, dispatched longest first) balance ragged contexts best; beyond the
+    // sequences an LPT workgroup can rank, one workgroup per item (no split, no merge).
+    // With fewer items than slots, or keys beyond one MFMA piece, stream-K splits evenly.
     const int G = num_q_heads / kv->num_kv_heads;
     const int nt = (G * rows + 15) / 16;
     const long long max_keys = (long long)max_blocks * kv->block_size;
     const long long items = (long long)num_seqs * kv->num_kv_heads;
     const long long slots = (long long)device_cu_count() * attn_occupancy(nt);
-    if (items >= slots && max_keys <= kMfmaMaxPartition) return {false, (int)((max_keys + 63) / 64 * 64)};
-    return {true, 0};
+    if (items >= slots && num_seqs <= kLptMaxSeqs) return {ATTN_SCHED_LPT, 0};
+    if (items >= slots && max_keys <= kMfmaMaxPartition)
+        return {ATTN_SCHED_GRID, (int)((max_keys + 63) / 64 * 64)};
+    return {ATTN_SCHED_STREAMK, 0};
 }
 
 size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
@@ -178,12 +182,12 @@ size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_head
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s) {
     const KV* kv = a.kv;
     KVView view = make_kv_view(kv, a.layer);
-    if (a.streamk || (attn_mfma_supported(kv, a.rows, a.num_q_heads) && a.partition % 64 == 0 &&
-                      a.partition <= kMfmaMaxPartition)) {
-        // Stream-K launches its own combine over its record layout.
+    if (a.sched != ATTN_SCHED_GRID || (attn_mfma_supported(kv, a.rows, a.num_q_heads) && a.partition % 64 == 0 &&
+                                       a.partition <= kMfmaMaxPartition)) {
+        // Stream-K and LPT launch their own merge over their record layout.
         gg_status_t st = launch_attn_mfma(a, view, s);
         if (st != GG_OK) return st;
-        if (a.streamk) return check_hip(hipGetLastError(), "verify_attention launch");
+        if (a.sched != ATTN_SCHED_GRID) return check_hip(hipGetLastError(), "verify_attention launch");
     } else {
         const int DC = (kv->head_dim + 63) / 64;
         dim3 grid(a.max_parts, a.num_q_heads, a.num_seqs * a.rows);

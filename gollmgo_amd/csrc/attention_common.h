@@ -93,9 +93,12 @@ __host__ __device__ constexpr int attn_occupancy(int nt) { return nt <= 2 ? 2 : 
 
 // How one verify_attention call is scheduled.
 struct AttnPlan {
-    bool streamk;   // stream-K over a fixed grid (MFMA path only)
-    int partition;  // otherwise: tokens per workgroup of the partition grid
+    int sched;      // ATTN_SCHED_*
+    int partition;  // ATTN_SCHED_GRID: tokens per workgroup
 };
+
+// LPT schedule: most sequences the plan kernel ranks (one per thread).
+constexpr int kLptMaxSeqs = 1024;
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens);
 

@@ -192,12 +192,127 @@ struct ChunkRegs {
     float ksc, vsc;  // INT8 pools: scales of the lane's V block, fetched with its V
 };
 
+// Block ids of one chunk as this lane uses them: k = the block of its K rows, v = the
+// block of its V columns and P run (-1: no block: past the keys, past the piece, or an
+// out-of-range table entry). The chunk's kNS ids are read with wave-uniform (scalar)
+// loads, so waiting for them never waits on the vector loads of K/V in flight, and are
+// narrowed to the lane's two right there, from registers: a later lane-dependent pick
+// from a stored array would be folded into an indexed load and spill.
+struct LaneBlocks {
+    int k, v;
+};
+
+// What a piece needs to start streaming: its first chunk's K/V in flight and the block
+// ids of its first two chunks. Filled by piece_start, either before the piece or, for the
+// next piece of the same workgroup, while the current one merges.
+template <gg_dtype_t DT>
+struct PieceIn {
+    ChunkRegs<PoolTraits<DT>::kEB> cur;
+    LaneBlocks bl_cur, bl_next;
+};
+
+// A piece: tokens [t0, t_end) of sequence b against kv head kvh, written to partition
+// slot `part` / record `rec` (both < 0: the output). Wave-uniform.
+struct PieceDesc {
+    int b, kvh, t0, t_end, part, rec;
+};
+
+template <gg_dtype_t DT>
+struct PieceIO {
+    static constexpr int kEB = PoolTraits<DT>::kEB;
+    using Geom = Geo<kEB>;
+    static constexpr int kNS = Geom::kNS;
+    static constexpr int kTok = Geom::kTok;
+
+    __device__ static __forceinline__ LaneBlocks chunk_blocks(const AttnArgs& a, const KVView& kv, int b, int t0,
+                                                              int nchunks, int ctx, int ch) {
+        const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
+        int q[kNS];
+#pragma unroll
+        for (int qb = 0; qb < kNS; ++qb) {
+            const int t = t0 + ch * kTok + 16 * qb;
+            int blk = (ch < nchunks && t < ctx) ? bt[t >> 4] : -1;
+            blk = __builtin_amdgcn_readfirstlane(blk);
+            q[qb] = (blk >= kv.num_blocks) ? -1 : blk;
+        }
+        const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4;
+        const int ik = Geom::bq(c16 >> 2), iv = Geom::bq(g4);
+        LaneBlocks r;
+        if constexpr (kNS == 4) {
+            r.k = ik == 0 ? q[0] : ik == 1 ? q[1] : ik == 2 ? q[2] : q[3];
+            r.v = iv == 0 ? q[0] : iv == 1 ? q[1] : iv == 2 ? q[2] : q[3];
+        } else {
+            r.k = ik == 0 ? q[0] : q[1];
+            r.v = iv == 0 ? q[0] : q[1];
+        }
+        return r;
+    }
+    // K rows: lane supplies M index c16 of every tile. Loads are unconditional (missing
+    // blocks read block 0); such tokens are always masked in S.
+    __device__ static __forceinline__ void load_k(const KVView& kv, const LaneBlocks bl, int kvh,
+                                                  ChunkRegs<kEB>& rg) {
+        const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4, kq = c16 >> 2;
+        const int blk = bl.k;
+        const uint8_t* base =
+            kv.kc + (((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * (size_t)(kBS * kD) + 32 * g4) * kEB;
+#pragma unroll
+        for (int s = 0; s < kNS; ++s) {
+            const int off = Geom::ob(kq) + 4 * s + (c16 & 3);
+#pragma unroll
+            for (int v = 0; v < Geom::kKVec; ++v) rg.k[s][v] = *(const uint4*)(base + (size_t)off * kD * kEB + 16 * v);
+        }
+    }
+    // V: lane owns block bq(g4), dim dt*16 + c16, offsets ob(g4) .. ob(g4)+16/kEB-1 (zeroed
+    // later when the block is missing or partly past the keys).
+    __device__ static __forceinline__ void load_v(const KVView& kv, const LaneBlocks bl, int kvh,
+                                                  ChunkRegs<kEB>& rg) {
+        const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4;
+        const int blk = bl.v;
+        if constexpr (DT == GG_DTYPE_INT8) {
+            // Scales first: the softmax that needs them then waits for nothing behind them.
+            const size_t si = (size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh;
+            rg.ksc = f16_bits_to_f32(kv.k_blk_scale[si]);
+            rg.vsc = f16_bits_to_f32(kv.v_blk_scale[si]);
+        }
+        const uint8_t* base = kv.vc + ((((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * kD) * kBS + Geom::ob(g4)) * kEB;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int d = dt * 16 + c16;
+            rg.v[dt] = *(const uint4*)(base + (size_t)d * kBS * kEB);
+        }
+    }
+    // Issue the first chunk of piece d (this wave's first chunk is chunk `wave`): block
+    // ids and K rows (start_k), then V columns (start_v).
+    __device__ static __forceinline__ void start_k(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
+                                                   PieceIn<DT>& in) {
+        const int ctx = seq_keys(a, d.b, kBS);
+        const int nchunks = (d.t_end - d.t0 + kTok - 1) / kTok;
+        const int wave_u = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+        in.bl_cur = chunk_blocks(a, kv, d.b, d.t0, nchunks, ctx, wave_u);
+        in.bl_next = chunk_blocks(a, kv, d.b, d.t0, nchunks, ctx, wave_u + kWaves);
+        load_k(kv, in.bl_cur, d.kvh, in.cur);
+    }
+    __device__ static __forceinline__ void start_v(const KVView& kv, const PieceDesc& d, PieceIn<DT>& in) {
+        load_v(kv, in.bl_cur, d.kvh, in.cur);
+    }
+    __device__ static __forceinline__ void start(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
+                                                 PieceIn<DT>& in) {
+        start_k(a, kv, d, in);
+        start_v(kv, d, in);
+    }
+};
+
 // One piece of work: tokens [t0, t_end) of sequence b against kv head kvh. The result
 // goes to the output (part < 0 && rec < 0), to partition slot `part` of the fixed
 // partition grid, or to stream-K record `rec`. Must be reached by the whole workgroup.
+//
+// `in` holds the piece's first chunk, already issued (PieceIO::start). With has_next,
+// the next piece's first chunk is issued into `in` as soon as this piece's chunk
+// loop ends, so its latency overlaps this piece's merge and the next Q staging.
 template <gg_dtype_t DT, int NT>
-__device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, int b, int kvh, int t0,
-                                           int t_end, int part, int rec) {
+__device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, const PieceDesc pd,
+                                           PieceIn<DT>& in, const bool has_next, const PieceDesc next) {
+    const int b = pd.b, kvh = pd.kvh, t0 = pd.t0, t_end = pd.t_end, part = pd.part, rec = pd.rec;
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
     constexpr int kEB = T::kEB;
@@ -209,7 +324,10 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     const int ctx = seq_keys(a, b, kBS);
     const int R = a.rows;
     const int nrows = a.row_counts ? a.row_counts[b] : R;
-    if (nrows <= 0 || nrows > ctx) return;
+    if (nrows <= 0 || nrows > ctx) {
+        if (has_next) PieceIO<DT>::start(a, kv, next, in);
+        return;
+    }
     const int Hq = a.num_q_heads;
     const int G = Hq / kv.Hkv;
     const int nvalid_rows = G * nrows;
@@ -328,73 +446,18 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         for (int dt = 0; dt < 8; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
-    const size_t head_stride = (size_t)kBS * kD;  // elements per (block, head) tile
-
-    // The kNS physical blocks of chunk ch, read with wave-uniform (scalar) loads so that
-    // waiting for them never waits on the vector loads of K/V in flight. -1 = no block
-    // (past the keys, past the partition, or an out-of-range table entry).
-    struct Blocks {
-        int q[kNS];
-    };
-    auto chunk_blocks = [&](int ch) -> Blocks {
-        Blocks r;
-#pragma unroll
-        for (int qb = 0; qb < kNS; ++qb) {
-            const int t = t0 + ch * kTok + 16 * qb;
-            int blk = (ch < nchunks && t < ctx) ? bt[t >> 4] : -1;
-            blk = __builtin_amdgcn_readfirstlane(blk);
-            r.q[qb] = (blk >= kv.num_blocks) ? -1 : blk;
-        }
-        return r;
-    };
-    auto pick = [](const Blocks& bl, int i) -> int {
-        if constexpr (kNS == 4) return i == 0 ? bl.q[0] : i == 1 ? bl.q[1] : i == 2 ? bl.q[2] : bl.q[3];
-        else return i == 0 ? bl.q[0] : bl.q[1];
-    };
-    // K rows: lane supplies M index c16 of every tile. Loads are unconditional (missing
-    // blocks read block 0); such tokens are always masked in S.
-    const int kq = c16 >> 2;
-    auto load_k = [&](const Blocks& bl, Regs& rg) {
-        const int blk = pick(bl, Geom::bq(kq));
-        const uint8_t* base = kv.kc + (((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * head_stride + 32 * g4) * kEB;
-#pragma unroll
-        for (int s = 0; s < kNS; ++s) {
-            const int off = Geom::ob(kq) + 4 * s + (c16 & 3);
-#pragma unroll
-            for (int v = 0; v < Geom::kKVec; ++v) rg.k[s][v] = *(const uint4*)(base + (size_t)off * kD * kEB + 16 * v);
-        }
-    };
-    // V: lane owns block bq(g4), dim dt*16 + c16, offsets ob(g4) .. ob(g4)+16/kEB-1 (zeroed
-    // later when the block is missing or partly past the keys).
-    auto load_v = [&](const Blocks& bl, Regs& rg) {
-        const int blk = pick(bl, Geom::bq(g4));
-        if constexpr (DT == GG_DTYPE_INT8) {
-            // Scales first: the softmax that needs them then waits for nothing behind them.
-            const size_t si = (size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh;
-            rg.ksc = f16_bits_to_f32(kv.k_blk_scale[si]);
-            rg.vsc = f16_bits_to_f32(kv.v_blk_scale[si]);
-        }
-        const uint8_t* base = kv.vc + ((((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * kD) * kBS + Geom::ob(g4)) * kEB;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const int d = dt * 16 + c16;
-            rg.v[dt] = *(const uint4*)(base + (size_t)d * kBS * kEB);
-        }
-    };
-
-    Regs cur;
+    using IO = PieceIO<DT>;
+    auto chunk_blocks = [&](int ch) { return IO::chunk_blocks(a, kv, b, t0, nchunks, ctx, ch); };
+    Regs& cur = in.cur;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     // Block ids run two chunks ahead and are requested after the softmax: the LDS
     // reads of Q at the top of the next chunk wait on every outstanding scalar load,
     // and by then these have had the whole P.V stage to arrive.
-    Blocks bl_cur = chunk_blocks(wave_u);
-    Blocks bl_next = chunk_blocks(wave_u + kWaves);
-    load_k(bl_cur, cur);
-    load_v(bl_cur, cur);
+    LaneBlocks& bl_cur = in.bl_cur;
+    LaneBlocks& bl_next = in.bl_next;
 
     for (int ch = wave_u; ch < nchunks; ch += kWaves) {
-        const int blk_v = pick(bl_cur, Geom::bq(g4));
+        const int blk_v = bl_cur.v;
         const int tc = t0 + ch * kTok;
         const int tlane = tc + 16 * Geom::bq(g4) + Geom::ob(g4);  // first token of the lane's P run
         // Valid offsets of the lane's V block (offsets counted from the block start).
@@ -445,7 +508,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             }
         }
         // Next chunk's K rows stream in while this chunk finishes.
-        load_k(bl_next, cur);
+        IO::load_k(kv, bl_next, kvh, cur);
 
         // ---- online softmax; P packed as MFMA A operands ----
         // Masked scores: causal (keys past the row's position, which covers keys past the
@@ -519,7 +582,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             }
         }
 
-        const Blocks bl_after = chunk_blocks(ch + 2 * kWaves);
+        const LaneBlocks bl_after = chunk_blocks(ch + 2 * kWaves);
 
         // ---- O += P . V; each V dim tile decoded once for all row tiles ----
         if (nvalid_v < kBS) {
@@ -548,10 +611,14 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             }
         }
         // Next chunk's V columns.
-        load_v(bl_next, cur);
+        IO::load_v(kv, bl_next, kvh, cur);
         bl_cur = bl_next;
         bl_next = bl_after;
     }
+
+    // The next piece of this workgroup starts streaming now: block ids and K rows before
+    // the merge, V columns after it (both buffers next to the O tiles would not fit).
+    if (has_next) IO::start_k(a, kv, next, in);
 
     // ---- merge the four waves' states through LDS ----
     __shared__ float s_m[kWaves][64];
@@ -616,6 +683,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         }
         __syncthreads();
     }
+    if (has_next) IO::start_v(kv, next, in);
 }
 
 // Fixed partition grid: workgroup (part, kvh, b) takes tokens [part*P, (part+1)*P).
@@ -626,7 +694,10 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(Attn
     const int P = a.partition;
     const int nparts = (ctx + P - 1) / P;
     if (part >= nparts) return;
-    attn_piece<DT, NT>(a, kv, b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1);
+    const PieceDesc d{b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1};
+    PieceIn<DT> in;
+    PieceIO<DT>::start(a, kv, d, in);
+    attn_piece<DT, NT>(a, kv, d, in, false, d);
 }
 
 // Chunks of work of sequence b (0 when it has nothing to compute).
@@ -693,36 +764,181 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
     }
     __syncthreads();
     // Loop state is wave-uniform 32-bit (chunk totals stay far below 2^31) and kept in
-    // scalar registers so that nothing but the piece itself holds vector registers.
+    // scalar registers.
     int b = __builtin_amdgcn_readfirstlane(s_b0);
     int gb = __builtin_amdgcn_readfirstlane((int)s_base0);  // chunk index where sequence b starts
     int g = __builtin_amdgcn_readfirstlane((int)g0);
     const int ge = __builtin_amdgcn_readfirstlane((int)g1);
-    while (g < ge && b < B) {
-        const int nch = __builtin_amdgcn_readfirstlane(seq_chunks(a, b, kTok));
-        const int wk = Hkv * nch;
-        if (nch == 0 || g >= gb + wk) {
-            gb += wk;
-            ++b;
-            continue;
+    // The next piece of [g, ge): advances (g, b, gb); false when the range is done.
+    auto next_piece = [&](PieceDesc& d) -> bool {
+        while (g < ge && b < B) {
+            const int nch = __builtin_amdgcn_readfirstlane(seq_chunks(a, b, kTok));
+            const int wk = Hkv * nch;
+            if (nch == 0 || g >= gb + wk) {
+                gb += wk;
+                ++b;
+                continue;
+            }
+            const int off = g - gb;
+            const int kvh = off / nch;
+            const int c0 = off % nch;
+            const int c1 = min(nch, c0 + (ge - g));
+            const int item = b * Hkv + kvh;
+            const bool whole = c0 == 0 && c1 == nch;
+            const int ctx = __builtin_amdgcn_readfirstlane(seq_keys(a, b, kBS));
+            d = PieceDesc{b, kvh, c0 * kTok, min(c1 * kTok, ctx), -1, whole ? -1 : w + item};
+            g = __builtin_amdgcn_readfirstlane(g + (c1 - c0));
+            return true;
         }
-        const int off = g - gb;
-        const int kvh = off / nch;
-        const int c0 = off % nch;
-        const int c1 = min(nch, c0 + (ge - g));
-        const int item = b * Hkv + kvh;
-        const bool whole = c0 == 0 && c1 == nch;
-        const int ctx = __builtin_amdgcn_readfirstlane(seq_keys(a, b, kBS));
-        attn_piece<DT, NT>(a, kv, b, kvh, c0 * kTok, min(c1 * kTok, ctx), -1, whole ? -1 : w + item);
-        g = __builtin_amdgcn_readfirstlane(g + (c1 - c0));
-        b = __builtin_amdgcn_readfirstlane(b);
-        gb = __builtin_amdgcn_readfirstlane(gb);
+        return false;
+    };
+    PieceDesc d;
+    while (next_piece(d)) {
+        PieceIn<DT> in;
+        PieceIO<DT>::start(a, kv, d, in);
+        attn_piece<DT, NT>(a, kv, d, in, false, d);
     }
+}
+
+// ---- LPT schedule: pieces of at most about the mean slot load, longest first ----
+//
+// Items longer than T = ceil(total chunks / resident slots) are cut into equal pieces of
+// at most T chunks. attn_lpt_plan_kernel orders the pieces by size, descending (ties:
+// sequence, then piece, then kv head), and workgroup p of the main launch runs piece p:
+// dispatched in order, the longest pieces start first and the shortest fill the tail.
+// attn_lpt_combine_kernel merges the partial records of split items. (Merging in the
+// last piece to finish needs device-scope fences, which write back / invalidate a whole
+// L2 here and cost more than the separate launch.)
+//
+// Plan layout (ints, in the workspace after the records), R = record bound:
+//   [0]                       number of pieces
+//   [16 + 4p ..]              piece p: (sequence, kv head | pieces per kv head << 16,
+//                             first chunk, end chunk); sequence -1 past the last piece
+//   [16 + 4R + 2b ..]         sequence b: (first piece, pieces per kv head)
+// Pieces of sequence b are first + j*Hkv + kvh.
+__device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
+__device__ __forceinline__ int* lpt_seq(int* plan, int recs) { return plan + 16 + 4 * recs; }
+
+// Sum over a 1024-thread workgroup (wave sums, then the 16 wave totals).
+__device__ __forceinline__ long long block_sum_1024(long long v, long long* s_w) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = v;
+    __syncthreads();
+    long long t = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) t += s_w[w];
+    return t;
+}
+
+// One 1024-thread workgroup (one sequence per thread): sizes, ranks and lays out the
+// pieces.
+__global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv, int tok, int slots, int recs) {
+    __shared__ int s_key[kLptMaxSeqs];  // piece size in chunks (0: no work)
+    __shared__ int s_cnt[kLptMaxSeqs];  // pieces of the sequence over all kv heads
+    __shared__ long long s_w[16];
+    const int B = a.num_seqs;
+    const int b = threadIdx.x;
+    const int nch = b < B ? seq_chunks(a, b, tok) : 0;
+    const long long C = block_sum_1024((long long)Hkv * nch, s_w);
+    const int T = (int)max((C + slots - 1) / slots, (long long)kStreamKMinChunks);
+    const int np = nch ? (nch + T - 1) / T : 0;
+    const int key = np ? (nch + np - 1) / np : 0;
+    const int cnt = np * Hkv;
+    if (b < B) {
+        s_key[b] = key;
+        s_cnt[b] = cnt;
+    }
+    const long long total = block_sum_1024(cnt, s_w);  // (its barriers also publish s_key / s_cnt)
+    int* plan = a.plan;
+    if (b == 0) plan[0] = (int)total;
+    if (b >= B) return;
+    int pos = 0;
+    for (int t = 0; t < B; ++t) {
+        const int kt = s_key[t];
+        if (kt > key || (kt == key && t < b)) pos += s_cnt[t];
+    }
+    int* seq = lpt_seq(plan, recs) + 2 * b;
+    seq[0] = pos;
+    seq[1] = np;
+    int4* table = (int4*)lpt_table(plan);
+    for (int j = 0; j < np; ++j) {
+        const int c0 = (int)((long long)j * nch / np), c1 = (int)((long long)(j + 1) * nch / np);
+        for (int h = 0; h < Hkv; ++h) table[pos + j * Hkv + h] = make_int4(b, h | (np << 16), c0, c1);
+    }
+    // Entries past the last piece tell their workgroups to exit.
+    for (int q = (int)total + b; q < recs; q += B) table[q] = make_int4(-1, 0, 0, 0);
+}
+
+// Workgroup p computes piece p of the plan (exits past the last piece).
+template <gg_dtype_t DT, int NT>
+__global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
+    constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
+    const int p = blockIdx.x;
+    // One load tells the workgroup everything about its piece.
+    const int4 e = ((const int4*)lpt_table(a.plan))[p];
+    const int b = e.x;
+    if (b < 0) return;  // past the last piece
+    const int kvh = e.y & 0xffff, np = e.y >> 16;
+    const int ctx = seq_keys(a, b, kBS);
+    const PieceDesc d{b, kvh, e.z * kTok, min(e.w * kTok, ctx), -1, np > 1 ? p : -1};
+    PieceIn<DT> in;
+    PieceIO<DT>::start(a, kv, d, in);
+    attn_piece<DT, NT>(a, kv, d, in, false, d);
+}
+
+// Merge the pieces of split items; workgroup (item, y) takes rows 4y .. 4y+3.
+__global__ void __launch_bounds__(128) attn_lpt_combine_kernel(AttnArgs a, int Hkv, int tok, int recs) {
+    const int item = blockIdx.x;
+    const int b = item / Hkv, kvh = item % Hkv;
+    if (seq_chunks(a, b, tok) == 0) return;  // no pieces
+    const int* seq = lpt_seq(a.plan, recs) + 2 * b;
+    const int first = seq[0], np = seq[1];
+    if (np <= 1) return;
+    const int G = a.num_q_heads / Hkv;
+    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int r = blockIdx.y * 4 + (threadIdx.x >> 5);
+    const int d4 = threadIdx.x & 31;
+    if (r >= G * nrows) return;
+    const int RW = G * a.rows;
+    float M = -1e30f, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < np; ++j) {
+        const size_t q = (size_t)(first + j * Hkv + kvh) * RW + r;
+        const float2 ml = *(const float2*)(a.ws_ml + q * 2);
+        const float4 v = ((const float4*)(a.ws_acc + q * kD))[d4];
+        const float mn = fmaxf(M, ml.x);
+        const float fo = __expf(M - mn), fn = __expf(ml.x - mn);
+        M = mn;
+        L = L * fo + ml.y * fn;
+        acc.x = acc.x * fo + v.x * fn;
+        acc.y = acc.y * fo + v.y * fn;
+        acc.z = acc.z * fo + v.z * fn;
+        acc.w = acc.w * fo + v.w * fn;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int j = r / G, g = r % G;
+    const size_t obase = (((size_t)b * a.rows + j) * a.num_q_heads + (size_t)kvh * G + g) * kD + 4 * d4;
+    store_from_f32(a.out, a.out_dtype, obase + 0, acc.x * inv);
+    store_from_f32(a.out, a.out_dtype, obase + 1, acc.y * inv);
+    store_from_f32(a.out, a.out_dtype, obase + 2, acc.z * inv);
+    store_from_f32(a.out, a.out_dtype, obase + 3, acc.w * inv);
 }
 
 template <gg_dtype_t DT>
 gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s) {
-    if (a.streamk) {
+    if (a.sched == ATTN_SCHED_LPT) {
+        const int recs = a.sk_grid + a.num_seqs * kv.Hkv;  // bound on the number of pieces
+        switch (nt) {
+            case 1: attn_mfma_lpt_kernel<DT, 1><<<recs, 256, 0, s>>>(a, kv); break;
+            case 2: attn_mfma_lpt_kernel<DT, 2><<<recs, 256, 0, s>>>(a, kv); break;
+            case 3: attn_mfma_lpt_kernel<DT, 3><<<recs, 256, 0, s>>>(a, kv); break;
+            case 4: attn_mfma_lpt_kernel<DT, 4><<<recs, 256, 0, s>>>(a, kv); break;
+            default: return fail(GG_ERR_INVALID, "attention: too many rows per kv head for the MFMA path");
+        }
+        return GG_OK;
+    }
+    if (a.sched == ATTN_SCHED_STREAMK) {
         const int grid = a.sk_grid;
         switch (nt) {
             case 1: attn_mfma_streamk_kernel<DT, 1><<<grid, 256, 0, s>>>(a, kv); break;
@@ -811,6 +1027,11 @@ __global__ void __launch_bounds__(128) attn_streamk_combine_kernel(AttnArgs a, i
 gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s) {
     const int G = a.num_q_heads / kv.Hkv;
     const int nt = (G * a.rows + 15) / 16;
+    const int tok = (kv.dt == GG_DTYPE_FP8_E4M3 || kv.dt == GG_DTYPE_INT8) ? 64 : 32;
+    if (a.sched == ATTN_SCHED_LPT && !a.plan_ready) {
+        const gg_status_t st = launch_attn_plan(a, s);
+        if (st != GG_OK) return st;
+    }
     gg_status_t st;
     switch (kv.dt) {
         case GG_DTYPE_BF16: st = launch_dt<GG_DTYPE_BF16>(a, kv, nt, s); break;
@@ -819,11 +1040,22 @@ gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s)
         case GG_DTYPE_INT8: st = launch_dt<GG_DTYPE_INT8>(a, kv, nt, s); break;
         default: return fail(GG_ERR_INVALID, "attention: pool dtype not on the MFMA path");
     }
-    if (st != GG_OK || !a.streamk) return st;
-    const int tok = (kv.dt == GG_DTYPE_FP8_E4M3 || kv.dt == GG_DTYPE_INT8) ? 64 : 32;
-    const int grid = a.sk_grid;
-    attn_streamk_combine_kernel<<<dim3(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4), 128, 0, s>>>(a, kv.Hkv, tok, grid);
+    if (st != GG_OK) return st;
+    const dim3 cgrid(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4);
+    if (a.sched == ATTN_SCHED_STREAMK) attn_streamk_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, a.sk_grid);
+    if (a.sched == ATTN_SCHED_LPT)
+        attn_lpt_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, a.sk_grid + a.num_seqs * kv.Hkv);
     return GG_OK;
+}
+
+gg_status_t launch_attn_plan(const AttnArgs& a, hipStream_t s) {
+    if (a.sched != ATTN_SCHED_LPT) return GG_OK;
+    if (a.num_seqs > kLptMaxSeqs) return fail(GG_ERR_INTERNAL, "attention: LPT plan over too many sequences");
+    const KV* kv = a.kv;
+    const int tok = (kv->dtype == GG_DTYPE_FP8_E4M3 || kv->dtype == GG_DTYPE_INT8) ? 64 : 32;
+    const int Hkv = kv->num_kv_heads;
+    attn_lpt_plan_kernel<<<1, 1024, 0, s>>>(a, Hkv, tok, a.sk_grid, a.sk_grid + a.num_seqs * Hkv);
+    return check_hip(hipGetLastError(), "verify_attention plan launch");
 }
 
 int attn_streamk_grid(const KV* kv, int rows, int num_q_heads) {
@@ -833,12 +1065,16 @@ int attn_streamk_grid(const KV* kv, int rows, int num_q_heads) {
     return device_cu_count() * attn_occupancy(nt);
 }
 
-size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, size_t* ml_elems) {
+size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, size_t* ml_elems,
+                                    size_t* acc_elems) {
     const size_t records = (size_t)attn_streamk_grid(kv, rows, num_q_heads) + (size_t)num_seqs * kv->num_kv_heads;
     const size_t rw = (size_t)(num_q_heads / kv->num_kv_heads) * rows;
     const size_t n_ml = records * rw * 2;
+    const size_t n_acc = records * rw * kD;
+    const size_t plan_ints = 16 + 4 * records + 2 * (size_t)num_seqs;
     if (ml_elems) *ml_elems = n_ml;
-    return (((n_ml + 63) / 64) * 64 + records * rw * kD) * sizeof(float);
+    if (acc_elems) *acc_elems = n_acc;
+    return (((n_ml + 63) / 64) * 64 + n_acc) * sizeof(float) + plan_ints * sizeof(int);
 }
 
 }  // namespace gg

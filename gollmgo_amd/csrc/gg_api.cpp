@@ -223,21 +223,26 @@ GG_API size_t gg_verify_attention_workspace_size(gg_kv_t kv, int num_seqs, int r
     if (!attn_shape_ok(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq)) return 0;
     if (partition_tokens < 0 || partition_tokens % 64 != 0) return 0;
     const AttnPlan plan = attn_plan(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, partition_tokens);
-    if (plan.streamk) return attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, nullptr);
+    if (plan.sched != ATTN_SCHED_GRID)
+        return attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, nullptr, nullptr);
     return attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, plan.partition);
 }
 
-GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
-                                       void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
-                                       const int32_t* row_counts, const int32_t* block_tables,
-                                       int max_blocks_per_seq, int num_seqs, int rows_per_seq,
-                                       int num_q_heads, float scale, int partition_tokens,
-                                       void* workspace, size_t workspace_bytes, void* stream) {
+// What one attention entry point does with the schedule plan.
+enum AttnCall { ATTN_CALL_SELF = 0, ATTN_CALL_PLANNED = 1, ATTN_CALL_PLAN_ONLY = 2 };
+
+static gg_status_t verify_attention_impl(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype, void* out,
+                                         gg_dtype_t out_dtype, const int32_t* ctx_lens, const int32_t* row_counts,
+                                         const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
+                                         int rows_per_seq, int num_q_heads, float scale, int partition_tokens,
+                                         void* workspace, size_t workspace_bytes, void* stream, AttnCall call) {
     clear_error();
+    const bool compute = call != ATTN_CALL_PLAN_ONLY;
     GG_CHECK_ARG(kv != nullptr, "gg_verify_attention: kv is NULL");
-    GG_CHECK_ARG(layer >= 0 && layer < kv->num_layers, "gg_verify_attention: layer out of range");
-    GG_CHECK_ARG(q && out && ctx_lens && block_tables, "gg_verify_attention: NULL buffer");
-    GG_CHECK_ARG(is_float_io(q_dtype) && is_float_io(out_dtype), "gg_verify_attention: q/out dtype must be F32/F16/BF16");
+    GG_CHECK_ARG(!compute || (layer >= 0 && layer < kv->num_layers), "gg_verify_attention: layer out of range");
+    GG_CHECK_ARG(ctx_lens && (!compute || (q && out && block_tables)), "gg_verify_attention: NULL buffer");
+    GG_CHECK_ARG(!compute || (is_float_io(q_dtype) && is_float_io(out_dtype)),
+                 "gg_verify_attention: q/out dtype must be F32/F16/BF16");
     GG_CHECK_ARG(attn_shape_ok(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq),
                  "gg_verify_attention: bad shape (num_q_heads must be a multiple of num_kv_heads)");
     GG_CHECK_ARG(partition_tokens >= 0 && partition_tokens % 64 == 0,
@@ -260,14 +265,14 @@ GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_
     a.scale = scale;
     a.kv_bs = kv->block_size;
     const AttnPlan plan = attn_plan(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, partition_tokens);
-    a.streamk = plan.streamk ? 1 : 0;
-    a.partition = plan.streamk ? kMfmaAutoPartition : plan.partition;
+    a.sched = plan.sched;
+    a.partition = plan.sched == ATTN_SCHED_GRID ? plan.partition : kMfmaAutoPartition;
     a.max_parts = (max_blocks_per_seq * kv->block_size + a.partition - 1) / a.partition;
     a.sk_min_chunks = kStreamKMinChunks;
-    size_t need, n_ml;
-    if (a.streamk) {
+    size_t need, n_ml, n_acc = 0;
+    if (a.sched != ATTN_SCHED_GRID) {
         a.sk_grid = attn_streamk_grid(kv, rows_per_seq, num_q_heads);
-        need = attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, &n_ml);
+        need = attn_streamk_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, &n_ml, &n_acc);
     } else {
         need = attn_workspace_bytes(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq, a.partition);
         n_ml = (size_t)num_seqs * rows_per_seq * num_q_heads * a.max_parts * 2;
@@ -277,8 +282,42 @@ GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_
     if (need) {
         a.ws_ml = (float*)workspace;
         a.ws_acc = (float*)workspace + ((n_ml + 63) / 64) * 64;
+        if (a.sched != ATTN_SCHED_GRID) a.plan = (int*)(a.ws_acc + n_acc);
     }
+    a.plan_ready = call == ATTN_CALL_PLANNED ? 1 : 0;
+    if (call == ATTN_CALL_PLAN_ONLY) return launch_attn_plan(a, (hipStream_t)stream);
     return launch_verify_attention(a, (hipStream_t)stream);
+}
+
+GG_API gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
+                                       void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                       const int32_t* row_counts, const int32_t* block_tables,
+                                       int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                       int num_q_heads, float scale, int partition_tokens,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+    return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,
+                                 max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, scale, partition_tokens,
+                                 workspace, workspace_bytes, stream, ATTN_CALL_SELF);
+}
+
+GG_API gg_status_t gg_verify_attention_plan(gg_kv_t kv, const int32_t* ctx_lens, const int32_t* row_counts,
+                                            int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                            int num_q_heads, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+    return verify_attention_impl(kv, 0, nullptr, GG_DTYPE_BF16, nullptr, GG_DTYPE_BF16, ctx_lens, row_counts,
+                                 nullptr, max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, 1.0f, 0,
+                                 workspace, workspace_bytes, stream, ATTN_CALL_PLAN_ONLY);
+}
+
+GG_API gg_status_t gg_verify_attention_planned(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
+                                               void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                               const int32_t* row_counts, const int32_t* block_tables,
+                                               int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                               int num_q_heads, float scale, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+    return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,
+                                 max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, scale, 0, workspace,
+                                 workspace_bytes, stream, ATTN_CALL_PLANNED);
 }
 
 // ---------------------------------------------------------------- acceptance

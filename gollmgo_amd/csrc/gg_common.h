@@ -77,20 +77,27 @@ struct AttnArgs {
     int max_parts;
     float* ws_ml;      // partition grid: [seqs][rows][Hq][max_parts][2]; stream-K: [records][G*R][2]
     float* ws_acc;     // partition grid: [seqs][rows][Hq][max_parts][D]; stream-K: [records][G*R][D]
-    int streamk;       // 1: stream-K schedule (MFMA path, automatic partitioning)
-    int sk_grid;       // stream-K workgroups (attn_streamk_grid)
+    int sched;         // ATTN_SCHED_*: how the (sequence, kv head) items are cut
+    int sk_grid;       // stream-K / LPT: resident workgroup slots (attn_streamk_grid)
+    int* plan;         // LPT: piece plan in the workspace, after the records
+    int plan_ready;    // LPT: the plan is already in the workspace (gg_verify_attention_plan)
     int sk_min_chunks;    // least chunks a stream-K workgroup takes
 };
-// Stream-K launch: workgroups for a shape on the current device, and the workspace it
-// needs (grid + num_seqs * Hkv partial records of G*rows rows; ml_elems receives the
-// float count of the (max, sum) part, which the P.V part follows 64-float aligned).
+// Attention schedules on the MFMA path (the generic path always uses the grid).
+enum { ATTN_SCHED_GRID = 0, ATTN_SCHED_STREAMK = 1, ATTN_SCHED_LPT = 2 };
+
+// Stream-K and LPT: resident workgroup slots for a shape on the current device, and the
+// workspace both need: grid + num_seqs * Hkv partial records of G*rows rows, as (max,
+// sum) pairs, then (64-float aligned) P.V rows, then the LPT plan (ints). ml_elems and
+// acc_elems receive the float counts of the first two parts.
 int attn_streamk_grid(const KV* kv, int rows, int num_q_heads);
 size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
-                                    size_t* ml_elems);
+                                    size_t* ml_elems, size_t* acc_elems);
 int device_cu_count();
 size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads,
                             int max_blocks, int partition);
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s);
+gg_status_t launch_attn_plan(const AttnArgs& a, hipStream_t s);  // no-op unless LPT
 
 size_t greedy_workspace_bytes(int num_seqs, int max_drafts, int vocab);
 gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs, int max_drafts,

@@ -134,8 +134,9 @@ class KVCache:
     def attention(self, layer: int, q: torch.Tensor, out: torch.Tensor, ctx_lens: torch.Tensor,
                   block_tables: torch.Tensor, scale: float, row_counts: Optional[torch.Tensor] = None,
                   partition_tokens: int = 0, workspace: Optional[torch.Tensor] = None,
-                  stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-        """q, out: [num_seqs, rows_per_seq, num_q_heads, head_dim]."""
+                  stream: Optional[torch.cuda.Stream] = None, planned: bool = False) -> torch.Tensor:
+        """q, out: [num_seqs, rows_per_seq, num_q_heads, head_dim]. planned=True uses the
+        schedule attention_plan put in `workspace` (required then)."""
         if q.dim() != 4 or q.shape[-1] != self.head_dim or out.shape != q.shape:
             raise ValueError("q/out must be [num_seqs, rows_per_seq, num_q_heads, head_dim]")
         B, R, Hq, _ = q.shape
@@ -143,14 +144,36 @@ class KVCache:
             raise ValueError("block_tables must be [num_seqs, max_blocks_per_seq]")
         mb = block_tables.shape[1]
         if workspace is None:
+            if planned:
+                raise ValueError("a planned call needs the workspace that holds the plan")
             workspace = self.attention_workspace(B, R, Hq, mb, partition_tokens)
         rc = _dev(row_counts, "row_counts", torch.int32) if row_counts is not None else None
+        if planned:
+            if partition_tokens:
+                raise ValueError("a planned call uses the automatic schedule (partition_tokens = 0)")
+            check(lib().gg_verify_attention_planned(
+                self.handle, layer, _dev(q, "q"), int(dtype_of(q)), _dev(out, "out"), int(dtype_of(out)),
+                _dev(ctx_lens, "ctx_lens", torch.int32), rc, _dev(block_tables, "block_tables", torch.int32),
+                mb, B, R, Hq, float(scale), workspace.data_ptr(), workspace.numel(), _stream(stream)),
+                "gg_verify_attention_planned")
+            return out
         check(lib().gg_verify_attention(
             self.handle, layer, _dev(q, "q"), int(dtype_of(q)), _dev(out, "out"), int(dtype_of(out)),
             _dev(ctx_lens, "ctx_lens", torch.int32), rc, _dev(block_tables, "block_tables", torch.int32),
             mb, B, R, Hq, float(scale), partition_tokens, workspace.data_ptr(), workspace.numel(),
             _stream(stream)), "gg_verify_attention")
         return out
+
+    def attention_plan(self, ctx_lens: torch.Tensor, rows_per_seq: int, num_q_heads: int,
+                       max_blocks_per_seq: int, workspace: torch.Tensor, row_counts: Optional[torch.Tensor] = None,
+                       stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Schedule of one verify step into `workspace`, for attention(..., planned=True) on
+        every layer while ctx_lens / row_counts keep their contents."""
+        rc = _dev(row_counts, "row_counts", torch.int32) if row_counts is not None else None
+        check(lib().gg_verify_attention_plan(
+            self.handle, _dev(ctx_lens, "ctx_lens", torch.int32), rc, max_blocks_per_seq, ctx_lens.numel(),
+            rows_per_seq, num_q_heads, workspace.data_ptr(), workspace.numel(), _stream(stream)),
+            "gg_verify_attention_plan")
 
 
 def greedy_workspace(num_seqs: int, max_drafts: int, vocab: int) -> torch.Tensor:

@@ -155,6 +155,30 @@ gg_status_t gg_verify_attention(gg_kv_t kv, int layer, const void* q, gg_dtype_t
                                 int num_q_heads, float scale, int partition_tokens,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* One verify step runs the same attention schedule for every layer: it depends only on
+ * ctx_lens, row_counts and the shape, not on the layer. These two calls let a caller
+ * compute that schedule once per step instead of once per layer. They have no
+ * counterpart in the reference (whose attention is one serial loop per query,
+ * kernels/gollmgo_paged_attn.cu:38-119).
+ *   gg_verify_attention_plan   : computes the schedule of (ctx_lens, row_counts,
+ *                                shape) into `workspace` (sized as for
+ *                                gg_verify_attention with partition_tokens = 0).
+ *   gg_verify_attention_planned: gg_verify_attention with partition_tokens = 0 that
+ *                                uses the schedule already in `workspace`.
+ * Contract: between the plan and a planned call, the contents of ctx_lens and
+ * row_counts, the shape and the workspace must be unchanged (stream order suffices:
+ * the plan is a kernel on `stream`). A stale plan gives wrong results. */
+gg_status_t gg_verify_attention_plan(gg_kv_t kv, const int32_t* ctx_lens, const int32_t* row_counts,
+                                     int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                     int num_q_heads, void* workspace, size_t workspace_bytes,
+                                     void* stream);
+gg_status_t gg_verify_attention_planned(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
+                                        void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                        const int32_t* row_counts, const int32_t* block_tables,
+                                        int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                        int num_q_heads, float scale, void* workspace,
+                                        size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Greedy acceptance.
  * Replaces Verify + argmax (internal/engine/speculative.go:68-84,

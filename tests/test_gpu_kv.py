@@ -380,6 +380,15 @@ def test_attention_full_size_configs(gpu, cid, explicit):
     agree = rel_err_per_vector(outs[0], outs[explicit])
     print(f"  config {cid}: auto vs partition {explicit}: rel diff {agree:.2e}")
     assert agree <= 1e-3
+    # The step's schedule computed once (gg_verify_attention_plan), then a planned call:
+    # identical to the call that plans for itself.
+    ws = kv.attention_workspace(cfg.num_seqs, cfg.rows, cfg.num_q_heads, bt.shape[1], 0)
+    kv.attention_plan(keys, cfg.rows, cfg.num_q_heads, bt.shape[1], ws)
+    o = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+    for _ in range(2):  # the plan serves any number of calls
+        kv.attention(0, q, o, keys, bt, scale, workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o.cpu().numpy(), outs[0])
     idx = np.argsort(lay.keys)[:2]
     k_s = v_s = None
     if cfg.kv_dtype == "fp8":
