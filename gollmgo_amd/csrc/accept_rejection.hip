@@ -46,6 +46,20 @@ struct RowStats {
     u64 wx;           // weight of the drafted token (0 if outside the nucleus)
 };
 
+constexpr int kCandCap = 4096;
+
+struct RowHist {
+    u64 mass[kBins];
+    unsigned int cnt[kBins];
+};
+
+struct RowPick {
+    int cbin;        // boundary coarse bin (-1: nothing to resolve)
+    int n_cand;      // elements of that bin gathered so far
+    u64 c_above;     // mass of the bins before it
+    u64 tp;          // ceil(top_p * Z)
+};
+
 __device__ __forceinline__ u64 shfl_xor_u64(u64 v, int o) {
     unsigned int lo = (unsigned int)v, hi = (unsigned int)(v >> 32);
     lo = __shfl_xor(lo, o);
@@ -153,12 +167,16 @@ struct Nucleus {
     }
 };
 
+// Exact per-row statistics in one 1024-thread block (passes over the whole row). With
+// `only_flagged`, rows whose nucleus boundary the segmented path already resolved
+// (flag 0) are skipped: this kernel is then the fallback for crowded boundary bins.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
     const void* __restrict__ logits, int K, int V, const int32_t* __restrict__ drafts,
     const int32_t* __restrict__ n_drafts, float inv_t, float top_p, int use_topp,
-    RowStats* __restrict__ stats) {
+    RowStats* __restrict__ stats, const int* __restrict__ only_flagged) {
     const int row = blockIdx.x;
+    if (only_flagged && only_flagged[row] == 0) return;
     const int R = K + 1;
     const int b = row / R, j = row % R;
     int n = n_drafts[b];
@@ -411,8 +429,13 @@ template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSegThreads) seg_max_kernel(const void* __restrict__ logits, int K, int V,
                                                               int nseg, int vec_ok,
                                                               const int32_t* __restrict__ n_drafts,
-                                                              float* __restrict__ seg_max) {
+                                                              float* __restrict__ seg_max, void* __restrict__ hist) {
     const int seg = blockIdx.x, row = blockIdx.y;
+    // Top-p: segment 0 clears the row's coarse histogram for the weight launch.
+    if (hist && seg == 0) {
+        u64* h = (u64*)hist + (size_t)row * (sizeof(RowHist) / sizeof(u64));
+        for (int i = threadIdx.x; i < (int)(sizeof(RowHist) / sizeof(u64)); i += kSegThreads) h[i] = 0;
+    }
     const int R = K + 1;
     const int b = row / R, j = row % R;
     int n = n_drafts[b];
@@ -467,6 +490,253 @@ __global__ void __launch_bounds__(kSegThreads) seg_z_kernel(const void* __restri
     }
     z = seg_block_sum(z, red);
     if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
+}
+
+// ---- Segmented top-p: the nucleus boundary without whole-row passes per block ----
+//
+// The boundary is the last element, in (logit desc, index asc) order, whose mass before
+// it is below Tp = ceil(p*Z) (or zero). Coarse bins of 1/64 nat on (m - l)/T are ordered
+// the same way, so: (B') the weights of each segment also go into a per-row histogram of
+// coarse bins (integer sums: exact in any order); (C') a block per row finds the boundary
+// bin and the mass above it; (D') the elements of that bin are gathered (usually a few
+// hundred); (E') a block per row sorts them by (key desc, index asc) and walks the
+// weights to the cut. A bin with more than kCandCap elements flags its row for the exact
+// row kernel instead.
+
+// B': per (row, segment) weight sum and coarse histogram (the row's histogram and pick
+// were cleared by segment 0 of the max launch).
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __restrict__ logits, int K, int V,
+                                                                int nseg, int vec_ok, float inv_t,
+                                                                const int32_t* __restrict__ n_drafts,
+                                                                const float* __restrict__ seg_max,
+                                                                u64* __restrict__ seg_z, RowHist* __restrict__ hist) {
+    const int seg = blockIdx.x, row = blockIdx.y;
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    int n = n_drafts[b];
+    n = n < 0 ? 0 : (n > K ? K : n);
+    if (j > n) return;
+    __shared__ float s_m;
+    __shared__ u64 red[kSegThreads / 64];
+    __shared__ u64 h_mass[kBins];
+    __shared__ unsigned int h_cnt[kBins];
+    for (int i = threadIdx.x; i < kBins; i += kSegThreads) {
+        h_mass[i] = 0;
+        h_cnt[i] = 0;
+    }
+    if (threadIdx.x == 0) s_m = row_max_from_segs(seg_max, row, nseg);
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    float x[32];
+    int idx[32];
+    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
+    __syncthreads();
+    const float m = s_m;
+    u64 z = 0;
+    if (finite_f(m)) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            if (!finite_f(x[k])) continue;
+            const u64 w = gg_weight(x[k], m, inv_t);
+            z += w;
+            const int bn = gg_coarse_bin(x[k], m, inv_t);
+            atomicAdd(&h_mass[bn], w);
+            atomicAdd(&h_cnt[bn], 1u);
+        }
+    }
+    z = seg_block_sum(z, red);  // (its barriers also complete the LDS histogram)
+    if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
+    RowHist& h = hist[row];
+    for (int i = threadIdx.x; i < kBins; i += kSegThreads) {
+        if (h_cnt[i]) {
+            atomicAdd(&h.mass[i], h_mass[i]);
+            atomicAdd(&h.cnt[i], h_cnt[i]);
+        }
+    }
+}
+
+// C': per row, the boundary coarse bin and the mass above it.
+__global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, float top_p,
+                                                               const int32_t* __restrict__ n_drafts,
+                                                               const float* __restrict__ seg_max,
+                                                               const u64* __restrict__ seg_z,
+                                                               const RowHist* __restrict__ hist,
+                                                               RowPick* __restrict__ pick) {
+    const int row = blockIdx.x;
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    int n = n_drafts[b];
+    n = n < 0 ? 0 : (n > K ? K : n);
+    if (j > n) return;
+    __shared__ int s_bin;
+    __shared__ u64 s_c;
+    const float m = row_max_from_segs(seg_max, row, nseg);
+    u64 z = 0;
+    for (int s = 0; s < nseg; ++s) z += seg_z[(size_t)row * nseg + s];
+    if (!finite_f(m) || z == 0) {
+        if (threadIdx.x == 0) pick[row] = RowPick{-1, 0, 0, 0};
+        return;
+    }
+    const u64 tp = (u64)ceil((double)top_p * (double)z);
+    if (threadIdx.x == 0) s_bin = -1;
+    __syncthreads();
+    pick_bin(hist[row].mass, hist[row].cnt, kBins, false, 0, tp, &s_bin, &s_c);
+    __syncthreads();
+    if (threadIdx.x == 0) pick[row] = RowPick{s_bin, 0, s_c, tp};
+}
+
+// D': per (row, segment), gather the elements of the boundary bin.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __restrict__ logits, int K, int V,
+                                                                 int nseg, int vec_ok, float inv_t,
+                                                                 const int32_t* __restrict__ n_drafts,
+                                                                 const float* __restrict__ seg_max,
+                                                                 RowPick* __restrict__ pick,
+                                                                 uint2* __restrict__ cand) {
+    const int seg = blockIdx.x, row = blockIdx.y;
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    int n = n_drafts[b];
+    n = n < 0 ? 0 : (n > K ? K : n);
+    if (j > n) return;
+    const int cbin = pick[row].cbin;
+    if (cbin < 0) return;
+    __shared__ float s_m;
+    if (threadIdx.x == 0) s_m = row_max_from_segs(seg_max, row, nseg);
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    float x[32];
+    int idx[32];
+    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
+    __syncthreads();
+    const float m = s_m;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        if (idx[k] >= V || !finite_f(x[k]) || gg_coarse_bin(x[k], m, inv_t) != cbin) continue;
+        const int slot = atomicAdd(&pick[row].n_cand, 1);
+        if (slot < kCandCap) cand[(size_t)row * kCandCap + slot] = make_uint2(__float_as_uint(x[k]), (unsigned)idx[k]);
+    }
+}
+
+// E': per row, sort the boundary bin's elements by (key desc, index asc) and cut; fills
+// the row's statistics, or flags the row for the exact row kernel (too many elements).
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict__ logits, int K, int V,
+                                                          int nseg, float inv_t,
+                                                          const int32_t* __restrict__ drafts,
+                                                          const int32_t* __restrict__ n_drafts,
+                                                          const float* __restrict__ seg_max,
+                                                          const RowPick* __restrict__ pick,
+                                                          const uint2* __restrict__ cand,
+                                                          RowStats* __restrict__ stats, int* __restrict__ flag) {
+    const int row = blockIdx.x;
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    int n = n_drafts[b];
+    n = n < 0 ? 0 : (n > K ? K : n);
+    if (j > n) return;
+    __shared__ u64 s_key[kCandCap];    // order key << 32 | (~index): descending = the nucleus order
+    __shared__ u64 red[1024 / 64];
+    __shared__ int s_last;
+    const RowPick pk = pick[row];
+    const float m = row_max_from_segs(seg_max, row, nseg);
+    if (pk.cbin < 0) {  // no finite logit or Z == 0: no nucleus
+        if (threadIdx.x == 0) {
+            stats[row] = RowStats{m, 0x7fffffff, 0ull, 0u, 1, 0ull};
+            flag[row] = 0;
+        }
+        return;
+    }
+    const int nc = pk.n_cand;
+    if (nc > kCandCap) {
+        if (threadIdx.x == 0) flag[row] = 1;
+        return;
+    }
+    int np2 = 1;
+    while (np2 < nc) np2 <<= 1;
+    for (int i = threadIdx.x; i < np2; i += 1024) {
+        if (i < nc) {
+            const uint2 c = cand[(size_t)row * kCandCap + i];
+            s_key[i] = ((u64)gg_order_key(__uint_as_float(c.x)) << 32) | (u64)(~c.y);
+        } else {
+            s_key[i] = 0;  // sorts last
+        }
+    }
+    __syncthreads();
+    // Bitonic sort, descending.
+    for (int k = 2; k <= np2; k <<= 1) {
+        for (int jj = k >> 1; jj > 0; jj >>= 1) {
+            for (int i = threadIdx.x; i < np2; i += 1024) {
+                const int ix = i ^ jj;
+                if (ix > i) {
+                    const u64 a = s_key[i], c = s_key[ix];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? (a < c) : (a > c)) {
+                        s_key[i] = c;
+                        s_key[ix] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // Weights in that order (the logit is recovered from the order key). Thread t owns
+    // elements [4t, 4t+4): an exclusive block scan of the thread sums gives each
+    // element's mass before it; the kept elements are a prefix (that mass never drops),
+    // so the cut is the largest kept position.
+    const int e0 = 4 * (int)threadIdx.x;
+    u64 w[4];
+    u64 tsum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        w[k] = 0;
+        if (e0 + k < nc) {
+            const unsigned int key = (unsigned int)(s_key[e0 + k] >> 32);
+            const unsigned int bits = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+            w[k] = gg_weight(__uint_as_float(bits), m, inv_t);
+        }
+        tsum += w[k];
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    u64 incl = tsum;
+    for (int o = 1; o < 64; o <<= 1) {
+        const u64 t = shfl_up_u64(incl, o);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) red[wv] = incl;
+    __syncthreads();
+    u64 before = pk.c_above + incl - tsum;
+    for (int i = 0; i < wv; ++i) before += red[i];
+    int last = -1;
+    u64 zp = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (e0 + k < nc && (before < pk.tp || before == 0)) {
+            last = e0 + k;
+            zp = before + w[k];
+        }
+        before += w[k];
+    }
+    if (threadIdx.x == 0) s_last = -1;
+    __syncthreads();
+    if (last >= 0) atomicMax(&s_last, last);
+    __syncthreads();
+    if (last >= 0 && last == s_last) {  // the owner of the cut (position 0 always qualifies)
+        const unsigned int lam = (unsigned int)(s_key[last] >> 32);
+        // Ties at the boundary key kept for index <= idx_cut; every index when all are.
+        const bool all_ties = last + 1 >= nc || (unsigned int)(s_key[last + 1] >> 32) != lam;
+        const int idx_cut = all_ties ? 0x7fffffff : (int)(~(unsigned int)(s_key[last] & 0xffffffffu));
+        RowStats st{m, idx_cut, zp, lam, 1, 0ull};
+        if (j < n) {
+            const int x = drafts[(size_t)b * K + j];
+            if (x >= 0 && x < V) {
+                const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+                Nucleus nu{m, inv_t, lam, idx_cut};
+                st.wx = nu.weight(ld<DT>(lp, x), x);
+            }
+        }
+        stats[row] = st;
+        flag[row] = 0;
+    }
 }
 
 // Per-row statistics seen by the decision: max, nucleus mass and nucleus boundary.
@@ -712,10 +982,14 @@ struct RejWs {
     u64* seg_z;
     SeqDecision* dec;
     SegOut* seg_out;
+    RowHist* hist;   // top-p only: coarse histogram per row
+    RowPick* pick;
+    uint2* cand;     // boundary-bin elements per row (logit bits, index)
+    int* flag;       // 1: the row needs the exact row kernel
     size_t bytes;
 };
 
-static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab) {
+static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, bool topp) {
     const size_t rows = (size_t)num_seqs * (max_drafts + 1);
     const int nseg = rej_nseg(vocab);
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -732,12 +1006,22 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab) {
     off += al((size_t)num_seqs * sizeof(SeqDecision));
     w.seg_out = (SegOut*)(p + off);
     off += al((size_t)num_seqs * nseg * sizeof(SegOut));
+    if (topp) {
+        w.hist = (RowHist*)(p + off);
+        off += al(rows * sizeof(RowHist));
+        w.pick = (RowPick*)(p + off);
+        off += al(rows * sizeof(RowPick));
+        w.cand = (uint2*)(p + off);
+        off += al(rows * kCandCap * sizeof(uint2));
+        w.flag = (int*)(p + off);
+        off += al(rows * sizeof(int));
+    }
     w.bytes = off;
     return w;
 }
 
 size_t rejection_workspace_bytes(int num_seqs, int max_drafts, int vocab) {
-    size_t own = rej_layout(nullptr, num_seqs, max_drafts, vocab).bytes;
+    size_t own = rej_layout(nullptr, num_seqs, max_drafts, vocab, true).bytes;
     size_t g = greedy_workspace_bytes(num_seqs, max_drafts, vocab);
     return own > g ? own : g;
 }
@@ -749,19 +1033,27 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                     hipStream_t s) {
     const float inv_t = 1.0f / temperature;
     const int use_topp = (top_p > 0.f && top_p < 1.f) ? 1 : 0;
-    const RejWs w = rej_layout(ws, num_seqs, max_drafts, vocab);
+    const RejWs w = rej_layout(ws, num_seqs, max_drafts, vocab, use_topp != 0);
     const int rows = num_seqs * (max_drafts + 1);
     const int nseg = rej_nseg(vocab);
     const int K = max_drafts;
     const size_t eb = dtype_bytes(dt);
     const int vec_ok = ((vocab * eb) % 16 == 0) && (((uintptr_t)logits) % 16 == 0);
 #define GG_REJ(DTV)                                                                                        \
+    seg_max_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, n_drafts,  \
+                                                                 w.seg_max, use_topp ? w.hist : nullptr);  \
     if (use_topp) {                                                                                        \
+        seg_zhist_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(                                    \
+            logits, K, vocab, nseg, vec_ok, inv_t, n_drafts, w.seg_max, w.seg_z, w.hist);                  \
+        row_pick_kernel<<<rows, kSegThreads, 0, s>>>(K, nseg, top_p, n_drafts, w.seg_max, w.seg_z, w.hist, \
+                                                     w.pick);                                              \
+        seg_gather_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(                                   \
+            logits, K, vocab, nseg, vec_ok, inv_t, n_drafts, w.seg_max, w.pick, w.cand);                   \
+        row_select_kernel<DTV><<<rows, 1024, 0, s>>>(logits, K, vocab, nseg, inv_t, drafts, n_drafts,      \
+                                                     w.seg_max, w.pick, w.cand, w.stats, w.flag);          \
         rejection_row_stats_kernel<DTV><<<rows, kThreads, 0, s>>>(logits, K, vocab, drafts, n_drafts,      \
-                                                                  inv_t, top_p, use_topp, w.stats);        \
+                                                                  inv_t, top_p, use_topp, w.stats, w.flag); \
     } else {                                                                                               \
-        seg_max_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,       \
-                                                                     n_drafts, w.seg_max);                 \
         seg_z_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, inv_t,  \
                                                                    n_drafts, w.seg_max, w.seg_z);          \
     }                                                                                                      \

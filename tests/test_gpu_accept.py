@@ -125,6 +125,28 @@ def test_rejection_ties_in_nucleus(gpu):
         assert np.array_equal(tok.cpu().numpy(), et), top_p
 
 
+def test_rejection_crowded_boundary_bin(gpu):
+    """Rows whose boundary coarse bin holds tens of thousands of tied logits (the exact
+    row kernel resolves those) next to rows the bin sort resolves, in one call."""
+    say("rejection crowded boundary bin")
+    rng = np.random.default_rng(33)
+    B, K, V = 4, 2, 128256
+    host = rng.normal(0, 1.5, (B, K + 1, V)).astype(np.float32)
+    host[:2] = rng.integers(-1, 2, (2, K + 1, V)).astype(np.float32)
+    lg = torch.from_numpy(host).to(torch.bfloat16)
+    host = lg.float().numpy()
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    n = np.full(B, K, np.int32)
+    u = rng.random((B, K + 1)).astype(np.float32)
+    for top_p in (0.2, 0.6, 0.9):
+        acc, tok = gv.accept_rejection(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(),
+                                       torch.from_numpy(u).cuda(), 1.0, top_p)
+        torch.cuda.synchronize()
+        ea, et = ora.accept_rejection(host, drafts, n, u, 1.0, top_p)
+        assert np.array_equal(acc.cpu().numpy(), ea), top_p
+        assert np.array_equal(tok.cpu().numpy(), et), top_p
+
+
 def test_rejection_small_temperature_is_greedy(gpu):
     say("rejection T->0")
     lg, host, drafts, n = logits_case(5, 3, 3000, "f32", seed=5)
