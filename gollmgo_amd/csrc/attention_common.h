@@ -99,6 +99,15 @@ struct AttnPlan {
 
 // LPT schedule: most sequences the plan kernel ranks (one per thread).
 constexpr int kLptMaxSeqs = 1024;
+// LPT piece length: at most T = ceil(C * kLptPieceNum / (slots * kLptPieceDen)) chunks
+// for C chunks of work over `slots` resident workgroups.
+constexpr int kLptPieceNum = 1;
+constexpr int kLptPieceDen = 1;
+// Bound on the number of LPT pieces (= main-grid workgroups and partial records): the
+// cuts of every item at T chunks give at most C/T + items pieces.
+__host__ __device__ constexpr int lpt_records(int slots, int num_seqs, int num_kv_heads) {
+    return (slots * kLptPieceDen + kLptPieceNum - 1) / kLptPieceNum + num_seqs * num_kv_heads;
+}
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens);
 

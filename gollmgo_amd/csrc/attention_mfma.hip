@@ -224,28 +224,43 @@ struct PieceIO {
     static constexpr int kNS = Geom::kNS;
     static constexpr int kTok = Geom::kTok;
 
-    __device__ static __forceinline__ LaneBlocks chunk_blocks(const AttnArgs& a, const KVView& kv, int b, int t0,
-                                                              int nchunks, int ctx, int ch) {
+    // Block ids of chunk `ch` of the piece [t0, t_end), in two steps: fetch_blocks issues
+    // the kNS table reads together (wave-uniform scalar loads; indices are clamped to the
+    // row, so they wait for neither the piece bounds nor the context length), and
+    // lane_blocks, called as late as possible, applies the bounds and narrows the ids
+    // to the lane's two.
+    struct RawBlocks {
+        int q[kNS];
+        int t;  // first token of the chunk
+    };
+    __device__ static __forceinline__ RawBlocks fetch_blocks(const AttnArgs& a, int b, int t0, int ch) {
         const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
+        RawBlocks r;
+        r.t = t0 + ch * kTok;
+#pragma unroll
+        for (int qb = 0; qb < kNS; ++qb) r.q[qb] = bt[min((r.t >> 4) + qb, a.max_blocks - 1)];
+        return r;
+    }
+    __device__ static __forceinline__ LaneBlocks lane_blocks(const KVView& kv, const RawBlocks& r, int t_end) {
         int q[kNS];
 #pragma unroll
         for (int qb = 0; qb < kNS; ++qb) {
-            const int t = t0 + ch * kTok + 16 * qb;
-            int blk = (ch < nchunks && t < ctx) ? bt[t >> 4] : -1;
-            blk = __builtin_amdgcn_readfirstlane(blk);
-            q[qb] = (blk >= kv.num_blocks) ? -1 : blk;
+            const int blk = r.q[qb];
+            q[qb] = (r.t + 16 * qb < t_end && blk < kv.num_blocks) ? blk : -1;
         }
         const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4;
         const int ik = Geom::bq(c16 >> 2), iv = Geom::bq(g4);
-        LaneBlocks r;
-        if constexpr (kNS == 4) {
-            r.k = ik == 0 ? q[0] : ik == 1 ? q[1] : ik == 2 ? q[2] : q[3];
-            r.v = iv == 0 ? q[0] : iv == 1 ? q[1] : iv == 2 ? q[2] : q[3];
-        } else {
-            r.k = ik == 0 ? q[0] : q[1];
-            r.v = iv == 0 ? q[0] : q[1];
+        LaneBlocks l{q[0], q[0]};
+#pragma unroll
+        for (int qb = 1; qb < kNS; ++qb) {
+            l.k = ik == qb ? q[qb] : l.k;
+            l.v = iv == qb ? q[qb] : l.v;
         }
-        return r;
+        return l;
+    }
+    __device__ static __forceinline__ LaneBlocks chunk_blocks(const AttnArgs& a, const KVView& kv, int b, int t0,
+                                                              int t_end, int ch) {
+        return lane_blocks(kv, fetch_blocks(a, b, t0, ch), t_end);
     }
     // K rows: lane supplies M index c16 of every tile. Loads are unconditional (missing
     // blocks read block 0); such tokens are always masked in S.
@@ -285,11 +300,9 @@ struct PieceIO {
     // ids and K rows (start_k), then V columns (start_v).
     __device__ static __forceinline__ void start_k(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
                                                    PieceIn<DT>& in) {
-        const int ctx = seq_keys(a, d.b, kBS);
-        const int nchunks = (d.t_end - d.t0 + kTok - 1) / kTok;
         const int wave_u = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-        in.bl_cur = chunk_blocks(a, kv, d.b, d.t0, nchunks, ctx, wave_u);
-        in.bl_next = chunk_blocks(a, kv, d.b, d.t0, nchunks, ctx, wave_u + kWaves);
+        in.bl_cur = chunk_blocks(a, kv, d.b, d.t0, d.t_end, wave_u);
+        in.bl_next = chunk_blocks(a, kv, d.b, d.t0, d.t_end, wave_u + kWaves);
         load_k(kv, in.bl_cur, d.kvh, in.cur);
     }
     __device__ static __forceinline__ void start_v(const KVView& kv, const PieceDesc& d, PieceIn<DT>& in) {
@@ -447,7 +460,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     }
 
     using IO = PieceIO<DT>;
-    auto chunk_blocks = [&](int ch) { return IO::chunk_blocks(a, kv, b, t0, nchunks, ctx, ch); };
+
     Regs& cur = in.cur;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     // Block ids run two chunks ahead and are requested after the softmax: the LDS
@@ -519,6 +532,17 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         const float mult = DT == GG_DTYPE_INT8 ? sscale * kblk_scale : sscale;
         constexpr int kNP = 4 * kNS;  // P values per lane per row tile
         uint4 pop[NT][Geom::kNPV][kIsBf16 ? 2 : 1];
+        // One wave-uniform branch around all the masking, so that chunks with nothing to
+        // mask (most of them) skip it instead of running it as selects.
+        if (__builtin_expect(need_mask, 0)) {
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int s = 0; s < kNS; ++s)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        sacc[rt][s][i] = (!blk_missing && (tlane + 4 * s + i) <= row_pos[rt]) ? sacc[rt][s][i] : -INFINITY;
+        }
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
             // The multiplier is positive, so the scaled maximum is the maximum of the raw
@@ -530,8 +554,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             for (int s = 0; s < kNS; ++s) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = sacc[rt][s][i];
-                    if (need_mask) v = (!blk_missing && (tlane + 4 * s + i) <= row_pos[rt]) ? v : -INFINITY;
+                    const float v = sacc[rt][s][i];
                     sc[4 * s + i] = v;
                     cmax = fmaxf(cmax, v);
                 }
@@ -582,7 +605,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             }
         }
 
-        const LaneBlocks bl_after = chunk_blocks(ch + 2 * kWaves);
+        const typename IO::RawBlocks raw_after = IO::fetch_blocks(a, b, t0, ch + 2 * kWaves);
 
         // ---- O += P . V; each V dim tile decoded once for all row tiles ----
         if (nvalid_v < kBS) {
@@ -613,7 +636,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         // Next chunk's V columns.
         IO::load_v(kv, bl_next, kvh, cur);
         bl_cur = bl_next;
-        bl_next = bl_after;
+        bl_next = IO::lane_blocks(kv, raw_after, t_end);
     }
 
     // The next piece of this workgroup starts streaming now: block ids and K rows before
@@ -813,7 +836,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
 // Plan layout (ints, in the workspace after the records), R = record bound:
 //   [0]                       number of pieces
 //   [16 + 4p ..]              piece p: (sequence, kv head | pieces per kv head << 16,
-//                             first chunk, end chunk); sequence -1 past the last piece
+//                             first token, end token); sequence -1 past the last piece
 //   [16 + 4R + 2b ..]         sequence b: (first piece, pieces per kv head)
 // Pieces of sequence b are first + j*Hkv + kvh.
 __device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
@@ -840,8 +863,10 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     const int B = a.num_seqs;
     const int b = threadIdx.x;
     const int nch = b < B ? seq_chunks(a, b, tok) : 0;
+    const int ctx = b < B ? seq_keys(a, b, kBS) : 0;
     const long long C = block_sum_1024((long long)Hkv * nch, s_w);
-    const int T = (int)max((C + slots - 1) / slots, (long long)kStreamKMinChunks);
+    const long long den = (long long)slots * kLptPieceDen;
+    const int T = (int)max((C * kLptPieceNum + den - 1) / den, (long long)kStreamKMinChunks);
     const int np = nch ? (nch + T - 1) / T : 0;
     const int key = np ? (nch + np - 1) / np : 0;
     const int cnt = np * Hkv;
@@ -864,7 +889,8 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     int4* table = (int4*)lpt_table(plan);
     for (int j = 0; j < np; ++j) {
         const int c0 = (int)((long long)j * nch / np), c1 = (int)((long long)(j + 1) * nch / np);
-        for (int h = 0; h < Hkv; ++h) table[pos + j * Hkv + h] = make_int4(b, h | (np << 16), c0, c1);
+        const int t0 = c0 * tok, t1 = min(c1 * tok, ctx);
+        for (int h = 0; h < Hkv; ++h) table[pos + j * Hkv + h] = make_int4(b, h | (np << 16), t0, t1);
     }
     // Entries past the last piece tell their workgroups to exit.
     for (int q = (int)total + b; q < recs; q += B) table[q] = make_int4(-1, 0, 0, 0);
@@ -873,15 +899,13 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
 // Workgroup p computes piece p of the plan (exits past the last piece).
 template <gg_dtype_t DT, int NT>
 __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
-    constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
     const int p = blockIdx.x;
     // One load tells the workgroup everything about its piece.
     const int4 e = ((const int4*)lpt_table(a.plan))[p];
     const int b = e.x;
     if (b < 0) return;  // past the last piece
     const int kvh = e.y & 0xffff, np = e.y >> 16;
-    const int ctx = seq_keys(a, b, kBS);
-    const PieceDesc d{b, kvh, e.z * kTok, min(e.w * kTok, ctx), -1, np > 1 ? p : -1};
+    const PieceDesc d{b, kvh, e.z, e.w, -1, np > 1 ? p : -1};
     PieceIn<DT> in;
     PieceIO<DT>::start(a, kv, d, in);
     attn_piece<DT, NT>(a, kv, d, in, false, d);
@@ -928,7 +952,7 @@ __global__ void __launch_bounds__(128) attn_lpt_combine_kernel(AttnArgs a, int H
 template <gg_dtype_t DT>
 gg_status_t launch_dt(const AttnArgs& a, const KVView& kv, int nt, hipStream_t s) {
     if (a.sched == ATTN_SCHED_LPT) {
-        const int recs = a.sk_grid + a.num_seqs * kv.Hkv;  // bound on the number of pieces
+        const int recs = lpt_records(a.sk_grid, a.num_seqs, kv.Hkv);
         switch (nt) {
             case 1: attn_mfma_lpt_kernel<DT, 1><<<recs, 256, 0, s>>>(a, kv); break;
             case 2: attn_mfma_lpt_kernel<DT, 2><<<recs, 256, 0, s>>>(a, kv); break;
@@ -1044,7 +1068,7 @@ gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s)
     const dim3 cgrid(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4);
     if (a.sched == ATTN_SCHED_STREAMK) attn_streamk_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, a.sk_grid);
     if (a.sched == ATTN_SCHED_LPT)
-        attn_lpt_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, a.sk_grid + a.num_seqs * kv.Hkv);
+        attn_lpt_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, lpt_records(a.sk_grid, a.num_seqs, kv.Hkv));
     return GG_OK;
 }
 
@@ -1054,7 +1078,7 @@ gg_status_t launch_attn_plan(const AttnArgs& a, hipStream_t s) {
     const KV* kv = a.kv;
     const int tok = (kv->dtype == GG_DTYPE_FP8_E4M3 || kv->dtype == GG_DTYPE_INT8) ? 64 : 32;
     const int Hkv = kv->num_kv_heads;
-    attn_lpt_plan_kernel<<<1, 1024, 0, s>>>(a, Hkv, tok, a.sk_grid, a.sk_grid + a.num_seqs * Hkv);
+    attn_lpt_plan_kernel<<<1, 1024, 0, s>>>(a, Hkv, tok, a.sk_grid, lpt_records(a.sk_grid, a.num_seqs, Hkv));
     return check_hip(hipGetLastError(), "verify_attention plan launch");
 }
 
@@ -1067,7 +1091,8 @@ int attn_streamk_grid(const KV* kv, int rows, int num_q_heads) {
 
 size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, size_t* ml_elems,
                                     size_t* acc_elems) {
-    const size_t records = (size_t)attn_streamk_grid(kv, rows, num_q_heads) + (size_t)num_seqs * kv->num_kv_heads;
+    // Records for LPT pieces; stream-K needs at most grid + items, which is no more.
+    const size_t records = (size_t)lpt_records(attn_streamk_grid(kv, rows, num_q_heads), num_seqs, kv->num_kv_heads);
     const size_t rw = (size_t)(num_q_heads / kv->num_kv_heads) * rows;
     const size_t n_ml = records * rw * 2;
     const size_t n_acc = records * rw * kD;
