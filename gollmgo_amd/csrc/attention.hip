@@ -17,6 +17,8 @@
 //   - attn_generic_kernel (here): any head_dim <= 1024 / block size / pool dtype,
 //     one wave per (row, head, partition), scalar online softmax. Used for the
 //     shapes the MFMA tiling does not cover (e.g. fp32 pools, head_dim 64).
+#include <type_traits>
+
 #include "gg_common.h"
 #include "attention_common.h"
 
@@ -25,7 +27,34 @@ namespace {
 
 constexpr int kMaxDC = 16;  // head_dim <= 1024 -> up to 16 dims per lane
 
-template <int DC>
+// One pool element as f32 (raw, before its block / head scale), pool type fixed.
+template <gg_dtype_t DT>
+__device__ __forceinline__ float pool_elem(const uint8_t* base, size_t i) {
+    if constexpr (DT == GG_DTYPE_F32) return ((const float*)base)[i];
+    else if constexpr (DT == GG_DTYPE_F16) return f16_bits_to_f32(((const uint16_t*)base)[i]);
+    else if constexpr (DT == GG_DTYPE_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[i]);
+    else if constexpr (DT == GG_DTYPE_FP8_E4M3) return fp8e4m3_to_f32(base[i]);
+    else return (float)((const int8_t*)base)[i];
+}
+
+// The pool elements in 16 bytes, as f32.
+template <gg_dtype_t DT>
+struct Pool16 {
+    static constexpr int kN = DT == GG_DTYPE_F32 ? 4 : (DT == GG_DTYPE_F16 || DT == GG_DTYPE_BF16) ? 8 : 16;
+    __device__ static __forceinline__ void decode(const uint4 r, float (&f)[kN]) {
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int k = 0; k < kN; ++k) {
+            if constexpr (DT == GG_DTYPE_F32) f[k] = __uint_as_float(w[k]);
+            else if constexpr (DT == GG_DTYPE_F16) f[k] = f16_bits_to_f32((uint16_t)(w[k >> 1] >> (16 * (k & 1))));
+            else if constexpr (DT == GG_DTYPE_BF16) f[k] = bf16_bits_to_f32((uint16_t)(w[k >> 1] >> (16 * (k & 1))));
+            else if constexpr (DT == GG_DTYPE_FP8_E4M3) f[k] = fp8e4m3_to_f32((uint8_t)(w[k >> 2] >> (8 * (k & 3))));
+            else f[k] = (float)(int8_t)(uint8_t)(w[k >> 2] >> (8 * (k & 3)));
+        }
+    }
+};
+
+template <gg_dtype_t DT, int DC>
 __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a, KVView kv) {
     const int part = blockIdx.x;
     const int h = blockIdx.y;
@@ -46,40 +75,82 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a, KVView kv)
     const int lane = threadIdx.x;
     const int D = kv.D;
 
-    float q[DC], acc[DC];
+    // A tile of 64 keys per step: lane i scores key t0 + 64k + i against the whole query
+    // (read from LDS), one wave max / sum per tile, then P.V with each lane owning dims
+    // lane + 64c and the tile's probabilities broadcast from their lanes.
+    __shared__ float s_q[64 * kMaxDC];
+    __shared__ float s_p[64];        // the tile's probabilities (times the V scale)
+    __shared__ size_t s_vrow[64];    // element offset of each key's V column 0
+    float acc[DC];
     const size_t qbase = ((size_t)z * a.num_q_heads + h) * D;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
         const int d = lane + 64 * c;
-        q[c] = d < D ? load_as_f32(a.q, a.q_dtype, qbase + d) : 0.f;
+        if (d < D) s_q[d] = load_as_f32(a.q, a.q_dtype, qbase + d);
         acc[c] = 0.f;
     }
+    __syncthreads();
     const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
     float m = -1e30f, l = 0.f;
-    for (int t = t0; t < t1; ++t) {
-        const int blk = bt[t / kv.bs];
-        const int off = t % kv.bs;
-        if (blk < 0 || blk >= kv.num_blocks) continue;  // invalid table entry: key skipped
-        float dot = 0.f;
-#pragma unroll
-        for (int c = 0; c < DC; ++c) {
-            const int d = lane + 64 * c;
-            if (d < D) dot += q[c] * kv.k_at(blk, kvh, off, d);
+    for (int tb = t0; tb < t1; tb += 64) {
+        const int t = tb + lane;
+        int blk = -1, off = 0;
+        if (t < t1) {
+            blk = bt[t / kv.bs];
+            off = t % kv.bs;
+            if (blk < 0 || blk >= kv.num_blocks) blk = -1;  // invalid table entry: key skipped
         }
-        for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
-        const float s = dot * a.scale * kv.k_scale(blk, kvh);
-        const float m_new = fmaxf(m, s);
+        float sc = -INFINITY;
+        if (blk >= 0) {
+            // The lane's key row is contiguous: 16-byte loads when rows are whole
+            // multiples of 16 bytes (pools are 256-byte aligned), else element loads.
+            const uint8_t* krow = kv.kc + (((size_t)blk * kv.Hkv + kvh) * kv.bs + off) * (size_t)D * dtype_bytes(DT);
+            float dot = 0.f;
+            constexpr int kN = Pool16<DT>::kN;
+            if (D % kN == 0) {
+#pragma unroll 4
+                for (int v = 0; v < D / kN; ++v) {
+                    float f[kN];
+                    Pool16<DT>::decode(((const uint4*)krow)[v], f);
+#pragma unroll
+                    for (int e = 0; e < kN; ++e) dot += s_q[v * kN + e] * f[e];
+                }
+            } else {
+#pragma unroll 16
+                for (int d = 0; d < D; ++d) dot += s_q[d] * pool_elem<DT>(krow, d);
+            }
+            sc = dot * a.scale * kv.k_scale(blk, kvh);
+        }
+        float mt = sc;
+        for (int o = 32; o > 0; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o));
+        const float m_new = fmaxf(m, mt);
         const float alpha = __expf(m - m_new);
-        const float p = __expf(s - m_new);
-        l = l * alpha + p;
-        const float pv = p * kv.v_scale(blk, kvh);
-#pragma unroll
-        for (int c = 0; c < DC; ++c) {
-            const int d = lane + 64 * c;
-            const float vv = d < D ? kv.v_at(blk, kvh, off, d) : 0.f;
-            acc[c] = acc[c] * alpha + pv * vv;
-        }
+        const float p = blk >= 0 ? __expf(sc - m_new) : 0.f;
+        float ps = p;
+        for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+        l = l * alpha + ps;
         m = m_new;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) acc[c] *= alpha;
+        // The tile's probabilities and V offsets go through LDS, so the key loop below
+        // has no cross-lane operations and unrolls into batches of independent loads.
+        // (Masked and skipped keys have p = 0 and read block 0.)
+        __syncthreads();  // the previous tile's readers are done
+        s_p[lane] = blk >= 0 ? p * kv.v_scale(blk, kvh) : 0.f;
+        s_vrow[lane] = ((size_t)max(blk, 0) * kv.Hkv + kvh) * (size_t)D * kv.bs + off;
+        __syncthreads();
+        const int ntile = min(64, t1 - tb);
+        const uint8_t* vc = kv.vc;
+#pragma unroll 16
+        for (int i = 0; i < ntile; ++i) {
+            const float pi = s_p[i];
+            const size_t vr = s_vrow[i];
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const int d = lane + 64 * c;
+                if (d < D) acc[c] += pi * pool_elem<DT>(vc, vr + (size_t)d * kv.bs);
+            }
+        }
     }
     if (nparts == 1) {
         const float inv = l > 0.f ? 1.0f / l : 0.f;
@@ -152,7 +223,18 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a, int D) {
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens) {
     if (partition_tokens > 0) return {ATTN_SCHED_GRID, partition_tokens};
-    if (!attn_mfma_supported(kv, rows, num_q_heads)) return {ATTN_SCHED_GRID, 512};
+    if (!attn_mfma_supported(kv, rows, num_q_heads)) {
+        // One wave per (row, head, partition): partitions of 64..512 keys, as many as
+        // it takes to reach about 2048 waves (the kernel's time is the longest wave's
+        // chain of 64-key tiles; the merge costs one small launch).
+        const long long waves = (long long)num_seqs * rows * num_q_heads;
+        const long long want = waves > 0 ? (2048 + waves - 1) / waves : 1;
+        const long long keys = (long long)max_blocks * kv->block_size;
+        long long part = (keys + want - 1) / want;
+        part = (part + 63) / 64 * 64;
+        part = part < 64 ? 64 : (part > 512 ? 512 : part);
+        return {ATTN_SCHED_GRID, (int)part};
+    }
     // Measured on MI355X: while the (sequence, kv head) items alone fill every resident
     // workgroup slot, longest-first pieces (LPT: items longer than the mean slot load cut
     // in equal pieces, dispatched longest first) balance ragged contexts best; beyond the
@@ -189,16 +271,29 @@ gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s) {
         if (st != GG_OK) return st;
         if (a.sched != ATTN_SCHED_GRID) return check_hip(hipGetLastError(), "verify_attention launch");
     } else {
-        const int DC = (kv->head_dim + 63) / 64;
+        // Dims per lane rounded up to 1, 2, 4, 8 or 16 (the excess lanes idle).
+        const int dc = (kv->head_dim + 63) / 64;
+        const int DC = dc <= 1 ? 1 : dc <= 2 ? 2 : dc <= 4 ? 4 : dc <= 8 ? 8 : 16;
+        if (dc > kMaxDC) return fail(GG_ERR_INVALID, "attention: head_dim too large");
         dim3 grid(a.max_parts, a.num_q_heads, a.num_seqs * a.rows);
-#define GG_GEN(N) \
-    case N: attn_generic_kernel<N><<<grid, 64, 0, s>>>(a, view); break;
-        switch (DC) {
-            GG_GEN(1) GG_GEN(2) GG_GEN(3) GG_GEN(4) GG_GEN(5) GG_GEN(6) GG_GEN(7) GG_GEN(8)
-            GG_GEN(9) GG_GEN(10) GG_GEN(11) GG_GEN(12) GG_GEN(13) GG_GEN(14) GG_GEN(15) GG_GEN(16)
-            default: return fail(GG_ERR_INVALID, "attention: head_dim too large");
+        auto launch = [&](auto dt_tag) {
+            constexpr gg_dtype_t DT = decltype(dt_tag)::value;
+            switch (DC) {
+                case 1: attn_generic_kernel<DT, 1><<<grid, 64, 0, s>>>(a, view); break;
+                case 2: attn_generic_kernel<DT, 2><<<grid, 64, 0, s>>>(a, view); break;
+                case 4: attn_generic_kernel<DT, 4><<<grid, 64, 0, s>>>(a, view); break;
+                case 8: attn_generic_kernel<DT, 8><<<grid, 64, 0, s>>>(a, view); break;
+                default: attn_generic_kernel<DT, 16><<<grid, 64, 0, s>>>(a, view); break;
+            }
+        };
+        switch (kv->dtype) {
+            case GG_DTYPE_F32: launch(std::integral_constant<gg_dtype_t, GG_DTYPE_F32>{}); break;
+            case GG_DTYPE_F16: launch(std::integral_constant<gg_dtype_t, GG_DTYPE_F16>{}); break;
+            case GG_DTYPE_BF16: launch(std::integral_constant<gg_dtype_t, GG_DTYPE_BF16>{}); break;
+            case GG_DTYPE_FP8_E4M3: launch(std::integral_constant<gg_dtype_t, GG_DTYPE_FP8_E4M3>{}); break;
+            case GG_DTYPE_INT8: launch(std::integral_constant<gg_dtype_t, GG_DTYPE_INT8>{}); break;
+            default: return fail(GG_ERR_INVALID, "attention: pool dtype");
         }
-#undef GG_GEN
     }
     if (a.max_parts > 1) {
         attn_combine_kernel<<<dim3(a.num_q_heads, a.num_seqs * a.rows), 128, 0, s>>>(a, kv->head_dim);
