@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU baseline sample")
     ap.add_argument("--partition", type=int, default=-1, help="override split-K partition tokens")
     ap.add_argument("--layers", type=int, default=0, help="override layer count (0 = config)")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="append the draft KV with gg_kv_append instead of inside the attention call")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches for `value` instead of replays of the captured step graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -159,6 +161,9 @@ def main():
     # The attention schedule depends only on the context lengths, shared by all layers of
     # a step: computed once per step (gg_verify_attention_plan), used by every layer.
     use_plan = cfg.partition == 0
+    # The draft rows' KV append rides in the attention call (gg_verify_append_attention_planned)
+    # where the pool allows it (not PER_BLOCK INT8, whose block scales need gg_kv_append).
+    fused = use_plan and cfg.kv_dtype != "int8" and not args.separate_append
 
     def step(record: bool):
         if hist is not None:
@@ -181,11 +186,15 @@ def main():
             if record:
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
                 e0.record()
-            kv.append(layer, k_new[layer], v_new[layer], append_slots)
+            if not fused:
+                kv.append(layer, k_new[layer], v_new[layer], append_slots)
             if record:
                 e1.record()
-            kv.attention(layer, q[layer], out, keys, bt, scale, partition_tokens=cfg.partition, workspace=ws_attn,
-                         planned=use_plan)
+            if fused:
+                kv.append_attention(layer, k_new[layer], v_new[layer], q[layer], out, keys, bt, scale, ws_attn)
+            else:
+                kv.attention(layer, q[layer], out, keys, bt, scale, partition_tokens=cfg.partition,
+                             workspace=ws_attn, planned=use_plan)
             if record:
                 e2.record()
                 ev["append"].append((e0, e1))
@@ -270,6 +279,8 @@ def main():
     blocks_used = int(((keys_np + bs - 1) // bs).sum())
     scale_bytes = H * 4 * 2 if cfg.kv_dtype == "fp8" else (blocks_used * H * 2 * 2 if cfg.kv_dtype == "int8" else 0)
     attn_bytes = kv_bytes + q_bytes + o_bytes + scale_bytes + blocks_used * 4
+    if fused:  # the draft rows' K/V read (bf16) and written to the pool by the same call
+        attn_bytes += B * R * H * D * 2 * (k_new.element_size() + eb)
     achieved = attn_bytes / (t_attn * 1e-6) / 1e9
     # One gg_verify_attention call: a single-piece plan (no workspace) is one launch of the
     # MFMA kernel; otherwise stream-K (or an explicit partition grid) plus its merge.
@@ -279,6 +290,9 @@ def main():
         attn_kernels = "attn_mfma_kernel (one workgroup per sequence x kv head)"
     elif cfg.partition:
         attn_kernels = "attn_mfma_kernel + attn_combine_kernel (partition grid)"
+    elif fused:
+        attn_kernels = ("gg_verify_append_attention_planned: draft-KV append in the final piece of each item + "
+                        "the library's automatic schedule (LPT pieces or stream-K) + merge")
     else:
         attn_kernels = "gg_verify_attention_planned: the library's automatic schedule (LPT pieces or stream-K) + merge"
     traffic, traffic_src = pmc_traffic(args.config)
@@ -306,6 +320,7 @@ def main():
             "layers": L, "vocab": V, "accept": cfg.accept, "temperature": cfg.temperature, "top_p": cfg.top_p,
             "draft_probs": cfg.draft_probs, "partition_tokens": cfg.partition or "auto",
             "shared_prefix_frac": cfg.shared_prefix_frac,
+            "draft_kv_append": "inside the attention call" if fused else "gg_kv_append",
         },
         "kernels_us": {"append_avg": round(t_app, 2), "attention_avg": round(t_attn, 2),
                        "attention_median": round(t_attn_med, 2), "accept_avg": round(t_acc, 2),

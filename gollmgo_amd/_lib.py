@@ -68,6 +68,8 @@ SIGNATURES = {
     "gg_verify_attention_plan": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "gg_verify_attention_planned": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _f,
                                          _vp, _sz, _vp]),
+    "gg_verify_append_attention_planned": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i,
+                                                _i, _i, _i, _f, _vp, _sz, _vp]),
     "gg_accept_greedy_workspace_size": (_sz, [_i, _i, _i]),
     "gg_accept_greedy": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gg_accept_rejection_workspace_size": (_sz, [_i, _i, _i]),

@@ -218,7 +218,25 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a, int D) {
     }
 }
 
+// Standalone draft-KV append from the block tables: workgroup (item) = (b, kvh).
+__global__ void __launch_bounds__(256) append_from_tables_kernel(AttnArgs a, KVView kv) {
+    append_item_rows(a, kv, blockIdx.x / kv.Hkv, blockIdx.x % kv.Hkv);
+}
+
 }  // namespace
+
+gg_status_t launch_append_from_tables(const AttnArgs& a, const KVView& kv, hipStream_t s) {
+    append_from_tables_kernel<<<a.num_seqs * kv.Hkv, 256, 0, s>>>(a, kv);
+    return check_hip(hipGetLastError(), "append launch");
+}
+
+bool attn_can_fuse_append(const AttnArgs& a) {
+    const KV* kv = a.kv;
+    if (!attn_mfma_supported(kv, a.rows, a.num_q_heads)) return false;
+    if (a.sched == ATTN_SCHED_LPT) return true;
+    return a.sched == ATTN_SCHED_GRID && a.partition % 64 == 0 && a.partition <= kMfmaMaxPartition &&
+           (long long)a.partition >= (long long)a.max_blocks * kv->block_size;
+}
 
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens) {
@@ -264,6 +282,10 @@ size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_head
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s) {
     const KV* kv = a.kv;
     KVView view = make_kv_view(kv, a.layer);
+    if (a.k_new && !a.fuse_append) {
+        const gg_status_t st = launch_append_from_tables(a, view, s);
+        if (st != GG_OK) return st;
+    }
     if (a.sched != ATTN_SCHED_GRID || (attn_mfma_supported(kv, a.rows, a.num_q_heads) && a.partition % 64 == 0 &&
                                        a.partition <= kMfmaMaxPartition)) {
         // Stream-K and LPT launch their own merge over their record layout.

@@ -112,5 +112,75 @@ AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int ma
                    int partition_tokens);
 
 gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s);
+gg_status_t launch_append_from_tables(const AttnArgs& a, const KVView& kv, hipStream_t s);
+
+#ifdef __HIPCC__
+// The draft-KV rows of item (b, kvh): row b*rows + j, j < the sequence's row count, goes to
+// key position ctx - row_count + j, ctx as the attention clamps it to the table row (slot
+// from the block table; entries outside the pool are skipped). Same conversions as gg_kv_append: rounding to the pool type, FP8 as
+// E4M3-satfinite of x * (1 / per-head scale). Not for PER_BLOCK INT8 pools; head_dim a
+// multiple of 8 and 16-byte aligned rows (checked by the entry point). Run by a whole
+// workgroup; the caller orders it before any read of those rows.
+__device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView& kv, int b, int kvh) {
+    const int ctx = seq_keys(a, b, kv.bs);
+    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    if (ctx <= 0 || nrows <= 0 || nrows > ctx) return;
+    const int D = kv.D, bs = kv.bs;
+    const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
+    uint8_t* kc = const_cast<uint8_t*>(kv.kc);
+    uint8_t* vc = const_cast<uint8_t*>(kv.vc);
+    const float kinv = kv.dt == GG_DTYPE_FP8_E4M3 ? kv.k_head_scale[kv.Hkv + kvh] : 1.f;
+    const float vinv = kv.dt == GG_DTYPE_FP8_E4M3 ? kv.v_head_scale[kv.Hkv + kvh] : 1.f;
+    // Eight consecutive dims per thread (one row's K run is contiguous, its V run strided).
+    const int groups = D / 8;
+    const int esz = (int)dtype_bytes(a.new_dtype);
+    for (int i = threadIdx.x; i < nrows * groups; i += blockDim.x) {
+        const int j = i / groups, d0 = (i % groups) * 8;
+        const int pos = ctx - nrows + j;
+        const int blk = bt[pos / bs];
+        if (blk < 0 || blk >= kv.num_blocks) continue;
+        const int off = pos % bs;
+        const size_t src = (((size_t)b * a.rows + j) * kv.Hkv + kvh) * D + d0;
+        float kx[8], vx[8];
+        if (esz == 4) {
+            const float4* kp = (const float4*)((const float*)a.k_new + src);
+            const float4* vp = (const float4*)((const float*)a.v_new + src);
+            const float4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+            kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w; kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
+            vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w; vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
+        } else {
+            const uint4 kw = *(const uint4*)((const uint16_t*)a.k_new + src);
+            const uint4 vw = *(const uint4*)((const uint16_t*)a.v_new + src);
+            const uint32_t ku[4] = {kw.x, kw.y, kw.z, kw.w}, vu[4] = {vw.x, vw.y, vw.z, vw.w};
+            const bool bf = a.new_dtype == GG_DTYPE_BF16;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t kh = (uint16_t)(ku[e >> 1] >> (16 * (e & 1)));
+                const uint16_t vh = (uint16_t)(vu[e >> 1] >> (16 * (e & 1)));
+                kx[e] = bf ? bf16_bits_to_f32(kh) : f16_bits_to_f32(kh);
+                vx[e] = bf ? bf16_bits_to_f32(vh) : f16_bits_to_f32(vh);
+            }
+        }
+        const size_t ki = (((size_t)blk * kv.Hkv + kvh) * bs + off) * D + d0;
+        const size_t vi = (((size_t)blk * kv.Hkv + kvh) * D + d0) * bs + off;
+        if (kv.dt == GG_DTYPE_FP8_E4M3) {
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t q = f32_to_fp8e4m3_sat(kx[e] * kinv);
+                if (e < 4) w0 |= q << (8 * e); else w1 |= q << (8 * (e - 4));
+                vc[vi + (size_t)e * bs] = f32_to_fp8e4m3_sat(vx[e] * vinv);
+            }
+            *(uint2*)(kc + ki) = make_uint2(w0, w1);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                store_from_f32(kc, kv.dt, ki + e, kx[e]);
+                store_from_f32(vc, kv.dt, vi + (size_t)e * bs, vx[e]);
+            }
+        }
+    }
+}
+#endif
 
 }  // namespace gg

@@ -235,7 +235,9 @@ static gg_status_t verify_attention_impl(gg_kv_t kv, int layer, const void* q, g
                                          gg_dtype_t out_dtype, const int32_t* ctx_lens, const int32_t* row_counts,
                                          const int32_t* block_tables, int max_blocks_per_seq, int num_seqs,
                                          int rows_per_seq, int num_q_heads, float scale, int partition_tokens,
-                                         void* workspace, size_t workspace_bytes, void* stream, AttnCall call) {
+                                         void* workspace, size_t workspace_bytes, void* stream, AttnCall call,
+                                         const void* k_new = nullptr, const void* v_new = nullptr,
+                                         gg_dtype_t new_dtype = GG_DTYPE_BF16) {
     clear_error();
     const bool compute = call != ATTN_CALL_PLAN_ONLY;
     GG_CHECK_ARG(kv != nullptr, "gg_verify_attention: kv is NULL");
@@ -285,6 +287,12 @@ static gg_status_t verify_attention_impl(gg_kv_t kv, int layer, const void* q, g
         if (a.sched != ATTN_SCHED_GRID) a.plan = (int*)(a.ws_acc + n_acc);
     }
     a.plan_ready = call == ATTN_CALL_PLANNED ? 1 : 0;
+    if (k_new) {
+        a.k_new = k_new;
+        a.v_new = v_new;
+        a.new_dtype = new_dtype;
+        a.fuse_append = attn_can_fuse_append(a) ? 1 : 0;
+    }
     if (call == ATTN_CALL_PLAN_ONLY) return launch_attn_plan(a, (hipStream_t)stream);
     return launch_verify_attention(a, (hipStream_t)stream);
 }
@@ -318,6 +326,26 @@ GG_API gg_status_t gg_verify_attention_planned(gg_kv_t kv, int layer, const void
     return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,
                                  max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, scale, 0, workspace,
                                  workspace_bytes, stream, ATTN_CALL_PLANNED);
+}
+
+GG_API gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, const void* k_new,
+                                                      const void* v_new, gg_dtype_t new_dtype, const void* q,
+                                                      gg_dtype_t q_dtype, void* out, gg_dtype_t out_dtype,
+                                                      const int32_t* ctx_lens, const int32_t* row_counts,
+                                                      const int32_t* block_tables, int max_blocks_per_seq,
+                                                      int num_seqs, int rows_per_seq, int num_q_heads, float scale,
+                                                      void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    GG_CHECK_ARG(kv != nullptr, "gg_verify_append_attention_planned: kv is NULL");
+    GG_CHECK_ARG(k_new && v_new, "gg_verify_append_attention_planned: NULL buffer");
+    GG_CHECK_ARG(is_float_io(new_dtype), "gg_verify_append_attention_planned: k/v dtype must be F32/F16/BF16");
+    GG_CHECK_ARG(kv->scale_mode != GG_SCALE_PER_BLOCK,
+                 "gg_verify_append_attention_planned: PER_BLOCK INT8 pools append with gg_kv_append");
+    GG_CHECK_ARG(kv->head_dim % 8 == 0 && (uintptr_t)k_new % 16 == 0 && (uintptr_t)v_new % 16 == 0,
+                 "gg_verify_append_attention_planned: needs head_dim % 8 == 0 and 16-byte aligned k_new/v_new");
+    return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,
+                                 max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, scale, 0, workspace,
+                                 workspace_bytes, stream, ATTN_CALL_PLANNED, k_new, v_new, new_dtype);
 }
 
 // ---------------------------------------------------------------- acceptance

@@ -164,6 +164,32 @@ class KVCache:
             _stream(stream)), "gg_verify_attention")
         return out
 
+    def append_attention(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, q: torch.Tensor,
+                         out: torch.Tensor, ctx_lens: torch.Tensor, block_tables: torch.Tensor, scale: float,
+                         workspace: torch.Tensor, row_counts: Optional[torch.Tensor] = None,
+                         stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """Draft-KV append of the verify rows and planned attention in one call
+        (gg_verify_append_attention_planned). k_new, v_new: [num_seqs * rows_per_seq,
+        Hkv, head_dim]; row b*R + j goes to key position ctx_lens[b] - row_count + j.
+        `workspace` must hold the step's plan (attention_plan)."""
+        if q.dim() != 4 or q.shape[-1] != self.head_dim or out.shape != q.shape:
+            raise ValueError("q/out must be [num_seqs, rows_per_seq, num_q_heads, head_dim]")
+        B, R, Hq, _ = q.shape
+        if k_new.shape != (B * R, self.num_kv_heads, self.head_dim) or v_new.shape != k_new.shape:
+            raise ValueError("k_new/v_new must be [num_seqs * rows_per_seq, num_kv_heads, head_dim]")
+        if block_tables.dim() != 2 or block_tables.shape[0] != B:
+            raise ValueError("block_tables must be [num_seqs, max_blocks_per_seq]")
+        if k_new.dtype != v_new.dtype:
+            raise ValueError("k_new and v_new must share a dtype")
+        rc = _dev(row_counts, "row_counts", torch.int32) if row_counts is not None else None
+        check(lib().gg_verify_append_attention_planned(
+            self.handle, layer, _dev(k_new, "k_new"), _dev(v_new, "v_new"), int(dtype_of(k_new)),
+            _dev(q, "q"), int(dtype_of(q)), _dev(out, "out"), int(dtype_of(out)),
+            _dev(ctx_lens, "ctx_lens", torch.int32), rc, _dev(block_tables, "block_tables", torch.int32),
+            block_tables.shape[1], B, R, Hq, float(scale), workspace.data_ptr(), workspace.numel(),
+            _stream(stream)), "gg_verify_append_attention_planned")
+        return out
+
     def attention_plan(self, ctx_lens: torch.Tensor, rows_per_seq: int, num_q_heads: int,
                        max_blocks_per_seq: int, workspace: torch.Tensor, row_counts: Optional[torch.Tensor] = None,
                        stream: Optional[torch.cuda.Stream] = None) -> None:

@@ -179,6 +179,29 @@ gg_status_t gg_verify_attention_planned(gg_kv_t kv, int layer, const void* q, gg
                                         int num_q_heads, float scale, void* workspace,
                                         size_t workspace_bytes, void* stream);
 
+/* Draft-KV append and planned attention of one layer in one call. Replaces the
+ * per-layer pair paged_kv_write + paged attention of run_layer
+ * (kernels/gollmgo_model.cu:610-625 then :651-687) for the verify rows.
+ *   k_new, v_new : device [num_seqs * rows_per_seq][Hkv][head_dim] of F32/F16/BF16; row
+ *                  b*rows_per_seq + j (j < the sequence's row count) is written to key
+ *                  position ctx_lens[b] - row_count + j through the block table (the slot
+ *                  gg_kv_append would be given, block*bs + offset), with gg_kv_append's
+ *                  conversions, before the attention reads it. Rows past the row count
+ *                  are ignored.
+ * Then as gg_verify_attention_planned. The result (pool contents and out) equals
+ * gg_kv_append with those slots followed by gg_verify_attention_planned. When the
+ * schedule gives every (sequence, kv head) one final piece (LPT or one piece per
+ * item), that piece's workgroup writes the rows itself (no extra launch); otherwise a
+ * launch of its own precedes the attention. PER_BLOCK INT8 pools are rejected
+ * (GG_ERR_INVALID): their scale update needs gg_kv_append. */
+gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, const void* k_new, const void* v_new,
+                                               gg_dtype_t new_dtype, const void* q, gg_dtype_t q_dtype,
+                                               void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                               const int32_t* row_counts, const int32_t* block_tables,
+                                               int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                               int num_q_heads, float scale, void* workspace,
+                                               size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Greedy acceptance.
  * Replaces Verify + argmax (internal/engine/speculative.go:68-84,

@@ -15,11 +15,12 @@ from helpers import say
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("cid,kv_dt", [(3, DType.FP8_E4M3), (5, DType.BF16)])
-def test_step_graph_replays_match_eager(gpu, cid, kv_dt):
+@pytest.mark.parametrize("cid,kv_dt,fused", [(3, DType.FP8_E4M3, True), (5, DType.BF16, False),
+                                             (5, DType.BF16, True)])
+def test_step_graph_replays_match_eager(gpu, cid, kv_dt, fused):
     cfg = scaled(CONFIGS[cid], num_seqs=24, layers=2, ctx=("uniform", 64, 700), vocab=5000,
                  history_len=512, repeat_rate=0.4, partition=0)
-    say(f"graph step config {cid}: B={cfg.num_seqs} L={cfg.layers}")
+    say(f"graph step config {cid}: B={cfg.num_seqs} L={cfg.layers} fused append={fused}")
     lay = build_layout(cfg)
     B, R, K, Hq, H, D, V, L = (cfg.num_seqs, cfg.rows, cfg.max_drafts, cfg.num_q_heads, cfg.num_kv_heads,
                                cfg.head_dim, cfg.vocab, cfg.layers)
@@ -59,6 +60,10 @@ def test_step_graph_replays_match_eager(gpu, cid, kv_dt):
             gv.ngram_draft(hist, hist_len, cfg.ngram_n, K, out=dr)
             kv.attention_plan(keys, R, Hq, bt.shape[1], ws_attn)
             for layer in range(L):
+                if fused:
+                    kv.append_attention(layer, k_new[layer], v_new[layer], q[layer], out[layer], keys, bt,
+                                        1.0 / math.sqrt(D), ws_attn)
+                    continue
                 kv.append(layer, k_new[layer], v_new[layer], slots)
                 kv.attention(layer, q[layer], out[layer], keys, bt, 1.0 / math.sqrt(D), workspace=ws_attn,
                              planned=True)

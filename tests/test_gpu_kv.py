@@ -405,3 +405,84 @@ def test_attention_full_size_configs(gpu, cid, explicit):
     print(f"  config {cid}: oracle rel err {err:.2e}")
     assert err <= TOL[cfg.kv_dtype]
     kv.close()
+
+
+# ------------------------------------------------------------------ fused append + attention
+
+def _derived_slots(lay, rows, bs, row_counts=None):
+    """Slots of the verify rows from the block tables (row b*R + j -> key position
+    keys[b] - row_count + j); -1 for rows past the row count."""
+    B = len(lay.keys)
+    slots = np.full(B * rows, -1, np.int32)
+    for b in range(B):
+        n = rows if row_counts is None else int(row_counts[b])
+        for j in range(n):
+            pos = int(lay.keys[b]) - n + j
+            slots[b * rows + j] = int(lay.block_tables[b, pos // bs]) * bs + pos % bs
+    return slots
+
+
+@pytest.mark.parametrize("cid,dt,B,ctx,rc", [
+    (3, "fp8", 64, ("uniform", 1024, 4096), False),   # LPT: final pieces append in-kernel
+    (5, "bf16", 64, ("uniform", 300, 2100), True),    # LPT, ragged row counts
+    (2, "f16", 6, ("uniform", 512, 3000), False),     # stream-K: append launch, then attention
+    (1, "f32", 4, ("list", 64, 128, 192, 256), True),  # generic path
+])
+def test_append_attention_fused_equals_separate(gpu, cid, dt, B, ctx, rc):
+    """gg_verify_append_attention_planned == gg_kv_append (slots from the block tables)
+    followed by gg_verify_attention_planned: pool bytes and outputs bit for bit."""
+    say(f"fused append+attention config {cid} dt={dt} B={B} row_counts={rc}")
+    cfg = scaled(CONFIGS[cid], num_seqs=B, ctx=ctx, layers=1, kv_dtype=dt)
+    lay = build_layout(cfg)
+    H, D, bs, R, Hq = cfg.num_kv_heads, cfg.head_dim, cfg.block_size, cfg.rows, cfg.num_q_heads
+    gen = torch.Generator(device="cuda").manual_seed(cfg.seed + 11)
+    fill = torch.from_numpy(lay.fill_slots).cuda()
+    kx = torch.randn(len(fill), H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    vx = torch.randn(len(fill), H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    k_new = torch.randn(B * R, H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    v_new = torch.randn(B * R, H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    q = torch.randn(B, R, Hq, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    row_counts = None
+    if rc:
+        row_counts = np.random.default_rng(cid).integers(1, R + 1, B).astype(np.int32)
+    slots = _derived_slots(lay, R, bs, row_counts)
+    if row_counts is None:
+        np.testing.assert_array_equal(slots, lay.append_slots)  # the layout's own slots
+    keys = torch.from_numpy(lay.keys).cuda()
+    bt = torch.from_numpy(lay.block_tables).cuda()
+    rc_t = torch.from_numpy(row_counts).cuda() if row_counts is not None else None
+    results = []
+    for fused in (True, False):
+        kv = make_cache(dt, H, D, bs, lay.num_blocks)
+        if dt == "fp8":
+            kv.set_head_scales(0, [4.5 / 448] * H, [4.5 / 448] * H)
+        kv.append(0, kx, vx, fill)
+        ws = kv.attention_workspace(B, R, Hq, bt.shape[1], 0)
+        kv.attention_plan(keys, R, Hq, bt.shape[1], ws, row_counts=rc_t)
+        out = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+        if fused:
+            kv.append_attention(0, k_new, v_new, q, out, keys, bt, 1 / math.sqrt(D), ws, row_counts=rc_t)
+        else:
+            kv.append(0, k_new, v_new, torch.from_numpy(slots).cuda())
+            kv.attention(0, q, out, keys, bt, 1 / math.sqrt(D), row_counts=rc_t, workspace=ws, planned=True)
+        torch.cuda.synchronize()
+        results.append((kv.k_pool(0).cpu().numpy(), kv.v_pool(0).cpu().numpy(), out.cpu().numpy()))
+        kv.close()
+    (fk, fv, fo), (sk, sv, so) = results
+    np.testing.assert_array_equal(fk, sk)
+    np.testing.assert_array_equal(fv, sv)
+    if rc:  # rows past a sequence's row count are not computed
+        for b in range(B):
+            fo[b, row_counts[b]:] = so[b, row_counts[b]:] = 0
+    np.testing.assert_array_equal(fo, so)
+
+
+def test_append_attention_rejects_per_block_int8(gpu):
+    kv = make_cache("int8", 2, 128, 16, 8)
+    z = torch.zeros(2, 2, 128, device="cuda", dtype=torch.bfloat16)
+    q = torch.zeros(1, 2, 2, 128, device="cuda", dtype=torch.bfloat16)
+    ws = kv.attention_workspace(1, 2, 2, 1, 0)
+    with pytest.raises(Exception, match="PER_BLOCK"):
+        kv.append_attention(0, z, z, q, torch.zeros_like(q), torch.tensor([4], dtype=torch.int32, device="cuda"),
+                            torch.zeros(1, 1, dtype=torch.int32, device="cuda"), 0.1, ws)
+    kv.close()
