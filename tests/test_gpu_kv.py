@@ -362,8 +362,8 @@ def _full_config_case(cid):
 @pytest.mark.parametrize("cid,explicit", [(2, 1024), (3, 1024), (4, 512), (5, 2048)])
 def test_attention_full_size_configs(gpu, cid, explicit):
     """Configs 2-5 at their real sizes. Size-independent property over every sequence:
-    the automatic schedule (stream-K for configs 2 and 4, one workgroup per item for 3
-    and 5) equals an explicit partition grid to 1e-3 (the schedules round P to the MFMA
+    the automatic schedule (LPT pieces for configs 2, 3 and 5, stream-K for 4) equals an
+    explicit partition grid to 1e-3 (the schedules round P to the MFMA
     type against different running maxima). Then the two shortest sequences against the
     fp64 oracle at the north-star tolerance."""
     say(f"attention full-size config {cid}")
