@@ -747,8 +747,11 @@ struct RowView {
     int idx_cut;
 };
 
-__device__ __forceinline__ RowView row_view(int row, int nseg, int use_topp, const RowStats* stats,
-                                            const float* seg_max, const u64* seg_z) {
+// The view of one row the decision needs (max, nucleus mass and boundary), evaluated by a
+// whole wave: lane s < nseg reads segment s (nseg <= 64), the wave reduces. Every lane
+// returns the same view.
+__device__ __forceinline__ RowView row_view_wave(int row, int nseg, int use_topp, const RowStats* stats,
+                                                 const float* seg_max, const u64* seg_z) {
     RowView v;
     if (use_topp) {
         const RowStats& st = stats[row];
@@ -756,28 +759,33 @@ __device__ __forceinline__ RowView row_view(int row, int nseg, int use_topp, con
         v.zp = st.zp;
         v.lam = st.lam;
         v.idx_cut = st.idx_cut;
-    } else {
-        v.m = row_max_from_segs(seg_max, row, nseg);
-        u64 z = 0;
-        for (int s = 0; s < nseg; ++s) z += seg_z[(size_t)row * nseg + s];
-        v.zp = z;
-        v.lam = 0;
-        v.idx_cut = 0x7fffffff;
+        return v;
     }
+    const int lane = threadIdx.x & 63;
+    float m = lane < nseg ? seg_max[(size_t)row * nseg + lane] : -INFINITY;
+    u64 z = lane < nseg ? seg_z[(size_t)row * nseg + lane] : 0ull;
+    for (int o = 32; o > 0; o >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, o));
+        z += shfl_xor_u64(z, o);
+    }
+    v.m = m;
+    v.zp = z;
+    v.lam = 0;
+    v.idx_cut = 0x7fffffff;
     return v;
 }
 
-// Acceptance walk of one sequence (identical in every block that evaluates it).
+// The acceptance walk of one sequence, run by a whole wave (every lane gets the result).
 template <gg_dtype_t DT>
-__device__ SeqDecision decide_seq(const void* logits, const float* dprobs, int K, int V, int b, int n,
-                                  const int32_t* drafts, const float* uniforms, float inv_t, int nseg,
-                                  int use_topp, const RowStats* stats, const float* seg_max,
-                                  const u64* seg_z) {
+__device__ SeqDecision decide_seq_wave(const void* logits, const float* dprobs, int K, int V, int b, int n,
+                                       const int32_t* drafts, const float* uniforms, float inv_t, int nseg,
+                                       int use_topp, const RowStats* stats, const float* seg_max,
+                                       const u64* seg_z) {
     const int R = K + 1;
     SeqDecision d{n, n, 0};
     for (int j = 0; j < n; ++j) {
         const int row = b * R + j;
-        const RowView rv = row_view(row, nseg, use_topp, stats, seg_max, seg_z);
+        const RowView rv = row_view_wave(row, nseg, use_topp, stats, seg_max, seg_z);
         const int x = drafts[(size_t)b * K + j];
         bool ok = false;
         if (x >= 0 && x < V && finite_f(rv.m)) {
@@ -815,11 +823,15 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_sums_kernel(
     __shared__ RowView s_rv;
     __shared__ u64 red[kSegThreads / 64];
     __shared__ int redi[kSegThreads / 64];
-    if (threadIdx.x == 0) {
-        s_d = decide_seq<DT>(logits, dprobs, K, V, b, n, drafts, uniforms, inv_t, nseg, use_topp, stats,
-                             seg_max, seg_z);
-        s_rv = row_view(b * R + s_d.row, nseg, use_topp, stats, seg_max, seg_z);
-        if (seg == 0) dec[b] = s_d;
+    if (threadIdx.x < 64) {
+        const SeqDecision dd = decide_seq_wave<DT>(logits, dprobs, K, V, b, n, drafts, uniforms, inv_t, nseg,
+                                                   use_topp, stats, seg_max, seg_z);
+        const RowView rv = row_view_wave(b * R + dd.row, nseg, use_topp, stats, seg_max, seg_z);
+        if (threadIdx.x == 0) {
+            s_d = dd;
+            s_rv = rv;
+            if (seg == 0) dec[b] = dd;
+        }
     }
     __syncthreads();
     const SeqDecision d = s_d;
@@ -865,6 +877,9 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_sums_kernel(
 }
 
 // E: per sequence: pick the segment holding floor(u * total), then the element inside it.
+// Wave 0 reduces and scans the segment sums (lane s = segment s); in the chosen segment
+// thread k owns the 32 consecutive elements [32k, 32k+32) and a block scan of the thread
+// sums finds the thread whose run crosses the target.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
     const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, float inv_t,
@@ -874,99 +889,111 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
     int32_t* __restrict__ out_tok) {
     const int b = blockIdx.x;
     const int R = K + 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __shared__ int s_seg, s_use_res, s_found;
     __shared__ u64 s_t;
-    __shared__ u64 s_scan[kSegThreads];
+    __shared__ u64 s_wsum[kSegThreads / 64];
     const SeqDecision d = dec[b];
-    if (threadIdx.x == 0) {
-        u64 tot_res = 0, tot_pl = 0;
-        int last_res = -1, last_pl = -1;
-        for (int s = 0; s < nseg; ++s) {
-            const SegOut o = seg_out[(size_t)b * nseg + s];
-            tot_res += o.sum_res;
-            tot_pl += o.sum_plain;
-            last_res = max(last_res, o.last_res);
-            last_pl = max(last_pl, o.last_plain);
+    if (wave == 0) {
+        const SegOut o = lane < nseg ? seg_out[(size_t)b * nseg + lane] : SegOut{0ull, 0ull, -1, -1};
+        u64 tot_res = o.sum_res, tot_pl = o.sum_plain;
+        int last_res = o.last_res, last_pl = o.last_plain;
+        for (int off = 32; off > 0; off >>= 1) {
+            tot_res += shfl_xor_u64(tot_res, off);
+            tot_pl += shfl_xor_u64(tot_pl, off);
+            last_res = max(last_res, __shfl_xor(last_res, off));
+            last_pl = max(last_pl, __shfl_xor(last_pl, off));
         }
         // A vanished residual falls back to the target row itself.
         const int use_res = (d.residual && tot_res > 0) ? 1 : 0;
         const u64 tot = use_res ? tot_res : tot_pl;
         const int last = use_res ? last_res : last_pl;
-        s_use_res = use_res;
-        s_seg = -1;
-        s_found = -1;
-        int token = 0;
+        int seg = -1;
+        u64 tt = 0;
         if (tot > 0) {
             const double u = (double)uniforms[(size_t)b * R + K];
             const u64 t = (u64)(u * (double)tot);
-            u64 c = 0;
-            for (int s = 0; s < nseg; ++s) {
-                const SegOut o = seg_out[(size_t)b * nseg + s];
-                const u64 v = use_res ? o.sum_res : o.sum_plain;
-                if (c + v > t) {
-                    s_seg = s;
-                    s_t = t - c;
-                    break;
-                }
-                c += v;
+            const u64 v = use_res ? o.sum_res : o.sum_plain;
+            u64 incl = v;
+            for (int off = 1; off < 64; off <<= 1) {
+                const u64 y = shfl_up_u64(incl, off);
+                if (lane >= off) incl += y;
             }
-            token = last >= 0 ? last : 0;  // used when no segment crosses (u >= 1)
+            // First segment whose inclusive prefix passes t.
+            const unsigned long long hit = __ballot(lane < nseg && incl > t);
+            if (hit) {
+                seg = __ffsll((long long)hit) - 1;
+                const u64 excl = incl - v;
+                tt = t - __shfl(excl, seg);
+            }
         }
-        s_found = token;
-        out_acc[b] = d.accepted;
+        if (lane == 0) {
+            s_use_res = use_res;
+            s_seg = seg;
+            s_t = tt;
+            s_found = tot > 0 ? (last >= 0 ? last : 0) : 0;  // no segment crosses (u >= 1)
+            out_acc[b] = d.accepted;
+        }
     }
     __syncthreads();
     if (s_seg < 0) {
         if (threadIdx.x == 0) out_tok[b] = s_found;
         return;
     }
-    // Scan the chosen segment: thread k owns 32 consecutive elements [32k, 32k+32).
     const int row = b * R + d.row;
-    const RowView rv = row_view(row, nseg, use_topp, stats, seg_max, seg_z);
+    const RowView rv = row_view_wave(row, nseg, use_topp, stats, seg_max, seg_z);
     const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    const float* qrow = (s_use_res && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
-    const int xr = s_use_res ? drafts[(size_t)b * K + d.row] : -1;
+    const bool use_res = s_use_res;
+    const float* qrow = (use_res && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
+    const int xr = use_res ? drafts[(size_t)b * K + d.row] : -1;
     const double zp_d = (double)rv.zp;
-    auto r_at = [&](int i) -> u64 {
-        if (i >= V) return 0ull;
-        const u64 w = nu.weight(ld<DT>(lp, i), i);
-        if (!s_use_res) return w;
-        u64 qf;
-        if (qrow) {
-            const float qi = qrow[i];
-            qf = (u64)(qi < 0.f ? 0.0 : (double)qi * zp_d);
-        } else {
-            qf = (i == xr) ? rv.zp : 0ull;
-        }
-        return w > qf ? w - qf : 0ull;
-    };
     const int e0 = s_seg * kSegElems + 32 * threadIdx.x;
+    u64 r[32];
     u64 mine = 0;
-    for (int k = 0; k < 32; ++k) mine += r_at(e0 + k);
-    s_scan[threadIdx.x] = mine;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        // Exclusive prefix of the per-thread sums (256 entries, serial: cheap).
-        u64 c = 0;
-        for (int k = 0; k < kSegThreads; ++k) {
-            const u64 v = s_scan[k];
-            s_scan[k] = c;
-            c += v;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const int i = e0 + k;
+        u64 w = 0;
+        if (i < V) {
+            w = nu.weight(ld<DT>(lp, i), i);
+            if (use_res) {
+                u64 qf;
+                if (qrow) {
+                    const float qi = qrow[i];
+                    qf = (u64)(qi < 0.f ? 0.0 : (double)qi * zp_d);
+                } else {
+                    qf = (i == xr) ? rv.zp : 0ull;
+                }
+                w = w > qf ? w - qf : 0ull;
+            }
         }
+        r[k] = w;
+        mine += w;
     }
+    // Exclusive block scan of the thread sums.
+    u64 incl = mine;
+    for (int off = 1; off < 64; off <<= 1) {
+        const u64 y = shfl_up_u64(incl, off);
+        if (lane >= off) incl += y;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
     __syncthreads();
+    u64 before = incl - mine;
+    for (int w = 0; w < wave; ++w) before += s_wsum[w];
     const u64 t = s_t;
-    const u64 before = s_scan[threadIdx.x];
     if (before <= t && before + mine > t) {
         u64 c = before;
+        int found = e0 + 31;
+#pragma unroll
         for (int k = 0; k < 32; ++k) {
-            c += r_at(e0 + k);
+            c += r[k];
             if (c > t) {
-                s_found = e0 + k;
+                found = e0 + k;
                 break;
             }
         }
+        s_found = found;
     }
     __syncthreads();
     if (threadIdx.x == 0) out_tok[b] = s_found;
