@@ -776,34 +776,62 @@ __device__ __forceinline__ RowView row_view_wave(int row, int nseg, int use_topp
 }
 
 // The acceptance walk of one sequence, run by a whole wave (every lane gets the result).
+// The rows' tests do not depend on each other, so they are evaluated together: groups of
+// g = 2^ceil(log2 nseg) lanes take one row each (lane s of a group reads segment s), 64/g
+// rows per pass; the walk then stops at the first failed row.
 template <gg_dtype_t DT>
 __device__ SeqDecision decide_seq_wave(const void* logits, const float* dprobs, int K, int V, int b, int n,
                                        const int32_t* drafts, const float* uniforms, float inv_t, int nseg,
                                        int use_topp, const RowStats* stats, const float* seg_max,
                                        const u64* seg_z) {
     const int R = K + 1;
-    SeqDecision d{n, n, 0};
-    for (int j = 0; j < n; ++j) {
-        const int row = b * R + j;
-        const RowView rv = row_view_wave(row, nseg, use_topp, stats, seg_max, seg_z);
-        const int x = drafts[(size_t)b * K + j];
-        bool ok = false;
-        if (x >= 0 && x < V && finite_f(rv.m)) {
-            const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-            Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
-            const u64 wx = nu.weight(ld<DT>(lp, x), x);
-            const double q = dprobs ? (double)dprobs[((size_t)b * K + j) * V + x] : 1.0;
-            const double u = (double)uniforms[(size_t)b * R + j];
-            ok = u * q * (double)rv.zp < (double)wx;
+    const int lane = threadIdx.x & 63;
+    int g = 1;
+    while (g < nseg) g <<= 1;
+    const int per_pass = 64 / g;
+    const int jl = lane / g, sl = lane % g;
+    for (int j0 = 0; j0 < n; j0 += per_pass) {
+        const int j = j0 + jl;
+        const bool live = j < n;
+        const int row = b * R + (live ? j : 0);
+        float m;
+        u64 zp;
+        unsigned int lam = 0;
+        int idx_cut = 0x7fffffff;
+        if (use_topp) {
+            const RowStats& st = stats[row];
+            m = st.m;
+            zp = st.zp;
+            lam = st.lam;
+            idx_cut = st.idx_cut;
+        } else {
+            m = sl < nseg ? seg_max[(size_t)row * nseg + sl] : -INFINITY;
+            zp = sl < nseg ? seg_z[(size_t)row * nseg + sl] : 0ull;
+            for (int o = g >> 1; o > 0; o >>= 1) {
+                m = fmaxf(m, __shfl_xor(m, o));
+                zp += shfl_xor_u64(zp, o);
+            }
         }
-        if (!ok) {
-            d.accepted = j;
-            d.row = j;
-            d.residual = 1;
-            break;
+        bool ok = true;
+        if (live) {
+            const int x = drafts[(size_t)b * K + j];
+            ok = false;
+            if (x >= 0 && x < V && finite_f(m)) {
+                const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+                Nucleus nu{m, inv_t, lam, idx_cut};
+                const u64 wx = nu.weight(ld<DT>(lp, x), x);
+                const double q = dprobs ? (double)dprobs[((size_t)b * K + j) * V + x] : 1.0;
+                const double u = (double)uniforms[(size_t)b * R + j];
+                ok = u * q * (double)zp < (double)wx;
+            }
+        }
+        const unsigned long long bad = __ballot(!ok && sl == 0);
+        if (bad) {
+            const int jf = j0 + (__ffsll((long long)bad) - 1) / g;
+            return SeqDecision{jf, jf, 1};
         }
     }
-    return d;
+    return SeqDecision{n, n, 0};
 }
 
 // D: per (sequence, segment): decide, then the segment's residual and plain weight
