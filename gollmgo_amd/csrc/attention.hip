@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a, KVView kv)
         if (blk >= 0) {
             // The lane's key row is contiguous: 16-byte loads when rows are whole
             // multiples of 16 bytes (pools are 256-byte aligned), else element loads.
-            const uint8_t* krow = kv.kc + (((size_t)blk * kv.Hkv + kvh) * kv.bs + off) * (size_t)D * dtype_bytes(DT);
+            const uint8_t* krow = kv.kc + (kv.tile0(blk, kvh) + (size_t)off * D) * dtype_bytes(DT);
             float dot = 0.f;
             constexpr int kN = Pool16<DT>::kN;
             if (D % kN == 0) {
@@ -137,7 +137,7 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a, KVView kv)
         // (Masked and skipped keys have p = 0 and read block 0.)
         __syncthreads();  // the previous tile's readers are done
         s_p[lane] = blk >= 0 ? p * kv.v_scale(blk, kvh) : 0.f;
-        s_vrow[lane] = ((size_t)max(blk, 0) * kv.Hkv + kvh) * (size_t)D * kv.bs + off;
+        s_vrow[lane] = kv.tile0(max(blk, 0), kvh) + off;
         __syncthreads();
         const int ntile = min(64, t1 - tb);
         const uint8_t* vc = kv.vc;

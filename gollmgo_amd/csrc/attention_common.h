@@ -31,12 +31,14 @@ struct KVView {
         }
         return 0.f;
     }
-    // Raw (unscaled) element of K[blk][h][off][d] and V[blk][h][d][off].
+    // Raw (unscaled) element of K[blk][h][off][d] and V[blk][h][d][off] (K and V tiles of a
+    // (block, head) alternate: tiles of one pool are 2 * bs * D elements apart).
+    __device__ __forceinline__ size_t tile0(int blk, int h) const { return ((size_t)blk * Hkv + h) * (2 * (size_t)bs * D); }
     __device__ __forceinline__ float k_at(int blk, int h, int off, int d) const {
-        return elem(kc, (((size_t)blk * Hkv + h) * bs + off) * D + d);
+        return elem(kc, tile0(blk, h) + (size_t)off * D + d);
     }
     __device__ __forceinline__ float v_at(int blk, int h, int off, int d) const {
-        return elem(vc, (((size_t)blk * Hkv + h) * D + d) * bs + off);
+        return elem(vc, tile0(blk, h) + (size_t)d * bs + off);
     }
     __device__ __forceinline__ float k_scale(int blk, int h) const {
         if (dt == GG_DTYPE_FP8_E4M3) return k_head_scale[h];
@@ -53,8 +55,8 @@ struct KVView {
 
 inline KVView make_kv_view(const KV* kv, int layer) {
     KVView v{};
-    v.kc = kv->k_pool + (size_t)layer * kv->layer_bytes;
-    v.vc = kv->v_pool + (size_t)layer * kv->layer_bytes;
+    v.kc = kv->k_pool + (size_t)layer * kv->layer_stride;
+    v.vc = kv->v_pool + (size_t)layer * kv->layer_stride;
     if (kv->scale_mode == GG_SCALE_PER_HEAD) {
         v.k_head_scale = (const float*)kv->k_scales + (size_t)layer * kv->scale_layer_elems;
         v.v_head_scale = (const float*)kv->v_scales + (size_t)layer * kv->scale_layer_elems;
@@ -161,8 +163,8 @@ __device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView
                 vx[e] = bf ? bf16_bits_to_f32(vh) : f16_bits_to_f32(vh);
             }
         }
-        const size_t ki = (((size_t)blk * kv.Hkv + kvh) * bs + off) * D + d0;
-        const size_t vi = (((size_t)blk * kv.Hkv + kvh) * D + d0) * bs + off;
+        const size_t ki = kv.tile0(blk, kvh) + (size_t)off * D + d0;
+        const size_t vi = kv.tile0(blk, kvh) + (size_t)d0 * bs + off;
         if (kv.dt == GG_DTYPE_FP8_E4M3) {
             uint32_t w0 = 0, w1 = 0;
 #pragma unroll

@@ -269,7 +269,7 @@ struct PieceIO {
         const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4, kq = c16 >> 2;
         const int blk = bl.k;
         const uint8_t* base =
-            kv.kc + (((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * (size_t)(kBS * kD) + 32 * g4) * kEB;
+            kv.kc + (((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * (size_t)(2 * kBS * kD) + 32 * g4) * kEB;
 #pragma unroll
         for (int s = 0; s < kNS; ++s) {
             const int off = Geom::ob(kq) + 4 * s + (c16 & 3);
@@ -289,7 +289,8 @@ struct PieceIO {
             rg.ksc = f16_bits_to_f32(kv.k_blk_scale[si]);
             rg.vsc = f16_bits_to_f32(kv.v_blk_scale[si]);
         }
-        const uint8_t* base = kv.vc + ((((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * kD) * kBS + Geom::ob(g4)) * kEB;
+        const uint8_t* base =
+            kv.vc + (((size_t)(blk < 0 ? 0 : blk) * kv.Hkv + kvh) * (size_t)(2 * kBS * kD) + Geom::ob(g4)) * kEB;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             const int d = dt * 16 + c16;

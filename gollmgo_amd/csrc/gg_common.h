@@ -30,9 +30,11 @@ struct KV {
     int device = 0;
     size_t elem_bytes = 2;
     size_t layer_bytes = 0;       // bytes of one layer's K (or V) pool
+    size_t tile_bytes = 0;        // one (block, head) tile of K (or V): block_size * head_dim elements
+    size_t layer_stride = 0;      // bytes between layers (K and V interleaved: 2 * layer_bytes)
     size_t scale_layer_elems = 0; // scales per layer per pool
-    uint8_t* k_pool = nullptr;    // [layers][layer_bytes]
-    uint8_t* v_pool = nullptr;
+    uint8_t* k_pool = nullptr;    // [layers][blocks][heads][K tile, V tile]: the allocation
+    uint8_t* v_pool = nullptr;    // k_pool + tile_bytes (inside that allocation)
     void* k_scales = nullptr;     // PER_HEAD: float[layers][Hkv]; PER_BLOCK: u16[layers][blocks][Hkv]
     void* v_scales = nullptr;
     float* block_amax = nullptr;  // PER_BLOCK staging: float[blocks][Hkv][2], kept at zero between calls

@@ -13,11 +13,13 @@
 namespace gg {
 namespace {
 
+// Element indices from the K and V pool bases. The K and V tiles of a (block, head)
+// alternate, so consecutive tiles of one pool are 2 * bs * D elements apart.
 __device__ __forceinline__ size_t k_index(int blk, int h, int off, int d, int Hkv, int bs, int D) {
-    return (((size_t)blk * Hkv + h) * bs + off) * D + d;
+    return ((size_t)blk * Hkv + h) * (2 * (size_t)bs * D) + (size_t)off * D + d;
 }
 __device__ __forceinline__ size_t v_index(int blk, int h, int off, int d, int Hkv, int bs, int D) {
-    return (((size_t)blk * Hkv + h) * D + d) * bs + off;
+    return ((size_t)blk * Hkv + h) * (2 * (size_t)bs * D) + (size_t)d * bs + off;
 }
 
 struct AppendArgs {
@@ -278,8 +280,8 @@ gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg
                              const int32_t* slots, int n_rows, hipStream_t s) {
     if (n_rows == 0) return GG_OK;
     AppendArgs a{};
-    a.kc = kv->k_pool + (size_t)layer * kv->layer_bytes;
-    a.vc = kv->v_pool + (size_t)layer * kv->layer_bytes;
+    a.kc = kv->k_pool + (size_t)layer * kv->layer_stride;
+    a.vc = kv->v_pool + (size_t)layer * kv->layer_stride;
     a.k = k;
     a.v = v;
     a.src = src;

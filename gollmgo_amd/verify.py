@@ -55,13 +55,17 @@ class _DeviceBuffer:
         }
 
 
+_ELEM_BYTES = {DType.F32: 4, DType.F16: 2, DType.BF16: 2, DType.FP8_E4M3: 1, DType.INT8: 1}
+
+
 def device_bytes(ptr: int, nbytes: int) -> torch.Tensor:
     """A uint8 torch view of `nbytes` of device memory at `ptr` (no copy)."""
     return torch.as_tensor(_DeviceBuffer(ptr, nbytes), device="cuda")
 
 
 class KVCache:
-    """Paged K/V pools for all layers (K[blk][Hkv][bs][D], V[blk][Hkv][D][bs])."""
+    """Paged K/V pools for all layers (K[blk][Hkv][bs][D], V[blk][Hkv][D][bs]; in device
+    memory the K and V tiles of each (block, head) are adjacent)."""
 
     def __init__(self, num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
                  head_dim: int, dtype: DType):
@@ -91,11 +95,21 @@ class KVCache:
     def layer_bytes(self) -> int:
         return lib().gg_kv_layer_bytes(self.handle)
 
+    def _pool(self, ptr: int) -> torch.Tensor:
+        # The K and V tiles of each (block, head) alternate in device memory; gather one
+        # pool's tiles into its logical [blocks][heads][tile] bytes (a device copy).
+        tile = self.block_size * self.head_dim * _ELEM_BYTES[self.dtype]
+        n = self.num_blocks * self.num_kv_heads
+        raw = device_bytes(ptr, (2 * n - 1) * tile)
+        return torch.as_strided(raw, (n, tile), (2 * tile, 1)).reshape(-1)
+
     def k_pool(self, layer: int) -> torch.Tensor:
-        return device_bytes(lib().gg_kv_k_layer_ptr(self.handle, layer), self.layer_bytes)
+        """Layer's K pool, K[blk][Hkv][bs][D], as uint8 bytes (a copy)."""
+        return self._pool(lib().gg_kv_k_layer_ptr(self.handle, layer))
 
     def v_pool(self, layer: int) -> torch.Tensor:
-        return device_bytes(lib().gg_kv_v_layer_ptr(self.handle, layer), self.layer_bytes)
+        """Layer's V pool, V[blk][Hkv][D][bs], as uint8 bytes (a copy)."""
+        return self._pool(lib().gg_kv_v_layer_ptr(self.handle, layer))
 
     def scales(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
         """(k, v) scales: PER_HEAD fp32 [Hkv]; PER_BLOCK fp16 [blocks, Hkv]."""

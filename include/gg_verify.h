@@ -18,9 +18,13 @@
  *   - handles are not thread-safe: one engine thread drives one handle, as the
  *     reference's single engine goroutine does (internal/engine/serving.go:160).
  *
- * KV layout in HBM (per layer, per K or V pool), chosen for 16-byte loads:
- *   K: [num_blocks][num_kv_heads][block_size][head_dim]   (token-major inside a block)
- *   V: [num_blocks][num_kv_heads][head_dim][block_size]   (dim-major inside a block)
+ * KV layout in HBM (per layer), chosen for 16-byte loads:
+ *   K tile of (block, head): [block_size][head_dim]   (token-major)
+ *   V tile of (block, head): [head_dim][block_size]   (dim-major)
+ *   layer: [num_blocks][num_kv_heads][K tile, V tile] — the two tiles of a (block,
+ *   head) are adjacent, so one item's block is one contiguous run. Logically the K pool
+ *   is K[num_blocks][num_kv_heads][block_size][head_dim] with consecutive tiles
+ *   2 * tile bytes apart (tile = block_size * head_dim * element bytes), likewise V.
  * A reference slot index (internal/kvcache/block_table.go:39) still addresses a
  * token: slot = physical_block * block_size + offset.
  */
@@ -92,13 +96,15 @@ gg_status_t gg_kv_create(int num_layers, int num_blocks, int block_size,
                          gg_scale_mode_t scale_mode, gg_kv_t* out);
 gg_status_t gg_kv_destroy(gg_kv_t kv);
 
-/* Device pointers to one layer's pools (NULL on bad arguments). */
+/* Device pointers to one layer's first K tile and first V tile (NULL on bad
+ * arguments); tiles of one pool follow every 2 * tile bytes. */
 void* gg_kv_k_layer_ptr(gg_kv_t kv, int layer);
 void* gg_kv_v_layer_ptr(gg_kv_t kv, int layer);
 /* PER_HEAD: float[num_kv_heads]; PER_BLOCK: uint16 (fp16 bits)[num_blocks][num_kv_heads]. */
 void* gg_kv_k_scale_ptr(gg_kv_t kv, int layer);
 void* gg_kv_v_scale_ptr(gg_kv_t kv, int layer);
-/* Bytes of one layer's K (or V) pool. */
+/* Bytes of one layer's K (or V) tiles (num_blocks * num_kv_heads * tile); a layer
+ * occupies twice that. */
 size_t gg_kv_layer_bytes(gg_kv_t kv);
 
 /* PER_HEAD only: upload host arrays k_scales[num_kv_heads], v_scales[num_kv_heads]
