@@ -89,8 +89,8 @@ GG_API gg_status_t gg_kv_create(int num_layers, int num_blocks, int block_size, 
     kv->layer_stride = 2 * kv->layer_bytes;
     (void)hipGetDevice(&kv->device);
     // One allocation: the K and V tiles of a (block, head) sit next to each other, so a
-    // workgroup reading one item's block reads one contiguous run (measured: ~4 % more
-    // HBM rate than two pools on the paged pattern).
+    // workgroup reading one item's block reads one contiguous run (a load-only probe of
+    // the paged pattern gains ~4 %, the attention kernel ~0.5 %).
     gg_status_t st = check_hip(hipMalloc((void**)&kv->k_pool, kv->layer_stride * num_layers), "hipMalloc(KV pool)");
     if (st == GG_OK) kv->v_pool = kv->k_pool + kv->tile_bytes;
     if (st == GG_OK && scale_mode == GG_SCALE_PER_HEAD) {
