@@ -174,3 +174,39 @@ def test_rejection_invalid_and_nonfinite(gpu):
     torch.cuda.synchronize()
     ea, et = ora.accept_rejection(host, drafts, n, u, 0.7, 0.9)
     assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
+
+
+@pytest.mark.parametrize("cid", [2, 3, 4, 5])
+def test_acceptance_full_size_configs(gpu, cid):
+    """Each config's acceptance at its real shape ([B, K+1, 128256] logits in the config's
+    dtype; config 3 with draft distributions, config 5 with top-p 0.95), inputs generated
+    as bench.py does, against the CPU oracle bit for bit."""
+    from gollmgo_amd.workloads import CONFIGS
+    cfg = CONFIGS[cid]
+    B, K, V = cfg.num_seqs, cfg.max_drafts, cfg.vocab
+    say(f"acceptance full size config {cid}: B={B} K={K} V={V} {cfg.accept}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(cfg.seed + 99)
+    logits = (torch.randn(B, K + 1, V, device="cuda", generator=g) * 2.0).to(TD[cfg.logits_dtype])
+    probs = torch.softmax(logits[:, :K].float() * 1.5, dim=-1).contiguous() if cfg.draft_probs else None
+    base = probs if probs is not None else logits[:, :K].float()
+    mode = base.argmax(dim=-1).to(torch.int32)
+    rand = torch.randint(0, V, (B, K), device="cuda", dtype=torch.int32, generator=g)
+    drafts = torch.where(torch.rand(B, K, device="cuda", generator=g) < 0.8, mode, rand).contiguous()
+    n = torch.randint(0, K + 1, (B,), device="cuda", dtype=torch.int32, generator=g)
+    host = logits.float().cpu().numpy()
+    if cfg.accept == "greedy":
+        acc, tok = gv.accept_greedy(logits, drafts, n)
+        torch.cuda.synchronize()
+        ea, et = ora.accept_greedy(host, drafts.cpu().numpy(), n.cpu().numpy())
+    else:
+        u = torch.rand(B, K + 1, device="cuda", generator=g)
+        acc, tok = gv.accept_rejection(logits, drafts, n, u, cfg.temperature, cfg.top_p, draft_probs=probs)
+        torch.cuda.synchronize()
+        ea, et = ora.accept_rejection(host, drafts.cpu().numpy(), n.cpu().numpy(), u.cpu().numpy(),
+                                      cfg.temperature, cfg.top_p,
+                                      probs.cpu().numpy() if probs is not None else None)
+    a, t = acc.cpu().numpy(), tok.cpu().numpy()
+    print(f"  accepted {int(a.sum())} of {int(n.sum())} drafts")
+    assert np.array_equal(a, ea)
+    assert np.array_equal(t, et)
