@@ -203,8 +203,7 @@ struct LaneBlocks {
 };
 
 // What a piece needs to start streaming: its first chunk's K/V in flight and the block
-// ids of its first two chunks. Filled by piece_start, either before the piece or, for the
-// next piece of the same workgroup, while the current one merges.
+// ids of its first two chunks (PieceIO::start).
 template <gg_dtype_t DT>
 struct PieceIn {
     ChunkRegs<PoolTraits<DT>::kEB> cur;
@@ -297,22 +296,15 @@ struct PieceIO {
             rg.v[dt] = *(const uint4*)(base + (size_t)d * kBS * kEB);
         }
     }
-    // Issue the first chunk of piece d (this wave's first chunk is chunk `wave`): block
-    // ids and K rows (start_k), then V columns (start_v).
-    __device__ static __forceinline__ void start_k(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
-                                                   PieceIn<DT>& in) {
+    // Issue the first chunk of piece d (this wave's first chunk is chunk `wave`): the block
+    // ids of its first two chunks, then the first chunk's K rows and V columns.
+    __device__ static __forceinline__ void start(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
+                                                 PieceIn<DT>& in) {
         const int wave_u = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         in.bl_cur = chunk_blocks(a, kv, d.b, d.t0, d.t_end, wave_u);
         in.bl_next = chunk_blocks(a, kv, d.b, d.t0, d.t_end, wave_u + kWaves);
         load_k(kv, in.bl_cur, d.kvh, in.cur);
-    }
-    __device__ static __forceinline__ void start_v(const KVView& kv, const PieceDesc& d, PieceIn<DT>& in) {
         load_v(kv, in.bl_cur, d.kvh, in.cur);
-    }
-    __device__ static __forceinline__ void start(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
-                                                 PieceIn<DT>& in) {
-        start_k(a, kv, d, in);
-        start_v(kv, d, in);
     }
 };
 
@@ -320,12 +312,10 @@ struct PieceIO {
 // goes to the output (part < 0 && rec < 0), to partition slot `part` of the fixed
 // partition grid, or to stream-K record `rec`. Must be reached by the whole workgroup.
 //
-// `in` holds the piece's first chunk, already issued (PieceIO::start). With has_next,
-// the next piece's first chunk is issued into `in` as soon as this piece's chunk
-// loop ends, so its latency overlaps this piece's merge and the next Q staging.
+// `in` holds the piece's first chunk, already issued (PieceIO::start).
 template <gg_dtype_t DT, int NT>
 __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, const PieceDesc pd,
-                                           PieceIn<DT>& in, const bool has_next, const PieceDesc next) {
+                                           PieceIn<DT>& in) {
     const int b = pd.b, kvh = pd.kvh, t0 = pd.t0, t_end = pd.t_end, part = pd.part, rec = pd.rec;
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
@@ -338,10 +328,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     const int ctx = seq_keys(a, b, kBS);
     const int R = a.rows;
     const int nrows = a.row_counts ? a.row_counts[b] : R;
-    if (nrows <= 0 || nrows > ctx) {
-        if (has_next) PieceIO<DT>::start(a, kv, next, in);
-        return;
-    }
+    if (nrows <= 0 || nrows > ctx) return;
     const int Hq = a.num_q_heads;
     const int G = Hq / kv.Hkv;
     const int nvalid_rows = G * nrows;
@@ -640,10 +627,6 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         bl_next = IO::lane_blocks(kv, raw_after, t_end);
     }
 
-    // The next piece of this workgroup starts streaming now: block ids and K rows before
-    // the merge, V columns after it (both buffers next to the O tiles would not fit).
-    if (has_next) IO::start_k(a, kv, next, in);
-
     // ---- merge the four waves' states through LDS ----
     __shared__ float s_m[kWaves][64];
     __shared__ float s_l[kWaves][64];
@@ -707,7 +690,6 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         }
         __syncthreads();
     }
-    if (has_next) IO::start_v(kv, next, in);
 }
 
 // Fixed partition grid: workgroup (part, kvh, b) takes tokens [part*P, (part+1)*P).
@@ -726,7 +708,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(Attn
     }
     PieceIn<DT> in;
     PieceIO<DT>::start(a, kv, d, in);
-    attn_piece<DT, NT>(a, kv, d, in, false, d);
+    attn_piece<DT, NT>(a, kv, d, in);
 }
 
 // Chunks of work of sequence b (0 when it has nothing to compute).
@@ -825,7 +807,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
     while (next_piece(d)) {
         PieceIn<DT> in;
         PieceIO<DT>::start(a, kv, d, in);
-        attn_piece<DT, NT>(a, kv, d, in, false, d);
+        attn_piece<DT, NT>(a, kv, d, in);
     }
 }
 
@@ -933,7 +915,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     } else {
         PieceIO<DT>::start(a, kv, d, in);
     }
-    attn_piece<DT, NT>(a, kv, d, in, false, d);
+    attn_piece<DT, NT>(a, kv, d, in);
 }
 
 // Merge the pieces of split items; workgroup (item, y) takes rows 4y .. 4y+3.
