@@ -845,8 +845,8 @@ __device__ __forceinline__ long long block_sum_1024(long long v, long long* s_w)
 // One 1024-thread workgroup (one sequence per thread): sizes, ranks and lays out the
 // pieces.
 __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv, int tok, int slots, int recs) {
-    __shared__ int s_key[kLptMaxSeqs];  // piece size in chunks (0: no work)
-    __shared__ int s_cnt[kLptMaxSeqs];  // pieces of the sequence over all kv heads
+    __shared__ __align__(16) int s_key[kLptMaxSeqs];  // piece size in chunks (0: no work)
+    __shared__ __align__(16) int s_cnt[kLptMaxSeqs];  // pieces of the sequence over all kv heads
     __shared__ long long s_w[16];
     const int B = a.num_seqs;
     const int b = threadIdx.x;
@@ -858,18 +858,28 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     const int np = nch ? (nch + T - 1) / T : 0;
     const int key = np ? (nch + np - 1) / np : 0;
     const int cnt = np * Hkv;
-    if (b < B) {
-        s_key[b] = key;
-        s_cnt[b] = cnt;
+    // (Entries past B, up to a multiple of 8, read as empty.)
+    if (b < ((B + 7) & ~7)) {
+        s_key[b] = b < B ? key : 0;
+        s_cnt[b] = b < B ? cnt : 0;
     }
     const long long total = block_sum_1024(cnt, s_w);  // (its barriers also publish s_key / s_cnt)
     int* plan = a.plan;
     if (b == 0) plan[0] = (int)total;
     if (b >= B) return;
+    // Pieces ahead of this sequence's: larger pieces, then equal pieces of lower sequences.
+    // Eight sequences per step from 16-byte LDS reads (independent adds, no serial chain).
     int pos = 0;
-    for (int t = 0; t < B; ++t) {
-        const int kt = s_key[t];
-        if (kt > key || (kt == key && t < b)) pos += s_cnt[t];
+    for (int t0 = 0; t0 < B; t0 += 8) {
+        const int4 k0 = *(const int4*)&s_key[t0], k1 = *(const int4*)&s_key[t0 + 4];
+        const int4 n0 = *(const int4*)&s_cnt[t0], n1 = *(const int4*)&s_cnt[t0 + 4];
+        const int kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const int nn[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int t = t0 + e;
+            pos += (kk[e] > key || (kk[e] == key && t < b)) ? nn[e] : 0;
+        }
     }
     int* seq = lpt_seq(plan, recs) + 2 * b;
     seq[0] = pos;
