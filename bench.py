@@ -39,8 +39,9 @@ def parse():
     ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU baseline sample")
     ap.add_argument("--partition", type=int, default=-1, help="override split-K partition tokens")
     ap.add_argument("--layers", type=int, default=0, help="override layer count (0 = config)")
-    ap.add_argument("--separate-append", action="store_true",
-                    help="append the draft KV with gg_kv_append instead of inside the attention call")
+    ap.add_argument("--append-in-call", action="store_true",
+                    help="append the draft KV through gg_verify_append_attention_planned (one call per "
+                         "layer) instead of gg_kv_append + gg_verify_attention_planned")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches for `value` instead of replays of the captured step graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -161,9 +162,10 @@ def main():
     # The attention schedule depends only on the context lengths, shared by all layers of
     # a step: computed once per step (gg_verify_attention_plan), used by every layer.
     use_plan = cfg.partition == 0
-    # The draft rows' KV append rides in the attention call (gg_verify_append_attention_planned)
-    # where the pool allows it (not PER_BLOCK INT8, whose block scales need gg_kv_append).
-    fused = use_plan and cfg.kv_dtype != "int8" and not args.separate_append
+    # --append-in-call: the draft rows' KV append through the attention entry point
+    # (gg_verify_append_attention_planned; not for PER_BLOCK INT8, whose block scales need
+    # gg_kv_append).
+    fused = use_plan and cfg.kv_dtype != "int8" and args.append_in_call
 
     def step(record: bool):
         if hist is not None:
@@ -291,7 +293,7 @@ def main():
     elif cfg.partition:
         attn_kernels = "attn_mfma_kernel + attn_combine_kernel (partition grid)"
     elif fused:
-        attn_kernels = ("gg_verify_append_attention_planned: draft-KV append in the final piece of each item + "
+        attn_kernels = ("gg_verify_append_attention_planned: draft-KV append launch + "
                         "the library's automatic schedule (LPT pieces or stream-K) + merge")
     else:
         attn_kernels = "gg_verify_attention_planned: the library's automatic schedule (LPT pieces or stream-K) + merge"
@@ -320,7 +322,7 @@ def main():
             "layers": L, "vocab": V, "accept": cfg.accept, "temperature": cfg.temperature, "top_p": cfg.top_p,
             "draft_probs": cfg.draft_probs, "partition_tokens": cfg.partition or "auto",
             "shared_prefix_frac": cfg.shared_prefix_frac,
-            "draft_kv_append": "inside the attention call" if fused else "gg_kv_append",
+            "draft_kv_append": "gg_verify_append_attention_planned" if fused else "gg_kv_append",
         },
         "kernels_us": {"append_avg": round(t_app, 2), "attention_avg": round(t_attn, 2),
                        "attention_median": round(t_attn_med, 2), "accept_avg": round(t_acc, 2),

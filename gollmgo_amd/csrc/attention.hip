@@ -230,14 +230,6 @@ gg_status_t launch_append_from_tables(const AttnArgs& a, const KVView& kv, hipSt
     return check_hip(hipGetLastError(), "append launch");
 }
 
-bool attn_can_fuse_append(const AttnArgs& a) {
-    const KV* kv = a.kv;
-    if (!attn_mfma_supported(kv, a.rows, a.num_q_heads)) return false;
-    if (a.sched == ATTN_SCHED_LPT) return true;
-    return a.sched == ATTN_SCHED_GRID && a.partition % 64 == 0 && a.partition <= kMfmaMaxPartition &&
-           (long long)a.partition >= (long long)a.max_blocks * kv->block_size;
-}
-
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens) {
     if (partition_tokens > 0) return {ATTN_SCHED_GRID, partition_tokens};
@@ -285,7 +277,7 @@ size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_head
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s) {
     const KV* kv = a.kv;
     KVView view = make_kv_view(kv, a.layer);
-    if (a.k_new && !a.fuse_append) {
+    if (a.k_new) {
         const gg_status_t st = launch_append_from_tables(a, view, s);
         if (st != GG_OK) return st;
     }

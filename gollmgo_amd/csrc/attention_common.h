@@ -122,7 +122,7 @@ gg_status_t launch_append_from_tables(const AttnArgs& a, const KVView& kv, hipSt
 // from the block table; entries outside the pool are skipped). Same conversions as gg_kv_append: rounding to the pool type, FP8 as
 // E4M3-satfinite of x * (1 / per-head scale). Not for PER_BLOCK INT8 pools; head_dim a
 // multiple of 8 and 16-byte aligned rows (checked by the entry point). Run by a whole
-// workgroup; the caller orders it before any read of those rows.
+// workgroup; launched before the attention that reads those rows.
 __device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView& kv, int b, int kvh) {
     const int ctx = seq_keys(a, b, kv.bs);
     const int nrows = a.row_counts ? a.row_counts[b] : a.rows;

@@ -701,11 +701,6 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(Attn
     const int nparts = (ctx + P - 1) / P;
     if (part >= nparts) return;
     const PieceDesc d{b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1};
-    if (a.fuse_append) {  // (only with one piece per item)
-        append_item_rows(a, kv, b, kvh);
-        __threadfence_block();
-        __syncthreads();
-    }
     PieceIn<DT> in;
     PieceIO<DT>::start(a, kv, d, in);
     attn_piece<DT, NT>(a, kv, d, in);
@@ -885,12 +880,8 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     seq[0] = pos;
     seq[1] = np;
     int4* table = (int4*)lpt_table(plan);
-    // Cuts at equal shares of the chunks, none after the first chunk that holds a draft row
-    // (position ctx - rows): the final piece covers them all.
-    const int last_cut = max(ctx - a.rows, 0) / tok;
     for (int j = 0; j < np; ++j) {
-        const int c0 = j == 0 ? 0 : min((int)((long long)j * nch / np), last_cut);
-        const int c1 = j + 1 == np ? nch : min((int)((long long)(j + 1) * nch / np), last_cut);
+        const int c0 = (int)((long long)j * nch / np), c1 = (int)((long long)(j + 1) * nch / np);
         const int t0 = c0 * tok, t1 = min(c1 * tok, ctx);
         for (int h = 0; h < Hkv; ++h) table[pos + j * Hkv + h] = make_int4(b, h | (np << 16), t0, t1);
     }
@@ -908,23 +899,8 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     if (b < 0) return;  // past the last piece
     const int kvh = e.y & 0xffff, np = e.y >> 16;
     const PieceDesc d{b, kvh, e.z, e.w, -1, np > 1 ? p : -1};
-    // The item's final piece holds every chunk its draft rows land in (the plan cuts no
-    // later than the first of them), so it appends them itself before reading them.
     PieceIn<DT> in;
-    if (a.fuse_append && e.w >= seq_keys(a, b, kBS)) {
-        // The first chunks' loads go out first when they end before the draft rows (the
-        // usual case); the rows' own chunks are read only after the barrier.
-        constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
-        const int nr = a.row_counts ? a.row_counts[b] : a.rows;
-        const bool early = e.z + 2 * kWaves * kTok <= e.w - nr;
-        if (early) PieceIO<DT>::start(a, kv, d, in);
-        append_item_rows(a, kv, b, kvh);
-        __threadfence_block();
-        __syncthreads();
-        if (!early) PieceIO<DT>::start(a, kv, d, in);
-    } else {
-        PieceIO<DT>::start(a, kv, d, in);
-    }
+    PieceIO<DT>::start(a, kv, d, in);
     attn_piece<DT, NT>(a, kv, d, in);
 }
 

@@ -293,7 +293,6 @@ static gg_status_t verify_attention_impl(gg_kv_t kv, int layer, const void* q, g
         a.k_new = k_new;
         a.v_new = v_new;
         a.new_dtype = new_dtype;
-        a.fuse_append = attn_can_fuse_append(a) ? 1 : 0;
     }
     if (call == ATTN_CALL_PLAN_ONLY) return launch_attn_plan(a, (hipStream_t)stream);
     return launch_verify_attention(a, (hipStream_t)stream);

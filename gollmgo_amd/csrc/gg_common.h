@@ -86,12 +86,10 @@ struct AttnArgs {
     int sk_min_chunks;    // least chunks a stream-K workgroup takes
     // Draft-KV rows appended by the same call (gg_verify_append_attention_planned): row
     // b*rows + j (j < the sequence's row count) is key position ctx - row_count + j, its
-    // slot taken from the block table. fuse_append: written by the workgroup of each item's
-    // final piece before it reads them, else by a launch of its own before the attention.
+    // slot taken from the block table; a launch of their own precedes the attention.
     const void* k_new;
     const void* v_new;
     gg_dtype_t new_dtype;
-    int fuse_append;
 };
 // Attention schedules on the MFMA path (the generic path always uses the grid).
 enum { ATTN_SCHED_GRID = 0, ATTN_SCHED_STREAMK = 1, ATTN_SCHED_LPT = 2 };
@@ -108,7 +106,6 @@ size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_head
                             int max_blocks, int partition);
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s);
 gg_status_t launch_attn_plan(const AttnArgs& a, hipStream_t s);  // no-op unless LPT
-bool attn_can_fuse_append(const AttnArgs& a);  // the schedule gives each item one final piece
 
 size_t greedy_workspace_bytes(int num_seqs, int max_drafts, int vocab);
 gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs, int max_drafts,
