@@ -62,6 +62,9 @@ SIGNATURES = {
     "gg_kv_layer_bytes": (_sz, [_vp]),
     "gg_kv_set_head_scales": (_i, [_vp, _i, C.POINTER(_f), C.POINTER(_f)]),
     "gg_kv_append": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    "gg_kv_snapshot_bytes": (_sz, [_vp, _i]),
+    "gg_kv_snapshot": (_i, [_vp, _vp, _i, _vp, _sz, _vp, _vp]),
+    "gg_kv_restore": (_i, [_vp, _vp, _i, _vp, _sz, _vp, _vp]),
     "gg_verify_attention_workspace_size": (_sz, [_vp, _i, _i, _i, _i, _i]),
     "gg_verify_attention": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i,
                                  _vp, _sz, _vp]),

@@ -184,6 +184,37 @@ GG_API gg_status_t gg_kv_set_head_scales(gg_kv_t kv, int layer, const float* k_s
                      "upload V scales");
 }
 
+GG_API size_t gg_kv_snapshot_bytes(gg_kv_t kv, int num_blocks) {
+    if (!kv || num_blocks < 0) return 0;
+    return (size_t)num_blocks * kv->num_layers * kv_swap_record_bytes(kv);
+}
+
+static gg_status_t kv_swap_check(gg_kv_t kv, const int32_t* block_ids, int num_blocks, void* staging,
+                                 size_t staging_bytes, const char* who) {
+    GG_CHECK_ARG(kv != nullptr, who);
+    GG_CHECK_ARG(num_blocks >= 0 && num_blocks <= (1 << 24), "KV swap: bad block count");
+    GG_CHECK_ARG(num_blocks == 0 || (block_ids && staging), "KV swap: NULL buffer");
+    GG_CHECK_ARG(((uintptr_t)staging % 16) == 0, "KV swap: staging must be 16-byte aligned");
+    GG_CHECK_ARG(staging_bytes >= gg_kv_snapshot_bytes(kv, num_blocks), "KV swap: staging too small");
+    return GG_OK;
+}
+
+GG_API gg_status_t gg_kv_snapshot(gg_kv_t kv, const int32_t* block_ids, int num_blocks, void* staging,
+                                  size_t staging_bytes, void* host_dst, void* stream) {
+    clear_error();
+    const gg_status_t st = kv_swap_check(kv, block_ids, num_blocks, staging, staging_bytes, "gg_kv_snapshot: kv is NULL");
+    if (st != GG_OK || num_blocks == 0) return st;
+    return launch_kv_snapshot(kv, block_ids, num_blocks, staging, host_dst, (hipStream_t)stream);
+}
+
+GG_API gg_status_t gg_kv_restore(gg_kv_t kv, const int32_t* block_ids, int num_blocks, void* staging,
+                                 size_t staging_bytes, const void* host_src, void* stream) {
+    clear_error();
+    const gg_status_t st = kv_swap_check(kv, block_ids, num_blocks, staging, staging_bytes, "gg_kv_restore: kv is NULL");
+    if (st != GG_OK || num_blocks == 0) return st;
+    return launch_kv_restore(kv, block_ids, num_blocks, staging, host_src, (hipStream_t)stream);
+}
+
 GG_API gg_status_t gg_kv_append(gg_kv_t kv, int layer, const void* k, const void* v,
                                 gg_dtype_t src_dtype, const int32_t* slot_mapping, int n_rows,
                                 void* stream) {

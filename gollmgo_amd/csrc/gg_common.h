@@ -56,6 +56,10 @@ __host__ __device__ inline bool is_float_io(gg_dtype_t t) {
 }
 
 // ---- launchers (defined in the .hip files) ----
+size_t kv_swap_record_bytes(const KV* kv);  // one (block, layer) record of a KV snapshot
+gg_status_t launch_kv_snapshot(KV* kv, const int32_t* ids, int n, void* staging, void* host_dst, hipStream_t s);
+gg_status_t launch_kv_restore(KV* kv, const int32_t* ids, int n, void* staging, const void* host_src,
+                              hipStream_t s);
 gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg_dtype_t src,
                              const int32_t* slots, int n_rows, hipStream_t s);
 

@@ -139,6 +139,33 @@ class KVCache:
                                  _dev(slot_mapping, "slot_mapping", torch.int32), n, _stream(stream)),
               "gg_kv_append")
 
+    def snapshot_bytes(self, num_blocks: int) -> int:
+        return lib().gg_kv_snapshot_bytes(self.handle, num_blocks)
+
+    def snapshot(self, block_ids: torch.Tensor, host: Optional[torch.Tensor] = None,
+                 staging: Optional[torch.Tensor] = None, stream: Optional[torch.cuda.Stream] = None):
+        """Snapshot of the given blocks over every layer (gg_kv_snapshot): returns
+        (staging, host); `host` (uint8, ideally pinned) receives a copy when given."""
+        n = int(block_ids.numel())
+        nbytes = self.snapshot_bytes(n)
+        if staging is None:
+            staging = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+        if host is not None and host.numel() < nbytes:
+            raise ValueError("host buffer too small")
+        check(lib().gg_kv_snapshot(self.handle, _dev(block_ids, "block_ids", torch.int32), n, staging.data_ptr(),
+                                   staging.numel(), host.data_ptr() if host is not None else None,
+                                   _stream(stream)), "gg_kv_snapshot")
+        return staging, host
+
+    def restore(self, block_ids: torch.Tensor, staging: torch.Tensor, host: Optional[torch.Tensor] = None,
+                stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Writes a snapshot back into blocks `block_ids` (gg_kv_restore), from `host` when
+        given (through `staging`), else from `staging`."""
+        n = int(block_ids.numel())
+        check(lib().gg_kv_restore(self.handle, _dev(block_ids, "block_ids", torch.int32), n, staging.data_ptr(),
+                                  staging.numel(), host.data_ptr() if host is not None else None,
+                                  _stream(stream)), "gg_kv_restore")
+
     def attention_workspace(self, num_seqs: int, rows_per_seq: int, num_q_heads: int,
                             max_blocks_per_seq: int, partition_tokens: int = 0) -> torch.Tensor:
         n = lib().gg_verify_attention_workspace_size(self.handle, num_seqs, rows_per_seq, num_q_heads,

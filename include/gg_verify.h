@@ -107,6 +107,26 @@ void* gg_kv_v_scale_ptr(gg_kv_t kv, int layer);
  * occupies twice that. */
 size_t gg_kv_layer_bytes(gg_kv_t kv);
 
+/* KV swap (preemption with swap semantics). Replaces SnapshotKV / RestoreKV
+ * (internal/backend/cuda/swap_bridge.go:53-153; interface internal/backend/runner.go:
+ * 94-106). A snapshot of num_blocks blocks holds, for block i of block_ids (device
+ * int32[num_blocks]) and every layer, that block's K and V tiles of all kv heads (plus
+ * its fp16 K/V scales for PER_BLOCK pools), as gg_kv_snapshot_bytes(kv, num_blocks)
+ * bytes ordered [block i][layer]; PER_HEAD scales stay with the pool.
+ *   gg_kv_snapshot: gathers the blocks into `staging` (device, 16-byte aligned, at least
+ *                   gg_kv_snapshot_bytes) and, if host_dst is not NULL, copies it there
+ *                   (hipMemcpyAsync on `stream`: pinned host memory makes it truly
+ *                   asynchronous). Ids outside the pool give zero records.
+ *   gg_kv_restore:  the reverse: host_src (if not NULL) -> staging -> blocks block_ids
+ *                   (any ids, e.g. freshly allocated ones; ids outside the pool are
+ *                   skipped). The snapshot is not consumed.
+ * Both are asynchronous on `stream`; call gg_sync before reusing host buffers. */
+size_t gg_kv_snapshot_bytes(gg_kv_t kv, int num_blocks);
+gg_status_t gg_kv_snapshot(gg_kv_t kv, const int32_t* block_ids, int num_blocks, void* staging,
+                           size_t staging_bytes, void* host_dst, void* stream);
+gg_status_t gg_kv_restore(gg_kv_t kv, const int32_t* block_ids, int num_blocks, void* staging,
+                          size_t staging_bytes, const void* host_src, void* stream);
+
 /* PER_HEAD only: upload host arrays k_scales[num_kv_heads], v_scales[num_kv_heads]
  * (synchronous). Scales must be finite and > 0. */
 gg_status_t gg_kv_set_head_scales(gg_kv_t kv, int layer, const float* k_scales,
