@@ -112,16 +112,12 @@ GG_API gg_status_t gg_kv_create(int num_layers, int num_blocks, int block_size, 
         if (st == GG_OK) st = check_hip(hipMalloc(&kv->v_scales, b), "hipMalloc(V scales)");
         if (st == GG_OK) st = check_hip(hipMemset(kv->k_scales, 0, b), "scales init");
         if (st == GG_OK) st = check_hip(hipMemset(kv->v_scales, 0, b), "scales init");
-        size_t ab = (size_t)num_blocks * num_kv_heads * 2 * sizeof(float);
-        if (st == GG_OK) st = check_hip(hipMalloc((void**)&kv->block_amax, ab), "hipMalloc(amax)");
-        if (st == GG_OK) st = check_hip(hipMemset(kv->block_amax, 0, ab), "amax init");
     }
     if (st != GG_OK) {
         std::string msg = t_last_error;
         (void)hipFree(kv->k_pool);
         (void)hipFree(kv->k_scales);
         (void)hipFree(kv->v_scales);
-        (void)hipFree(kv->block_amax);
         delete kv;
         set_error(msg);
         return st;
@@ -136,7 +132,6 @@ GG_API gg_status_t gg_kv_destroy(gg_kv_t kv) {
     (void)hipFree(kv->k_pool);
     (void)hipFree(kv->k_scales);
     (void)hipFree(kv->v_scales);
-    (void)hipFree(kv->block_amax);
     delete kv;
     return GG_OK;
 }

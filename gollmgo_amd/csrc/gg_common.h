@@ -37,7 +37,6 @@ struct KV {
     uint8_t* v_pool = nullptr;    // k_pool + tile_bytes (inside that allocation)
     void* k_scales = nullptr;     // PER_HEAD: float[layers][Hkv]; PER_BLOCK: u16[layers][blocks][Hkv]
     void* v_scales = nullptr;
-    float* block_amax = nullptr;  // PER_BLOCK staging: float[blocks][Hkv][2], kept at zero between calls
 };
 
 __host__ __device__ inline size_t dtype_bytes(gg_dtype_t t) {

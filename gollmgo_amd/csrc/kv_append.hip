@@ -39,7 +39,6 @@ struct AppendArgs {
     const float* v_inv;
     uint16_t* k_bscale;    // PER_BLOCK fp16 scales [blocks][Hkv]
     uint16_t* v_bscale;
-    float* amax;           // PER_BLOCK staging [blocks][Hkv][2]
 };
 
 // Plain / per-head-scaled append: grid (n_rows), one thread per (head, dim) element.
@@ -156,121 +155,121 @@ void launch_vec(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
     }
 }
 
-// ---- PER_BLOCK int8: three passes (amax, quantise/requantise, publish) ----
-
-__device__ __forceinline__ float warp_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
-// Pass A: per (row, head) amax of K and V, folded into the block's staging slot.
-// Non-negative floats order like their bit patterns, so atomicMax on the bits is exact.
-__global__ void __launch_bounds__(64) append_amax_kernel(AppendArgs a) {
-    const int r = blockIdx.x, h = blockIdx.y;
-    const int slot = a.slots[r];
-    if (slot < 0 || slot >= a.num_slots) return;
-    const int blk = slot / a.bs;
-    float mk = 0.f, mv = 0.f;
-    for (int d = threadIdx.x; d < a.D; d += 64) {
-        size_t i = ((size_t)r * a.Hkv + h) * a.D + d;
-        float kx = fabsf(load_as_f32(a.k, a.src, i));
-        float vx = fabsf(load_as_f32(a.v, a.src, i));
-        mk = fmaxf(mk, kx == kx ? kx : 0.f);
-        mv = fmaxf(mv, vx == vx ? vx : 0.f);
-    }
-    mk = warp_max(mk);
-    mv = warp_max(mv);
-    if (threadIdx.x == 0) {
-        unsigned int* p = (unsigned int*)(a.amax + ((size_t)blk * a.Hkv + h) * 2);
-        atomicMax(p, __float_as_uint(fminf(mk, 3.0e38f)));
-        atomicMax(p + 1, __float_as_uint(fminf(mv, 3.0e38f)));
-    }
-}
+// ---- PER_BLOCK int8: one launch ----
+//
+// A block's new rows are adjacent in the slot mapping (the verify rows of a sequence are),
+// so the first row of each run of rows in one block (its leader) owns the block for the
+// call. Workgroup (r, h) exits unless row r leads a run; otherwise, for kv head h: amax of
+// the run's K and V over its rows and dims, the block's new scale max(old, fp16(amax /
+// 127)), the run's rows quantised with it, the rows already in the block re-quantised
+// when the scale grew, and the scale published. No atomics, no staging.
 
 __device__ __forceinline__ uint16_t f32_to_f16_rne_bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// The leader of row r is the first row of the run of adjacent rows in the same block.
-__device__ __forceinline__ int find_leader(const int32_t* slots, int r, int bs) {
-    const int blk = slots[r] / bs;
-    int l = r;
-    while (l > 0) {
-        int s = slots[l - 1];
-        if (s < 0 || s / bs != blk) break;  // out-of-range slots never match a valid block
-        --l;
-    }
-    return l;
-}
+__device__ __forceinline__ bool slot_ok(int s, long long num_slots) { return s >= 0 && s < num_slots; }
 
-struct BlockScale {
-    float old_s, new_s, inv_new;
-};
-
-__device__ __forceinline__ BlockScale block_scale(const AppendArgs& a, int blk, int h, int which,
-                                                  bool fresh) {
-    const uint16_t* sc = which == 0 ? a.k_bscale : a.v_bscale;
-    float old_s = fresh ? 0.f : f16_bits_to_f32(sc[(size_t)blk * a.Hkv + h]);
-    float am = a.amax[((size_t)blk * a.Hkv + h) * 2 + which];
-    float cand = f16_bits_to_f32(f32_to_f16_rne_bits(am / 127.0f));
-    BlockScale b;
-    b.old_s = old_s;
-    b.new_s = fmaxf(old_s, cand);
-    b.inv_new = b.new_s > 0.f ? 1.0f / b.new_s : 0.f;
-    return b;
-}
-
-// Pass B: quantise every new row with its block's new scale; the leader row also
-// re-quantises the tokens that were already in the block when the scale grew.
 __global__ void __launch_bounds__(256) append_int8_block_kernel(AppendArgs a) {
-    const int r = blockIdx.x;
+    const int r = blockIdx.x, h = blockIdx.y;
     const int slot = a.slots[r];
-    if (slot < 0 || slot >= a.num_slots) return;
-    const int blk = slot / a.bs, off = slot % a.bs;
-    const int lead = find_leader(a.slots, r, a.bs);
-    const int lead_off = a.slots[lead] % a.bs;
+    if (!slot_ok(slot, a.num_slots)) return;
+    const int blk = slot / a.bs;
+    if (r > 0) {
+        const int p = a.slots[r - 1];
+        if (slot_ok(p, a.num_slots) && p / a.bs == blk) return;  // not the run's leader
+    }
+    int len = 1;
+    while (r + len < a.n_rows) {
+        const int q = a.slots[r + len];
+        if (!slot_ok(q, a.num_slots) || q / a.bs != blk) break;
+        ++len;
+    }
+    const int lead_off = slot % a.bs;
     const bool fresh = lead_off == 0;
     int8_t* kc = (int8_t*)a.kc;
     int8_t* vc = (int8_t*)a.vc;
-    const int n = a.Hkv * a.D;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const int h = i / a.D, d = i % a.D;
-        BlockScale ks = block_scale(a, blk, h, 0, fresh);
-        BlockScale vs = block_scale(a, blk, h, 1, fresh);
-        const size_t src_i = (size_t)r * n + i;
-        kc[k_index(blk, h, off, d, a.Hkv, a.bs, a.D)] = f32_to_i8_sat(load_as_f32(a.k, a.src, src_i) * ks.inv_new);
-        vc[v_index(blk, h, off, d, a.Hkv, a.bs, a.D)] = f32_to_i8_sat(load_as_f32(a.v, a.src, src_i) * vs.inv_new);
-        if (r == lead && lead_off > 0) {
-            for (int t = 0; t < lead_off; ++t) {
-                if (ks.new_s != ks.old_s) {
-                    size_t ki = k_index(blk, h, t, d, a.Hkv, a.bs, a.D);
-                    kc[ki] = f32_to_i8_sat(((float)kc[ki] * ks.old_s) * ks.inv_new);
-                }
-                if (vs.new_s != vs.old_s) {
-                    size_t vi = v_index(blk, h, t, d, a.Hkv, a.bs, a.D);
-                    vc[vi] = f32_to_i8_sat(((float)vc[vi] * vs.old_s) * vs.inv_new);
-                }
+    const int nel = len * a.D;
+    __shared__ float red[2][4];
+    // The run's values (at most 8 per thread for runs of <= 2048 elements) stay in registers
+    // between the amax and the quantisation.
+    constexpr int kCache = 8;
+    const bool cached = nel <= kCache * 256;
+    float kv_k[kCache], kv_v[kCache];
+    float mk = 0.f, mv = 0.f;
+#pragma unroll
+    for (int c = 0; c < kCache; ++c) {
+        const int i = threadIdx.x + c * 256;
+        kv_k[c] = kv_v[c] = 0.f;
+        if (cached && i < nel) {
+            const int j = i / a.D, d = i % a.D;
+            const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
+            kv_k[c] = load_as_f32(a.k, a.src, src);
+            kv_v[c] = load_as_f32(a.v, a.src, src);
+        }
+    }
+    for (int i = threadIdx.x; i < nel; i += blockDim.x) {
+        float kx, vx;
+        if (cached) {
+            kx = kv_k[(i - threadIdx.x) / 256];
+            vx = kv_v[(i - threadIdx.x) / 256];
+        } else {
+            const int j = i / a.D, d = i % a.D;
+            const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
+            kx = load_as_f32(a.k, a.src, src);
+            vx = load_as_f32(a.v, a.src, src);
+        }
+        kx = fabsf(kx);
+        vx = fabsf(vx);
+        mk = fmaxf(mk, kx == kx ? kx : 0.f);
+        mv = fmaxf(mv, vx == vx ? vx : 0.f);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        mk = fmaxf(mk, __shfl_xor(mk, o));
+        mv = fmaxf(mv, __shfl_xor(mv, o));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red[0][threadIdx.x >> 6] = mk;
+        red[1][threadIdx.x >> 6] = mv;
+    }
+    __syncthreads();
+    mk = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    mv = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    mk = fminf(mk, 3.0e38f);
+    mv = fminf(mv, 3.0e38f);
+    const size_t si = (size_t)blk * a.Hkv + h;
+    const float k_old = fresh ? 0.f : f16_bits_to_f32(a.k_bscale[si]);
+    const float v_old = fresh ? 0.f : f16_bits_to_f32(a.v_bscale[si]);
+    const float k_new = fmaxf(k_old, f16_bits_to_f32(f32_to_f16_rne_bits(mk / 127.0f)));
+    const float v_new = fmaxf(v_old, f16_bits_to_f32(f32_to_f16_rne_bits(mv / 127.0f)));
+    const float k_inv = k_new > 0.f ? 1.0f / k_new : 0.f;
+    const float v_inv = v_new > 0.f ? 1.0f / v_new : 0.f;
+    for (int i = threadIdx.x; i < nel; i += blockDim.x) {
+        const int j = i / a.D, d = i % a.D;
+        const int off = lead_off + j;
+        const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
+        const float kx = cached ? kv_k[(i - threadIdx.x) / 256] : load_as_f32(a.k, a.src, src);
+        const float vx = cached ? kv_v[(i - threadIdx.x) / 256] : load_as_f32(a.v, a.src, src);
+        kc[k_index(blk, h, off, d, a.Hkv, a.bs, a.D)] = f32_to_i8_sat(kx * k_inv);
+        vc[v_index(blk, h, off, d, a.Hkv, a.bs, a.D)] = f32_to_i8_sat(vx * v_inv);
+    }
+    // Rows already in the block follow a grown scale.
+    if (lead_off > 0 && (k_new != k_old || v_new != v_old)) {
+        for (int i = threadIdx.x; i < lead_off * a.D; i += blockDim.x) {
+            const int t = i / a.D, d = i % a.D;
+            if (k_new != k_old) {
+                const size_t ki = k_index(blk, h, t, d, a.Hkv, a.bs, a.D);
+                kc[ki] = f32_to_i8_sat(((float)kc[ki] * k_old) * k_inv);
+            }
+            if (v_new != v_old) {
+                const size_t vi = v_index(blk, h, t, d, a.Hkv, a.bs, a.D);
+                vc[vi] = f32_to_i8_sat(((float)vc[vi] * v_old) * v_inv);
             }
         }
     }
-}
-
-// Pass C: leaders publish the new block scales and clear the staging slots.
-__global__ void __launch_bounds__(64) append_int8_publish_kernel(AppendArgs a) {
-    const int r = blockIdx.x;
-    const int slot = a.slots[r];
-    if (slot < 0 || slot >= a.num_slots) return;
-    const int lead = find_leader(a.slots, r, a.bs);
-    if (lead != r) return;
-    const int blk = slot / a.bs;
-    const bool fresh = (slot % a.bs) == 0;
-    for (int h = threadIdx.x; h < a.Hkv; h += blockDim.x) {
-        BlockScale ks = block_scale(a, blk, h, 0, fresh);
-        BlockScale vs = block_scale(a, blk, h, 1, fresh);
-        a.k_bscale[(size_t)blk * a.Hkv + h] = f32_to_f16_rne_bits(ks.new_s);
-        a.v_bscale[(size_t)blk * a.Hkv + h] = f32_to_f16_rne_bits(vs.new_s);
-        a.amax[((size_t)blk * a.Hkv + h) * 2 + 0] = 0.f;
-        a.amax[((size_t)blk * a.Hkv + h) * 2 + 1] = 0.f;
+    if (threadIdx.x == 0) {
+        a.k_bscale[si] = f32_to_f16_rne_bits(k_new);
+        a.v_bscale[si] = f32_to_f16_rne_bits(v_new);
     }
 }
 
@@ -303,10 +302,7 @@ gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg
     if (kv->scale_mode == GG_SCALE_PER_BLOCK) {
         a.k_bscale = (uint16_t*)kv->k_scales + (size_t)layer * kv->scale_layer_elems;
         a.v_bscale = (uint16_t*)kv->v_scales + (size_t)layer * kv->scale_layer_elems;
-        a.amax = kv->block_amax;
-        append_amax_kernel<<<dim3(n_rows, kv->num_kv_heads), 64, 0, s>>>(a);
-        append_int8_block_kernel<<<n_rows, 256, 0, s>>>(a);
-        append_int8_publish_kernel<<<n_rows, 64, 0, s>>>(a);
+        append_int8_block_kernel<<<dim3(n_rows, kv->num_kv_heads), 256, 0, s>>>(a);
     } else if (a.D % 8 == 0 && a.dst != GG_DTYPE_INT8 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0) {
         switch (src) {
             case GG_DTYPE_F32: launch_vec<GG_DTYPE_F32>(a, a.dst, s); break;
