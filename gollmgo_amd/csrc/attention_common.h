@@ -166,14 +166,18 @@ __device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView
         const size_t ki = kv.tile0(blk, kvh) + (size_t)off * D + d0;
         const size_t vi = kv.tile0(blk, kvh) + (size_t)d0 * bs + off;
         if (kv.dt == GG_DTYPE_FP8_E4M3) {
-            uint32_t w0 = 0, w1 = 0;
+            uint32_t w[2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t q = f32_to_fp8e4m3_sat(kx[e] * kinv);
-                if (e < 4) w0 |= q << (8 * e); else w1 |= q << (8 * (e - 4));
-                vc[vi + (size_t)e * bs] = f32_to_fp8e4m3_sat(vx[e] * vinv);
+            for (int e = 0; e < 8; e += 4)
+                w[e >> 2] = f32x2_to_fp8e4m3_sat(kx[e] * kinv, kx[e + 1] * kinv) |
+                            (f32x2_to_fp8e4m3_sat(kx[e + 2] * kinv, kx[e + 3] * kinv) << 16);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t vw = f32x2_to_fp8e4m3_sat(vx[e] * vinv, vx[e + 1] * vinv);
+                vc[vi + (size_t)e * bs] = (uint8_t)vw;
+                vc[vi + (size_t)(e + 1) * bs] = (uint8_t)(vw >> 8);
             }
-            *(uint2*)(kc + ki) = make_uint2(w0, w1);
+            *(uint2*)(kc + ki) = make_uint2(w[0], w[1]);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {

@@ -183,34 +183,21 @@ __device__ __forceinline__ float fp8e4m3_to_f32(uint8_t b) {
     return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
-// fp32 -> E4M3 with round-to-nearest-even and saturation to +-448 (the
-// __NV_SATFINITE convention of kernels/gollmgo_model.cu:254). NaN -> 0x7F|sign.
-__device__ __forceinline__ uint8_t f32_to_fp8e4m3_sat(float f) {
-    uint32_t u = __float_as_uint(f);
-    uint8_t sign = (uint8_t)((u >> 24) & 0x80);
-    uint32_t a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return (uint8_t)(sign | 0x7F);
-    if (a >= 0x43E00000u) return (uint8_t)(sign | 0x7E);  // >= 448 (incl. inf) saturates
-    int e = (int)(a >> 23) - 127;
-    if (e < -6) {
-        // Subnormal range: value = k * 2^-9, k in [0,8]; RNE on k.
-        float af = __uint_as_float(a);
-        float k = af * 512.0f;  // exact scaling
-        float r = __builtin_rintf(k);  // ties-to-even
-        uint32_t ki = (uint32_t)r;
-        return (uint8_t)(sign | ki);  // ki == 8 encodes the smallest normal (e=1,m=0)
-    }
-    // Normal: keep 3 mantissa bits, RNE on the remaining 20.
-    uint32_t mant = a & 0x7fffffu;
-    uint32_t keep = mant >> 20;
-    uint32_t rest = mant & 0xfffffu;
-    uint32_t half = 0x80000u;
-    uint32_t biased = (uint32_t)(e + 7);
-    uint32_t code = (biased << 3) | keep;
-    if (rest > half || (rest == half && (keep & 1))) code += 1;
-    if (code > 0x7E) code = 0x7E;
-    return (uint8_t)(sign | code);
+// fp32 -> E4M3 with round-to-nearest-even and saturation to +-448 (the __NV_SATFINITE
+// convention of kernels/gollmgo_model.cu:254), NaN -> 0x7F | sign. Two values at a time
+// (bits 0-7: a, bits 8-15: b) through the gfx950 hardware conversion v_cvt_pk_fp8_f32
+// (OCP E4M3, round to nearest even, subnormals kept): the inputs are first clamped to
+// +-448, so the conversion never overflows, and NaN inputs are mapped afterwards.
+__device__ __forceinline__ uint32_t f32x2_to_fp8e4m3_sat(float a, float b) {
+    const float ca = __builtin_amdgcn_fmed3f(a, -448.f, 448.f);
+    const float cb = __builtin_amdgcn_fmed3f(b, -448.f, 448.f);
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, 0, false) & 0xffffu;
+    if (__builtin_isnan(a)) w = (w & 0xff00u) | ((__float_as_uint(a) >> 24) & 0x80u) | 0x7Fu;
+    if (__builtin_isnan(b)) w = (w & 0x00ffu) | (((__float_as_uint(b) >> 24) & 0x80u) << 8) | 0x7F00u;
+    return w;
 }
+
+__device__ __forceinline__ uint8_t f32_to_fp8e4m3_sat(float f) { return (uint8_t)f32x2_to_fp8e4m3_sat(f, 0.f); }
 
 // Symmetric int8: round-half-even, clamp to +-127 (kernels/gollmgo_model.cu:258-268).
 __device__ __forceinline__ int8_t f32_to_i8_sat(float f) {

@@ -133,11 +133,16 @@ __global__ void __launch_bounds__(256) append_vec_kernel(AppendArgs a) {
                                                      kb[4] | ((uint32_t)kb[5] << 16), kb[6] | ((uint32_t)kb[7] << 16));
     } else {  // FP8-E4M3, per-head scales
         const float kinv = a.k_inv[h], vinv = a.v_inv[h];
-        uint32_t kw[2] = {0u, 0u};
+        uint32_t kw[2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            kw[j >> 2] |= (uint32_t)f32_to_fp8e4m3_sat(kx[j] * kinv) << (8 * (j & 3));
-            a.vc[vi + (size_t)j * a.bs] = f32_to_fp8e4m3_sat(vx[j] * vinv);
+        for (int j = 0; j < 8; j += 4)
+            kw[j >> 2] = f32x2_to_fp8e4m3_sat(kx[j] * kinv, kx[j + 1] * kinv) |
+                         (f32x2_to_fp8e4m3_sat(kx[j + 2] * kinv, kx[j + 3] * kinv) << 16);
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const uint32_t vw = f32x2_to_fp8e4m3_sat(vx[j] * vinv, vx[j + 1] * vinv);
+            a.vc[vi + (size_t)j * a.bs] = (uint8_t)vw;
+            a.vc[vi + (size_t)(j + 1) * a.bs] = (uint8_t)(vw >> 8);
         }
         *(uint2*)(a.kc + ki) = make_uint2(kw[0], kw[1]);
     }

@@ -50,6 +50,40 @@ def test_append_bit_exact(gpu, dt, src):
     kv.close()
 
 
+@pytest.mark.parametrize("D", [128, 36])  # 128: vectorised kernel; 36: one element per thread
+@pytest.mark.parametrize("scale", [1.0, 0.25])
+def test_append_fp8_edge_values(gpu, D, scale):
+    """FP8 quantise-on-write at the format's edges, bit for bit against the oracle's
+    encoder (itself pinned to torch's float8_e4m3fn cast): every code and the midpoint
+    between neighbouring codes (ties to even, subnormals included), both signs and zeros,
+    values past 448 up to infinity (saturate), NaN (0x7F | sign)."""
+    say(f"append fp8 edge values D={D} scale={scale}")
+    codes = np.arange(0, 0x7F, dtype=np.uint8)
+    vals = ora.fp8_decode(codes).astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    near = np.concatenate([np.nextafter(mids.astype(np.float32), np.float32(0)),
+                           np.nextafter(mids.astype(np.float32), np.float32(1e9))])
+    big = np.array([448.0, 448.5, 460.0, 463.99, 464.0, 470.0, 480.0, 1e6, 3.4e38, np.inf, np.nan, 0.0], np.float32)
+    x = np.concatenate([vals, mids, near, big, [2.0 ** -10, 2.0 ** -9 * 0.5, 2.0 ** -12, 1e-30]]).astype(np.float32)
+    x = np.concatenate([x, -x]) * np.float32(scale)  # x * (1/scale) recovers the value exactly
+    H, bs = 2, 16
+    per_row = H * D
+    n = (len(x) + per_row - 1) // per_row
+    flat = np.zeros(n * per_row, np.float32)
+    flat[:len(x)] = x
+    k = flat.reshape(n, H, D)
+    v = np.roll(flat, 7).reshape(n, H, D)
+    nb = (n + bs - 1) // bs + 2
+    kv = make_cache("fp8", H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    kv.set_head_scales(0, [scale] * H, [scale] * H)
+    mirror.set_head_scales(np.full(H, scale, np.float32), np.full(H, scale, np.float32))
+    slots = np.arange(bs, bs + n, dtype=np.int32)
+    append_rows(kv, mirror, k, v, slots, "f32")
+    mirror.compare_with_device()
+    kv.close()
+
+
 # ------------------------------------------------------------------ attention
 
 def run_attention_case(dt, B, R, Hq, H, D, bs, ctx, partition=0, src="f32", seed=0, q_dt="f32",
