@@ -908,22 +908,27 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
 __global__ void __launch_bounds__(128) attn_lpt_combine_kernel(AttnArgs a, int Hkv, int tok, int recs) {
     const int item = blockIdx.x;
     const int b = item / Hkv, kvh = item % Hkv;
-    if (seq_chunks(a, b, tok) == 0) return;  // no pieces
     const int* seq = lpt_seq(a.plan, recs) + 2 * b;
-    const int first = seq[0], np = seq[1];
+    const int first = seq[0], np = seq[1];  // (np == 0: no keys, no pieces)
     if (np <= 1) return;
     const int G = a.num_q_heads / Hkv;
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
     const int r = blockIdx.y * 4 + (threadIdx.x >> 5);
     const int d4 = threadIdx.x & 31;
-    if (r >= G * nrows) return;
     const int RW = G * a.rows;
+    if (r >= RW) return;
+    // Rows past row_counts[b] hold no records: their results are not stored below. The
+    // first two pieces' records are requested together (every split item has two or more).
+    const size_t q0 = (size_t)(first + kvh) * RW + r, q1 = q0 + (size_t)Hkv * RW;
+    const float2 ml0 = *(const float2*)(a.ws_ml + q0 * 2), ml1 = *(const float2*)(a.ws_ml + q1 * 2);
+    const float4 v0 = ((const float4*)(a.ws_acc + q0 * kD))[d4], v1 = ((const float4*)(a.ws_acc + q1 * kD))[d4];
+    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    if (r >= G * nrows) return;
     float M = -1e30f, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j = 0; j < np; ++j) {
         const size_t q = (size_t)(first + j * Hkv + kvh) * RW + r;
-        const float2 ml = *(const float2*)(a.ws_ml + q * 2);
-        const float4 v = ((const float4*)(a.ws_acc + q * kD))[d4];
+        const float2 ml = j == 0 ? ml0 : j == 1 ? ml1 : *(const float2*)(a.ws_ml + q * 2);
+        const float4 v = j == 0 ? v0 : j == 1 ? v1 : ((const float4*)(a.ws_acc + q * kD))[d4];
         const float mn = fmaxf(M, ml.x);
         const float fo = __expf(M - mn), fn = __expf(ml.x - mn);
         M = mn;
