@@ -464,8 +464,11 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         // Valid offsets of the lane's V block (offsets counted from the block start).
         const int nvalid_v = blk_v < 0 ? 0 : ctx - (tc + 16 * Geom::bq(g4));
 
-        // (A missing block reads block 0's scales; its tokens are masked either way.)
-        const float kblk_scale = DT == GG_DTYPE_INT8 ? cur.ksc : 1.f;
+        // (A missing block reads block 0's scales; its tokens are masked either way.) A K
+        // scale of 0 (a block never written, or one whose rows are all zero, so every K
+        // byte is 0) is taken as 1: the scores it scales are 0 either way, and masked
+        // scores must stay -inf rather than become -inf * 0 = NaN.
+        const float kblk_scale = DT == GG_DTYPE_INT8 ? (cur.ksc > 0.f ? cur.ksc : 1.f) : 1.f;
         const float vblk_scale = DT == GG_DTYPE_INT8 ? cur.vsc : 1.f;
 
         // ---- S^T = K . Q^T for kTok tokens x all row tiles; each K tile decoded once ----

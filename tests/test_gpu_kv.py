@@ -136,7 +136,8 @@ MFMA_SHAPES = [
     # (B, R, Hq, H, ctx) with D=128, bs=16 -> MFMA path (G*R <= 64)
     (3, 5, 24, 8, [40, 700, 1500]),          # 3B geometry, 1 row tile
     (4, 6, 32, 8, [100, 1030, 2047, 64]),    # 8B geometry, 2 row tiles
-    (2, 9, 32, 8, [5000, 777]),              # config-4 geometry, 3 row tiles
+    (2, 9, 32, 8, [5000, 777]),              # config-4 geometry, 3 row tiles (stream-K)
+    (32, 9, 32, 8, [37 * i % 700 + 20 for i in range(32)]),  # 3 row tiles, LPT pieces
     (2, 16, 16, 4, [300, 129]),              # 4 row tiles
     (2, 1, 8, 8, [31, 65]),                  # decode-only (R=1)
 ]
@@ -302,6 +303,56 @@ def test_attention_config_layouts(gpu):
         print(f"  config {cid}: rel err {err:.2e}")
         assert err <= TOL[cfg.kv_dtype]
         kv.close()
+
+
+@pytest.mark.parametrize("R", [1, 6, 9])  # one, two and three row tiles (G = 4, D = 128)
+def test_attention_int8_zero_scale_blocks(gpu, R):
+    """PER_BLOCK INT8 blocks whose scale is 0: a block never written (block 0, which missing
+    table entries and keys past the context read) and blocks whose rows are all zero
+    (amax 0). Masked keys in them must get weight 0, not NaN; against the oracle."""
+    say(f"attention int8 zero-scale blocks R={R}")
+    B, Hq, H, D, bs = 3, 32, 8, 128, 16
+    keys = np.array([40, 70, 10], np.int32) + R
+    nbs = [(int(k) + bs - 1) // bs for k in keys]
+    nb = sum(nbs) + 3
+    rng = np.random.default_rng(77 + R)
+    perm = 1 + rng.permutation(nb - 1)  # block 0 stays unwritten
+    bt = np.zeros((B, max(nbs) + 1), np.int32)
+    p = 0
+    for b in range(B):
+        bt[b, :nbs[b]] = perm[p:p + nbs[b]]
+        p += nbs[b]
+    kv = make_cache("int8", H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    slots, kk, vv = [], [], []
+    for b in range(B):
+        for t in range(int(keys[b])):
+            slots.append(bt[b, t // bs] * bs + t % bs)
+            zero = (b == 0 and t >= 32) or b == 2  # sequence 0's third block, all of sequence 2
+            kk.append(np.zeros((H, D), np.float32) if zero else rng.normal(0, 1, (H, D)).astype(np.float32))
+            vv.append(np.zeros((H, D), np.float32) if zero else rng.normal(0, 1, (H, D)).astype(np.float32))
+    append_rows(kv, mirror, np.stack(kk), np.stack(vv), np.array(slots, np.int32), "f32")
+    mirror.sync_from_device()
+    ks, _ = mirror.scales_for_oracle()
+    assert ks.reshape(nb, H)[bt[0, 2]].max() == 0 and ks.reshape(nb, H)[0].max() == 0
+    q = rng.normal(0, 1, (B, R, Hq, D)).astype(np.float32)
+    qt = torch.from_numpy(q).to(torch.bfloat16).cuda()
+    qh = qt.float().cpu().numpy()
+    for part in (0, 64):
+        out = torch.zeros(B, R, Hq, D, dtype=torch.float32, device="cuda")
+        kv.attention(0, qt, out, torch.from_numpy(keys).cuda(), torch.from_numpy(bt).cuda(), 1 / math.sqrt(D),
+                     partition_tokens=part)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        ksc, vsc = mirror.scales_for_oracle()
+        ref = ora.attention(qh, mirror.kc, mirror.vc, "int8", H, D, bs, keys, bt, 1 / math.sqrt(D), ksc, vsc)
+        assert np.isfinite(got).all()
+        # Sequence 2 attends to zero values only: its output is exactly 0.
+        assert not got[2].any()
+        err = rel_err_per_vector(got[:2], ref[:2])
+        print(f"  partition {part}: rel err {err:.2e}")
+        assert err <= TOL["int8"]
+    kv.close()
 
 
 @pytest.mark.parametrize("dt", ["bf16", "fp8", "int8", "f32"])
