@@ -176,6 +176,39 @@ def test_rejection_invalid_and_nonfinite(gpu):
     assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
 
 
+@pytest.mark.parametrize("seed", range(40))
+def test_acceptance_random_cases(gpu, seed):
+    """Seeded random acceptance calls (logit type, batch, drafts, vocabulary sizes around
+    the segment and vector widths, temperature, top-p, draft distributions, value spread
+    and ties), greedy and rejection, bit for bit against the oracle."""
+    r = np.random.default_rng(500 + seed)
+    dt = ["f32", "bf16", "f16"][seed % 3]
+    B = int(r.integers(1, 9))
+    K = int(r.integers(0, 9))
+    V = int(r.choice([7, 100, 2048, 4099, 8191, 8192, 8193, 20000, 65537]))
+    sd = float(r.choice([0.5, 2.0, 6.0]))
+    T = float(r.choice([0.3, 0.8, 1.0, 1.7]))
+    top_p = float(r.choice([1.0, 0.999, 0.95, 0.5, 0.1]))
+    with_q = K > 0 and bool(r.random() < 0.5)
+    say(f"acceptance random case {seed}: dt={dt} B={B} K={K} V={V} sd={sd} T={T} top_p={top_p} q={with_q}")
+    lg, host, drafts, n, q, u = rejection_case(B, K, V, dt, seed=700 + seed, with_q=with_q, sd=sd)
+    if r.random() < 0.3:  # coarse values: many ties
+        host = np.round(host)
+        lg = torch.from_numpy(host).to(TD[dt])
+        host = lg.float().numpy()
+    d_t, n_t, u_t = torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda()
+    acc, tok = gv.accept_greedy(lg.cuda(), d_t, n_t)
+    torch.cuda.synchronize()
+    ea, et = ora.accept_greedy(host, drafts, n)
+    assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
+    acc, tok = gv.accept_rejection(lg.cuda(), d_t, n_t, u_t, T, top_p,
+                                   draft_probs=torch.from_numpy(q).cuda() if q is not None else None)
+    torch.cuda.synchronize()
+    ea, et = ora.accept_rejection(host, drafts, n, u, T, top_p, q)
+    assert np.array_equal(acc.cpu().numpy(), ea)
+    assert np.array_equal(tok.cpu().numpy(), et)
+
+
 @pytest.mark.parametrize("cid", [2, 3, 4, 5])
 def test_acceptance_full_size_configs(gpu, cid):
     """Each config's acceptance at its real shape ([B, K+1, 128256] logits in the config's

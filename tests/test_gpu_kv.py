@@ -305,6 +305,36 @@ def test_attention_config_layouts(gpu):
         kv.close()
 
 
+def _random_case(seed):
+    """A seeded random attention case: pool type, geometry (MFMA tiling or not), contexts
+    (some empty or single-key), row counts, partition, query type and value spread."""
+    r = np.random.default_rng(1000 + seed)
+    dt = ["bf16", "f16", "fp8", "int8", "f32"][seed % 5]
+    H = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 4, 8]))
+    R = int(r.integers(1, 10))
+    D = 128 if dt != "f32" and r.random() < 0.8 else int(r.choice([64, 96, 128]))
+    B = int(r.integers(1, 7))
+    ctx = [int(x) for x in r.integers(0, 1500, B)]
+    if B > 1:
+        ctx[int(r.integers(0, B))] = int(r.choice([0, 1, 15, 16, 17, 63, 64, 65]))
+    rows = [int(x) for x in r.integers(0, R + 1, B)] if r.random() < 0.4 else None
+    return dict(dt=dt, B=B, R=R, Hq=H * G, H=H, D=D, bs=16, ctx=ctx, partition=int(r.choice([0, 0, 64, 256])),
+                src=str(r.choice(["f32", "bf16"])), seed=seed, q_dt=str(r.choice(["f32", "bf16", "f16"])),
+                row_counts=rows, kv_sd=float(r.choice([0.5, 1.0, 3.0])))
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_attention_random_cases(gpu, seed):
+    """Seeded random cases across pool types, geometries (both kernels), contexts, row
+    counts, partitions and query types, against the oracle at the north-star tolerances."""
+    c = _random_case(seed)
+    say(f"attention random case {seed}: {c}")
+    err = run_attention_case(**c)
+    print(f"  rel err {err:.2e}")
+    assert err <= TOL[c["dt"]]
+
+
 @pytest.mark.parametrize("R", [1, 6, 9])  # one, two and three row tiles (G = 4, D = 128)
 def test_attention_int8_zero_scale_blocks(gpu, R):
     """PER_BLOCK INT8 blocks whose scale is 0: a block never written (block 0, which missing
