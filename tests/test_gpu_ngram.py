@@ -61,3 +61,37 @@ def test_ngram_long_history_crosses_tiles(gpu):
     h[100:103] = [1, 2, 3]
     h[-2:] = [1, 2]     # the only match is far from the end (several LDS tiles back)
     assert run([h], 3, 3) == [ora.ngram_draft(h, 3, 3)]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_ngram_random_mixed(gpu, seed):
+    """Seeded batches mixing history lengths on both sides of the LDS-resident limit
+    (12288 tokens) and past the tile width, small alphabets (many matches, so chained
+    lookups run long) and large ones, odd row strides (unaligned rows), n = 2..9."""
+    r = np.random.default_rng(900 + seed)
+    n = int(r.integers(2, 10))
+    k = int(r.integers(0, 9))
+    B = int(r.integers(1, 12))
+    alphabet = int(r.choice([2, 5, 50, 32000]))
+    lens = [int(r.choice([0, 1, n - 1, n, int(r.integers(0, 4000)), 12287, 12288, 12289, int(r.integers(12289, 30000))]))
+            for _ in range(B)]
+    hists = []
+    for L in lens:
+        h = r.integers(0, alphabet, L)
+        if L > 2 * n and r.random() < 0.5:  # plant the final key far back in the history
+            pos = int(r.integers(0, L - 2 * n))
+            h[pos:pos + n - 1] = h[L - (n - 1):]
+        hists.append(h.tolist())
+    stride = max(1, max(lens)) + int(r.integers(0, 3))  # 1 or 2 extra: rows not 16-byte aligned
+    say(f"ngram random case {seed}: n={n} k={k} lens={lens} alphabet={alphabet} stride={stride}")
+    h = np.zeros((B, stride), np.int32)
+    ln = np.zeros(B, np.int32)
+    for b, x in enumerate(hists):
+        h[b, :len(x)] = x
+        ln[b] = len(x)
+    d, nn = gv.ngram_draft(torch.from_numpy(h).cuda(), torch.from_numpy(ln).cuda(), n, k)
+    torch.cuda.synchronize()
+    d, nn = d.cpu().numpy(), nn.cpu().numpy()
+    got = [d[b, :nn[b]].tolist() for b in range(B)]
+    want = [ora.ngram_draft(x, n, k) for x in hists]
+    assert got == want
