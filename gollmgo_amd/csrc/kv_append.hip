@@ -162,9 +162,9 @@ void launch_vec(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
 
 // ---- PER_BLOCK int8: one launch ----
 //
-// A block's new rows are adjacent in the slot mapping (the verify rows of a sequence are),
-// so the first row of each run of rows in one block (its leader) owns the block for the
-// call. Workgroup (r, h) exits unless row r leads a run; otherwise, for kv head h: amax of
+// A block's new rows are adjacent in the slot mapping (the verify rows of a sequence are;
+// skipped rows may sit between them), so the first row of each run of rows in one block
+// (its leader) owns the block for the call. Workgroup (r, h) exits unless row r leads a run; otherwise, for kv head h: amax of
 // the run's K and V over its rows and dims, the block's new scale max(old, fp16(amax /
 // 127)), the run's rows quantised with it, the rows already in the block re-quantised
 // when the scale grew, and the scale published. No atomics, no staging.
@@ -180,26 +180,32 @@ __global__ void __launch_bounds__(256) append_int8_block_kernel(AppendArgs a) {
     const int slot = a.slots[r];
     if (!slot_ok(slot, a.num_slots)) return;
     const int blk = slot / a.bs;
-    if (r > 0) {
-        const int p = a.slots[r - 1];
-        if (slot_ok(p, a.num_slots) && p / a.bs == blk) return;  // not the run's leader
+    // Skipped rows (negative or out-of-range slots) do not break a run: row r leads unless
+    // the nearest earlier row that is not skipped lands in the same block.
+    for (int p = r - 1; p >= 0; --p) {
+        const int q = a.slots[p];
+        if (!slot_ok(q, a.num_slots)) continue;
+        if (q / a.bs == blk) return;  // not the run's leader
+        break;
     }
-    int len = 1;
-    while (r + len < a.n_rows) {
-        const int q = a.slots[r + len];
-        if (!slot_ok(q, a.num_slots) || q / a.bs != blk) break;
-        ++len;
+    // The run spans rows [r, e): up to the next row that lands in another block.
+    int e = r + 1;
+    while (e < a.n_rows) {
+        const int q = a.slots[e];
+        if (slot_ok(q, a.num_slots) && q / a.bs != blk) break;
+        ++e;
     }
     const int lead_off = slot % a.bs;
     const bool fresh = lead_off == 0;
     int8_t* kc = (int8_t*)a.kc;
     int8_t* vc = (int8_t*)a.vc;
-    const int nel = len * a.D;
+    const int nel = (e - r) * a.D;
     __shared__ float red[2][4];
     // The run's values (at most 8 per thread for runs of <= 2048 elements) stay in registers
-    // between the amax and the quantisation.
+    // between the amax and the quantisation; skipped rows read as 0.
     constexpr int kCache = 8;
     const bool cached = nel <= kCache * 256;
+    auto row_ok = [&](int j) { return slot_ok(a.slots[r + j], a.num_slots); };
     float kv_k[kCache], kv_v[kCache];
     float mk = 0.f, mv = 0.f;
 #pragma unroll
@@ -208,21 +214,25 @@ __global__ void __launch_bounds__(256) append_int8_block_kernel(AppendArgs a) {
         kv_k[c] = kv_v[c] = 0.f;
         if (cached && i < nel) {
             const int j = i / a.D, d = i % a.D;
-            const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
-            kv_k[c] = load_as_f32(a.k, a.src, src);
-            kv_v[c] = load_as_f32(a.v, a.src, src);
+            if (row_ok(j)) {
+                const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
+                kv_k[c] = load_as_f32(a.k, a.src, src);
+                kv_v[c] = load_as_f32(a.v, a.src, src);
+            }
         }
     }
     for (int i = threadIdx.x; i < nel; i += blockDim.x) {
-        float kx, vx;
+        float kx = 0.f, vx = 0.f;
         if (cached) {
             kx = kv_k[(i - threadIdx.x) / 256];
             vx = kv_v[(i - threadIdx.x) / 256];
         } else {
             const int j = i / a.D, d = i % a.D;
-            const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
-            kx = load_as_f32(a.k, a.src, src);
-            vx = load_as_f32(a.v, a.src, src);
+            if (row_ok(j)) {
+                const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
+                kx = load_as_f32(a.k, a.src, src);
+                vx = load_as_f32(a.v, a.src, src);
+            }
         }
         kx = fabsf(kx);
         vx = fabsf(vx);
@@ -251,7 +261,9 @@ __global__ void __launch_bounds__(256) append_int8_block_kernel(AppendArgs a) {
     const float v_inv = v_new > 0.f ? 1.0f / v_new : 0.f;
     for (int i = threadIdx.x; i < nel; i += blockDim.x) {
         const int j = i / a.D, d = i % a.D;
-        const int off = lead_off + j;
+        const int sj = a.slots[r + j];
+        if (!slot_ok(sj, a.num_slots)) continue;
+        const int off = sj % a.bs;
         const size_t src = ((size_t)(r + j) * a.Hkv + h) * a.D + d;
         const float kx = cached ? kv_k[(i - threadIdx.x) / 256] : load_as_f32(a.k, a.src, src);
         const float vx = cached ? kv_v[(i - threadIdx.x) / 256] : load_as_f32(a.v, a.src, src);

@@ -140,7 +140,8 @@ gg_status_t gg_kv_set_head_scales(gg_kv_t kv, int layer, const float* k_scales,
  *   slot_mapping : device int32[n_rows]; slot = block*block_size + offset; a
  *                  negative slot skips the row.
  * PER_BLOCK pools: rows that land in the same block in one call must be adjacent
- * in slot_mapping with increasing offsets (as BlockTable.Append produces them,
+ * in slot_mapping (skipped rows may sit between them) with increasing offsets (as
+ * BlockTable.Append produces them,
  * internal/kvcache/block_table.go:24-42). Such a block's scale becomes
  * max(old scale, amax(new rows)/127) rounded to fp16; rows already in the block
  * are re-quantised to the new scale. Appends never target a block whose refcount

@@ -493,7 +493,8 @@ void ora_kv_append_q(uint8_t* kc, uint8_t* vc, int dt, int H, int D, int bs, con
         }
         return;
     }
-    /* int8 per block: process runs of adjacent rows in the same block. */
+    /* int8 per block: process runs of adjacent rows in the same block (skipped rows, slot
+     * < 0, may sit inside a run and are passed over). */
     int r = 0;
     while (r < n) {
         if (slots[r] < 0) {
@@ -502,7 +503,7 @@ void ora_kv_append_q(uint8_t* kc, uint8_t* vc, int dt, int H, int D, int bs, con
         }
         int blk = slots[r] / bs;
         int e = r;
-        while (e < n && slots[e] >= 0 && slots[e] / bs == blk) ++e;
+        while (e < n && (slots[e] < 0 || slots[e] / bs == blk)) ++e;
         int lead_off = slots[r] % bs;
         for (int h = 0; h < H; ++h) {
             for (int which = 0; which < 2; ++which) {
@@ -511,7 +512,7 @@ void ora_kv_append_q(uint8_t* kc, uint8_t* vc, int dt, int H, int D, int bs, con
                 float* sc = which ? v_bscale : k_bscale;
                 float am = 0.f;
                 for (int rr = r; rr < e; ++rr)
-                    for (int d = 0; d < D; ++d) {
+                    for (int d = 0; d < D && slots[rr] >= 0; ++d) {
                         float a = fabsf(src[((size_t)rr * H + h) * D + d]);
                         if (a == a && a > am) am = a;
                     }
@@ -526,6 +527,7 @@ void ora_kv_append_q(uint8_t* kc, uint8_t* vc, int dt, int H, int D, int bs, con
                             pool[i] = (uint8_t)ora_int8_encode(((float)(int8_t)pool[i] * old_s) * inv);
                         }
                 for (int rr = r; rr < e; ++rr) {
+                    if (slots[rr] < 0) continue;
                     int o = slots[rr] % bs;
                     for (int d = 0; d < D; ++d) {
                         size_t i = which ? v_off(blk, h, o, d, H, bs, D) : k_off(blk, h, o, d, H, bs, D);

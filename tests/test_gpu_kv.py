@@ -84,6 +84,53 @@ def test_append_fp8_edge_values(gpu, D, scale):
     kv.close()
 
 
+@pytest.mark.parametrize("seed", range(15))
+def test_append_random_cases(gpu, seed):
+    """Seeded random append sequences: pool type, block size, head count and dim, source
+    type, several calls that extend a few sequences' block runs (as BlockTable.Append
+    does, so a block's rows in one call are adjacent), skipped rows; bit for bit against
+    the mirror after every call."""
+    r = np.random.default_rng(300 + seed)
+    dt = ["f32", "f16", "bf16", "fp8", "int8"][seed % 5]
+    src = str(r.choice(["f32", "bf16", "f16"]))
+    bs = int(r.choice([8, 16, 32]))
+    H = int(r.choice([1, 2, 8]))
+    D = int(r.choice([64, 96, 128, 40]))
+    nb = 64
+    say(f"append random case {seed}: dt={dt} src={src} bs={bs} H={H} D={D}")
+    kv = make_cache(dt, H, D, bs, nb)
+    mirror = PoolMirror(kv)
+    if dt == "fp8":
+        ks = r.uniform(0.005, 0.05, H).astype(np.float32)
+        vs = r.uniform(0.005, 0.05, H).astype(np.float32)
+        kv.set_head_scales(0, ks, vs)
+        mirror.set_head_scales(ks, vs)
+    free = list(r.permutation(nb))
+    seqs = [[] for _ in range(int(r.integers(1, 5)))]  # per sequence: its blocks
+    lens = [0] * len(seqs)
+    for call in range(4):
+        slots = []
+        for i in range(len(seqs)):
+            for _ in range(int(r.integers(0, 2 * bs))):
+                if lens[i] % bs == 0:
+                    if not free:
+                        break
+                    seqs[i].append(int(free.pop()))
+                slots.append(seqs[i][-1] * bs + lens[i] % bs)
+                lens[i] += 1
+        if r.random() < 0.3 and slots:
+            slots.insert(int(r.integers(0, len(slots) + 1)), -1)  # a skipped row
+        if not slots:
+            continue
+        slots = np.array(slots, np.int32)
+        sd = float(r.choice([0.1, 1.0, 4.0])) * (call + 1)
+        k = r.normal(0, sd, (len(slots), H, D)).astype(np.float32)
+        v = r.normal(0, sd, (len(slots), H, D)).astype(np.float32)
+        append_rows(kv, mirror, k, v, slots, src)
+        mirror.compare_with_device()
+    kv.close()
+
+
 # ------------------------------------------------------------------ attention
 
 def run_attention_case(dt, B, R, Hq, H, D, bs, ctx, partition=0, src="f32", seed=0, q_dt="f32",

@@ -406,3 +406,29 @@ def test_kv_append_int8_block_scales(ora):
     assert ks[0] == s1
     want = ora.int8_encode((old.astype(np.float32) * s0) * np.float32(1 / s1))
     assert np.array_equal(K[0, 0, :2], want)
+
+
+def test_kv_append_int8_skipped_rows_inside_a_run(ora):
+    """A skipped row (slot < 0) between two rows of one block does not split the block's
+    run: the call equals the same call without the skipped row (one scale from the amax
+    of both rows, one re-quantisation)."""
+    H, D, bs, nblk = 2, 8, 8, 3
+    rng = np.random.default_rng(5)
+    first = rng.normal(0, 1, (3, H, D)).astype(np.float32)
+    rows = rng.normal(0, 1, (3, H, D)).astype(np.float32)
+    rows[2] *= 9.0  # the last row grows the scale
+    pools = []
+    for slots, kk in ((np.array([11, -1, 12, 13], np.int32), np.concatenate([rows[:1], rows[:1] * 0 + 99, rows[1:]])),
+                      (np.array([11, 12, 13], np.int32), rows)):
+        kc = np.zeros(nblk * H * bs * D, np.uint8)
+        vc = np.zeros_like(kc)
+        ks = np.zeros(nblk * H, np.float32)
+        vs = np.zeros(nblk * H, np.float32)
+        ora.kv_append_q(kc, vc, "int8", H, D, bs, first, first, np.array([8, 9, 10], np.int32), k_bscale=ks, v_bscale=vs)
+        ora.kv_append_q(kc, vc, "int8", H, D, bs, kk, kk, slots, k_bscale=ks, v_bscale=vs)
+        pools.append((kc, vc, ks, vs))
+    for x, y in zip(*pools):
+        assert np.array_equal(x, y)
+    # The block's scale is the amax of every row it holds over 127 (rounded to fp16).
+    amax = np.abs(np.concatenate([first, rows])).max(axis=(0, 2))
+    assert np.array_equal(pools[1][2][H:2 * H], ora.f16_round_c((amax / np.float32(127)).astype(np.float32)))
