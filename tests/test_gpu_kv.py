@@ -382,6 +382,29 @@ def test_attention_random_cases(gpu, seed):
     assert err <= TOL[c["dt"]]
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_attention_random_lpt_cases(gpu, seed):
+    """Seeded random batches large enough for the LPT schedule (items fill half the
+    resident workgroup slots or more): ragged short contexts, empty sequences, random row
+    counts, one to three row tiles, every MFMA pool type; against the oracle."""
+    r = np.random.default_rng(2000 + seed)
+    dt = ["bf16", "f16", "fp8", "int8"][seed % 4]
+    H = 8
+    G = int(r.choice([1, 2, 4]))
+    R = int(r.integers(1, 10))
+    B = int(r.integers(40, 120))
+    ctx = [int(x) for x in r.integers(0, 400, B)]
+    for i in r.integers(0, B, 4):
+        ctx[int(i)] = int(r.choice([0, 1, 16, 63, 64, 65, 1500]))
+    rows = [int(x) for x in r.integers(0, R + 1, B)] if r.random() < 0.5 else None
+    c = dict(dt=dt, B=B, R=R, Hq=H * G, H=H, D=128, bs=16, ctx=ctx, src="bf16", seed=seed, q_dt="bf16",
+             row_counts=rows)
+    say(f"attention random LPT case {seed}: dt={dt} B={B} R={R} G={G} rows={'ragged' if rows else 'all'}")
+    err = run_attention_case(**c)
+    print(f"  rel err {err:.2e}")
+    assert err <= TOL[dt]
+
+
 @pytest.mark.parametrize("R", [1, 6, 9])  # one, two and three row tiles (G = 4, D = 128)
 def test_attention_int8_zero_scale_blocks(gpu, R):
     """PER_BLOCK INT8 blocks whose scale is 0: a block never written (block 0, which missing
@@ -585,7 +608,7 @@ def _derived_slots(lay, rows, bs, row_counts=None):
 
 
 @pytest.mark.parametrize("cid,dt,B,ctx,rc", [
-    (3, "fp8", 64, ("uniform", 1024, 4096), False),   # LPT: final pieces append in-kernel
+    (3, "fp8", 64, ("uniform", 1024, 4096), False),   # LPT: append launch, then attention
     (5, "bf16", 64, ("uniform", 300, 2100), True),    # LPT, ragged row counts
     (2, "f16", 6, ("uniform", 512, 3000), False),     # stream-K: append launch, then attention
     (1, "f32", 4, ("list", 64, 128, 192, 256), True),  # generic path
