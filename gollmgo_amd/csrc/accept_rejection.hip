@@ -48,9 +48,11 @@ struct RowStats {
 
 constexpr int kCandCap = 4096;
 
+// Coarse-bin masses of one row. (Only the mass: weights do not increase down the bins,
+// so a bin with no mass sits where the whole row's mass lies before it and can never
+// hold the boundary; the boundary bin's element count comes from the gather.)
 struct RowHist {
     u64 mass[kBins];
-    unsigned int cnt[kBins];
 };
 
 struct RowPick {
@@ -109,8 +111,8 @@ __device__ int block_max_i(int v, int* red) {
 __device__ __forceinline__ bool finite_f(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
 // Wave 0 scans the histogram from bin `top` downward (descending key order when
-// `desc`) and returns the LAST non-empty bin whose mass-above C satisfies C < tp ||
-// C == 0; *c_above receives its C. Bins are ordered so that larger logits come first.
+// `desc`) and returns the LAST non-empty bin (count > 0; mass > 0 when cnt is null)
+// whose mass-above C satisfies C < tp || C == 0; *c_above receives its C. Bins are ordered so that larger logits come first.
 __device__ void pick_bin(const u64* mass, const unsigned int* cnt, int nbins, bool desc, u64 base,
                          u64 tp, int* out_bin, u64* out_c) {
     if (threadIdx.x >= 64) return;
@@ -131,7 +133,8 @@ __device__ void pick_bin(const u64* mass, const unsigned int* cnt, int nbins, bo
     u64 best_c = 0;
     for (int k = 0; k < per; ++k) {
         const int bn = bin_at(lane * per + k);
-        if (cnt[bn] > 0 && (c < tp || c == 0)) {
+        const bool nonempty = cnt ? cnt[bn] > 0 : mass[bn] > 0;
+        if (nonempty && (c < tp || c == 0)) {
             best = lane * per + k;
             best_c = c;
         }
@@ -454,10 +457,20 @@ __global__ void __launch_bounds__(kSegThreads) seg_max_kernel(const void* __rest
     if (threadIdx.x == 0) seg_max[(size_t)row * nseg + seg] = m;
 }
 
-__device__ __forceinline__ float row_max_from_segs(const float* seg_max, int row, int nseg) {
-    float m = -INFINITY;
-    for (int s = 0; s < nseg; ++s) m = fmaxf(m, seg_max[(size_t)row * nseg + s]);
+// Row max and weight sum over the per-segment values, by a whole wave (lane s reads
+// segment s; nseg <= 64): one load round trip rather than a chain of nseg, which every
+// block of a launch would otherwise wait for.
+__device__ __forceinline__ float row_max_wave(const float* seg_max, int row, int nseg) {
+    const int lane = threadIdx.x & 63;
+    float m = lane < nseg ? seg_max[(size_t)row * nseg + lane] : -INFINITY;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     return m;
+}
+__device__ __forceinline__ u64 row_z_wave(const u64* seg_z, int row, int nseg) {
+    const int lane = threadIdx.x & 63;
+    u64 z = lane < nseg ? seg_z[(size_t)row * nseg + lane] : 0ull;
+    for (int o = 32; o > 0; o >>= 1) z += shfl_xor_u64(z, o);
+    return z;
 }
 
 // B: per (row, segment) sum of fixed-point weights.
@@ -473,15 +486,12 @@ __global__ void __launch_bounds__(kSegThreads) seg_z_kernel(const void* __restri
     int n = n_drafts[b];
     n = n < 0 ? 0 : (n > K ? K : n);
     if (j > n) return;
-    __shared__ float s_m;
     __shared__ u64 red[kSegThreads / 64];
-    if (threadIdx.x == 0) s_m = row_max_from_segs(seg_max, row, nseg);
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    __syncthreads();
-    const float m = s_m;
+    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
     u64 z = 0;
     if (finite_f(m)) {
 #pragma unroll
@@ -517,21 +527,15 @@ __global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __re
     int n = n_drafts[b];
     n = n < 0 ? 0 : (n > K ? K : n);
     if (j > n) return;
-    __shared__ float s_m;
     __shared__ u64 red[kSegThreads / 64];
     __shared__ u64 h_mass[kBins];
-    __shared__ unsigned int h_cnt[kBins];
-    for (int i = threadIdx.x; i < kBins; i += kSegThreads) {
-        h_mass[i] = 0;
-        h_cnt[i] = 0;
-    }
-    if (threadIdx.x == 0) s_m = row_max_from_segs(seg_max, row, nseg);
+    for (int i = threadIdx.x; i < kBins; i += kSegThreads) h_mass[i] = 0;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    __syncthreads();
-    const float m = s_m;
+    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
+    __syncthreads();  // the cleared histogram
     u64 z = 0;
     if (finite_f(m)) {
 #pragma unroll
@@ -540,18 +544,14 @@ __global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __re
             const u64 w = gg_weight(x[k], m, inv_t);
             z += w;
             const int bn = gg_coarse_bin(x[k], m, inv_t);
-            atomicAdd(&h_mass[bn], w);
-            atomicAdd(&h_cnt[bn], 1u);
+            if (w) atomicAdd(&h_mass[bn], w);
         }
     }
     z = seg_block_sum(z, red);  // (its barriers also complete the LDS histogram)
     if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
     RowHist& h = hist[row];
     for (int i = threadIdx.x; i < kBins; i += kSegThreads) {
-        if (h_cnt[i]) {
-            atomicAdd(&h.mass[i], h_mass[i]);
-            atomicAdd(&h.cnt[i], h_cnt[i]);
-        }
+        if (h_mass[i]) atomicAdd(&h.mass[i], h_mass[i]);
     }
 }
 
@@ -570,9 +570,8 @@ __global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, 
     if (j > n) return;
     __shared__ int s_bin;
     __shared__ u64 s_c;
-    const float m = row_max_from_segs(seg_max, row, nseg);
-    u64 z = 0;
-    for (int s = 0; s < nseg; ++s) z += seg_z[(size_t)row * nseg + s];
+    const float m = row_max_wave(seg_max, row, nseg);
+    const u64 z = row_z_wave(seg_z, row, nseg);
     if (!finite_f(m) || z == 0) {
         if (threadIdx.x == 0) pick[row] = RowPick{-1, 0, 0, 0};
         return;
@@ -580,7 +579,7 @@ __global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, 
     const u64 tp = (u64)ceil((double)top_p * (double)z);
     if (threadIdx.x == 0) s_bin = -1;
     __syncthreads();
-    pick_bin(hist[row].mass, hist[row].cnt, kBins, false, 0, tp, &s_bin, &s_c);
+    pick_bin(hist[row].mass, nullptr, kBins, false, 0, tp, &s_bin, &s_c);
     __syncthreads();
     if (threadIdx.x == 0) pick[row] = RowPick{s_bin, 0, s_c, tp};
 }
@@ -601,19 +600,24 @@ __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __r
     if (j > n) return;
     const int cbin = pick[row].cbin;
     if (cbin < 0) return;
-    __shared__ float s_m;
-    if (threadIdx.x == 0) s_m = row_max_from_segs(seg_max, row, nseg);
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    __syncthreads();
-    const float m = s_m;
+    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
+    // One counter update per wave and element step (ballot, then each lane's rank).
+    const int lane = threadIdx.x & 63;
+    const unsigned long long below = (1ull << lane) - 1ull;
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
-        if (idx[k] >= V || !finite_f(x[k]) || gg_coarse_bin(x[k], m, inv_t) != cbin) continue;
-        const int slot = atomicAdd(&pick[row].n_cand, 1);
-        if (slot < kCandCap) cand[(size_t)row * kCandCap + slot] = make_uint2(__float_as_uint(x[k]), (unsigned)idx[k]);
+        const bool hit = idx[k] < V && finite_f(x[k]) && gg_coarse_bin(x[k], m, inv_t) == cbin;
+        const unsigned long long mask = __ballot(hit);
+        if (!mask) continue;
+        int base = 0;
+        if (lane == __ffsll((long long)mask) - 1) base = atomicAdd(&pick[row].n_cand, __popcll(mask));
+        base = __shfl(base, __ffsll((long long)mask) - 1);
+        const int slot = base + __popcll(mask & below);
+        if (hit && slot < kCandCap) cand[(size_t)row * kCandCap + slot] = make_uint2(__float_as_uint(x[k]), (unsigned)idx[k]);
     }
 }
 
@@ -638,7 +642,7 @@ __global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict
     __shared__ u64 red[1024 / 64];
     __shared__ int s_last;
     const RowPick pk = pick[row];
-    const float m = row_max_from_segs(seg_max, row, nseg);
+    const float m = row_max_wave(seg_max, row, nseg);
     if (pk.cbin < 0) {  // no finite logit or Z == 0: no nucleus
         if (threadIdx.x == 0) {
             stats[row] = RowStats{m, 0x7fffffff, 0ull, 0u, 1, 0ull};
