@@ -540,11 +540,10 @@ __global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __re
     if (finite_f(m)) {
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
-            if (!finite_f(x[k])) continue;
-            const u64 w = gg_weight(x[k], m, inv_t);
+            const bool fin = finite_f(x[k]);
+            const u64 w = fin ? gg_weight(x[k], m, inv_t) : 0ull;
             z += w;
-            const int bn = gg_coarse_bin(x[k], m, inv_t);
-            if (w) atomicAdd(&h_mass[bn], w);
+            if (w) atomicAdd(&h_mass[gg_coarse_bin(x[k], m, inv_t)], w);
         }
     }
     z = seg_block_sum(z, red);  // (its barriers also complete the LDS histogram)
@@ -605,19 +604,27 @@ __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __r
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
     const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
-    // One counter update per wave and element step (ballot, then each lane's rank).
-    const int lane = threadIdx.x & 63;
-    const unsigned long long below = (1ull << lane) - 1ull;
+    // The lane's hits as a bit mask first (vector work only), then one counter update per
+    // lane that has any, and its candidates written in order.
+    uint32_t hits = 0;
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         const bool hit = idx[k] < V && finite_f(x[k]) && gg_coarse_bin(x[k], m, inv_t) == cbin;
-        const unsigned long long mask = __ballot(hit);
-        if (!mask) continue;
-        int base = 0;
-        if (lane == __ffsll((long long)mask) - 1) base = atomicAdd(&pick[row].n_cand, __popcll(mask));
-        base = __shfl(base, __ffsll((long long)mask) - 1);
-        const int slot = base + __popcll(mask & below);
-        if (hit && slot < kCandCap) cand[(size_t)row * kCandCap + slot] = make_uint2(__float_as_uint(x[k]), (unsigned)idx[k]);
+        hits |= (uint32_t)hit << k;
+    }
+    if (hits) {
+        int slot = atomicAdd(&pick[row].n_cand, __popc(hits));
+        while (hits) {
+            const int k = __ffs(hits) - 1;
+            hits &= hits - 1;
+            float xv = 0.f;
+            int iv = 0;
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk)
+                if (kk == k) xv = x[kk], iv = idx[kk];
+            if (slot < kCandCap) cand[(size_t)row * kCandCap + slot] = make_uint2(__float_as_uint(xv), (unsigned)iv);
+            ++slot;
+        }
     }
 }
 

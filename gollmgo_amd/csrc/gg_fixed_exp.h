@@ -18,9 +18,11 @@
 
 #define GG_FIX_SCALE 34359738368.0f /* 2^35 */
 
-GG_HD float gg_expf_fixed(float x) {
-    if (!(x >= -80.0f)) return 0.0f;  // e^-80 < 2^-115: weight 0; also catches NaN
-    if (x > 0.0f) x = 0.0f;           // callers pass x <= 0
+GG_HD float gg_expf_fixed(float x_in) {
+    // e^-80 < 2^-115: weight 0 (also for NaN). Written with selects rather than an early
+    // return, so that vector code evaluates it without branching per element.
+    const bool live = x_in >= -80.0f;
+    const float x = live ? (x_in > 0.0f ? 0.0f : x_in) : 0.0f;  // callers pass x <= 0
     const float kf = __builtin_floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
     float r = __builtin_fmaf(kf, -0.693145751953125f, x);
     r = __builtin_fmaf(kf, -1.42860682030941723212e-6f, r);
@@ -38,7 +40,7 @@ GG_HD float gg_expf_fixed(float x) {
         float f;
     } s;
     s.u = (unsigned int)(k + 127) << 23;
-    return p * s.f;
+    return live ? p * s.f : 0.0f;
 }
 
 // Fixed-point weight of logit l given the row max m and 1/T (all finite).
