@@ -47,6 +47,7 @@ struct RowStats {
 };
 
 constexpr int kCandCap = 4096;
+constexpr int kFindThreads = 1024;  // draw find: threads per sequence
 
 // Coarse-bin masses of one row. (Only the mass: weights do not increase down the bins,
 // so a bin with no mass sits where the whole row's mass lies before it and can never
@@ -917,10 +918,10 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_sums_kernel(
 
 // E: per sequence: pick the segment holding floor(u * total), then the element inside it.
 // Wave 0 reduces and scans the segment sums (lane s = segment s); in the chosen segment
-// thread k owns the 32 consecutive elements [32k, 32k+32) and a block scan of the thread
-// sums finds the thread whose run crosses the target.
+// thread k of 1024 owns the 8 consecutive elements [8k, 8k+8) and a block scan of the
+// thread sums finds the thread whose run crosses the target.
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
+__global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
     const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, float inv_t,
     int use_topp, const int32_t* __restrict__ drafts, const float* __restrict__ uniforms,
     const RowStats* __restrict__ stats, const float* __restrict__ seg_max, const u64* __restrict__ seg_z,
@@ -931,7 +932,7 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __shared__ int s_seg, s_use_res, s_found;
     __shared__ u64 s_t;
-    __shared__ u64 s_wsum[kSegThreads / 64];
+    __shared__ u64 s_wsum[kFindThreads / 64];
     const SeqDecision d = dec[b];
     if (wave == 0) {
         const SegOut o = lane < nseg ? seg_out[(size_t)b * nseg + lane] : SegOut{0ull, 0ull, -1, -1};
@@ -987,11 +988,12 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
     const float* qrow = (use_res && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
     const int xr = use_res ? drafts[(size_t)b * K + d.row] : -1;
     const double zp_d = (double)rv.zp;
-    const int e0 = s_seg * kSegElems + 32 * threadIdx.x;
-    u64 r[32];
+    constexpr int kPer = kSegElems / kFindThreads;
+    const int e0 = s_seg * kSegElems + kPer * threadIdx.x;
+    u64 r[kPer];
     u64 mine = 0;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
+    for (int k = 0; k < kPer; ++k) {
         const int i = e0 + k;
         u64 w = 0;
         if (i < V) {
@@ -1023,9 +1025,9 @@ __global__ void __launch_bounds__(kSegThreads) seg_draw_find_kernel(
     const u64 t = s_t;
     if (before <= t && before + mine > t) {
         u64 c = before;
-        int found = e0 + 31;
+        int found = e0 + kPer - 1;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
+        for (int k = 0; k < kPer; ++k) {
             c += r[k];
             if (c > t) {
                 found = e0 + k;
@@ -1126,7 +1128,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     seg_draw_sums_kernel<DTV><<<dim3(nseg, num_seqs), kSegThreads, 0, s>>>(                                \
         logits, q, K, vocab, nseg, vec_ok, inv_t, use_topp, drafts, n_drafts, uniforms, w.stats,           \
         w.seg_max, w.seg_z, w.dec, w.seg_out);                                                             \
-    seg_draw_find_kernel<DTV><<<num_seqs, kSegThreads, 0, s>>>(logits, q, K, vocab, nseg, inv_t, use_topp, \
+    seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(logits, q, K, vocab, nseg, inv_t, use_topp, \
                                                                drafts, uniforms, w.stats, w.seg_max,       \
                                                                w.seg_z, w.dec, w.seg_out, out_acc, out_tok);
     switch (dt) {
