@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(64) attn_generic_kernel(AttnArgs a, KVView kv)
     const int h = blockIdx.y;
     const int z = blockIdx.z;  // b*R + j
     const int b = z / a.rows, j = z % a.rows;
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int nrows = seq_rows(a, b);
     if (j >= nrows) return;
     const int ctx = seq_keys(a, b, kv.bs);
     if (ctx <= 0 || nrows > ctx) return;
@@ -178,7 +178,7 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a, int D) {
     const int h = blockIdx.x;
     const int z = blockIdx.y;
     const int b = z / a.rows, j = z % a.rows;
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int nrows = seq_rows(a, b);
     if (j >= nrows) return;
     const int ctx = seq_keys(a, b, a.kv_bs);
     const int nparts = (ctx + a.partition - 1) / a.partition;

@@ -79,6 +79,12 @@ __device__ __forceinline__ int seq_keys(const AttnArgs& a, int b, int bs) {
     const int cap = a.max_blocks * bs;
     return c < 0 ? 0 : (c > cap ? cap : c);
 }
+// Verify rows of sequence b: row_counts[b], or rows_per_seq when the array is NULL. A count
+// above rows_per_seq gives no rows: nothing of the sequence is computed or written.
+__device__ __forceinline__ int seq_rows(const AttnArgs& a, int b) {
+    const int n = a.row_counts ? a.row_counts[b] : a.rows;
+    return n > a.rows ? 0 : n;
+}
 #endif
 
 inline bool attn_mfma_supported(const KV* kv, int rows, int num_q_heads) {
@@ -125,7 +131,7 @@ gg_status_t launch_append_from_tables(const AttnArgs& a, const KVView& kv, hipSt
 // workgroup; launched before the attention that reads those rows.
 __device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView& kv, int b, int kvh) {
     const int ctx = seq_keys(a, b, kv.bs);
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int nrows = seq_rows(a, b);
     if (ctx <= 0 || nrows <= 0 || nrows > ctx) return;
     const int D = kv.D, bs = kv.bs;
     const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;

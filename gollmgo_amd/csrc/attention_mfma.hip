@@ -27,6 +27,12 @@
 #include "attention_common.h"
 
 namespace gg {
+#ifdef GG_TRACE
+// Debug builds (-DGG_TRACE) only: the LPT kernel's per-workgroup timeline in wall-clock
+// ticks (100 MHz): [4p] start, [4p+1] end, [4p+2] CU id (__smid), [4p+3] when wave 0's
+// first chunk had arrived. gg_debug_trace_ptr gives its device address.
+__device__ long long g_trace[65536 * 4];
+#endif
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -327,7 +333,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 
     const int ctx = seq_keys(a, b, kBS);
     const int R = a.rows;
-    const int nrows = a.row_counts ? a.row_counts[b] : R;
+    const int nrows = seq_rows(a, b);
     if (nrows <= 0 || nrows > ctx) return;
     const int Hq = a.num_q_heads;
     const int G = Hq / kv.Hkv;
@@ -513,6 +519,9 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         }
         // Next chunk's K rows stream in while this chunk finishes.
         IO::load_k(kv, bl_next, kvh, cur);
+#ifdef GG_TRACE
+        if (ch == wave_u && threadIdx.x == 0) g_trace[4 * blockIdx.x + 3] = wall_clock64();
+#endif
 
         // ---- online softmax; P packed as MFMA A operands ----
         // Masked scores: causal (keys past the row's position, which covers keys past the
@@ -712,7 +721,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(Attn
 // Chunks of work of sequence b (0 when it has nothing to compute).
 __device__ __forceinline__ int seq_chunks(const AttnArgs& a, int b, int tok) {
     const int ctx = seq_keys(a, b, kBS);
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int nrows = seq_rows(a, b);
     if (nrows <= 0 || nrows > ctx) return 0;
     return (ctx + tok - 1) / tok;
 }
@@ -896,6 +905,9 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
 template <gg_dtype_t DT, int NT>
 __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
     const int p = blockIdx.x;
+#ifdef GG_TRACE
+    const long long tr_t0 = wall_clock64();
+#endif
     // One load tells the workgroup everything about its piece.
     const int4 e = ((const int4*)lpt_table(a.plan))[p];
     const int b = e.x;
@@ -905,6 +917,13 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     PieceIn<DT> in;
     PieceIO<DT>::start(a, kv, d, in);
     attn_piece<DT, NT>(a, kv, d, in);
+#ifdef GG_TRACE
+    if (threadIdx.x == 0) {
+        g_trace[4 * p + 0] = tr_t0;
+        g_trace[4 * p + 1] = wall_clock64();
+        g_trace[4 * p + 2] = (long long)__smid() | (1LL << 32);
+    }
+#endif
 }
 
 // Merge the pieces of split items; workgroup (item, y) takes rows 4y .. 4y+3.
@@ -924,7 +943,7 @@ __global__ void __launch_bounds__(128) attn_lpt_combine_kernel(AttnArgs a, int H
     const size_t q0 = (size_t)(first + kvh) * RW + r, q1 = q0 + (size_t)Hkv * RW;
     const float2 ml0 = *(const float2*)(a.ws_ml + q0 * 2), ml1 = *(const float2*)(a.ws_ml + q1 * 2);
     const float4 v0 = ((const float4*)(a.ws_acc + q0 * kD))[d4], v1 = ((const float4*)(a.ws_acc + q1 * kD))[d4];
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int nrows = seq_rows(a, b);
     if (r >= G * nrows) return;
     float M = -1e30f, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -992,7 +1011,7 @@ __global__ void __launch_bounds__(128) attn_streamk_combine_kernel(AttnArgs a, i
     const int item = blockIdx.x;
     const int b = item / Hkv, kvh = item % Hkv;
     const int G = a.num_q_heads / Hkv;
-    const int nrows = a.row_counts ? a.row_counts[b] : a.rows;
+    const int nrows = seq_rows(a, b);
     const int r = blockIdx.y * 4 + (threadIdx.x >> 5);
     const int d4 = threadIdx.x & 31;
     const int nch = seq_chunks(a, b, tok);
@@ -1102,5 +1121,13 @@ size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int nu
     if (acc_elems) *acc_elems = n_acc;
     return (((n_ml + 63) / 64) * 64 + n_acc) * sizeof(float) + plan_ints * sizeof(int);
 }
+
+#ifdef GG_TRACE
+extern "C" __attribute__((visibility("default"))) void* gg_debug_trace_ptr() {
+    void* p = nullptr;
+    (void)hipGetSymbolAddress(&p, HIP_SYMBOL(g_trace));
+    return p;
+}
+#endif
 
 }  // namespace gg

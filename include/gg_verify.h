@@ -165,7 +165,8 @@ gg_status_t gg_kv_append(gg_kv_t kv, int layer, const void* k, const void* v,
  *                 of sequence b sits at position ctx_lens[b]-row_counts[b]+j and
  *                 attends to keys [0, that position] (causal rule of
  *                 naive_attention, kernels/gollmgo_ops.cu:178). Rows j >=
- *                 row_counts[b] are not written.
+ *                 row_counts[b] are not written; a count above rows_per_seq
+ *                 (or <= 0) writes nothing of that sequence.
  *   block_tables: device int32[num_seqs][max_blocks_per_seq] of physical blocks
  *   scale       : softmax scale (1/sqrt(head_dim) in the reference)
  *   partition_tokens: split-K partition length, a multiple of 64. 0 = automatic:

@@ -223,6 +223,65 @@ def test_attention_ragged_rows(gpu, dt):
     assert err <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt,H,Hq,D,B,partition", [
+    ("fp8", 8, 32, 128, 3, 0),      # MFMA, automatic schedule (stream-K at this size)
+    ("bf16", 8, 32, 128, 600, 0),   # MFMA, LPT pieces (items fill the slots)
+    ("bf16", 8, 32, 128, 3, 256),   # MFMA, explicit partition grid
+    ("f32", 2, 8, 64, 3, 64),       # generic path
+])
+def test_attention_row_count_above_rows(gpu, dt, H, Hq, D, B, partition):
+    """A row count above rows_per_seq is no sequence at all: its output rows stay as they
+    were, and every other sequence is computed as usual."""
+    say(f"attention row_count > rows dt={dt} B={B} partition={partition}")
+    R, bs = 4, 16
+    rng = np.random.default_rng(11)
+    ctx = rng.integers(20, 700, B).astype(np.int32)
+    rc = rng.integers(1, R + 1, B).astype(np.int32)
+    bad = [1, B - 1]
+    rc[bad] = [R + 3, R + 1]
+    good_rc = rc.copy()
+    good_rc[bad] = R  # the oracle's view of the other sequences; bad rows are not compared
+    keys = ctx + np.where(rc > R, R, rc)
+    nbs = (keys + bs - 1) // bs
+    bt = np.zeros((B, int(nbs.max())), np.int32)
+    perm = rng.permutation(int(nbs.sum()) + 4)
+    p0 = 0
+    for b in range(B):
+        bt[b, :nbs[b]] = perm[p0:p0 + nbs[b]]
+        p0 += nbs[b]
+    kv = make_cache(dt, H, D, bs, int(nbs.sum()) + 4)
+    mirror = PoolMirror(kv)
+    slots = np.concatenate([bt[b, np.arange(keys[b]) // bs] * bs + np.arange(keys[b]) % bs
+                            for b in range(B)]).astype(np.int32)
+    kk = rng.normal(0, 1, (len(slots), H, D)).astype(np.float32)
+    vv = rng.normal(0, 1, (len(slots), H, D)).astype(np.float32)
+    if dt == "fp8":
+        ks, vs = per_head_amax_scales(kk), per_head_amax_scales(vv)
+        kv.set_head_scales(0, ks, vs)
+        mirror.set_head_scales(ks, vs)
+    append_rows(kv, mirror, kk, vv, slots, "bf16")
+    mirror.sync_from_device()
+    q = rng.normal(0, 1, (B, R, Hq, D)).astype(np.float32)
+    qt = torch.from_numpy(q).to(torch.bfloat16).cuda()
+    out = torch.full((B, R, Hq, D), 7.0, dtype=torch.float32, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    kv.attention(0, qt, out, torch.from_numpy(keys.astype(np.int32)).cuda(), torch.from_numpy(bt).cuda(), scale,
+                 row_counts=torch.from_numpy(rc).cuda(), partition_tokens=partition)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.all(got[bad] == 7.0), "a sequence with row_counts > rows_per_seq was written"
+    ksc, vsc = mirror.scales_for_oracle()
+    ref = ora.attention(qt.float().cpu().numpy(), mirror.kc, mirror.vc, dt, H, D, bs, keys, bt, scale, ksc, vsc,
+                        row_counts=good_rc)
+    ok = np.ones(B, bool)
+    ok[bad] = False
+    mask = (np.arange(R)[None, :] < rc[:, None]) & ok[:, None]
+    assert np.all(got[~mask & ok[:, None]] == 7.0), "rows past row_counts were written"
+    err = rel_err_per_vector(got[mask], ref[mask])
+    kv.close()
+    assert err <= TOL[dt]
+
+
 def test_attention_reference_paged_vs_naive_inputs(gpu):
     """The reference's test_paged_vs_naive inputs (srand(42), 9 tokens, 4 heads, D=16,
     block size 4, identity slots; kernels/gollmgo_paged_attn_test.cu:39-217), fp16 pool."""
