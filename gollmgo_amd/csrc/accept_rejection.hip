@@ -353,6 +353,10 @@ __global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
 
 constexpr int kSegThreads = 256;
 constexpr int kSegElems = 8192;  // 32 logits per thread
+#ifndef GG_ZHIST_SEGS
+#define GG_ZHIST_SEGS 4
+#endif
+constexpr int kZhistSegs = GG_ZHIST_SEGS;  // segments per block of the top-p weight launch
 
 struct SegOut {
     u64 sum_res;     // residual weights of the segment (final row)
@@ -522,7 +526,7 @@ __global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __re
                                                                 const int32_t* __restrict__ n_drafts,
                                                                 const float* __restrict__ seg_max,
                                                                 u64* __restrict__ seg_z, RowHist* __restrict__ hist) {
-    const int seg = blockIdx.x, row = blockIdx.y;
+    const int row = blockIdx.y;
     const int R = K + 1;
     const int b = row / R, j = row % R;
     int n = n_drafts[b];
@@ -532,23 +536,34 @@ __global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __re
     __shared__ u64 h_mass[kBins];
     for (int i = threadIdx.x; i < kBins; i += kSegThreads) h_mass[i] = 0;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    float x[32];
-    int idx[32];
-    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
+    // kZhistSegs consecutive segments per block: their weights meet in one LDS histogram,
+    // flushed to the row's once (the global atomics are the launch's cost, not the loads).
+    // The next segment's logits are requested before the current one is weighed.
+    const int seg0 = blockIdx.x * kZhistSegs;
+    const int seg1 = min(seg0 + kZhistSegs, nseg);
+    float xn[32];
+    int idxn[32];
+    load_seg<DT>(lp, V, seg0, vec_ok, xn, idxn);
+    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the first segment)
     __syncthreads();  // the cleared histogram
-    u64 z = 0;
-    if (finite_f(m)) {
+    for (int seg = seg0; seg < seg1; ++seg) {
+        float x[32];
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            const bool fin = finite_f(x[k]);
-            const u64 w = fin ? gg_weight(x[k], m, inv_t) : 0ull;
-            z += w;
-            if (w) atomicAdd(&h_mass[gg_coarse_bin(x[k], m, inv_t)], w);
+        for (int k = 0; k < 32; ++k) x[k] = xn[k];
+        if (seg + 1 < seg1) load_seg<DT>(lp, V, seg + 1, vec_ok, xn, idxn);
+        u64 z = 0;
+        if (finite_f(m)) {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const bool fin = finite_f(x[k]);
+                const u64 w = fin ? gg_weight(x[k], m, inv_t) : 0ull;
+                z += w;
+                if (w) atomicAdd(&h_mass[gg_coarse_bin(x[k], m, inv_t)], w);
+            }
         }
+        z = seg_block_sum(z, red);  // (its barriers also complete the LDS histogram)
+        if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
     }
-    z = seg_block_sum(z, red);  // (its barriers also complete the LDS histogram)
-    if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
     RowHist& h = hist[row];
     for (int i = threadIdx.x; i < kBins; i += kSegThreads) {
         if (h_mass[i]) atomicAdd(&h.mass[i], h_mass[i]);
@@ -598,13 +613,14 @@ __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __r
     int n = n_drafts[b];
     n = n < 0 ? 0 : (n > K ? K : n);
     if (j > n) return;
-    const int cbin = pick[row].cbin;
-    if (cbin < 0) return;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
+    // The boundary bin and the row max are requested after the segment.
+    const int cbin = pick[row].cbin;
+    const float m = row_max_wave(seg_max, row, nseg);
+    if (cbin < 0) return;
     // The lane's hits as a bit mask first (vector work only), then one counter update per
     // lane that has any, and its candidates written in order.
     uint32_t hits = 0;
@@ -1111,7 +1127,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     seg_max_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, n_drafts,  \
                                                                  w.seg_max, use_topp ? w.hist : nullptr);  \
     if (use_topp) {                                                                                        \
-        seg_zhist_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(                                    \
+        seg_zhist_kernel<DTV><<<dim3((nseg + kZhistSegs - 1) / kZhistSegs, rows), kSegThreads, 0, s>>>(                                    \
             logits, K, vocab, nseg, vec_ok, inv_t, n_drafts, w.seg_max, w.seg_z, w.hist);                  \
         row_pick_kernel<<<rows, kSegThreads, 0, s>>>(K, nseg, top_p, n_drafts, w.seg_max, w.seg_z, w.hist, \
                                                      w.pick);                                              \
