@@ -105,14 +105,21 @@ __global__ void __launch_bounds__(256) append_vec_kernel(AppendArgs a) {
     const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= (long long)a.n_rows * groups) return;
     const int r = (int)(gid / groups), g = (int)(gid % groups);
-    const int slot = a.slots[r];
-    if (slot < 0 || slot >= a.num_slots) return;
-    const int blk = slot / a.bs, off = slot % a.bs;
     const int i0 = g * 8, h = i0 / a.D, d0 = i0 % a.D;
+    // The source row does not depend on the slot: its loads go out together with the
+    // slot's, so the call waits for one round trip before converting, not two.
     const size_t src_i = (size_t)r * a.Hkv * a.D + i0;
     float kx[8], vx[8];
     load8<SRC>(a.k, src_i, kx);
     load8<SRC>(a.v, src_i, vx);
+    float kinv = 1.f, vinv = 1.f;
+    if constexpr (DST == GG_DTYPE_FP8_E4M3) {
+        kinv = a.k_inv[h];
+        vinv = a.v_inv[h];
+    }
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int blk = slot / a.bs, off = slot % a.bs;
     const size_t ki = k_index(blk, h, off, d0, a.Hkv, a.bs, a.D);  // 8 contiguous elements
     const size_t vi = v_index(blk, h, off, d0, a.Hkv, a.bs, a.D);  // stride bs per element
     if constexpr (DST == GG_DTYPE_F32) {
@@ -132,7 +139,6 @@ __global__ void __launch_bounds__(256) append_vec_kernel(AppendArgs a) {
         *(uint4*)((uint16_t*)a.kc + ki) = make_uint4(kb[0] | ((uint32_t)kb[1] << 16), kb[2] | ((uint32_t)kb[3] << 16),
                                                      kb[4] | ((uint32_t)kb[5] << 16), kb[6] | ((uint32_t)kb[7] << 16));
     } else {  // FP8-E4M3, per-head scales
-        const float kinv = a.k_inv[h], vinv = a.v_inv[h];
         uint32_t kw[2];
 #pragma unroll
         for (int j = 0; j < 8; j += 4)
@@ -145,6 +151,65 @@ __global__ void __launch_bounds__(256) append_vec_kernel(AppendArgs a) {
             a.vc[vi + (size_t)(j + 1) * a.bs] = (uint8_t)(vw >> 8);
         }
         *(uint2*)(a.kc + ki) = make_uint2(kw[0], kw[1]);
+    }
+}
+
+// 2-byte sources into 1- and 2-byte pools: one thread per (row, kv head, dim pair), so a
+// wave writes one head's row: its K run is 64 adjacent 2- or 4-byte stores, and each V
+// store of the wave covers one dim-major tile at a 16-offset stride (the eight-dims-per-
+// thread kernel spreads every V store of a wave over eight tiles' worth of lines).
+template <gg_dtype_t SRC, gg_dtype_t DST>
+__global__ void __launch_bounds__(256) append_pair_kernel(AppendArgs a) {
+    const int pairs = a.Hkv * a.D / 2;  // dim pairs per row
+    const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long long)a.n_rows * pairs) return;
+    const int r = (int)(gid / pairs), q = (int)(gid % pairs);
+    const int i0 = 2 * q, h = i0 / a.D, d0 = i0 % a.D;
+    const size_t src_i = (size_t)r * a.Hkv * a.D + i0;
+    const uint32_t kw = *(const uint32_t*)((const uint16_t*)a.k + src_i);
+    const uint32_t vw = *(const uint32_t*)((const uint16_t*)a.v + src_i);
+    float kinv = 1.f, vinv = 1.f;
+    if constexpr (DST == GG_DTYPE_FP8_E4M3) {
+        kinv = a.k_inv[h];
+        vinv = a.v_inv[h];
+    }
+    const int slot = a.slots[r];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int blk = slot / a.bs, off = slot % a.bs;
+    auto f = [](uint16_t b) { return SRC == GG_DTYPE_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b); };
+    const float k0 = f((uint16_t)kw), k1 = f((uint16_t)(kw >> 16));
+    const float v0 = f((uint16_t)vw), v1 = f((uint16_t)(vw >> 16));
+    const size_t ki = k_index(blk, h, off, d0, a.Hkv, a.bs, a.D);
+    const size_t vi = v_index(blk, h, off, d0, a.Hkv, a.bs, a.D);
+    if constexpr (DST == GG_DTYPE_FP8_E4M3) {
+        *(uint16_t*)(a.kc + ki) = (uint16_t)f32x2_to_fp8e4m3_sat(k0 * kinv, k1 * kinv);
+        const uint32_t vb = f32x2_to_fp8e4m3_sat(v0 * vinv, v1 * vinv);
+        a.vc[vi] = (uint8_t)vb;
+        a.vc[vi + a.bs] = (uint8_t)(vb >> 8);
+    } else {
+        uint16_t kb0, kb1, vb0, vb1;
+        if constexpr (SRC == DST) {
+            kb0 = (uint16_t)kw, kb1 = (uint16_t)(kw >> 16), vb0 = (uint16_t)vw, vb1 = (uint16_t)(vw >> 16);
+        } else {
+            kb0 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(k0) : f32_to_f16_bits(k0);
+            kb1 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(k1) : f32_to_f16_bits(k1);
+            vb0 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
+            vb1 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
+        }
+        *(uint32_t*)((uint16_t*)a.kc + ki) = kb0 | ((uint32_t)kb1 << 16);
+        ((uint16_t*)a.vc)[vi] = vb0;
+        ((uint16_t*)a.vc)[vi + a.bs] = vb1;
+    }
+}
+
+template <gg_dtype_t SRC>
+void launch_pair(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
+    const long long threads = (long long)a.n_rows * (a.Hkv * a.D / 2);
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    switch (dst) {
+        case GG_DTYPE_F16: append_pair_kernel<SRC, GG_DTYPE_F16><<<grid, 256, 0, s>>>(a); break;
+        case GG_DTYPE_BF16: append_pair_kernel<SRC, GG_DTYPE_BF16><<<grid, 256, 0, s>>>(a); break;
+        default: append_pair_kernel<SRC, GG_DTYPE_FP8_E4M3><<<grid, 256, 0, s>>>(a); break;
     }
 }
 
@@ -321,10 +386,17 @@ gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg
         a.v_bscale = (uint16_t*)kv->v_scales + (size_t)layer * kv->scale_layer_elems;
         append_int8_block_kernel<<<dim3(n_rows, kv->num_kv_heads), 256, 0, s>>>(a);
     } else if (a.D % 8 == 0 && a.dst != GG_DTYPE_INT8 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0) {
+        const bool pair = src != GG_DTYPE_F32 && a.dst != GG_DTYPE_F32;
         switch (src) {
             case GG_DTYPE_F32: launch_vec<GG_DTYPE_F32>(a, a.dst, s); break;
-            case GG_DTYPE_F16: launch_vec<GG_DTYPE_F16>(a, a.dst, s); break;
-            default: launch_vec<GG_DTYPE_BF16>(a, a.dst, s); break;
+            case GG_DTYPE_F16:
+                if (pair) launch_pair<GG_DTYPE_F16>(a, a.dst, s);
+                else launch_vec<GG_DTYPE_F16>(a, a.dst, s);
+                break;
+            default:
+                if (pair) launch_pair<GG_DTYPE_BF16>(a, a.dst, s);
+                else launch_vec<GG_DTYPE_BF16>(a, a.dst, s);
+                break;
         }
     } else {
         append_direct_kernel<<<n_rows, 256, 0, s>>>(a);
