@@ -154,20 +154,21 @@ __global__ void __launch_bounds__(256) append_vec_kernel(AppendArgs a) {
     }
 }
 
-// 2-byte sources into 1- and 2-byte pools: one thread per (row, kv head, dim pair), so a
-// wave writes one head's row: its K run is 64 adjacent 2- or 4-byte stores, and each V
-// store of the wave covers one dim-major tile at a 16-offset stride (the eight-dims-per-
-// thread kernel spreads every V store of a wave over eight tiles' worth of lines).
+// 2-byte sources into 1- and 2-byte pools: one thread per (row, kv head, dim), so a wave
+// writes 64 dims of one head's row. Its K run is 64 adjacent stores, and each V store of
+// the wave lands in a single dim-major tile at the 16-offset stride (16 or 32 bytes): the
+// fewest cache lines per store. (Eight dims per thread spread every V store of a wave over
+// eight tiles' worth of lines; two dims per thread, two.)
 template <gg_dtype_t SRC, gg_dtype_t DST>
-__global__ void __launch_bounds__(256) append_pair_kernel(AppendArgs a) {
-    const int pairs = a.Hkv * a.D / 2;  // dim pairs per row
+__global__ void __launch_bounds__(256) append_dim_kernel(AppendArgs a) {
+    const int per = a.Hkv * a.D;
     const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (long long)a.n_rows * pairs) return;
-    const int r = (int)(gid / pairs), q = (int)(gid % pairs);
-    const int i0 = 2 * q, h = i0 / a.D, d0 = i0 % a.D;
+    if (gid >= (long long)a.n_rows * per) return;
+    const int r = (int)(gid / per), i0 = (int)(gid % per);
+    const int h = i0 / a.D, d0 = i0 % a.D;
     const size_t src_i = (size_t)r * a.Hkv * a.D + i0;
-    const uint32_t kw = *(const uint32_t*)((const uint16_t*)a.k + src_i);
-    const uint32_t vw = *(const uint32_t*)((const uint16_t*)a.v + src_i);
+    const uint16_t kw = ((const uint16_t*)a.k)[src_i];
+    const uint16_t vw = ((const uint16_t*)a.v)[src_i];
     float kinv = 1.f, vinv = 1.f;
     if constexpr (DST == GG_DTYPE_FP8_E4M3) {
         kinv = a.k_inv[h];
@@ -177,39 +178,29 @@ __global__ void __launch_bounds__(256) append_pair_kernel(AppendArgs a) {
     if (slot < 0 || slot >= a.num_slots) return;
     const int blk = slot / a.bs, off = slot % a.bs;
     auto f = [](uint16_t b) { return SRC == GG_DTYPE_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b); };
-    const float k0 = f((uint16_t)kw), k1 = f((uint16_t)(kw >> 16));
-    const float v0 = f((uint16_t)vw), v1 = f((uint16_t)(vw >> 16));
     const size_t ki = k_index(blk, h, off, d0, a.Hkv, a.bs, a.D);
     const size_t vi = v_index(blk, h, off, d0, a.Hkv, a.bs, a.D);
     if constexpr (DST == GG_DTYPE_FP8_E4M3) {
-        *(uint16_t*)(a.kc + ki) = (uint16_t)f32x2_to_fp8e4m3_sat(k0 * kinv, k1 * kinv);
-        const uint32_t vb = f32x2_to_fp8e4m3_sat(v0 * vinv, v1 * vinv);
-        a.vc[vi] = (uint8_t)vb;
-        a.vc[vi + a.bs] = (uint8_t)(vb >> 8);
+        const uint32_t w = f32x2_to_fp8e4m3_sat(f(kw) * kinv, f(vw) * vinv);
+        a.kc[ki] = (uint8_t)w;
+        a.vc[vi] = (uint8_t)(w >> 8);
+    } else if constexpr (SRC == DST) {
+        ((uint16_t*)a.kc)[ki] = kw;
+        ((uint16_t*)a.vc)[vi] = vw;
     } else {
-        uint16_t kb0, kb1, vb0, vb1;
-        if constexpr (SRC == DST) {
-            kb0 = (uint16_t)kw, kb1 = (uint16_t)(kw >> 16), vb0 = (uint16_t)vw, vb1 = (uint16_t)(vw >> 16);
-        } else {
-            kb0 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(k0) : f32_to_f16_bits(k0);
-            kb1 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(k1) : f32_to_f16_bits(k1);
-            vb0 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
-            vb1 = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
-        }
-        *(uint32_t*)((uint16_t*)a.kc + ki) = kb0 | ((uint32_t)kb1 << 16);
-        ((uint16_t*)a.vc)[vi] = vb0;
-        ((uint16_t*)a.vc)[vi + a.bs] = vb1;
+        ((uint16_t*)a.kc)[ki] = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(f(kw)) : f32_to_f16_bits(f(kw));
+        ((uint16_t*)a.vc)[vi] = DST == GG_DTYPE_BF16 ? f32_to_bf16_bits(f(vw)) : f32_to_f16_bits(f(vw));
     }
 }
 
 template <gg_dtype_t SRC>
-void launch_pair(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
-    const long long threads = (long long)a.n_rows * (a.Hkv * a.D / 2);
+void launch_dim(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
+    const long long threads = (long long)a.n_rows * (a.Hkv * a.D);
     const unsigned grid = (unsigned)((threads + 255) / 256);
     switch (dst) {
-        case GG_DTYPE_F16: append_pair_kernel<SRC, GG_DTYPE_F16><<<grid, 256, 0, s>>>(a); break;
-        case GG_DTYPE_BF16: append_pair_kernel<SRC, GG_DTYPE_BF16><<<grid, 256, 0, s>>>(a); break;
-        default: append_pair_kernel<SRC, GG_DTYPE_FP8_E4M3><<<grid, 256, 0, s>>>(a); break;
+        case GG_DTYPE_F16: append_dim_kernel<SRC, GG_DTYPE_F16><<<grid, 256, 0, s>>>(a); break;
+        case GG_DTYPE_BF16: append_dim_kernel<SRC, GG_DTYPE_BF16><<<grid, 256, 0, s>>>(a); break;
+        default: append_dim_kernel<SRC, GG_DTYPE_FP8_E4M3><<<grid, 256, 0, s>>>(a); break;
     }
 }
 
@@ -386,15 +377,15 @@ gg_status_t launch_kv_append(KV* kv, int layer, const void* k, const void* v, gg
         a.v_bscale = (uint16_t*)kv->v_scales + (size_t)layer * kv->scale_layer_elems;
         append_int8_block_kernel<<<dim3(n_rows, kv->num_kv_heads), 256, 0, s>>>(a);
     } else if (a.D % 8 == 0 && a.dst != GG_DTYPE_INT8 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0) {
-        const bool pair = src != GG_DTYPE_F32 && a.dst != GG_DTYPE_F32;
+        const bool per_dim = src != GG_DTYPE_F32 && a.dst != GG_DTYPE_F32;
         switch (src) {
             case GG_DTYPE_F32: launch_vec<GG_DTYPE_F32>(a, a.dst, s); break;
             case GG_DTYPE_F16:
-                if (pair) launch_pair<GG_DTYPE_F16>(a, a.dst, s);
+                if (per_dim) launch_dim<GG_DTYPE_F16>(a, a.dst, s);
                 else launch_vec<GG_DTYPE_F16>(a, a.dst, s);
                 break;
             default:
-                if (pair) launch_pair<GG_DTYPE_BF16>(a, a.dst, s);
+                if (per_dim) launch_dim<GG_DTYPE_BF16>(a, a.dst, s);
                 else launch_vec<GG_DTYPE_BF16>(a, a.dst, s);
                 break;
         }
