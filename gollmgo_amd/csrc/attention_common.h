@@ -108,11 +108,16 @@ struct AttnPlan {
 // LPT schedule: most sequences the plan kernel ranks (one per thread).
 constexpr int kLptMaxSeqs = 1024;
 // LPT piece length: at most T = ceil(C * kLptPieceNum / (slots * kLptPieceDen)) chunks
-// for C chunks of work over `slots` resident workgroups.
-constexpr int kLptPieceNum = 1;
-constexpr int kLptPieceDen = 1;
+// for C chunks of work over `slots` resident workgroups. 1.5 times the mean slot load,
+// measured on MI355X (attention µs at factors 1 / 4/3 / 3/2 / 7/4 / 2): config 3
+// 129.7 / 125.9 / 122.0 / 126.5 / 126.6, config 2 73.6 / 69.5 / 71.6 / 76.4 / 78.6,
+// config 5 unchanged. Fewer items are split (fewer merges and partial records) while the
+// longest-first order still balances the slots.
+constexpr int kLptPieceNum = 3;
+constexpr int kLptPieceDen = 2;
 // Bound on the number of LPT pieces (= main-grid workgroups and partial records): the
-// cuts of every item at T chunks give at most C/T + items pieces.
+// cuts of every item at T chunks give at most C/T + items pieces. (Stream-K needs
+// grid + items records, which is more: the workspace holds the larger of the two.)
 __host__ __device__ constexpr int lpt_records(int slots, int num_seqs, int num_kv_heads) {
     return (slots * kLptPieceDen + kLptPieceNum - 1) / kLptPieceNum + num_seqs * num_kv_heads;
 }

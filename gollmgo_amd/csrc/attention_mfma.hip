@@ -26,6 +26,8 @@
 #include "gg_common.h"
 #include "attention_common.h"
 
+#include <algorithm>
+
 namespace gg {
 #ifdef GG_TRACE
 // Debug builds (-DGG_TRACE) only: the LPT kernel's per-workgroup timeline in wall-clock
@@ -1111,8 +1113,10 @@ int attn_streamk_grid(const KV* kv, int rows, int num_q_heads) {
 
 size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, size_t* ml_elems,
                                     size_t* acc_elems) {
-    // Records for LPT pieces; stream-K needs at most grid + items, which is no more.
-    const size_t records = (size_t)lpt_records(attn_streamk_grid(kv, rows, num_q_heads), num_seqs, kv->num_kv_heads);
+    // Records for LPT pieces or for stream-K's grid + items, whichever bound is larger.
+    const int grid = attn_streamk_grid(kv, rows, num_q_heads);
+    const size_t items = (size_t)num_seqs * kv->num_kv_heads;
+    const size_t records = std::max((size_t)lpt_records(grid, num_seqs, kv->num_kv_heads), (size_t)grid + items);
     const size_t rw = (size_t)(num_q_heads / kv->num_kv_heads) * rows;
     const size_t n_ml = records * rw * 2;
     const size_t n_acc = records * rw * kD;
