@@ -24,7 +24,7 @@ def make_cache(dt, H, D, bs, nb, layers=1):
 # ------------------------------------------------------------------ append
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "fp8", "int8"])
-@pytest.mark.parametrize("src", ["f32", "bf16"])
+@pytest.mark.parametrize("src", ["f32", "bf16", "f16"])
 def test_append_bit_exact(gpu, dt, src):
     say(f"append dt={dt} src={src}")
     H, D, bs, nb = 4, 128, 16, 40
