@@ -176,6 +176,43 @@ def test_rejection_invalid_and_nonfinite(gpu):
     assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
 
 
+@pytest.mark.parametrize("top_p", [1.0, 0.8])
+def test_rejection_emitted_token_follows_target(gpu, top_p):
+    """Speculative sampling (Leviathan et al. 2023): the first emitted token is distributed
+    as the target p whatever the draft distribution q is. With top-p, p is the target
+    restricted to its nucleus and renormalised (sampling.go:139-173: keep while the mass
+    before an item is < p), so drafts outside the nucleus are always rejected. Checked on
+    the GPU over 40000 sequences with one draft each, against float64 softmax."""
+    rng = np.random.default_rng(11)
+    V, N = 5, 40000
+    base = np.array([1.0, 0.2, -0.5, 0.7, -1.0], np.float32)
+    q = np.array([0.05, 0.3, 0.4, 0.1, 0.15], np.float32)
+    drafts = rng.choice(V, size=(N, 1), p=q / q.sum()).astype(np.int32)
+    u = rng.random((N, 2)).astype(np.float32)
+    say(f"rejection emitted-token distribution top_p={top_p}")
+    acc, tok = gv.accept_rejection(torch.from_numpy(np.broadcast_to(base, (N, 2, V)).copy()).cuda(),
+                                   torch.from_numpy(drafts).cuda(), torch.ones(N, dtype=torch.int32).cuda(),
+                                   torch.from_numpy(u).cuda(), 1.0, top_p,
+                                   draft_probs=torch.from_numpy(np.broadcast_to(q, (N, 1, V)).copy()).cuda())
+    torch.cuda.synchronize()
+    acc, tok = acc.cpu().numpy(), tok.cpu().numpy()
+    p = np.exp(base.astype(np.float64) - base.max())
+    p /= p.sum()
+    if top_p < 1.0:
+        keep, cum = np.zeros(V, bool), 0.0
+        for i in np.argsort(-p, kind="stable"):
+            if cum >= top_p:
+                break
+            keep[i], cum = True, cum + p[i]
+        assert keep.tolist() == [True, True, False, True, False]  # the nucleus {0, 3, 1}
+        p = np.where(keep, p, 0.0)
+        p /= p.sum()
+        assert not acc[~keep[drafts[:, 0]]].any()  # drafts outside the nucleus never pass
+    first = np.where(acc == 1, drafts[:, 0], tok)
+    freq = np.bincount(first, minlength=V) / N
+    assert np.abs(freq - p).max() < 0.01, (freq, p)
+
+
 @pytest.mark.parametrize("seed", range(40))
 def test_acceptance_random_cases(gpu, seed):
     """Seeded random acceptance calls (logit type, batch, drafts, vocabulary sizes around
