@@ -557,23 +557,27 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
                    const int32_t* row_counts, const int32_t* block_tables, int max_blocks, int B, int R,
                    int Hq, float scale, int threads, int num_blocks) {
     const int G = Hq / H;
+    /* One work item per (sequence, row, query head), so that a single long sequence
+     * still spreads over every thread. */
+    const long items = (long)B * R * Hq;
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #pragma omp parallel for schedule(dynamic, 1)
 #else
     (void)threads;
 #endif
-    for (int b = 0; b < B; ++b) {
+    for (long w = 0; w < items; ++w) {
+        const int b = (int)(w / ((long)R * Hq)), j = (int)((w / Hq) % R), hq = (int)(w % Hq);
         int ctx = ctx_lens[b];
         if (ctx < 0) ctx = 0;
         if (ctx > max_blocks * bs) ctx = max_blocks * bs;
         const int nr = row_counts ? row_counts[b] : R;
-        if (nr <= 0 || nr > ctx) continue;
+        if (nr <= 0 || nr > ctx || j >= nr) continue;
         double* sc = (double*)malloc(sizeof(double) * (size_t)(ctx > 0 ? ctx : 1));
         double* acc = (double*)malloc(sizeof(double) * (size_t)D);
-        for (int j = 0; j < nr; ++j) {
+        {
             const int pos = ctx - nr + j;
-            for (int hq = 0; hq < Hq; ++hq) {
+            {
                 const int h = hq / G;
                 const float* qv = q + (((size_t)b * R + j) * Hq + hq) * D;
                 double mx = -INFINITY;

@@ -1,6 +1,7 @@
 """GPU parity: draft-KV append (bit-exact) and verify attention
 against the CPU oracle, through the C ABI."""
 import math
+import os
 
 import numpy as np
 import pytest
@@ -441,6 +442,24 @@ def test_attention_random_cases(gpu, seed):
     assert err <= TOL[c["dt"]]
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_attention_random_long_contexts(gpu, seed):
+    """Seeded long contexts (8k-32k keys) with R = 9 verify rows on the 8B geometry (three
+    row tiles; the automatic schedule, which is stream-K at this batch, and the 512-token
+    partition grid), against the fp64 oracle at the north-star tolerance."""
+    r = np.random.default_rng(3000 + seed)
+    dt = ["int8", "fp8", "bf16", "int8"][seed]
+    B = 2
+    ctx = [int(x) for x in r.integers(8192, 32768, B)]
+    partition = [0, 512][seed % 2]
+    c = dict(dt=dt, B=B, R=9, Hq=32, H=8, D=128, bs=16, ctx=ctx, partition=partition, src="bf16", seed=seed,
+             q_dt="bf16")
+    say(f"attention random long-context case {seed}: dt={dt} ctx={ctx} partition={partition}")
+    err = run_attention_case(**c)
+    print(f"  rel err {err:.2e}")
+    assert err <= TOL[dt]
+
+
 @pytest.mark.parametrize("seed", range(10))
 def test_attention_random_lpt_cases(gpu, seed):
     """Seeded random batches large enough for the LPT schedule (items fill half the
@@ -609,7 +628,10 @@ def test_attention_full_size_configs(gpu, cid, explicit):
     the automatic schedule (LPT pieces for configs 2, 3 and 5, stream-K for 4) equals an
     explicit partition grid to 1e-3 (the schedules round P to the MFMA
     type against different running maxima). Then the two shortest sequences against the
-    fp64 oracle at the north-star tolerance."""
+    fp64 oracle at the north-star tolerance: the two shortest sequences and the longest
+    (config 3's ~8k-key FP8 contexts, config 4's 16k-32k-key INT8 ones), so that deep
+    block-table indices, per-block scales far into the table and merges of many pieces
+    are checked against textbook attention too."""
     say(f"attention full-size config {cid}")
     cfg, lay, kv, q, keys, bt = _full_config_case(cid)
     D = cfg.head_dim
@@ -633,7 +655,8 @@ def test_attention_full_size_configs(gpu, cid, explicit):
         kv.attention(0, q, o, keys, bt, scale, workspace=ws, planned=True)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(o.cpu().numpy(), outs[0])
-    idx = np.argsort(lay.keys)[:2]
+    order = np.argsort(lay.keys, kind="stable")
+    idx = np.array(sorted({int(order[0]), int(order[1]), int(order[-1])}))
     k_s = v_s = None
     if cfg.kv_dtype == "fp8":
         a, b = kv.scales(0)
@@ -644,7 +667,7 @@ def test_attention_full_size_configs(gpu, cid, explicit):
     say(f"  oracle on sequences {idx.tolist()} (keys {lay.keys[idx].tolist()})")
     ref = ora.attention(q[idx].float().cpu().numpy(), kv.k_pool(0).cpu().numpy(), kv.v_pool(0).cpu().numpy(),
                         cfg.kv_dtype, cfg.num_kv_heads, D, cfg.block_size, lay.keys[idx], lay.block_tables[idx],
-                        scale, k_s, v_s, threads=8)
+                        scale, k_s, v_s, threads=min(os.cpu_count() or 1, 16))
     err = rel_err_per_vector(outs[0][idx], ref)
     print(f"  config {cid}: oracle rel err {err:.2e}")
     assert err <= TOL[cfg.kv_dtype]
