@@ -73,6 +73,8 @@ SIGNATURES = {
                                          _vp, _sz, _vp]),
     "gg_verify_append_attention_planned": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i,
                                                 _i, _i, _i, _f, _vp, _sz, _vp]),
+    "gg_verify_attention_noalloc_max_bytes": (_sz, []),
+    "gg_verify_attention_noalloc": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     "gg_accept_greedy_workspace_size": (_sz, [_i, _i, _i]),
     "gg_accept_greedy": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gg_accept_rejection_workspace_size": (_sz, [_i, _i, _i]),

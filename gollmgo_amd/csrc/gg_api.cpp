@@ -8,6 +8,8 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
+#include <string>
 #include <vector>
 
 namespace gg {
@@ -373,6 +375,68 @@ GG_API gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, con
     return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,
                                  max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, scale, 0, workspace,
                                  workspace_bytes, stream, ATTN_CALL_PLANNED, k_new, v_new, new_dtype);
+}
+
+// ---------------------------------------------------------------- attention without allocation
+
+// Scratch of gg_verify_attention_noalloc: a file-scope device array, one copy per GPU the
+// library runs on, held until the process ends. Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in for the symbol): it uses the device
+// address that hipGetSymbolAddress returns, looked up once per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up on the first call on
+// that device, with the device current).
+gg_status_t scratch_ptr(void** out) {
+    int d = 0;
+    gg_status_t st = check_hip(hipGetDevice(&d), "hipGetDevice");
+    if (st != GG_OK) return st;
+    if (d < 0 || d >= kMaxDevices) return fail(GG_ERR_INTERNAL, "gg_verify_attention_noalloc: device id too large");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[d]) {
+        void* p = nullptr;
+        st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (st != GG_OK) return st;
+        g_scratch_ptr[d] = p;
+    }
+    *out = g_scratch_ptr[d];
+    return GG_OK;
+}
+}  // namespace
+
+GG_API size_t gg_verify_attention_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+GG_API gg_status_t gg_verify_attention_noalloc(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
+                                               void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                               const int32_t* row_counts, const int32_t* block_tables,
+                                               int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                               int num_q_heads, float scale, void* stream) {
+    clear_error();
+    GG_CHECK_ARG(kv != nullptr, "gg_verify_attention_noalloc: kv is NULL");
+    GG_CHECK_ARG(attn_shape_ok(kv, num_seqs, rows_per_seq, num_q_heads, max_blocks_per_seq),
+                 "gg_verify_attention_noalloc: bad shape (num_q_heads must be a multiple of num_kv_heads)");
+    // The size check comes before any device call.
+    const size_t need = gg_verify_attention_workspace_size(kv, num_seqs, rows_per_seq, num_q_heads,
+                                                           max_blocks_per_seq, 0);
+    if (need > kNoAllocScratchBytes)
+        return fail(GG_ERR_INVALID, "gg_verify_attention_noalloc: the call needs " + std::to_string(need) +
+                                        " bytes of scratch, above the library's fixed " +
+                                        std::to_string(kNoAllocScratchBytes) +
+                                        " (use gg_verify_attention with a workspace)");
+    void* ws = nullptr;
+    if (need) {
+        const gg_status_t st = scratch_ptr(&ws);
+        if (st != GG_OK) return st;
+    }
+    return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,
+                                 max_blocks_per_seq, num_seqs, rows_per_seq, num_q_heads, scale, 0, ws, need,
+                                 stream, ATTN_CALL_SELF);
 }
 
 // ---------------------------------------------------------------- acceptance

@@ -229,6 +229,23 @@ gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, const void
                                                int num_q_heads, float scale, void* workspace,
                                                size_t workspace_bytes, void* stream);
 
+/* Attention without allocation. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same as gg_verify_attention with partition_tokens = 0 (the
+ * automatic schedule; identical results), but its scratch is a fixed device array inside
+ * the library, gg_verify_attention_noalloc_max_bytes() bytes (32 MiB) per GPU, held until
+ * the process ends. Calls that would need more scratch than that
+ * (gg_verify_attention_workspace_size(..., 0) above the limit) return GG_ERR_INVALID before
+ * touching the device. The call allocates nothing. Every call on one GPU shares that
+ * array: calls that overlap on one GPU (on different streams, or from several threads)
+ * race and give wrong results; serialise them on one stream. */
+size_t gg_verify_attention_noalloc_max_bytes(void);
+gg_status_t gg_verify_attention_noalloc(gg_kv_t kv, int layer, const void* q, gg_dtype_t q_dtype,
+                                        void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,
+                                        const int32_t* row_counts, const int32_t* block_tables,
+                                        int max_blocks_per_seq, int num_seqs, int rows_per_seq,
+                                        int num_q_heads, float scale, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Greedy acceptance.
  * Replaces Verify + argmax (internal/engine/speculative.go:68-84,
