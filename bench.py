@@ -364,16 +364,22 @@ def pmc_traffic(config_id: int):
 
 def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, uniforms, scale):
     """The CPU oracle (a C port of the reference's host logic and of its attention
-    semantics) timed on this host on a bounded sample of the same workload:
-    attention of layer 0 for the first S sequences, scaled by L layers, plus the
-    acceptance of the same S sequences."""
+    semantics) timed on this host on bounded samples of the same workload, at every usable
+    core and at one thread. A sample is the attention of layer 0 for the first S sequences,
+    scaled by L layers, plus the acceptance of the same S sequences (and their n-gram
+    drafts when the config has token histories). `value` is the all-cores figure; the
+    one-thread figure uses a smaller sample of the same shape. The Go engine's own host
+    loops (NGramDrafter.Draft and Verify, internal/engine/speculative.go:24-84) are also
+    timed at one thread per sequence."""
     import numpy as np
-    import torch
 
     from oracle import oracle as ora
 
-    S = min(args.cpu_seqs, cfg.num_seqs)
-    threads = min(os.cpu_count() or 1, 16)
+    nproc = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = nproc
     kc = kv.k_pool(0).cpu().numpy()
     vc = kv.v_pool(0).cpu().numpy()
     ks = vs = None
@@ -383,37 +389,67 @@ def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, u
     elif cfg.kv_dtype == "int8":
         k_s, v_s = kv.scales(0)
         ks, vs = k_s.float().cpu().numpy().reshape(-1), v_s.float().cpu().numpy().reshape(-1)
-    qh = q[0, :S].float().cpu().numpy()
-    t0 = time.perf_counter()
-    ora.attention(qh, kc, vc, cfg.kv_dtype, cfg.num_kv_heads, cfg.head_dim, cfg.block_size, lay.keys[:S],
-                  lay.block_tables[:S], scale, ks, vs, threads=threads)
-    t_attn = time.perf_counter() - t0
-    t_dr = 0.0
+    hist = None
     if cfg.history_len:
         from gollmgo_amd.workloads import make_histories
-        h = make_histories(cfg, cfg.history_len)[:S]
+        hist = make_histories(cfg, cfg.history_len)
+
+    def sample(S, threads):
+        qh = q[0, :S].float().cpu().numpy()
         t0 = time.perf_counter()
-        for row in h:
-            ora.ngram_draft(row, cfg.ngram_n, cfg.max_drafts)
-        t_dr = time.perf_counter() - t0
-    lg = logits[:S].float().cpu().numpy()
-    dp = draft_probs[:S].cpu().numpy() if draft_probs is not None else None
-    dr = drafts[:S].cpu().numpy()
-    nd = n_drafts[:S].cpu().numpy()
-    un = uniforms[:S].cpu().numpy()
-    t0 = time.perf_counter()
-    if cfg.accept == "rejection":
-        ora.accept_rejection(lg, dr, nd, un, cfg.temperature, cfg.top_p, dp)
+        ora.attention(qh, kc, vc, cfg.kv_dtype, cfg.num_kv_heads, cfg.head_dim, cfg.block_size, lay.keys[:S],
+                      lay.block_tables[:S], scale, ks, vs, threads=threads)
+        t_attn = time.perf_counter() - t0
+        t_dr = 0.0
+        if hist is not None:
+            t0 = time.perf_counter()
+            ora.ngram_draft_batch(hist[:S], np.full(S, hist.shape[1], np.int32), cfg.ngram_n, cfg.max_drafts,
+                                  threads=threads)
+            t_dr = time.perf_counter() - t0
+        lg = logits[:S].float().cpu().numpy()
+        dp = draft_probs[:S].cpu().numpy() if draft_probs is not None else None
+        dr, nd, un = drafts[:S].cpu().numpy(), n_drafts[:S].cpu().numpy(), uniforms[:S].cpu().numpy()
+        t0 = time.perf_counter()
+        if cfg.accept == "rejection":
+            ora.accept_rejection(lg, dr, nd, un, cfg.temperature, cfg.top_p, dp)
+        else:
+            ora.accept_greedy(lg, dr, nd)
+        t_acc = time.perf_counter() - t0
+        step_s = cfg.layers * t_attn + t_acc + t_dr
+        desc = (f"{S} of {cfg.num_seqs} sequences: layer-0 attention ({t_attn:.2f} s, fp64, {threads} thread(s)) "
+                f"x {cfg.layers} layers + {cfg.accept} acceptance ({t_acc:.2f} s, 1 thread)"
+                + (f" + n-gram drafts ({t_dr:.3f} s)" if hist is not None else ""))
+        return {"value": round(S * cfg.rows / step_s, 2), "threads": threads, "sample": desc,
+                "attention_s_per_layer": round(t_attn, 3), "accept_s": round(t_acc, 3)}
+
+    S = min(args.cpu_seqs, cfg.num_seqs)
+    all_cores = sample(S, usable)
+    one_thread = sample(max(1, S // 16), 1)
+
+    # The Go engine's host loops, one thread: Draft over a history of the config's (or, for
+    # configs without one, config 5's 8192-token) shape, Verify over one sequence's K draft
+    # rows of the config's logits (greedy argmax scan, the engine's own check).
+    if hist is None:
+        from gollmgo_amd.workloads import CONFIGS, make_histories
+        dh = make_histories(CONFIGS[5], CONFIGS[5].history_len)[:16]
     else:
-        ora.accept_greedy(lg, dr, nd)
-    t_acc = time.perf_counter() - t0
-    step_s = cfg.layers * t_attn + t_acc + t_dr
-    return {"value": round(S * cfg.rows / step_s, 2), "unit": "verified tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{S} of {cfg.num_seqs} sequences: layer-0 attention ({t_attn:.2f} s, fp64, OpenMP over "
-                      f"sequences) x {cfg.layers} layers + {cfg.accept} acceptance ({t_acc:.2f} s, 1 thread)"
-                      + (f" + n-gram drafts ({t_dr:.2f} s, 1 thread)" if cfg.history_len else ""),
-            "attention_s_per_layer": round(t_attn, 3), "accept_s": round(t_acc, 3)}
+        dh = hist[:16]
+    t0 = time.perf_counter()
+    ora.ngram_draft_batch(dh, np.full(len(dh), dh.shape[1], np.int32), 3, cfg.max_drafts, threads=1)
+    draft_us = (time.perf_counter() - t0) / len(dh) * 1e6
+    nv = min(16, cfg.num_seqs)
+    lg = logits[:nv].float().cpu().numpy()
+    t0 = time.perf_counter()
+    ora.accept_greedy(lg, drafts[:nv].cpu().numpy(), n_drafts[:nv].cpu().numpy())
+    verify_us = (time.perf_counter() - t0) / nv * 1e6
+    return {"value": all_cores["value"], "unit": "verified tokens/s", "cores": usable, "kind": "port",
+            "sample": all_cores["sample"], "nproc": nproc, "usable_cpus": usable,
+            "all_cores": all_cores, "one_thread": one_thread,
+            "go_engine_loops_one_thread": {
+                "ngram_draft_us_per_seq": round(draft_us, 1),
+                "ngram_history_tokens": int(dh.shape[1]),
+                "verify_greedy_us_per_seq": round(verify_us, 1),
+                "verify_rows_x_vocab": [cfg.rows, int(logits.shape[-1])]}}
 
 
 if __name__ == "__main__":

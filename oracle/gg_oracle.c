@@ -617,6 +617,173 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
     }
 }
 
+/* --------------------------------------------- sampler draw parity (test helper) */
+
+/* Stable LSD radix sort of idx[0..n) by key[idx] ascending, four 16-bit passes. */
+static void radix_sort_idx(const uint64_t* key, int n, int* idx, int* tmp) {
+    int* cnt = (int*)malloc(sizeof(int) * 65537);
+    for (int pass = 0; pass < 4; ++pass) {
+        const int sh = 16 * pass;
+        memset(cnt, 0, sizeof(int) * 65537);
+        for (int i = 0; i < n; ++i) cnt[((key[idx[i]] >> sh) & 0xffff) + 1]++;
+        for (int d = 0; d < 65536; ++d) cnt[d + 1] += cnt[d];
+        for (int i = 0; i < n; ++i) tmp[cnt[(key[idx[i]] >> sh) & 0xffff]++] = idx[i];
+        memcpy(idx, tmp, sizeof(int) * (size_t)n);
+    }
+    free(cnt);
+}
+
+/* Order key of a finite float, ascending in (value desc): -0 counts as +0. */
+static uint64_t desc_key_f32(float x) {
+    if (x == 0.0f) x = 0.0f;
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u); /* ascending order of values */
+    return (uint64_t)(~u);
+}
+static uint64_t desc_key_pos_f64(double x) { /* x >= 0 */
+    uint64_t u;
+    memcpy(&u, &x, 8);
+    return ~u;
+}
+
+/* For each of B rows of logits (V finite values) and U supplied uniforms per row, the
+ * token of two samplers:
+ *   tok_f64  : Sampler.Sample (sampling.go:40-72) in float64 without top-k: scaled =
+ *              float64(l) * (1/T) (:57-61), softmax (:112-136), topPFilter (:139-173;
+ *              equal probabilities in index order, which sort.Slice leaves open),
+ *              categoricalSample (:176-192) with the uniform in place of rng.Float64();
+ *   tok_fixed: the final draw of ora_accept_rejection for a row with no drafts: the
+ *              fixed-point weights and nucleus of row_weights, then the first index
+ *              whose inclusive prefix exceeds floor(u * total).
+ * dist[row*U + k] is the distance of u from the nearer float64 CDF boundary of
+ * tok_f64 (min(u - cum_before, cum_through - u)); nucleus_diff[row] counts the tokens
+ * kept by one nucleus and not by the other. */
+void ora_draw_parity(const float* logits, int B, int V, double temperature, double top_p,
+                     const float* uniforms, int U, int32_t* tok_fixed, int32_t* tok_f64, double* dist,
+                     int32_t* nucleus_diff, int threads) {
+    const float inv_t = 1.0f / (float)temperature;
+    const double inv_t64 = 1.0 / temperature;
+    const int use_p = top_p > 0 && top_p < 1;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#else
+    (void)threads;
+#endif
+    for (int b = 0; b < B; ++b) {
+        const float* row = logits + (size_t)b * V;
+        uint64_t* w = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+        uint64_t* key = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+        double* pr = (double*)malloc(sizeof(double) * (size_t)V);
+        double* kept = (double*)malloc(sizeof(double) * (size_t)V);
+        double* cdf = (double*)malloc(sizeof(double) * (size_t)V);
+        uint64_t* pre = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+        int* idx = (int*)malloc(sizeof(int) * (size_t)V);
+        int* tmp = (int*)malloc(sizeof(int) * (size_t)V);
+        /* fixed point */
+        float m = row[0];
+        for (int i = 1; i < V; ++i)
+            if (row[i] > m) m = row[i];
+        uint64_t z = 0;
+        for (int i = 0; i < V; ++i) {
+            w[i] = ora_weight(row[i], m, inv_t);
+            z += w[i];
+        }
+        if (use_p) {
+            const uint64_t tp = (uint64_t)ceil(top_p * (double)z);
+            for (int i = 0; i < V; ++i) {
+                idx[i] = i;
+                key[i] = desc_key_f32(row[i]);
+            }
+            radix_sort_idx(key, V, idx, tmp);
+            uint64_t cum = 0;
+            int k = 0;
+            for (; k < V; ++k) {
+                if (cum >= tp && cum > 0) break;
+                cum += w[idx[k]];
+            }
+            for (; k < V; ++k) w[idx[k]] = 0;
+        }
+        uint64_t tot = 0;
+        for (int i = 0; i < V; ++i) {
+            tot += w[i];
+            pre[i] = tot;
+        }
+        /* float64 sampler */
+        double mx = (double)row[0] * inv_t64;
+        for (int i = 1; i < V; ++i)
+            if ((double)row[i] * inv_t64 > mx) mx = (double)row[i] * inv_t64;
+        double sum = 0;
+        for (int i = 0; i < V; ++i) {
+            pr[i] = exp((double)row[i] * inv_t64 - mx);
+            sum += pr[i];
+        }
+        for (int i = 0; i < V; ++i) pr[i] /= sum;
+        for (int i = 0; i < V; ++i) kept[i] = use_p ? 0.0 : pr[i];
+        if (use_p) {
+            for (int i = 0; i < V; ++i) {
+                idx[i] = i;
+                key[i] = desc_key_pos_f64(pr[i]);
+            }
+            radix_sort_idx(key, V, idx, tmp);
+            double cum = 0;
+            for (int k = 0; k < V; ++k) {
+                if (cum >= top_p && cum > 0) break;
+                kept[idx[k]] = pr[idx[k]];
+                cum += pr[idx[k]];
+            }
+            double s2 = 0;
+            for (int i = 0; i < V; ++i) s2 += kept[i];
+            for (int i = 0; i < V; ++i) kept[i] /= s2;
+        }
+        double c = 0;
+        int nd = 0;
+        for (int i = 0; i < V; ++i) {
+            c += kept[i];
+            cdf[i] = c;
+            nd += (kept[i] > 0) != (w[i] > 0);
+        }
+        nucleus_diff[b] = nd;
+        for (int k = 0; k < U; ++k) {
+            const double u = (double)uniforms[(size_t)b * U + k];
+            /* first i with u < cdf[i] (cdf is non-decreasing) */
+            int lo = 0, hi = V;
+            while (lo < hi) {
+                const int mid = (lo + hi) / 2;
+                if (u < cdf[mid]) hi = mid;
+                else lo = mid + 1;
+            }
+            int tf = lo;
+            if (tf == V) { /* fallback: last nonzero */
+                tf = 0;
+                for (int i = V - 1; i >= 0; --i)
+                    if (kept[i] > 0) {
+                        tf = i;
+                        break;
+                    }
+            }
+            const double before = tf > 0 ? cdf[tf - 1] : 0.0;
+            const double d0 = u - before, d1 = cdf[tf] - u;
+            dist[(size_t)b * U + k] = d0 < d1 ? d0 : d1;
+            tok_f64[(size_t)b * U + k] = tf;
+            int tq = 0;
+            if (tot > 0) {
+                const uint64_t t = (uint64_t)(u * (double)tot);
+                int l2 = 0, h2 = V;
+                while (l2 < h2) {
+                    const int mid = (l2 + h2) / 2;
+                    if (pre[mid] > t) h2 = mid;
+                    else l2 = mid + 1;
+                }
+                tq = l2 < V ? l2 : 0;
+            }
+            tok_fixed[(size_t)b * U + k] = tq;
+        }
+        free(w); free(key); free(pr); free(kept); free(cdf); free(pre); free(idx); free(tmp);
+    }
+}
+
 /* ------------------------------------------------------- array helpers */
 
 void ora_fp8_encode_n(const float* x, uint8_t* out, long n) {
