@@ -9,20 +9,28 @@
 // mass before an item is below p (sampling.go:139-173), and the categorical
 // draw "first index whose running sum exceeds u" (sampling.go:176-192).
 //
-// Arithmetic is exact integer fixed point (see gg_fixed_exp.h): w_i =
-// floor(exp((l_i - max)/T) * 2^35); nucleus order is (logit desc, index asc).
-//   kernel 1 (row_stats), one 1024-thread block per (sequence, row <= n):
-//     max; Z = sum w; with top-p the boundary logit of the nucleus is found by a
-//     2048-bin histogram of (max-l)/T in 1/64-nat slices followed by three
-//     11/11/10-bit radix levels on the order key (LDS u64 atomics: exact), and a
-//     9+9-bit index select when the boundary value is tied and cut.
-//     Without top-p the same statistics come from two segmented launches (segment
-//     max, then segment sums of w) over (row, 8192-logit segment) blocks.
-//   draw sums, one block per (sequence, segment): walks the drafts (accept iff
-//     u*q(x)*Zp < w(x)), then sums the final row's segment of max(0, w -
-//     floor(q*Zp)) (first rejection) or of w (bonus, row n);
-//   draw find, one block per sequence: locates floor(u*total) among the segment sums,
-//     then inside that one segment.
+// Arithmetic is exact integer fixed point (gg_fixed_exp.h): a row is cut into segments
+// of 8192 logits and logit i of segment s weighs W_i = e_i * f_s, e_i = weight(l_i, m_s),
+// f_s = weight(m_s, m) (m_s the segment max, m the row max, weight(l, a) =
+// floor(exp_gg((l - a)/T) * 2^35)); sums are exact 128-bit integers. The nucleus order
+// is (logit desc, index asc). Launches:
+//   seg_pass, one block per (row, segment): the segment max m_s and E_s = sum of e_i (with
+//     top-p also the segment's coarse histogram of e on an absolute 1/16-nat grid). The
+//     only read of the whole logits: m and Z = sum f_s * E_s follow from the segments.
+//   top-p only: row_pick (per row, the segment histograms merged exactly into the row's
+//     and its boundary bin), decide_bounds (per sequence, every draft the bounds of the
+//     nucleus mass already decide, and the rows left open or holding the final draw
+//     flagged), seg_gather (flagged rows: each segment's kept sum above the boundary bin
+//     and that bin's elements), row_select (flagged rows: an LDS sort of those elements to
+//     the exact cut). A row whose boundary bin is crowded falls back to the exact
+//     single-block row kernel (three 11/11/10-bit radix levels on the order key and a
+//     9+9-bit index select of a tied cut).
+//   decide, one wave per sequence: the acceptance walk (accept iff u*q(x)*Zp < W(x)) and
+//     the view of the final row.
+//   seg_residual (dense draft distributions only), one block per (sequence, segment):
+//     the final row's residual sums, W - min(W, floor(q*Zp)) in the segment's units.
+//   draw find, one block per sequence: the segment holding floor(u*total) (segment masses
+//     from the sums above), then the element inside it.
 // The draft distributions are read only at drafted tokens and on the final row.
 #pragma clang fp contract(off)
 
@@ -33,34 +41,30 @@ namespace gg {
 namespace {
 
 constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / 64;
 constexpr int kBins = 2048;
 typedef unsigned long long u64;
+typedef gg_u128 u128;
 
 struct RowStats {
+    u128 zp;          // nucleus mass
+    u128 wx;          // weight of the drafted token (0 if outside the nucleus)
     float m;          // max finite logit (or -inf when none)
     int idx_cut;      // ties at the boundary key are kept for index <= idx_cut
-    u64 zp;           // nucleus mass (== Z without top-p)
     unsigned int lam; // boundary order key (0 = keep every finite logit)
     int valid;        // row was evaluated
-    u64 wx;           // weight of the drafted token (0 if outside the nucleus)
 };
 
 constexpr int kCandCap = 4096;
 constexpr int kFindThreads = 1024;  // draw find: threads per sequence
 
-// Coarse-bin masses of one row. (Only the mass: weights do not increase down the bins,
-// so a bin with no mass sits where the whole row's mass lies before it and can never
-// hold the boundary; the boundary bin's element count comes from the gather.)
-struct RowHist {
-    u64 mass[kBins];
-};
-
+// The nucleus boundary of one row (top-p), from the coarse histogram: the boundary bin,
+// the mass of the bins before it and its own mass.
 struct RowPick {
-    int cbin;        // boundary coarse bin (-1: nothing to resolve)
+    u128 c_above;    // mass of the bins before the boundary bin
+    u128 m_bin;      // mass of the boundary bin
+    u128 tp;         // ceil(top_p * Z)
+    int cbin;        // boundary coarse bin (-1: no finite logit or Z == 0)
     int n_cand;      // elements of that bin gathered so far
-    u64 c_above;     // mass of the bins before it
-    u64 tp;          // ceil(top_p * Z)
 };
 
 __device__ __forceinline__ u64 shfl_xor_u64(u64 v, int o) {
@@ -75,73 +79,60 @@ __device__ __forceinline__ u64 shfl_up_u64(u64 v, int o) {
     hi = __shfl_up(hi, o);
     return ((u64)hi << 32) | lo;
 }
-
-__device__ u64 block_sum_u64(u64 v, u64* red) {
-    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_u64(v, o);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    u64 t = 0;
-    for (int i = 0; i < kWaves; ++i) t += red[i];
-    return t;
+__device__ __forceinline__ u128 shfl_xor_u128(u128 v, int o) {
+    return ((u128)shfl_xor_u64((u64)(v >> 64), o) << 64) | shfl_xor_u64((u64)v, o);
 }
-
-__device__ float block_max_f(float v, float* red) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int i = 1; i < kWaves; ++i) t = fmaxf(t, red[i]);
-    return t;
+__device__ __forceinline__ u128 shfl_up_u128(u128 v, int o) {
+    return ((u128)shfl_up_u64((u64)(v >> 64), o) << 64) | shfl_up_u64((u64)v, o);
 }
-
-__device__ int block_max_i(int v, int* red) {
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    int t = red[0];
-    for (int i = 1; i < kWaves; ++i) t = max(t, red[i]);
-    return t;
+__device__ __forceinline__ u128 shfl_u128(u128 v, int src) {
+    const u64 lo = (u64)v, hi = (u64)(v >> 64);
+    const unsigned int a = __shfl((unsigned int)lo, src), b = __shfl((unsigned int)(lo >> 32), src);
+    const unsigned int c = __shfl((unsigned int)hi, src), d = __shfl((unsigned int)(hi >> 32), src);
+    return ((u128)(((u64)d << 32) | c) << 64) | (((u64)b << 32) | a);
+}
+// Exact 128-bit add into (lo, hi) words with atomics (LDS or global): the carry out of
+// the low word goes into the high word.
+__device__ __forceinline__ void atomic_add_u128(u64* lo, u64* hi, u128 v) {
+    const u64 vl = (u64)v, vh = (u64)(v >> 64);
+    const u64 old = vl ? atomicAdd(lo, vl) : 0ull;
+    const u64 carry = (vl && old + vl < old) ? 1ull : 0ull;
+    if (vh + carry) atomicAdd(hi, vh + carry);
 }
 
 __device__ __forceinline__ bool finite_f(float x) { return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u; }
 
-// Wave 0 scans the histogram from bin `top` downward (descending key order when
-// `desc`) and returns the LAST non-empty bin (count > 0; mass > 0 when cnt is null)
-// whose mass-above C satisfies C < tp || C == 0; *c_above receives its C. Bins are ordered so that larger logits come first.
-__device__ void pick_bin(const u64* mass, const unsigned int* cnt, int nbins, bool desc, u64 base,
-                         u64 tp, int* out_bin, u64* out_c) {
+// Wave 0 scans the histogram from bin 0 upward (larger logits first; descending bin
+// index order when `desc`) and returns the LAST non-empty bin (count > 0; mass > 0
+// when cnt is null) whose mass-above C satisfies C < tp || C == 0; *out_c receives
+// its C. Masses are (lo, hi) word pairs.
+__device__ void pick_bin(const u64* mlo, const u64* mhi, const unsigned int* cnt, int nbins, bool desc, u128 base,
+                         u128 tp, int* out_bin, u128* out_c) {
     if (threadIdx.x >= 64) return;
     const int lane = threadIdx.x;
     const int per = nbins / 64;
-    // Logical position p runs over bins in order of decreasing logit.
     auto bin_at = [&](int p) { return desc ? nbins - 1 - p : p; };
-    u64 local = 0;
-    for (int k = 0; k < per; ++k) local += mass[bin_at(lane * per + k)];
-    // Exclusive prefix over lanes.
-    u64 incl = local;
+    auto mass = [&](int bn) { return ((u128)mhi[bn] << 64) | mlo[bn]; };
+    u128 local = 0;
+    for (int k = 0; k < per; ++k) local += mass(bin_at(lane * per + k));
+    u128 incl = local;
     for (int o = 1; o < 64; o <<= 1) {
-        u64 t = shfl_up_u64(incl, o);
+        const u128 t = shfl_up_u128(incl, o);
         if (lane >= o) incl += t;
     }
-    u64 c = base + incl - local;
+    u128 c = base + incl - local;
     int best = -1;
-    u64 best_c = 0;
+    u128 best_c = 0;
     for (int k = 0; k < per; ++k) {
         const int bn = bin_at(lane * per + k);
-        const bool nonempty = cnt ? cnt[bn] > 0 : mass[bn] > 0;
+        const u128 mb = mass(bn);
+        const bool nonempty = cnt ? cnt[bn] > 0 : mb > 0;
         if (nonempty && (c < tp || c == 0)) {
             best = lane * per + k;
             best_c = c;
         }
-        c += mass[bn];
+        c += mb;
     }
-    // Highest qualifying logical position across lanes.
     int bp = best;
     for (int o = 32; o > 0; o >>= 1) bp = max(bp, __shfl_xor(bp, o));
     if (best == bp && best >= 0) {
@@ -157,6 +148,12 @@ __device__ __forceinline__ float ld(const void* p, size_t i) {
     else return f16_bits_to_f32(((const uint16_t*)p)[i]);
 }
 
+// The segment factor f_s of segment max ms against row max m (0 for an empty segment).
+__device__ __forceinline__ u64 seg_factor(float ms, float m, float inv_t) {
+    return finite_f(ms) ? gg_weight(ms, m, inv_t) : 0ull;
+}
+
+// The nucleus of one row and the weights inside it.
 struct Nucleus {
     float m, inv_t;
     unsigned int lam;
@@ -166,185 +163,13 @@ struct Nucleus {
         const unsigned int k = gg_order_key(l);
         return k > lam || (k == lam && i <= idx_cut);
     }
-    __device__ __forceinline__ u64 weight(float l, int i) const {
-        return kept(l, i) ? gg_weight(l, m, inv_t) : 0ull;
+    // W of logit l at index i, given its segment max ms.
+    __device__ __forceinline__ u128 weight(float l, int i, float ms) const {
+        if (!kept(l, i)) return 0;
+        return (u128)gg_weight(l, ms, inv_t) * seg_factor(ms, m, inv_t);
     }
 };
 
-// Exact per-row statistics in one 1024-thread block (passes over the whole row). With
-// `only_flagged`, rows whose nucleus boundary the segmented path already resolved
-// (flag 0) are skipped: this kernel is then the fallback for crowded boundary bins.
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
-    const void* __restrict__ logits, int K, int V, const int32_t* __restrict__ drafts,
-    const int32_t* __restrict__ n_drafts, float inv_t, float top_p, int use_topp,
-    RowStats* __restrict__ stats, const int* __restrict__ only_flagged) {
-    const int row = blockIdx.x;
-    if (only_flagged && only_flagged[row] == 0) return;
-    const int R = K + 1;
-    const int b = row / R, j = row % R;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
-    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-
-    __shared__ u64 hmass[kBins];
-    __shared__ unsigned int hcnt[kBins];
-    __shared__ u64 red64[kWaves];
-    __shared__ float redf[kWaves];
-    __shared__ int redi[kWaves];
-    __shared__ int s_bin;
-    __shared__ u64 s_c;
-
-    // Pass 1: max over finite logits.
-    float m = -INFINITY;
-    for (int i = threadIdx.x; i < V; i += kThreads) {
-        const float l = ld<DT>(lp, i);
-        if (finite_f(l)) m = fmaxf(m, l);
-    }
-    m = block_max_f(m, redf);
-
-    RowStats st{};
-    st.m = m;
-    st.valid = 1;
-    st.lam = 0;
-    st.idx_cut = 0x7fffffff;
-    if (!finite_f(m)) {
-        // No finite logit: every weight is zero.
-        if (threadIdx.x == 0) {
-            st.zp = 0;
-            st.wx = 0;
-            stats[row] = st;
-        }
-        return;
-    }
-
-    // Pass 2: Z (and the coarse histogram when top-p is on).
-    if (use_topp) {
-        for (int i = threadIdx.x; i < kBins; i += kThreads) {
-            hmass[i] = 0;
-            hcnt[i] = 0;
-        }
-        __syncthreads();
-    }
-    u64 z = 0;
-    for (int i = threadIdx.x; i < V; i += kThreads) {
-        const float l = ld<DT>(lp, i);
-        if (!finite_f(l)) continue;
-        const u64 w = gg_weight(l, m, inv_t);
-        z += w;
-        if (use_topp) {
-            const int bn = gg_coarse_bin(l, m, inv_t);
-            atomicAdd(&hmass[bn], w);
-            atomicAdd(&hcnt[bn], 1u);
-        }
-    }
-    z = block_sum_u64(z, red64);
-
-    u64 zp = z;
-    unsigned int lam = 0;
-    int idx_cut = 0x7fffffff;
-    if (use_topp && z > 0) {
-        const u64 tp = (u64)ceil((double)top_p * (double)z);
-        __syncthreads();
-        pick_bin(hmass, hcnt, kBins, false, 0, tp, &s_bin, &s_c);
-        __syncthreads();
-        const int cbin = s_bin;
-        u64 c_above = s_c;
-        // Radix levels over the order key of elements in the coarse bin.
-        unsigned int prefix = 0, pmask = 0;
-        const int shifts[3] = {21, 10, 0};
-        const int widths[3] = {11, 11, 10};
-        for (int lv = 0; lv < 3; ++lv) {
-            const int nb = 1 << widths[lv];
-            __syncthreads();
-            for (int i = threadIdx.x; i < kBins; i += kThreads) {
-                hmass[i] = 0;
-                hcnt[i] = 0;
-            }
-            __syncthreads();
-            for (int i = threadIdx.x; i < V; i += kThreads) {
-                const float l = ld<DT>(lp, i);
-                if (!finite_f(l)) continue;
-                if (gg_coarse_bin(l, m, inv_t) != cbin) continue;
-                const unsigned int key = gg_order_key(l);
-                if ((key & pmask) != prefix) continue;
-                const int d = (key >> shifts[lv]) & (nb - 1);
-                atomicAdd(&hmass[d], gg_weight(l, m, inv_t));
-                atomicAdd(&hcnt[d], 1u);
-            }
-            __syncthreads();
-            // Pad unused bins (10-bit level) with empties: the scan covers kBins.
-            pick_bin(hmass, hcnt, kBins, true, c_above, tp, &s_bin, &s_c);
-            __syncthreads();
-            const unsigned int dsel = (unsigned int)s_bin;
-            c_above = s_c;
-            prefix |= dsel << shifts[lv];
-            pmask |= (unsigned int)(nb - 1) << shifts[lv];
-        }
-        lam = prefix;
-        // Ties at the boundary key: count and weight.
-        const unsigned int n_tie = hcnt[prefix & 0x3ff];
-        const u64 m_tie = hmass[prefix & 0x3ff];
-        const u64 w_tie = n_tie ? m_tie / n_tie : 0;
-        u64 n_keep = n_tie;
-        if (w_tie > 0) {
-            const u64 need = (tp - c_above + w_tie - 1) / w_tie;
-            if (need < n_keep) n_keep = need;
-        }
-        zp = c_above + n_keep * w_tie;
-        if (n_keep < n_tie) {
-            // Index of the n_keep-th smallest index among the ties (two 9-bit levels).
-            unsigned int iprefix = 0, imask = 0;
-            unsigned int remaining = (unsigned int)n_keep;  // >= 1
-            const int ish[2] = {9, 0};
-            for (int lv = 0; lv < 2; ++lv) {
-                __syncthreads();
-                for (int i = threadIdx.x; i < 512; i += kThreads) hcnt[i] = 0;
-                __syncthreads();
-                for (int i = threadIdx.x; i < V; i += kThreads) {
-                    const float l = ld<DT>(lp, i);
-                    if (!finite_f(l) || gg_order_key(l) != lam) continue;
-                    if (((unsigned int)i & imask) != iprefix) continue;
-                    atomicAdd(&hcnt[((unsigned int)i >> ish[lv]) & 511u], 1u);
-                }
-                __syncthreads();
-                if (threadIdx.x == 0) {
-                    unsigned int acc = 0;
-                    int d = 0;
-                    for (; d < 512; ++d) {
-                        if (acc + hcnt[d] >= remaining) break;
-                        acc += hcnt[d];
-                    }
-                    s_bin = d;
-                    s_c = acc;
-                }
-                __syncthreads();
-                remaining -= (unsigned int)s_c;
-                iprefix |= (unsigned int)s_bin << ish[lv];
-                imask |= 511u << ish[lv];
-            }
-            idx_cut = (int)iprefix;
-        }
-    }
-
-    if (threadIdx.x == 0) {
-        st.zp = zp;
-        st.lam = lam;
-        st.idx_cut = idx_cut;
-        st.wx = 0;
-        if (j < n) {
-            const int x = drafts[(size_t)b * K + j];
-            if (x >= 0 && x < V) {
-                Nucleus nu{m, inv_t, lam, idx_cut};
-                st.wx = nu.weight(ld<DT>(lp, x), x);
-            }
-        }
-        stats[row] = st;
-    }
-}
-
-// Block-wide inclusive scan of u64 (1024 threads), returns inclusive value.
 // ---------------------------------------------------------------------------
 // Segmented path. A row of V logits is cut into segments of kSegElems; every
 // (row, segment) pair is one 256-thread block, so a launch has thousands of blocks.
@@ -352,22 +177,34 @@ __global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
 // order-free, so the result is the same bit pattern whatever the schedule.
 
 constexpr int kSegThreads = 256;
-constexpr int kSegElems = 8192;  // 32 logits per thread
-// Segments per block of the top-p weight launch (measured on MI355X, config 5: one, two,
-// four or sixteen segments per block take 418, 387, 382, 391 µs per acceptance call).
-constexpr int kZhistSegs = 4;
+constexpr int kSegElems = GG_ACCEPT_SEG;  // 32 logits per thread
+static_assert(kSegElems == kSegThreads * 32, "segment = 32 logits per thread");
+// Coarse nucleus bins, 1/16 nat wide on an absolute grid: cb(l) = floor(l/T * 16), and a
+// logit's bin relative to a maximum a is cb(a) - cb(l). Both terms are integers, so a bin
+// relative to a segment max turns into the bin relative to the row max by adding
+// cb(m) - cb(m_s): the segments' histograms merge exactly. cb is monotone, so the bins
+// follow the nucleus order.
+constexpr int kSegBins = 400;   // per segment: e > 0 needs (m_s - l)/T < 24.3 nats (389 bins)
+constexpr int kRowBins = 1024;  // per row (the last bin takes everything further down)
+__device__ __forceinline__ int cb_abs(float l, float inv_t) {
+    const float y = fminf(fmaxf(l * inv_t * 16.0f, -1.0e9f), 1.0e9f);
+    return (int)__builtin_floorf(y);
+}
 
-struct SegOut {
-    u64 sum_res;     // residual weights of the segment (final row)
-    u64 sum_plain;   // nucleus weights of the segment (final row)
-    int last_res;    // last index with a non-zero residual weight (-1: none)
-    int last_plain;
+// Residual weight sums of one segment of a sequence's final row (dense draft
+// distributions only), in units of W.
+struct SegSum {
+    u128 res;
 };
+
+// Per-row state of the top-p decision: certain outcome from the coarse bounds, or
+// resolved from the exact nucleus.
+constexpr int kRowAccept = 1, kRowReject = 2, kRowUnsure = 3;
 
 struct SeqDecision {
     int accepted;
     int row;         // row of the final draw
-    int residual;    // 1: draw from max(0, w - floor(q*Zp)), 0: from w
+    int residual;    // 1: draw from W - min(W, floor(q*Zp)), 0: from W
 };
 
 __device__ __forceinline__ float seg_block_max(float v, float* red) {
@@ -388,18 +225,9 @@ __device__ __forceinline__ u64 seg_block_sum(u64 v, u64* red) {
     for (int i = 0; i < kSegThreads / 64; ++i) t += red[i];
     return t;
 }
-__device__ __forceinline__ int seg_block_maxi(int v, int* red) {
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    int t = red[0];
-    for (int i = 1; i < kSegThreads / 64; ++i) t = max(t, red[i]);
-    return t;
-}
-
 // The 32 logits a thread owns in a segment: elements base + 8*threadIdx + {0..7} of each
 // of the four 2048-element quarters (16-byte loads; scalar fallback for odd rows).
+// Elements past the row read as NaN (never finite, never weighed).
 template <gg_dtype_t DT>
 __device__ __forceinline__ void load_seg(const void* row, int V, int seg, bool vec_ok, float (&x)[32],
                                          int (&idx)[32]) {
@@ -431,203 +259,297 @@ __device__ __forceinline__ void load_seg(const void* row, int V, int seg, bool v
     }
 }
 
-// A: per (row, segment) max over finite logits.
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) seg_max_kernel(const void* __restrict__ logits, int K, int V,
-                                                              int nseg, int vec_ok,
-                                                              const int32_t* __restrict__ n_drafts,
-                                                              float* __restrict__ seg_max, void* __restrict__ hist) {
-    const int seg = blockIdx.x, row = blockIdx.y;
-    // Top-p: segment 0 clears the row's coarse histogram for the weight launch.
-    if (hist && seg == 0) {
-        u64* h = (u64*)hist + (size_t)row * (sizeof(RowHist) / sizeof(u64));
-        for (int i = threadIdx.x; i < (int)(sizeof(RowHist) / sizeof(u64)); i += kSegThreads) h[i] = 0;
-    }
-    const int R = K + 1;
-    const int b = row / R, j = row % R;
+__device__ __forceinline__ int live_rows(const int32_t* n_drafts, int b, int K) {
     int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
-    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    float x[32];
-    int idx[32];
-    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    float m = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-        if (finite_f(x[k])) m = fmaxf(m, x[k]);
-    __shared__ float red[kSegThreads / 64];
-    m = seg_block_max(m, red);
-    if (threadIdx.x == 0) seg_max[(size_t)row * nseg + seg] = m;
+    return n < 0 ? 0 : (n > K ? K : n);
 }
 
-// Row max and weight sum over the per-segment values, by a whole wave (lane s reads
-// segment s; nseg <= 64): one load round trip rather than a chain of nseg, which every
-// block of a launch would otherwise wait for.
+// Row max and Z = sum of f_s * E_s over the per-segment values, by a whole wave (lane s
+// reads segment s; nseg <= 64): one load round trip rather than a chain of nseg. Every
+// lane returns the same values.
 __device__ __forceinline__ float row_max_wave(const float* seg_max, int row, int nseg) {
     const int lane = threadIdx.x & 63;
     float m = lane < nseg ? seg_max[(size_t)row * nseg + lane] : -INFINITY;
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     return m;
 }
-__device__ __forceinline__ u64 row_z_wave(const u64* seg_z, int row, int nseg) {
+__device__ __forceinline__ u128 row_z_wave(const float* seg_max, const u64* seg_e, int row, int nseg, float m,
+                                           float inv_t) {
     const int lane = threadIdx.x & 63;
-    u64 z = lane < nseg ? seg_z[(size_t)row * nseg + lane] : 0ull;
-    for (int o = 32; o > 0; o >>= 1) z += shfl_xor_u64(z, o);
+    u128 z = 0;
+    if (lane < nseg && finite_f(m)) {
+        const float ms = seg_max[(size_t)row * nseg + lane];
+        z = (u128)seg_e[(size_t)row * nseg + lane] * seg_factor(ms, m, inv_t);
+    }
+    for (int o = 32; o > 0; o >>= 1) z += shfl_xor_u128(z, o);
     return z;
 }
 
-// B: per (row, segment) sum of fixed-point weights.
+// Eight consecutive logits [e0, e0 + 8) of a row (16-byte loads when aligned; NaN past
+// the row).
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) seg_z_kernel(const void* __restrict__ logits, int K, int V,
-                                                            int nseg, int vec_ok, float inv_t,
-                                                            const int32_t* __restrict__ n_drafts,
-                                                            const float* __restrict__ seg_max,
-                                                            u64* __restrict__ seg_z) {
+__device__ __forceinline__ void load8(const void* row, int V, int e0, bool vec_ok, float (&x)[8]) {
+    if (vec_ok && e0 + 8 <= V) {
+        if constexpr (DT == GG_DTYPE_F32) {
+            const float4 a = *(const float4*)((const float*)row + e0), c = *(const float4*)((const float*)row + e0 + 4);
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+        } else {
+            const uint4 r4 = *(const uint4*)((const uint16_t*)row + e0);
+            const uint32_t wv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint16_t h = (uint16_t)(wv[k >> 1] >> ((k & 1) * 16));
+                x[k] = DT == GG_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = e0 + k < V ? ld<DT>(row, e0 + k) : NAN;
+    }
+}
+
+// A: per (row, segment): the segment max m_s and E_s = sum of weight(l, m_s); with top-p
+// also the segment's coarse histogram of e over bins cb(m_s) - cb(l) (written out: the
+// row max, needed to merge, is not known yet). The only full read of the logits.
+template <gg_dtype_t DT, bool kTopP>
+__global__ void __launch_bounds__(kSegThreads) seg_pass_kernel(const void* __restrict__ logits, int K, int V,
+                                                               int nseg, int vec_ok, float inv_t,
+                                                               const int32_t* __restrict__ n_drafts,
+                                                               float* __restrict__ seg_max, u64* __restrict__ seg_e,
+                                                               u64* __restrict__ seg_hist) {
     const int seg = blockIdx.x, row = blockIdx.y;
     const int R = K + 1;
     const int b = row / R, j = row % R;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
-    __shared__ u64 red[kSegThreads / 64];
+    if (j > live_rows(n_drafts, b, K)) return;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the segment)
-    u64 z = 0;
-    if (finite_f(m)) {
-#pragma unroll
-        for (int k = 0; k < 32; ++k)
-            if (finite_f(x[k])) z += gg_weight(x[k], m, inv_t);
-    }
-    z = seg_block_sum(z, red);
-    if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
-}
-
-// ---- Segmented top-p: the nucleus boundary without whole-row passes per block ----
-//
-// The boundary is the last element, in (logit desc, index asc) order, whose mass before
-// it is below Tp = ceil(p*Z) (or zero). Coarse bins of 1/64 nat on (m - l)/T are ordered
-// the same way, so: (B') the weights of each segment also go into a per-row histogram of
-// coarse bins (integer sums: exact in any order); (C') a block per row finds the boundary
-// bin and the mass above it; (D') the elements of that bin are gathered (usually a few
-// hundred); (E') a block per row sorts them by (key desc, index asc) and walks the
-// weights to the cut. A bin with more than kCandCap elements flags its row for the exact
-// row kernel instead.
-
-// B': per (row, segment) weight sum and coarse histogram (the row's histogram and pick
-// were cleared by segment 0 of the max launch).
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) seg_zhist_kernel(const void* __restrict__ logits, int K, int V,
-                                                                int nseg, int vec_ok, float inv_t,
-                                                                const int32_t* __restrict__ n_drafts,
-                                                                const float* __restrict__ seg_max,
-                                                                u64* __restrict__ seg_z, RowHist* __restrict__ hist) {
-    const int row = blockIdx.y;
-    const int R = K + 1;
-    const int b = row / R, j = row % R;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
+    __shared__ float redf[kSegThreads / 64];
     __shared__ u64 red[kSegThreads / 64];
-    __shared__ u64 h_mass[kBins];
-    for (int i = threadIdx.x; i < kBins; i += kSegThreads) h_mass[i] = 0;
-    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    // kZhistSegs consecutive segments per block: their weights meet in one LDS histogram,
-    // flushed to the row's once (the global atomics are the launch's cost, not the loads).
-    // The next segment's logits are requested before the current one is weighed.
-    const int seg0 = blockIdx.x * kZhistSegs;
-    const int seg1 = min(seg0 + kZhistSegs, nseg);
-    float xn[32];
-    int idxn[32];
-    load_seg<DT>(lp, V, seg0, vec_ok, xn, idxn);
-    const float m = row_max_wave(seg_max, row, nseg);  // (requested after the first segment)
-    __syncthreads();  // the cleared histogram
-    for (int seg = seg0; seg < seg1; ++seg) {
-        float x[32];
+    __shared__ u64 h[kTopP ? kSegBins : 1];
+    if constexpr (kTopP) {
+        for (int i = threadIdx.x; i < kSegBins; i += kSegThreads) h[i] = 0;
+    }
+    float ms = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) x[k] = xn[k];
-        if (seg + 1 < seg1) load_seg<DT>(lp, V, seg + 1, vec_ok, xn, idxn);
-        u64 z = 0;
-        if (finite_f(m)) {
+    for (int k = 0; k < 32; ++k)
+        if (finite_f(x[k])) ms = fmaxf(ms, x[k]);
+    ms = seg_block_max(ms, redf);  // (its barriers also publish the cleared histogram)
+    u64 e = 0;
+    if (finite_f(ms)) {
+        const int cbm = kTopP ? cb_abs(ms, inv_t) : 0;
 #pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                const bool fin = finite_f(x[k]);
-                const u64 w = fin ? gg_weight(x[k], m, inv_t) : 0ull;
-                z += w;
-                if (w) atomicAdd(&h_mass[gg_coarse_bin(x[k], m, inv_t)], w);
+        for (int k = 0; k < 32; ++k) {
+            if (!finite_f(x[k])) continue;
+            const u64 w = gg_weight(x[k], ms, inv_t);
+            e += w;
+            if constexpr (kTopP) {
+                if (w) atomicAdd(&h[min(cbm - cb_abs(x[k], inv_t), kSegBins - 1)], w);
             }
         }
-        z = seg_block_sum(z, red);  // (its barriers also complete the LDS histogram)
-        if (threadIdx.x == 0) seg_z[(size_t)row * nseg + seg] = z;
     }
-    RowHist& h = hist[row];
-    for (int i = threadIdx.x; i < kBins; i += kSegThreads) {
-        if (h_mass[i]) atomicAdd(&h.mass[i], h_mass[i]);
+    e = seg_block_sum(e, red);  // (its barriers also complete the histogram)
+    if (threadIdx.x == 0) {
+        seg_max[(size_t)row * nseg + seg] = ms;
+        seg_e[(size_t)row * nseg + seg] = e;
+    }
+    if constexpr (kTopP) {
+        u64* out = seg_hist + ((size_t)row * nseg + seg) * kSegBins;
+        for (int i = threadIdx.x; i < kSegBins; i += kSegThreads) out[i] = h[i];
     }
 }
 
-// C': per row, the boundary coarse bin and the mass above it.
-__global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, float top_p,
+// The row bin of logit l: cb(m) - cb(l), capped at the last bin.
+__device__ __forceinline__ int row_bin(float l, int cbm, float inv_t) {
+    return min(cbm - cb_abs(l, inv_t), kRowBins - 1);
+}
+
+// ---- Top-p: the nucleus boundary ----
+//
+// The boundary is the last element, in (logit desc, index asc) order, whose mass before
+// it is below Tp = ceil(p*Z) (or zero). (B) A block per row merges the segments'
+// histograms into the row's (bins shifted by cb(m) - cb(m_s), masses scaled by f_s:
+// exact) and finds the boundary bin and the mass above it. (C) One wave per sequence
+// decides every draft whose outcome the bounds already fix: the nucleus mass lies in
+// [C, C + M] (C the mass above the boundary bin, M its mass), a draft in a bin above the
+// boundary bin is in the nucleus and one below is out. The rows left open, and the row
+// of the final draw, are flagged. (D) For flagged rows only, the boundary bin's
+// elements are gathered (usually a few hundred to a few thousand) together with each
+// segment's sum of e above the boundary bin; (E) a block per flagged row sorts them by
+// (key desc, index asc) and walks the weights to the exact cut. A boundary bin with more
+// than kCandCap elements falls back to the exact single-block row kernel.
+
+// B: per row, merge the segment histograms; the boundary bin, the mass above it and its
+// own mass. Thread t owns row bins t, t + 256, ...: row bin r gathers f_s * H_s[r - shift_s]
+// over the segments (the last row bin everything from there down), no atomics.
+__global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, float inv_t, float top_p,
                                                                const int32_t* __restrict__ n_drafts,
                                                                const float* __restrict__ seg_max,
-                                                               const u64* __restrict__ seg_z,
-                                                               const RowHist* __restrict__ hist,
+                                                               const u64* __restrict__ seg_e,
+                                                               const u64* __restrict__ seg_hist,
                                                                RowPick* __restrict__ pick) {
     const int row = blockIdx.x;
     const int R = K + 1;
     const int b = row / R, j = row % R;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
+    if (j > live_rows(n_drafts, b, K)) return;
+    __shared__ u64 hlo[kRowBins], hhi[kRowBins];
+    __shared__ int s_shift[64];
+    __shared__ u64 s_f[64];
     __shared__ int s_bin;
-    __shared__ u64 s_c;
+    __shared__ u128 s_c;
     const float m = row_max_wave(seg_max, row, nseg);
-    const u64 z = row_z_wave(seg_z, row, nseg);
+    const u128 z = row_z_wave(seg_max, seg_e, row, nseg, m, inv_t);
     if (!finite_f(m) || z == 0) {
-        if (threadIdx.x == 0) pick[row] = RowPick{-1, 0, 0, 0};
+        if (threadIdx.x == 0) pick[row] = RowPick{0, 0, 0, -1, 0};
         return;
     }
-    const u64 tp = (u64)ceil((double)top_p * (double)z);
+    const int cbm = cb_abs(m, inv_t);
+    if (threadIdx.x < nseg) {
+        const float ms = seg_max[(size_t)row * nseg + threadIdx.x];
+        const u64 f = seg_factor(ms, m, inv_t);
+        s_f[threadIdx.x] = f;
+        s_shift[threadIdx.x] = f ? cbm - cb_abs(ms, inv_t) : kRowBins;  // (no mass: no bins)
+    }
+    __syncthreads();
+    const u64* hrow = seg_hist + (size_t)row * nseg * kSegBins;
+    for (int r = threadIdx.x; r < kRowBins; r += kSegThreads) {
+        u128 acc = 0;
+        for (int sg = 0; sg < nseg; ++sg) {
+            const int lo = r - s_shift[sg];
+            if (lo >= kSegBins || lo < 0 && r < kRowBins - 1) continue;
+            const u64* hs = hrow + (size_t)sg * kSegBins;
+            u64 v = 0;
+            if (r < kRowBins - 1) {
+                v = hs[lo];
+                acc += (u128)v * s_f[sg];
+            } else {  // the last row bin: every segment bin from there down
+                u128 t = 0;
+                for (int bn = lo < 0 ? 0 : lo; bn < kSegBins; ++bn) t += hs[bn];
+                acc += t * s_f[sg];
+            }
+        }
+        hlo[r] = (u64)acc;
+        hhi[r] = (u64)(acc >> 64);
+    }
+    const u128 tp = gg_u128_floor(ceil((double)top_p * gg_u128_to_double(z)));
     if (threadIdx.x == 0) s_bin = -1;
     __syncthreads();
-    pick_bin(hist[row].mass, nullptr, kBins, false, 0, tp, &s_bin, &s_c);
+    pick_bin(hlo, hhi, nullptr, kRowBins, false, 0, tp, &s_bin, &s_c);
     __syncthreads();
-    if (threadIdx.x == 0) pick[row] = RowPick{s_bin, 0, s_c, tp};
+    if (threadIdx.x == 0) {
+        const int cb = s_bin;
+        pick[row] = RowPick{s_c, ((u128)hhi[cb] << 64) | hlo[cb], tp, cb, 0};
+    }
 }
 
-// D': per (row, segment), gather the elements of the boundary bin.
+// The bounds test of one draft: kRowAccept / kRowReject when the coarse bounds decide
+// it, kRowUnsure otherwise. W of the draft token x is e_x * f_x when x lies above the
+// boundary bin.
+template <gg_dtype_t DT>
+__device__ __forceinline__ int bounds_test(const void* lp, const float* rsm, const RowPick& pk, float m, float inv_t,
+                                           int x, int V, double u, double q) {
+    if (pk.cbin < 0 || x < 0 || x >= V) return kRowReject;  // no mass, or no token: W(x) = 0
+    const float l = ld<DT>(lp, x);
+    if (!finite_f(l)) return kRowReject;
+    const int rb = row_bin(l, cb_abs(m, inv_t), inv_t);
+    if (rb > pk.cbin) return kRowReject;  // below the boundary bin: outside the nucleus
+    if (rb == pk.cbin) return kRowUnsure;
+    const float ms = rsm[x / kSegElems];
+    const double wx = gg_u128_to_double((u128)gg_weight(l, ms, inv_t) * seg_factor(ms, m, inv_t));
+    if (u * q * gg_u128_to_double(pk.c_above + pk.m_bin) < wx) return kRowAccept;  // Zp <= C + M
+    if (!(u * q * gg_u128_to_double(pk.c_above) < wx)) return kRowReject;          // Zp >= C
+    return kRowUnsure;
+}
+
+// C: per sequence, one wave: the rows' bound outcomes; flags the rows that need the exact
+// nucleus (an open row and every row after it through the first certain rejection, or
+// just the row of the final draw when the bounds settle the walk).
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restrict__ logits,
+                                                           const float* __restrict__ dprobs, int K, int V, int nseg,
+                                                           float inv_t, const int32_t* __restrict__ drafts,
+                                                           const int32_t* __restrict__ n_drafts,
+                                                           const float* __restrict__ uniforms,
+                                                           const float* __restrict__ seg_max,
+                                                           const RowPick* __restrict__ pick,
+                                                           int* __restrict__ status, int* __restrict__ flag) {
+    const int b = blockIdx.x;
+    const int R = K + 1;
+    const int n = live_rows(n_drafts, b, K);
+    const int lane = threadIdx.x;
+    // The rows one after another (row_max_wave needs the whole wave on one row); lane 0
+    // tests each draft.
+    for (int j = 0; j < n; ++j) {
+        const int row = b * R + j;
+        const float m = row_max_wave(seg_max, row, nseg);
+        if (lane == 0) {
+            const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+            const int x = drafts[(size_t)b * K + j];
+            const double q = (dprobs && x >= 0 && x < V) ? gg_clean_q(dprobs[((size_t)b * K + j) * V + x]) : 1.0;
+            const double u = (double)uniforms[(size_t)b * R + j];
+            status[row] = bounds_test<DT>(lp, seg_max + (size_t)row * nseg, pick[row], m, inv_t, x, V, u, q);
+        }
+    }
+    if (lane == 0) {
+        // Walk: the first row that is not a certain acceptance.
+        int j0 = n;
+        for (int j = 0; j < n; ++j)
+            if (status[b * R + j] != kRowAccept) {
+                j0 = j;
+                break;
+            }
+        int jend = j0;  // flag rows j0 .. jend
+        if (j0 < n && status[b * R + j0] == kRowUnsure) {
+            jend = n;
+            for (int j = j0 + 1; j < n; ++j)
+                if (status[b * R + j] == kRowReject) {
+                    jend = j;
+                    break;
+                }
+        }
+        for (int j = 0; j <= n; ++j) flag[b * R + j] = (j >= j0 && j <= jend) ? 1 : 0;
+    }
+}
+
+// D: per (flagged row, segment): the sum of e over the elements above the boundary bin
+// (all in the nucleus), and the boundary bin's elements gathered for the cut.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __restrict__ logits, int K, int V,
                                                                  int nseg, int vec_ok, float inv_t,
                                                                  const int32_t* __restrict__ n_drafts,
+                                                                 const int* __restrict__ flag,
                                                                  const float* __restrict__ seg_max,
                                                                  RowPick* __restrict__ pick,
-                                                                 uint2* __restrict__ cand) {
+                                                                 uint2* __restrict__ cand, u64* __restrict__ seg_keep) {
     const int seg = blockIdx.x, row = blockIdx.y;
     const int R = K + 1;
     const int b = row / R, j = row % R;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
+    if (j > live_rows(n_drafts, b, K) || !flag[row]) return;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    // The boundary bin and the row max are requested after the segment.
+    __shared__ u64 red[kSegThreads / 64];
     const int cbin = pick[row].cbin;
     const float m = row_max_wave(seg_max, row, nseg);
-    if (cbin < 0) return;
-    // The lane's hits as a bit mask first (vector work only), then one counter update per
-    // lane that has any, and its candidates written in order.
+    const float ms = seg_max[(size_t)row * nseg + seg];
+    const int cbm = cb_abs(m, inv_t);
+    // Above the boundary bin: kept; in it: gathered (a bit mask first, then one counter
+    // update per lane that has any and its candidates written in order).
+    u64 keep = 0;
     uint32_t hits = 0;
+    if (cbin >= 0 && finite_f(ms)) {
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const bool hit = idx[k] < V && finite_f(x[k]) && gg_coarse_bin(x[k], m, inv_t) == cbin;
-        hits |= (uint32_t)hit << k;
+        for (int k = 0; k < 32; ++k) {
+            if (!finite_f(x[k])) continue;
+            const int rb = row_bin(x[k], cbm, inv_t);
+            if (rb < cbin) keep += gg_weight(x[k], ms, inv_t);
+            hits |= (uint32_t)(rb == cbin) << k;
+        }
     }
+    keep = seg_block_sum(keep, red);
+    if (threadIdx.x == 0) seg_keep[(size_t)row * nseg + seg] = keep;
     if (hits) {
         int slot = atomicAdd(&pick[row].n_cand, __popc(hits));
         while (hits) {
@@ -644,38 +566,46 @@ __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __r
     }
 }
 
-// E': per row, sort the boundary bin's elements by (key desc, index asc) and cut; fills
-// the row's statistics, or flags the row for the exact row kernel (too many elements).
+// The logit of an order key (inverse of gg_order_key).
+__device__ __forceinline__ float logit_of_key(unsigned int key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// E: per flagged row, sort the boundary bin's elements by (key desc, index asc) and cut;
+// the row's exact statistics, and the kept elements' e added to their segments' sums.
+// A crowded bin (more than kCandCap elements) flags the row for the exact row kernel.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict__ logits, int K, int V,
                                                           int nseg, float inv_t,
                                                           const int32_t* __restrict__ drafts,
                                                           const int32_t* __restrict__ n_drafts,
+                                                          const int* __restrict__ flag,
                                                           const float* __restrict__ seg_max,
                                                           const RowPick* __restrict__ pick,
                                                           const uint2* __restrict__ cand,
-                                                          RowStats* __restrict__ stats, int* __restrict__ flag) {
+                                                          RowStats* __restrict__ stats, u64* __restrict__ seg_keep,
+                                                          int* __restrict__ crowded) {
     const int row = blockIdx.x;
     const int R = K + 1;
     const int b = row / R, j = row % R;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    if (j > n) return;
+    const int n = live_rows(n_drafts, b, K);
+    if (j > n || !flag[row]) return;
     __shared__ u64 s_key[kCandCap];    // order key << 32 | (~index): descending = the nucleus order
-    __shared__ u64 red[1024 / 64];
+    __shared__ u128 red[1024 / 64];
+    __shared__ u64 s_segk[64];
     __shared__ int s_last;
     const RowPick pk = pick[row];
     const float m = row_max_wave(seg_max, row, nseg);
     if (pk.cbin < 0) {  // no finite logit or Z == 0: no nucleus
         if (threadIdx.x == 0) {
-            stats[row] = RowStats{m, 0x7fffffff, 0ull, 0u, 1, 0ull};
-            flag[row] = 0;
+            stats[row] = RowStats{0, 0, m, 0x7fffffff, 0u, 1};
+            crowded[row] = 0;
         }
         return;
     }
     const int nc = pk.n_cand;
     if (nc > kCandCap) {
-        if (threadIdx.x == 0) flag[row] = 1;
+        if (threadIdx.x == 0) crowded[row] = 1;
         return;
     }
     int np2 = 1;
@@ -688,6 +618,7 @@ __global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict
             s_key[i] = 0;  // sorts last
         }
     }
+    if (threadIdx.x < 64) s_segk[threadIdx.x] = 0;
     __syncthreads();
     // Bitonic sort, descending.
     for (int k = 2; k <= np2; k <<= 1) {
@@ -706,40 +637,49 @@ __global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict
             __syncthreads();
         }
     }
-    // Weights in that order (the logit is recovered from the order key). Thread t owns
-    // elements [4t, 4t+4): an exclusive block scan of the thread sums gives each
-    // element's mass before it; the kept elements are a prefix (that mass never drops),
-    // so the cut is the largest kept position.
-    const int e0 = 4 * (int)threadIdx.x;
-    u64 w[4];
-    u64 tsum = 0;
+    // Weights in that order (logit from the order key, segment max from the index).
+    // Thread t owns positions [4t, 4t+4): an exclusive block scan of the thread sums gives
+    // each element's mass before it; the kept elements are a prefix (that mass never
+    // drops), so the cut is the largest kept position. Candidates span at most
+    // kCandCap = 4 * 1024 positions.
+    const int p0 = 4 * (int)threadIdx.x;
+    u128 w[4];
+    u64 ev[4];
+    int sv[4];
+    u128 tsum = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         w[k] = 0;
-        if (e0 + k < nc) {
-            const unsigned int key = (unsigned int)(s_key[e0 + k] >> 32);
-            const unsigned int bits = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
-            w[k] = gg_weight(__uint_as_float(bits), m, inv_t);
+        ev[k] = 0;
+        sv[k] = 0;
+        if (p0 + k < nc) {
+            const u64 key = s_key[p0 + k];
+            const int i = (int)(~(unsigned int)(key & 0xffffffffu));
+            sv[k] = i / kSegElems;
+            const float ms = seg_max[(size_t)row * nseg + sv[k]];
+            ev[k] = gg_weight(logit_of_key((unsigned int)(key >> 32)), ms, inv_t);
+            w[k] = (u128)ev[k] * seg_factor(ms, m, inv_t);
         }
         tsum += w[k];
     }
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    u64 incl = tsum;
+    u128 incl = tsum;
     for (int o = 1; o < 64; o <<= 1) {
-        const u64 t = shfl_up_u64(incl, o);
+        const u128 t = shfl_up_u128(incl, o);
         if (lane >= o) incl += t;
     }
     if (lane == 63) red[wv] = incl;
     __syncthreads();
-    u64 before = pk.c_above + incl - tsum;
+    u128 before = pk.c_above + incl - tsum;
     for (int i = 0; i < wv; ++i) before += red[i];
     int last = -1;
-    u64 zp = 0;
+    u128 zp = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        if (e0 + k < nc && (before < pk.tp || before == 0)) {
-            last = e0 + k;
+        if (p0 + k < nc && (before < pk.tp || before == 0)) {
+            last = p0 + k;
             zp = before + w[k];
+            if (ev[k]) atomicAdd(&s_segk[sv[k]], ev[k]);
         }
         before += w[k];
     }
@@ -747,285 +687,463 @@ __global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict
     __syncthreads();
     if (last >= 0) atomicMax(&s_last, last);
     __syncthreads();
+    // The kept candidates' e into their segments' sums (seg_gather_kernel wrote the part
+    // above the boundary bin).
+    if (threadIdx.x < nseg && s_segk[threadIdx.x]) seg_keep[(size_t)row * nseg + threadIdx.x] += s_segk[threadIdx.x];
     if (last >= 0 && last == s_last) {  // the owner of the cut (position 0 always qualifies)
         const unsigned int lam = (unsigned int)(s_key[last] >> 32);
         // Ties at the boundary key kept for index <= idx_cut; every index when all are.
         const bool all_ties = last + 1 >= nc || (unsigned int)(s_key[last + 1] >> 32) != lam;
         const int idx_cut = all_ties ? 0x7fffffff : (int)(~(unsigned int)(s_key[last] & 0xffffffffu));
-        RowStats st{m, idx_cut, zp, lam, 1, 0ull};
+        RowStats st{zp, 0, m, idx_cut, lam, 1};
         if (j < n) {
             const int x = drafts[(size_t)b * K + j];
             if (x >= 0 && x < V) {
                 const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
                 Nucleus nu{m, inv_t, lam, idx_cut};
-                st.wx = nu.weight(ld<DT>(lp, x), x);
+                st.wx = nu.weight(ld<DT>(lp, x), x, seg_max[(size_t)row * nseg + x / kSegElems]);
             }
         }
         stats[row] = st;
-        flag[row] = 0;
+        crowded[row] = 0;
     }
 }
 
-// Per-row statistics seen by the decision: max, nucleus mass and nucleus boundary.
+// Exact per-row nucleus statistics in one 1024-thread block (passes over the whole row),
+// for the rows row_select_kernel found crowded; also rewrites the row's per-segment sums
+// of kept e. Uses the segment maxima and sums of seg_pass_kernel.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
+    const void* __restrict__ logits, int K, int V, int nseg, const int32_t* __restrict__ drafts,
+    const int32_t* __restrict__ n_drafts, float inv_t, float top_p, const int* __restrict__ flag,
+    const int* __restrict__ crowded, const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
+    RowStats* __restrict__ stats, u64* __restrict__ seg_keep) {
+    const int row = blockIdx.x;
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    const int n = live_rows(n_drafts, b, K);
+    if (j > n || !flag[row] || crowded[row] == 0) return;
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    const float* rms = seg_max + (size_t)row * nseg;
+
+    __shared__ u64 hlo[kBins], hhi[kBins];
+    __shared__ unsigned int hcnt[kBins];
+    __shared__ int s_bin;
+    __shared__ u128 s_c;
+
+    const float m = row_max_wave(seg_max, row, nseg);  // (every wave computes it)
+    const u128 z = row_z_wave(seg_max, seg_e, row, nseg, m, inv_t);
+    // Crowded rows have a finite max and Z > 0 (row_pick found a boundary bin).
+    const u128 tp = gg_u128_floor(ceil((double)top_p * gg_u128_to_double(z)));
+    auto w_of = [&](float l, int i) -> u128 {
+        const float ms = rms[i / kSegElems];
+        return (u128)gg_weight(l, ms, inv_t) * seg_factor(ms, m, inv_t);
+    };
+    auto clear = [&]() {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kBins; i += kThreads) {
+            hlo[i] = hhi[i] = 0;
+            hcnt[i] = 0;
+        }
+        __syncthreads();
+    };
+
+    // Coarse bins (1/64 nat of (m - l)/T), then three radix levels on the order key
+    // within the boundary bin, then the ties at the boundary key by index.
+    clear();
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+        const float l = ld<DT>(lp, i);
+        if (!finite_f(l)) continue;
+        const int bn = gg_coarse_bin(l, m, inv_t);
+        atomic_add_u128(&hlo[bn], &hhi[bn], w_of(l, i));
+        atomicAdd(&hcnt[bn], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) s_bin = -1;
+    __syncthreads();
+    pick_bin(hlo, hhi, hcnt, kBins, false, 0, tp, &s_bin, &s_c);
+    __syncthreads();
+    const int cbin = s_bin;
+    u128 c_above = s_c;
+    unsigned int prefix = 0, pmask = 0;
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+    for (int lv = 0; lv < 3; ++lv) {
+        const int nb = 1 << widths[lv];
+        clear();
+        for (int i = threadIdx.x; i < V; i += kThreads) {
+            const float l = ld<DT>(lp, i);
+            if (!finite_f(l)) continue;
+            if (gg_coarse_bin(l, m, inv_t) != cbin) continue;
+            const unsigned int key = gg_order_key(l);
+            if ((key & pmask) != prefix) continue;
+            const int d = (key >> shifts[lv]) & (nb - 1);
+            atomic_add_u128(&hlo[d], &hhi[d], w_of(l, i));
+            atomicAdd(&hcnt[d], 1u);
+        }
+        __syncthreads();
+        // (Unused bins of the 10-bit level stay empty: the scan covers kBins.)
+        pick_bin(hlo, hhi, hcnt, kBins, true, c_above, tp, &s_bin, &s_c);
+        __syncthreads();
+        prefix |= (unsigned int)s_bin << shifts[lv];
+        pmask |= (unsigned int)(nb - 1) << shifts[lv];
+        c_above = s_c;
+    }
+    const unsigned int lam = prefix;
+    // The ties at the boundary key, in index order: a tie is kept while the mass before
+    // it is below tp (or zero), i.e. every tie through the first one whose inclusive mass
+    // reaches tp. Two 9-bit levels over the index find that tie; when none reaches tp,
+    // every tie is kept.
+    const unsigned int dl = prefix & 0x3ffu;
+    const u128 m_tie = ((u128)hhi[dl] << 64) | hlo[dl];
+    int idx_cut = 0x7fffffff;
+    u128 zp = c_above + m_tie;
+    if (c_above + m_tie >= tp) {
+        unsigned int iprefix = 0, imask = 0;
+        u128 base = c_above;
+        const int ish[2] = {9, 0};
+        for (int lv = 0; lv < 2; ++lv) {
+            clear();
+            for (int i = threadIdx.x; i < V; i += kThreads) {
+                const float l = ld<DT>(lp, i);
+                if (!finite_f(l) || gg_order_key(l) != lam) continue;
+                if (((unsigned int)i & imask) != iprefix) continue;
+                const int d = ((unsigned int)i >> ish[lv]) & 511u;
+                atomic_add_u128(&hlo[d], &hhi[d], w_of(l, i));
+                atomicAdd(&hcnt[d], 1u);
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                // The first index bin, in order, holding a tie at which the inclusive
+                // mass reaches tp (the mass before the first tie is c_above: below tp,
+                // or zero, in which case the first tie is kept whatever its weight).
+                u128 acc = base;
+                int d = 0;
+                for (; d < 511; ++d) {
+                    const u128 md = ((u128)hhi[d] << 64) | hlo[d];
+                    if (hcnt[d] && acc + md >= tp) break;
+                    acc += md;
+                }
+                s_bin = d;
+                s_c = acc;
+            }
+            __syncthreads();
+            base = s_c;
+            iprefix |= (unsigned int)s_bin << ish[lv];
+            imask |= 511u << ish[lv];
+        }
+        idx_cut = (int)iprefix;
+        zp = base + w_of(logit_of_key(lam), idx_cut);
+    }
+    // The kept elements' e per segment.
+    const Nucleus nu{m, inv_t, lam, idx_cut};
+    __shared__ u64 s_segk[64];
+    __syncthreads();
+    if (threadIdx.x < 64) s_segk[threadIdx.x] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+        const float l = ld<DT>(lp, i);
+        if (!nu.kept(l, i)) continue;
+        const u64 e = gg_weight(l, rms[i / kSegElems], inv_t);
+        if (e) atomicAdd(&s_segk[i / kSegElems], e);
+    }
+    __syncthreads();
+    if (threadIdx.x < nseg) seg_keep[(size_t)row * nseg + threadIdx.x] = s_segk[threadIdx.x];
+    if (threadIdx.x == 0) {
+        RowStats st{zp, 0, m, idx_cut, lam, 1};
+        if (j < n) {
+            const int x = drafts[(size_t)b * K + j];
+            if (x >= 0 && x < V) st.wx = nu.weight(ld<DT>(lp, x), x, rms[x / kSegElems]);
+        }
+        stats[row] = st;
+    }
+}
+
+// Per-row statistics seen by the draw: max, nucleus mass and nucleus boundary.
 struct RowView {
+    u128 zp;
     float m;
-    u64 zp;
     unsigned int lam;
     int idx_cut;
 };
 
-// The view of one row the decision needs (max, nucleus mass and boundary), evaluated by a
-// whole wave: lane s < nseg reads segment s (nseg <= 64), the wave reduces. Every lane
-// returns the same view.
-__device__ __forceinline__ RowView row_view_wave(int row, int nseg, int use_topp, const RowStats* stats,
-                                                 const float* seg_max, const u64* seg_z) {
+// A sequence's decision and the view of its final row, written by decide_kernel.
+struct SeqPlan {
     RowView v;
-    if (use_topp) {
-        const RowStats& st = stats[row];
-        v.m = st.m;
-        v.zp = st.zp;
-        v.lam = st.lam;
-        v.idx_cut = st.idx_cut;
-        return v;
-    }
-    const int lane = threadIdx.x & 63;
-    float m = lane < nseg ? seg_max[(size_t)row * nseg + lane] : -INFINITY;
-    u64 z = lane < nseg ? seg_z[(size_t)row * nseg + lane] : 0ull;
-    for (int o = 32; o > 0; o >>= 1) {
-        m = fmaxf(m, __shfl_xor(m, o));
-        z += shfl_xor_u64(z, o);
-    }
-    v.m = m;
-    v.zp = z;
-    v.lam = 0;
-    v.idx_cut = 0x7fffffff;
-    return v;
-}
+    SeqDecision d;
+};
 
-// The acceptance walk of one sequence, run by a whole wave (every lane gets the result).
-// The rows' tests do not depend on each other, so they are evaluated together: groups of
-// g = 2^ceil(log2 nseg) lanes take one row each (lane s of a group reads segment s), 64/g
-// rows per pass; the walk then stops at the first failed row.
+// F: per sequence, one wave: the acceptance walk and the view of the final row. Without
+// top-p every row's values come from the segment maxima and sums; with top-p a row the
+// bounds decided keeps that outcome and a flagged row is tested on its exact nucleus.
 template <gg_dtype_t DT>
-__device__ SeqDecision decide_seq_wave(const void* logits, const float* dprobs, int K, int V, int b, int n,
-                                       const int32_t* drafts, const float* uniforms, float inv_t, int nseg,
-                                       int use_topp, const RowStats* stats, const float* seg_max,
-                                       const u64* seg_z) {
+__global__ void __launch_bounds__(64) decide_kernel(const void* __restrict__ logits, const float* __restrict__ dprobs,
+                                                    int K, int V, int nseg, float inv_t, int use_topp,
+                                                    const int32_t* __restrict__ drafts,
+                                                    const int32_t* __restrict__ n_drafts,
+                                                    const float* __restrict__ uniforms,
+                                                    const RowStats* __restrict__ stats,
+                                                    const int* __restrict__ status, const int* __restrict__ flag,
+                                                    const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
+                                                    SeqPlan* __restrict__ plan) {
+    const int b = blockIdx.x;
     const int R = K + 1;
-    const int lane = threadIdx.x & 63;
+    const int n = live_rows(n_drafts, b, K);
+    // The rows' tests do not depend on each other, so they run together: groups of
+    // g = 2^ceil(log2 nseg) lanes take one row each (lane s of a group reads segment s),
+    // 64/g rows per pass; the walk stops at the first failed row.
+    const int lane = threadIdx.x;
     int g = 1;
     while (g < nseg) g <<= 1;
     const int per_pass = 64 / g;
     const int jl = lane / g, sl = lane % g;
+    int a = n, residual = 0;
     for (int j0 = 0; j0 < n; j0 += per_pass) {
         const int j = j0 + jl;
         const bool live = j < n;
         const int row = b * R + (live ? j : 0);
-        float m;
-        u64 zp;
-        unsigned int lam = 0;
-        int idx_cut = 0x7fffffff;
-        if (use_topp) {
-            const RowStats& st = stats[row];
-            m = st.m;
-            zp = st.zp;
-            lam = st.lam;
-            idx_cut = st.idx_cut;
-        } else {
-            m = sl < nseg ? seg_max[(size_t)row * nseg + sl] : -INFINITY;
-            zp = sl < nseg ? seg_z[(size_t)row * nseg + sl] : 0ull;
-            for (int o = g >> 1; o > 0; o >>= 1) {
-                m = fmaxf(m, __shfl_xor(m, o));
-                zp += shfl_xor_u64(zp, o);
-            }
-        }
+        const int x = live ? drafts[(size_t)b * K + j] : -1;
         bool ok = true;
-        if (live) {
-            const int x = drafts[(size_t)b * K + j];
+        if (use_topp && !flag[row]) {
+            ok = status[row] == kRowAccept;
+        } else {
+            float m;
+            u128 zp, wx = 0;
+            if (use_topp) {
+                const RowStats st = stats[row];
+                m = st.m;
+                zp = st.zp;
+                wx = st.wx;
+            } else {
+                const float ms = sl < nseg ? seg_max[(size_t)row * nseg + sl] : -INFINITY;
+                m = ms;
+                for (int o = g >> 1; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+                zp = (sl < nseg && finite_f(m)) ? (u128)seg_e[(size_t)row * nseg + sl] * seg_factor(ms, m, inv_t) : 0;
+                for (int o = g >> 1; o > 0; o >>= 1) zp += shfl_xor_u128(zp, o);
+                if (x >= 0 && x < V && finite_f(m)) {
+                    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+                    const Nucleus nu{m, inv_t, 0u, 0x7fffffff};
+                    wx = nu.weight(ld<DT>(lp, x), x, seg_max[(size_t)row * nseg + x / kSegElems]);
+                }
+            }
             ok = false;
             if (x >= 0 && x < V && finite_f(m)) {
-                const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-                Nucleus nu{m, inv_t, lam, idx_cut};
-                const u64 wx = nu.weight(ld<DT>(lp, x), x);
-                const double q = dprobs ? (double)dprobs[((size_t)b * K + j) * V + x] : 1.0;
+                const double q = dprobs ? gg_clean_q(dprobs[((size_t)b * K + j) * V + x]) : 1.0;
                 const double u = (double)uniforms[(size_t)b * R + j];
-                ok = u * q * (double)zp < (double)wx;
+                ok = u * q * gg_u128_to_double(zp) < gg_u128_to_double(wx);
             }
         }
-        const unsigned long long bad = __ballot(!ok && sl == 0);
+        const unsigned long long bad = __ballot(live && !ok && sl == 0);
         if (bad) {
-            const int jf = j0 + (__ffsll((long long)bad) - 1) / g;
-            return SeqDecision{jf, jf, 1};
+            a = j0 + (__ffsll((long long)bad) - 1) / g;
+            residual = 1;
+            break;
         }
     }
-    return SeqDecision{n, n, 0};
+    const int row = b * R + a;
+    RowView v;
+    if (use_topp) {
+        const RowStats st = stats[row];
+        v = RowView{st.zp, st.m, st.lam, st.idx_cut};
+    } else {
+        v.m = row_max_wave(seg_max, row, nseg);
+        v.zp = row_z_wave(seg_max, seg_e, row, nseg, v.m, inv_t);
+        v.lam = 0;
+        v.idx_cut = 0x7fffffff;
+    }
+    if (threadIdx.x == 0) plan[b] = SeqPlan{v, SeqDecision{a, a, residual}};
 }
 
-// D: per (sequence, segment): decide, then the segment's residual and plain weight
-// sums on the final row (and the last non-zero index of each).
+// G (dense draft distributions only): per (sequence, segment) the residual weight sum of
+// the final row's segment, f_s * sum of rq, rq = e - min(e, floor(q * Zp / f_s)) over the
+// nucleus (the rejected draft's q row read once). Thread t of kSumThreads owns kSumRuns
+// runs of eight logits, run r at offset (r * kSumThreads + t) * 8 of the segment.
+#ifndef GG_SUM_THREADS
+#define GG_SUM_THREADS 512
+#endif
+constexpr int kSumThreads = GG_SUM_THREADS;
+constexpr int kSumRuns = kSegElems / (kSumThreads * 8);
+static_assert(kSumRuns * kSumThreads * 8 == kSegElems, "segment = runs of eight logits per thread");
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) seg_draw_sums_kernel(
+__global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
     const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
-    float inv_t, int use_topp, const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
-    const float* __restrict__ uniforms, const RowStats* __restrict__ stats,
-    const float* __restrict__ seg_max, const u64* __restrict__ seg_z, SeqDecision* __restrict__ dec,
-    SegOut* __restrict__ seg_out) {
+    float inv_t, const float* __restrict__ seg_max, const SeqPlan* __restrict__ plan, SegSum* __restrict__ seg_sum) {
     const int seg = blockIdx.x, b = blockIdx.y;
     const int R = K + 1;
-    int n = n_drafts[b];
-    n = n < 0 ? 0 : (n > K ? K : n);
-    __shared__ SeqDecision s_d;
-    __shared__ RowView s_rv;
-    __shared__ u64 red[kSegThreads / 64];
-    __shared__ int redi[kSegThreads / 64];
-    if (threadIdx.x < 64) {
-        const SeqDecision dd = decide_seq_wave<DT>(logits, dprobs, K, V, b, n, drafts, uniforms, inv_t, nseg,
-                                                   use_topp, stats, seg_max, seg_z);
-        const RowView rv = row_view_wave(b * R + dd.row, nseg, use_topp, stats, seg_max, seg_z);
-        if (threadIdx.x == 0) {
-            s_d = dd;
-            s_rv = rv;
-            if (seg == 0) dec[b] = dd;
-        }
-    }
-    __syncthreads();
-    const SeqDecision d = s_d;
-    const RowView rv = s_rv;
+    constexpr int kW = kSumThreads / 64;
+    __shared__ u64 red64[kW];
+    const SeqDecision d = plan[b].d;
+    if (!d.residual) return;  // the bonus draw needs no residual
+    const RowView rv = plan[b].v;
     const int row = b * R + d.row;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    float x[32];
-    int idx[32];
-    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
-    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
-    const float* qrow = (d.residual && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
-    const int xr = d.residual ? drafts[(size_t)b * K + d.row] : -1;
-    const double zp_d = (double)rv.zp;
-    u64 s_res = 0, s_pl = 0;
-    int l_res = -1, l_pl = -1;
-    const bool row_ok = finite_f(rv.m);
+    const float* qrow = dprobs + ((size_t)b * K + d.row) * V;
+    float x[kSumRuns][8], q[kSumRuns][8];
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const int i = idx[k];
-        if (i >= V || !row_ok) continue;
-        const u64 w = nu.weight(x[k], i);
-        u64 r = w;
-        if (d.residual) {
-            u64 qf;
-            if (qrow) {
-                const float qi = qrow[i];
-                qf = (u64)(qi < 0.f ? 0.0 : (double)qi * zp_d);
-            } else {
-                qf = (i == xr) ? rv.zp : 0ull;
-            }
-            r = w > qf ? w - qf : 0ull;
-        }
-        s_res += r;
-        s_pl += w;
-        if (r) l_res = max(l_res, i);
-        if (w) l_pl = max(l_pl, i);
+    for (int r = 0; r < kSumRuns; ++r) {
+        const int e0 = seg * kSegElems + (r * kSumThreads + (int)threadIdx.x) * 8;
+        load8<DT>(lp, V, e0, vec_ok, x[r]);
+        load8<GG_DTYPE_F32>(qrow, V, e0, vec_ok && ((uintptr_t)qrow % 16) == 0, q[r]);
     }
-    s_res = seg_block_sum(s_res, red);
-    s_pl = seg_block_sum(s_pl, red);
-    l_res = seg_block_maxi(l_res, redi);
-    l_pl = seg_block_maxi(l_pl, redi);
-    if (threadIdx.x == 0) seg_out[(size_t)b * nseg + seg] = SegOut{s_res, s_pl, l_res, l_pl};
+    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
+    const float ms = seg_max[(size_t)row * nseg + seg];
+    const u64 f = (finite_f(rv.m) && finite_f(ms)) ? seg_factor(ms, rv.m, inv_t) : 0ull;
+    const double zpf = f ? gg_u128_to_double(rv.zp) / (double)f : 0.0;
+    u64 s_res = 0;
+#pragma unroll
+    for (int r = 0; r < kSumRuns; ++r) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = seg * kSegElems + (r * kSumThreads + (int)threadIdx.x) * 8 + k;
+            const bool keep = f && nu.kept(x[r][k], i);  // (NaN past the row: never kept)
+            const u64 e = keep ? gg_weight(x[r][k], ms, inv_t) : 0ull;
+            const double qd = gg_clean_q(q[r][k]) * zpf;
+            s_res += (e && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
+        }
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int o = 32; o > 0; o >>= 1) s_res += shfl_xor_u64(s_res, o);
+    if (lane == 0) red64[wv] = s_res;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        u64 tr = 0;
+        for (int w = 0; w < kW; ++w) tr += red64[w];
+        seg_sum[(size_t)b * nseg + seg] = SegSum{(u128)tr * f};
+    }
 }
 
-// E: per sequence: pick the segment holding floor(u * total), then the element inside it.
-// Wave 0 reduces and scans the segment sums (lane s = segment s); in the chosen segment
-// thread k of 1024 owns the 8 consecutive elements [8k, 8k+8) and a block scan of the
-// thread sums finds the thread whose run crosses the target.
+// H: per sequence, the draw. Wave 0 forms the final row's per-segment masses (lane s =
+// segment s): plain = f_s * (sum of kept e); residual = the dense sums above, or with
+// one-hot q the plain mass less the rejected draft's e - rq; picks the segment holding
+// floor(u * total) (the last segment with mass when none passes it, u >= 1). In that
+// segment thread k of 1024 owns the 8 consecutive elements [8k, 8k+8): their integer
+// weights (e, or rq) and a block scan find the element (or the last non-zero one).
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
-    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, float inv_t,
-    int use_topp, const int32_t* __restrict__ drafts, const float* __restrict__ uniforms,
-    const RowStats* __restrict__ stats, const float* __restrict__ seg_max, const u64* __restrict__ seg_z,
-    const SeqDecision* __restrict__ dec, const SegOut* __restrict__ seg_out, int32_t* __restrict__ out_acc,
+    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
+    float inv_t, int use_topp, const int32_t* __restrict__ drafts, const float* __restrict__ uniforms,
+    const float* __restrict__ seg_max, const u64* __restrict__ seg_e, const u64* __restrict__ seg_keep,
+    const SeqPlan* __restrict__ plan, const SegSum* __restrict__ seg_sum, int32_t* __restrict__ out_acc,
     int32_t* __restrict__ out_tok) {
     const int b = blockIdx.x;
     const int R = K + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __shared__ int s_seg, s_use_res, s_found;
-    __shared__ u64 s_t;
+    __shared__ int s_seg, s_use_res, s_found, s_last_mode;
+    __shared__ u128 s_t;
     __shared__ u64 s_wsum[kFindThreads / 64];
-    const SeqDecision d = dec[b];
+    const SeqDecision d = plan[b].d;
+    const RowView rv = plan[b].v;
+    const int row = b * R + d.row;
+    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+    const bool dense = d.residual && dprobs;
+    const int xr = d.residual ? drafts[(size_t)b * K + d.row] : -1;
+    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
     if (wave == 0) {
-        const SegOut o = lane < nseg ? seg_out[(size_t)b * nseg + lane] : SegOut{0ull, 0ull, -1, -1};
-        u64 tot_res = o.sum_res, tot_pl = o.sum_plain;
-        int last_res = o.last_res, last_pl = o.last_plain;
+        u128 pl = 0, res = 0;
+        if (lane < nseg) {
+            const float ms = seg_max[(size_t)row * nseg + lane];
+            const u64 f = (finite_f(rv.m) && finite_f(ms)) ? seg_factor(ms, rv.m, inv_t) : 0ull;
+            const u64 ek = use_topp ? seg_keep[(size_t)row * nseg + lane] : seg_e[(size_t)row * nseg + lane];
+            pl = (u128)ek * f;
+            if (dense) {
+                res = seg_sum[(size_t)b * nseg + lane].res;
+            } else if (d.residual) {
+                res = pl;
+                if (xr >= 0 && xr < V && xr / kSegElems == lane && f) {
+                    const float l = ld<DT>(lp, xr);
+                    const u64 e = nu.kept(l, xr) ? gg_weight(l, ms, inv_t) : 0ull;
+                    const double zpf = gg_u128_to_double(rv.zp) / (double)f;
+                    const u64 rq = (e && (double)e > zpf) ? e - (u64)__builtin_floor(zpf) : 0ull;
+                    res -= (u128)(e - rq) * f;
+                }
+            }
+        }
+        u128 tot_res = res, tot_pl = pl;
         for (int off = 32; off > 0; off >>= 1) {
-            tot_res += shfl_xor_u64(tot_res, off);
-            tot_pl += shfl_xor_u64(tot_pl, off);
-            last_res = max(last_res, __shfl_xor(last_res, off));
-            last_pl = max(last_pl, __shfl_xor(last_pl, off));
+            tot_res += shfl_xor_u128(tot_res, off);
+            tot_pl += shfl_xor_u128(tot_pl, off);
         }
         // A vanished residual falls back to the target row itself.
         const int use_res = (d.residual && tot_res > 0) ? 1 : 0;
-        const u64 tot = use_res ? tot_res : tot_pl;
-        const int last = use_res ? last_res : last_pl;
-        int seg = -1;
-        u64 tt = 0;
+        const u128 tot = use_res ? tot_res : tot_pl;
+        const u128 v = use_res ? res : pl;
+        int seg = -1, last_mode = 0;
+        u128 tt = 0;
         if (tot > 0) {
             const double u = (double)uniforms[(size_t)b * R + K];
-            const u64 t = (u64)(u * (double)tot);
-            const u64 v = use_res ? o.sum_res : o.sum_plain;
-            u64 incl = v;
+            const u128 t = gg_u128_floor(u * gg_u128_to_double(tot));
+            u128 incl = v;
             for (int off = 1; off < 64; off <<= 1) {
-                const u64 y = shfl_up_u64(incl, off);
+                const u128 y = shfl_up_u128(incl, off);
                 if (lane >= off) incl += y;
             }
-            // First segment whose inclusive prefix passes t.
+            // First segment whose inclusive prefix passes t; none (u >= 1): the last
+            // segment with mass, searched for its last non-zero element.
             const unsigned long long hit = __ballot(lane < nseg && incl > t);
             if (hit) {
                 seg = __ffsll((long long)hit) - 1;
-                const u64 excl = incl - v;
-                tt = t - __shfl(excl, seg);
+                tt = t - shfl_u128(incl - v, seg);
+            } else {
+                const unsigned long long nz = __ballot(lane < nseg && v > 0);
+                seg = 63 - __clzll((long long)nz);
+                last_mode = 1;
             }
         }
         if (lane == 0) {
             s_use_res = use_res;
             s_seg = seg;
             s_t = tt;
-            s_found = tot > 0 ? (last >= 0 ? last : 0) : 0;  // no segment crosses (u >= 1)
+            s_last_mode = last_mode;
+            s_found = 0;
             out_acc[b] = d.accepted;
         }
     }
     __syncthreads();
-    if (s_seg < 0) {
-        if (threadIdx.x == 0) out_tok[b] = s_found;
+    if (s_seg < 0) {  // no mass at all
+        if (threadIdx.x == 0) out_tok[b] = 0;
         return;
     }
-    const int row = b * R + d.row;
-    const RowView rv = row_view_wave(row, nseg, use_topp, stats, seg_max, seg_z);
-    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
-    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     const bool use_res = s_use_res;
-    const float* qrow = (use_res && dprobs) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
-    const int xr = use_res ? drafts[(size_t)b * K + d.row] : -1;
-    const double zp_d = (double)rv.zp;
+    const float* qrow = (use_res && dense) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
+    const float ms = seg_max[(size_t)row * nseg + s_seg];
+    // The chosen segment has mass, so its factor f is positive; its weights are f times
+    // integers (e, or rq in units of e), so the element whose prefix passes the target
+    // tt is the one whose integer prefix passes tq = floor(tt / f).
+    const u64 f = seg_factor(ms, rv.m, inv_t);
+    const double zpf = f ? gg_u128_to_double(rv.zp) / (double)f : 0.0;
+    const u128 tt = s_t;
+    u64 tq = f ? (u64)(gg_u128_to_double(tt) / (double)f) : 0ull;  // within one of floor(tt / f)
+    while (f && (u128)tq * f > tt) --tq;
+    while (f && (u128)(tq + 1) * f <= tt) ++tq;
     constexpr int kPer = kSegElems / kFindThreads;
+    static_assert(kPer == 8, "eight consecutive logits per thread");
     const int e0 = s_seg * kSegElems + kPer * threadIdx.x;
+    float xl[kPer], ql[kPer];
+    load8<DT>(lp, V, e0, vec_ok, xl);
+    if (qrow) load8<GG_DTYPE_F32>(qrow, V, e0, vec_ok && ((uintptr_t)qrow % 16) == 0, ql);
     u64 r[kPer];
     u64 mine = 0;
+    int last_nz = -1;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = e0 + k;
-        u64 w = 0;
-        if (i < V) {
-            w = nu.weight(ld<DT>(lp, i), i);
-            if (use_res) {
-                u64 qf;
-                if (qrow) {
-                    const float qi = qrow[i];
-                    qf = (u64)(qi < 0.f ? 0.0 : (double)qi * zp_d);
-                } else {
-                    qf = (i == xr) ? rv.zp : 0ull;
-                }
-                w = w > qf ? w - qf : 0ull;
-            }
+        const u64 e = nu.kept(xl[k], i) ? gg_weight(xl[k], ms, inv_t) : 0ull;  // (NaN past the row)
+        u64 w = e;
+        if (use_res) {
+            const double qv = qrow ? gg_clean_q(ql[k]) : (i == xr ? 1.0 : 0.0);
+            const double qd = qv * zpf;
+            w = (e && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
         }
         r[k] = w;
         mine += w;
+        last_nz = w ? i : last_nz;
+    }
+    if (s_last_mode) {
+        for (int o = 32; o > 0; o >>= 1) last_nz = max(last_nz, __shfl_xor(last_nz, o));
+        if (lane == 0 && last_nz >= 0) atomicMax(&s_found, last_nz);
+        __syncthreads();
+        if (threadIdx.x == 0) out_tok[b] = s_found;
+        return;
     }
     // Exclusive block scan of the thread sums.
     u64 incl = mine;
@@ -1037,14 +1155,13 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
     __syncthreads();
     u64 before = incl - mine;
     for (int w = 0; w < wave; ++w) before += s_wsum[w];
-    const u64 t = s_t;
-    if (before <= t && before + mine > t) {
+    if (before <= tq && before + mine > tq) {
         u64 c = before;
         int found = e0 + kPer - 1;
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             c += r[k];
-            if (c > t) {
+            if (c > tq) {
                 found = e0 + k;
                 break;
             }
@@ -1060,15 +1177,18 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
 static int rej_nseg(int vocab) { return (vocab + kSegElems - 1) / kSegElems; }
 
 struct RejWs {
-    RowStats* stats;
     float* seg_max;
-    u64* seg_z;
-    SeqDecision* dec;
-    SegOut* seg_out;
-    RowHist* hist;   // top-p only: coarse histogram per row
+    u64* seg_e;
+    SeqPlan* plan;
+    SegSum* seg_sum;   // dense draft distributions: residual sums per (sequence, segment)
+    RowStats* stats;   // top-p: exact nucleus statistics of flagged rows
+    u64* seg_hist;     // top-p: coarse histogram per (row, segment)
     RowPick* pick;
-    uint2* cand;     // boundary-bin elements per row (logit bits, index)
-    int* flag;       // 1: the row needs the exact row kernel
+    int* status;       // top-p: bound outcome per row
+    int* flag;         // top-p: row needs the exact nucleus
+    int* crowded;      // top-p: row needs the exact row kernel
+    uint2* cand;       // top-p: boundary-bin elements per row (logit bits, index)
+    u64* seg_keep;     // top-p: per (row, segment) sum of kept e
     size_t bytes;
 };
 
@@ -1079,25 +1199,24 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
     size_t off = 0;
     RejWs w{};
     uint8_t* p = (uint8_t*)base;
-    w.stats = (RowStats*)(p + off);
-    off += al(rows * sizeof(RowStats));
-    w.seg_max = (float*)(p + off);
-    off += al(rows * nseg * sizeof(float));
-    w.seg_z = (u64*)(p + off);
-    off += al(rows * nseg * sizeof(u64));
-    w.dec = (SeqDecision*)(p + off);
-    off += al((size_t)num_seqs * sizeof(SeqDecision));
-    w.seg_out = (SegOut*)(p + off);
-    off += al((size_t)num_seqs * nseg * sizeof(SegOut));
+    auto take = [&](size_t bytes) {
+        void* q = p + off;
+        off += al(bytes);
+        return q;
+    };
+    w.seg_max = (float*)take(rows * nseg * sizeof(float));
+    w.seg_e = (u64*)take(rows * nseg * sizeof(u64));
+    w.plan = (SeqPlan*)take((size_t)num_seqs * sizeof(SeqPlan));
+    w.seg_sum = (SegSum*)take((size_t)num_seqs * nseg * sizeof(SegSum));
     if (topp) {
-        w.hist = (RowHist*)(p + off);
-        off += al(rows * sizeof(RowHist));
-        w.pick = (RowPick*)(p + off);
-        off += al(rows * sizeof(RowPick));
-        w.cand = (uint2*)(p + off);
-        off += al(rows * kCandCap * sizeof(uint2));
-        w.flag = (int*)(p + off);
-        off += al(rows * sizeof(int));
+        w.stats = (RowStats*)take(rows * sizeof(RowStats));
+        w.seg_hist = (u64*)take(rows * nseg * kSegBins * sizeof(u64));
+        w.pick = (RowPick*)take(rows * sizeof(RowPick));
+        w.status = (int*)take(rows * sizeof(int));
+        w.flag = (int*)take(rows * sizeof(int));
+        w.crowded = (int*)take(rows * sizeof(int));
+        w.cand = (uint2*)take(rows * kCandCap * sizeof(uint2));
+        w.seg_keep = (u64*)take(rows * nseg * sizeof(u64));
     }
     w.bytes = off;
     return w;
@@ -1122,30 +1241,41 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     const int K = max_drafts;
     const size_t eb = dtype_bytes(dt);
     const int vec_ok = ((vocab * eb) % 16 == 0) && (((uintptr_t)logits) % 16 == 0);
-#define GG_REJ(DTV)                                                                                        \
-    seg_max_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, n_drafts,  \
-                                                                 w.seg_max, use_topp ? w.hist : nullptr);  \
-    if (use_topp) {                                                                                        \
-        seg_zhist_kernel<DTV><<<dim3((nseg + kZhistSegs - 1) / kZhistSegs, rows), kSegThreads, 0, s>>>(                                    \
-            logits, K, vocab, nseg, vec_ok, inv_t, n_drafts, w.seg_max, w.seg_z, w.hist);                  \
-        row_pick_kernel<<<rows, kSegThreads, 0, s>>>(K, nseg, top_p, n_drafts, w.seg_max, w.seg_z, w.hist, \
-                                                     w.pick);                                              \
-        seg_gather_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(                                   \
-            logits, K, vocab, nseg, vec_ok, inv_t, n_drafts, w.seg_max, w.pick, w.cand);                   \
-        row_select_kernel<DTV><<<rows, 1024, 0, s>>>(logits, K, vocab, nseg, inv_t, drafts, n_drafts,      \
-                                                     w.seg_max, w.pick, w.cand, w.stats, w.flag);          \
-        rejection_row_stats_kernel<DTV><<<rows, kThreads, 0, s>>>(logits, K, vocab, drafts, n_drafts,      \
-                                                                  inv_t, top_p, use_topp, w.stats, w.flag); \
-    } else {                                                                                               \
-        seg_z_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, inv_t,  \
-                                                                   n_drafts, w.seg_max, w.seg_z);          \
-    }                                                                                                      \
-    seg_draw_sums_kernel<DTV><<<dim3(nseg, num_seqs), kSegThreads, 0, s>>>(                                \
-        logits, q, K, vocab, nseg, vec_ok, inv_t, use_topp, drafts, n_drafts, uniforms, w.stats,           \
-        w.seg_max, w.seg_z, w.dec, w.seg_out);                                                             \
-    seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(logits, q, K, vocab, nseg, inv_t, use_topp, \
-                                                               drafts, uniforms, w.stats, w.seg_max,       \
-                                                               w.seg_z, w.dec, w.seg_out, out_acc, out_tok);
+#define GG_REJ(DTV)                                                                                          \
+    if (use_topp) {                                                                                          \
+        seg_pass_kernel<DTV, true><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,  \
+                                                                            inv_t, n_drafts, w.seg_max,      \
+                                                                            w.seg_e, w.seg_hist);            \
+        row_pick_kernel<<<rows, kSegThreads, 0, s>>>(K, nseg, inv_t, top_p, n_drafts, w.seg_max, w.seg_e,    \
+                                                     w.seg_hist, w.pick);                                    \
+        decide_bounds_kernel<DTV><<<num_seqs, 64, 0, s>>>(logits, q, K, vocab, nseg, inv_t, drafts,          \
+                                                          n_drafts, uniforms, w.seg_max, w.pick, w.status,   \
+                                                          w.flag);                                           \
+        seg_gather_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,      \
+                                                                        inv_t, n_drafts, w.flag, w.seg_max,  \
+                                                                        w.pick, w.cand, w.seg_keep);         \
+        row_select_kernel<DTV><<<rows, 1024, 0, s>>>(logits, K, vocab, nseg, inv_t, drafts, n_drafts,        \
+                                                     w.flag, w.seg_max, w.pick, w.cand, w.stats, w.seg_keep, \
+                                                     w.crowded);                                             \
+        rejection_row_stats_kernel<DTV><<<rows, kThreads, 0, s>>>(logits, K, vocab, nseg, drafts, n_drafts,  \
+                                                                  inv_t, top_p, w.flag, w.crowded,           \
+                                                                  w.seg_max, w.seg_e, w.stats, w.seg_keep);  \
+    } else {                                                                                                 \
+        seg_pass_kernel<DTV, false><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, \
+                                                                             inv_t, n_drafts, w.seg_max,     \
+                                                                             w.seg_e, nullptr);              \
+    }                                                                                                        \
+    decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(logits, q, K, vocab, nseg, inv_t, use_topp, drafts, n_drafts,  \
+                                              uniforms, w.stats, w.status, w.flag, w.seg_max, w.seg_e,       \
+                                              w.plan);                                                       \
+    if (q)                                                                                                   \
+        seg_residual_kernel<DTV><<<dim3(nseg, num_seqs), kSumThreads, 0, s>>>(logits, q, K, vocab, nseg,     \
+                                                                              vec_ok, inv_t, w.seg_max,      \
+                                                                              w.plan, w.seg_sum);            \
+    seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(logits, q, K, vocab, nseg, vec_ok, inv_t,     \
+                                                               use_topp, drafts, uniforms, w.seg_max,        \
+                                                               w.seg_e, w.seg_keep, w.plan, w.seg_sum,       \
+                                                               out_acc, out_tok);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_REJ(GG_DTYPE_BF16) break;

@@ -65,3 +65,41 @@ GG_HD int gg_coarse_bin(float l, float m, float inv_t) {
     const float y = -((l - m) * inv_t) * 64.0f;
     return y >= 2047.0f ? 2047 : (int)y;
 }
+
+// ---- Exact 128-bit weights (segment-relative) ----
+//
+// A row is cut into segments of GG_ACCEPT_SEG logits. Logit i of segment s weighs
+//     W_i = e_i * f_s,  e_i = gg_weight(l_i, m_s, 1/T),  f_s = gg_weight(m_s, m, 1/T)
+// with m_s the segment's max finite logit and m the row's: both factors need only one
+// maximum each, so the logits are read once, and every sum is an exact 128-bit
+// integer (order-free). Doubles enter only through the two conversions below, written
+// out so that host and device round identically.
+#define GG_ACCEPT_SEG 8192
+typedef unsigned __int128 gg_u128;
+
+// ((x3 * 2^32 + x2) * 2^32 + x1) * 2^32 + x0 over the four 32-bit pieces, each step a
+// double operation (the pieces and the power-of-two products are exact).
+GG_HD double gg_u128_to_double(gg_u128 x) {
+    double d = (double)(unsigned int)(x >> 96) * 4294967296.0 + (double)(unsigned int)(x >> 64);
+    d = d * 4294967296.0 + (double)(unsigned int)(x >> 32);
+    return d * 4294967296.0 + (double)(unsigned int)x;
+}
+// floor(d) for 0 <= d < 2^128; 0 for d <= 0 or NaN. Each 32-bit piece is split off with
+// exact operations (power-of-two scalings, floors and the subtraction of a value that
+// shares d's leading bits), so only 32-bit conversions are needed.
+GG_HD gg_u128 gg_u128_floor(double d) {
+    if (!(d > 0.0)) return 0;
+    const double p32 = 4294967296.0, i32 = 1.0 / 4294967296.0;
+    const double hd = __builtin_floor(d * (i32 * i32));
+    const double ld = d - hd * (p32 * p32);
+    const double hh = __builtin_floor(hd * i32), hl = hd - hh * p32;
+    const double lh = __builtin_floor(ld * i32), ll = ld - lh * p32;
+    const unsigned long long hi = ((unsigned long long)(unsigned int)hh << 32) | (unsigned int)hl;
+    const unsigned long long lo = ((unsigned long long)(unsigned int)lh << 32) | (unsigned int)ll;
+    return ((gg_u128)hi << 64) | lo;
+}
+// A draft probability as the acceptance rule uses it: finite and in (0, 1], else 0.
+GG_HD double gg_clean_q(float q) {
+    if (!(q > 0.0f) || !(q <= 3.402823466e38f)) return 0.0;
+    return q > 1.0f ? 1.0 : (double)q;
+}

@@ -311,46 +311,105 @@ static int cmp_logit_desc(const void* a, const void* b) {
     return x->idx - y->idx;
 }
 
-/* Nucleus-filtered fixed-point weights of one row: w_out[i] (0 outside), returns Zp. */
-static uint64_t row_weights(const float* row, int V, float inv_t, float top_p, uint64_t* w_out, ora_il* scratch) {
+/* Exact 128-bit weights. A row is cut into segments of ORA_SEG logits (the device's
+ * segment size). Logit i of segment s weighs
+ *     W_i = e_i * f_s,   e_i = weight(l_i, m_s),   f_s = weight(m_s, m)
+ * with m_s the segment's max finite logit, m the row's, and weight(l, a) =
+ * floor(exp_gg((l - a) / T) * 2^35) (ora_weight). Both factors need only one maximum
+ * each, so a device reads every logit once; W_i / Z equals the softmax probability to
+ * within the exp's ~4e-7 relative error. Sums are exact 128-bit integers; conversions
+ * to double are written out over 32-bit pieces below, identical on host and device
+ * (gollmgo_amd/csrc/gg_fixed_exp.h states the same rule). */
+#define ORA_SEG 8192
+typedef unsigned __int128 u128;
+static double u128_to_double(u128 x) {
+    double d = (double)(uint32_t)(x >> 96) * 4294967296.0 + (double)(uint32_t)(x >> 64);
+    d = d * 4294967296.0 + (double)(uint32_t)(x >> 32);
+    return d * 4294967296.0 + (double)(uint32_t)x;
+}
+/* floor(d) for 0 <= d < 2^128 (0 for d <= 0 or NaN). */
+static u128 u128_floor(double d) {
+    if (!(d > 0.0)) return 0;
+    const double hd = floor(d / 18446744073709551616.0);
+    const double ld = d - hd * 18446744073709551616.0;
+    return ((u128)(uint64_t)hd << 64) | (u128)(uint64_t)ld;
+}
+/* A draft probability as the rule uses it: finite and in (0, 1], anything else 0. */
+static double clean_q(float q) {
+    if (!(q > 0.0f) || !isfinite(q)) return 0.0;
+    return q > 1.0f ? 1.0 : (double)q;
+}
+
+/* Nucleus-filtered weights of one row: w_out[i] (0 outside the nucleus), returns Zp.
+ * When e_out / f_out are given they receive e_i (0 outside the nucleus) and f_s. */
+static u128 row_weights_ef(const float* row, int V, float inv_t, float top_p, u128* w_out, ora_il* scratch,
+                           uint64_t* e_out, uint64_t* f_out) {
+    const int nseg = (V + ORA_SEG - 1) / ORA_SEG;
+    float* ms = (float*)malloc(sizeof(float) * (size_t)nseg);
     float m = -INFINITY;
-    for (int i = 0; i < V; ++i)
-        if (isfinite(row[i]) && row[i] > m) m = row[i];
+    for (int s = 0; s < nseg; ++s) {
+        ms[s] = -INFINITY;
+        for (int i = s * ORA_SEG; i < V && i < (s + 1) * ORA_SEG; ++i)
+            if (isfinite(row[i]) && row[i] > ms[s]) ms[s] = row[i];
+        if (ms[s] > m) m = ms[s];
+    }
     if (!isfinite(m)) {
-        memset(w_out, 0, sizeof(uint64_t) * (size_t)V);
+        memset(w_out, 0, sizeof(u128) * (size_t)V);
+        if (e_out) memset(e_out, 0, sizeof(uint64_t) * (size_t)V);
+        if (f_out) memset(f_out, 0, sizeof(uint64_t) * (size_t)nseg);
+        free(ms);
         return 0;
     }
-    uint64_t z = 0;
+    if (f_out)
+        for (int s = 0; s < nseg; ++s) f_out[s] = isfinite(ms[s]) ? ora_weight(ms[s], m, inv_t) : 0;
+    u128 z = 0;
     int nf = 0;
     for (int i = 0; i < V; ++i) {
-        w_out[i] = isfinite(row[i]) ? ora_weight(row[i], m, inv_t) : 0;
-        z += w_out[i];
+        const int s = i / ORA_SEG;
+        w_out[i] = 0;
+        if (e_out) e_out[i] = 0;
         if (isfinite(row[i])) {
+            const uint64_t f = ora_weight(ms[s], m, inv_t);
+            const uint64_t e = ora_weight(row[i], ms[s], inv_t);
+            w_out[i] = (u128)e * f;
+            if (e_out) e_out[i] = e;
             scratch[nf].idx = i;
             scratch[nf].l = row[i] == 0.0f ? 0.0f : row[i];
             ++nf;
         }
+        z += w_out[i];
     }
+    free(ms);
     if (!(top_p > 0.f && top_p < 1.f) || z == 0) return z;
     /* topPFilter: walk in (logit desc, index asc) order; keep while the mass before
      * the item is below p (cumulative >= p && cumulative > 0 stops the walk). */
-    uint64_t tp = (uint64_t)ceil((double)top_p * (double)z);
+    const u128 tp = u128_floor(ceil((double)top_p * u128_to_double(z)));
     qsort(scratch, (size_t)nf, sizeof(ora_il), cmp_logit_desc);
-    uint64_t cum = 0;
+    u128 cum = 0;
     int k = 0;
     for (; k < nf; ++k) {
         if (cum >= tp && cum > 0) break;
         cum += w_out[scratch[k].idx];
     }
-    for (; k < nf; ++k) w_out[scratch[k].idx] = 0;
+    for (; k < nf; ++k) {
+        w_out[scratch[k].idx] = 0;
+        if (e_out) e_out[scratch[k].idx] = 0;
+    }
     return cum;
 }
+static u128 row_weights(const float* row, int V, float inv_t, float top_p, u128* w_out, ora_il* scratch) {
+    return row_weights_ef(row, V, inv_t, top_p, w_out, scratch, NULL, NULL);
+}
 
-/* Speculative sampling (Leviathan et al. 2023, Alg. 1) over fixed-point weights:
- *   accept draft j iff u_j * q_j(x_j) * Zp_j < w_j(x_j)   (doubles, left to right)
- *   first rejection at row a: draw from r_i = max(0, w_i - floor(q_i * Zp_a));
- *     if every r_i is 0, draw from w of row a itself;
- *   all accepted: draw from w of row n;
+/* Speculative sampling (Leviathan et al. 2023, Alg. 1) over the exact weights W:
+ *   accept draft j iff u_j * q_j(x_j) * Zp_j < W_j(x_j)   (doubles, left to right;
+ *     q as clean_q; W and Zp through u128_to_double)
+ *   first rejection at row a: draw from r_i = f_s * (e_i - min(e_i, floor(q_i * Zp_a / f_s)))
+ *     (the residual max(0, W_i - q_i * Zp) rounded in the segment's units of e; the
+ *     quotient Zp / f_s and the product are doubles; q is one-hot at the draft when no
+ *     draft distribution is given; r_i = 0 where f_s = 0); if every r_i is 0, draw from
+ *     W of row a itself;
+ *   all accepted: draw from W of row n;
  *   draw(u, r): t = floor(u * sum r); first i with inclusive prefix > t; else the
  *     last i with r_i > 0; else 0.
  * logits [B][K+1][V] (fp32 values), dprobs [B][K][V] or NULL (one-hot q),
@@ -359,8 +418,10 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
                           const int32_t* drafts, const int32_t* n_drafts, const float* uniforms,
                           float temperature, float top_p, int32_t* out_acc, int32_t* out_tok) {
     const float inv_t = 1.0f / temperature;
-    uint64_t* w = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
-    uint64_t* r = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    u128* w = (u128*)malloc(sizeof(u128) * (size_t)V);
+    u128* r = (u128*)malloc(sizeof(u128) * (size_t)V);
+    uint64_t* e = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    uint64_t* f = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)((V + ORA_SEG - 1) / ORA_SEG));
     ora_il* scratch = (ora_il*)malloc(sizeof(ora_il) * (size_t)V);
     for (int b = 0; b < B; ++b) {
         int n = n_drafts[b];
@@ -368,35 +429,35 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
         if (n > K) n = K;
         const float* lg = logits + (size_t)b * (K + 1) * V;
         int a = n;
-        uint64_t zp = 0;
+        u128 zp = 0;
         for (int j = 0; j < n; ++j) {
             zp = row_weights(lg + (size_t)j * V, V, inv_t, top_p, w, scratch);
             int x = drafts[(size_t)b * K + j];
             int ok = 0;
             if (x >= 0 && x < V) {
-                double q = dprobs ? (double)dprobs[((size_t)b * K + j) * V + x] : 1.0;
+                double q = dprobs ? clean_q(dprobs[((size_t)b * K + j) * V + x]) : 1.0;
                 double u = (double)uniforms[(size_t)b * (K + 1) + j];
-                ok = u * q * (double)zp < (double)w[x];
+                ok = u * q * u128_to_double(zp) < u128_to_double(w[x]);
             }
             if (!ok) {
                 a = j;
                 break;
             }
         }
-        zp = row_weights(lg + (size_t)a * V, V, inv_t, top_p, w, scratch);
-        uint64_t tot = 0;
+        zp = row_weights_ef(lg + (size_t)a * V, V, inv_t, top_p, w, scratch, e, f);
+        const double zpd = u128_to_double(zp);
+        u128 tot = 0;
         int residual = a < n;
         if (residual) {
             int xr = drafts[(size_t)b * K + a];
             for (int i = 0; i < V; ++i) {
-                uint64_t qf;
-                if (dprobs) {
-                    float qi = dprobs[((size_t)b * K + a) * V + i];
-                    qf = qi < 0.f ? 0 : (uint64_t)((double)qi * (double)zp);
-                } else {
-                    qf = i == xr ? zp : 0;
-                }
-                r[i] = w[i] > qf ? w[i] - qf : 0;
+                const uint64_t fs = f[i / ORA_SEG];
+                r[i] = 0;
+                if (fs == 0 || e[i] == 0) continue;
+                const double qv = dprobs ? clean_q(dprobs[((size_t)b * K + a) * V + i]) : (i == xr ? 1.0 : 0.0);
+                const double qd = qv * (zpd / (double)fs);
+                const uint64_t rq = (double)e[i] > qd ? e[i] - (uint64_t)floor(qd) : 0;
+                r[i] = (u128)rq * fs;
                 tot += r[i];
             }
         }
@@ -410,8 +471,8 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
         int tok = 0;
         if (tot > 0) {
             double u = (double)uniforms[(size_t)b * (K + 1) + K];
-            uint64_t t = (uint64_t)(u * (double)tot);
-            uint64_t c = 0;
+            const u128 t = u128_floor(u * u128_to_double(tot));
+            u128 c = 0;
             int found = -1;
             for (int i = 0; i < V; ++i) {
                 c += r[i];
@@ -433,7 +494,21 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
     }
     free(w);
     free(r);
+    free(e);
+    free(f);
     free(scratch);
+}
+
+/* The exact weights of one row as float64 values W_i / 2^70 (tests read the
+ * distribution through this; Zp is returned the same way). */
+double ora_row_weights_f64(const float* row, int V, float temperature, float top_p, double* out) {
+    u128* w = (u128*)malloc(sizeof(u128) * (size_t)V);
+    ora_il* scratch = (ora_il*)malloc(sizeof(ora_il) * (size_t)V);
+    const u128 zp = row_weights(row, V, 1.0f / temperature, top_p, w, scratch);
+    for (int i = 0; i < V; ++i) out[i] = u128_to_double(w[i]) / 1180591620717411303424.0; /* 2^70 */
+    free(w);
+    free(scratch);
+    return u128_to_double(zp) / 1180591620717411303424.0;
 }
 
 /* ------------------------------------------------------------- KV cache */
@@ -673,39 +748,18 @@ void ora_draw_parity(const float* logits, int B, int V, double temperature, doub
 #endif
     for (int b = 0; b < B; ++b) {
         const float* row = logits + (size_t)b * V;
-        uint64_t* w = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+        u128* w = (u128*)malloc(sizeof(u128) * (size_t)V);
         uint64_t* key = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
         double* pr = (double*)malloc(sizeof(double) * (size_t)V);
         double* kept = (double*)malloc(sizeof(double) * (size_t)V);
         double* cdf = (double*)malloc(sizeof(double) * (size_t)V);
-        uint64_t* pre = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+        u128* pre = (u128*)malloc(sizeof(u128) * (size_t)V);
         int* idx = (int*)malloc(sizeof(int) * (size_t)V);
         int* tmp = (int*)malloc(sizeof(int) * (size_t)V);
-        /* fixed point */
-        float m = row[0];
-        for (int i = 1; i < V; ++i)
-            if (row[i] > m) m = row[i];
-        uint64_t z = 0;
-        for (int i = 0; i < V; ++i) {
-            w[i] = ora_weight(row[i], m, inv_t);
-            z += w[i];
-        }
-        if (use_p) {
-            const uint64_t tp = (uint64_t)ceil(top_p * (double)z);
-            for (int i = 0; i < V; ++i) {
-                idx[i] = i;
-                key[i] = desc_key_f32(row[i]);
-            }
-            radix_sort_idx(key, V, idx, tmp);
-            uint64_t cum = 0;
-            int k = 0;
-            for (; k < V; ++k) {
-                if (cum >= tp && cum > 0) break;
-                cum += w[idx[k]];
-            }
-            for (; k < V; ++k) w[idx[k]] = 0;
-        }
-        uint64_t tot = 0;
+        ora_il* scratch = (ora_il*)malloc(sizeof(ora_il) * (size_t)V);
+        /* fixed point: the acceptance's own row weights and nucleus */
+        row_weights(row, V, inv_t, (float)top_p, w, scratch);
+        u128 tot = 0;
         for (int i = 0; i < V; ++i) {
             tot += w[i];
             pre[i] = tot;
@@ -769,7 +823,7 @@ void ora_draw_parity(const float* logits, int B, int V, double temperature, doub
             tok_f64[(size_t)b * U + k] = tf;
             int tq = 0;
             if (tot > 0) {
-                const uint64_t t = (uint64_t)(u * (double)tot);
+                const u128 t = u128_floor(u * u128_to_double(tot));
                 int l2 = 0, h2 = V;
                 while (l2 < h2) {
                     const int mid = (l2 + h2) / 2;
@@ -780,7 +834,7 @@ void ora_draw_parity(const float* logits, int B, int V, double temperature, doub
             }
             tok_fixed[(size_t)b * U + k] = tq;
         }
-        free(w); free(key); free(pr); free(kept); free(cdf); free(pre); free(idx); free(tmp);
+        free(w); free(key); free(pr); free(kept); free(cdf); free(pre); free(idx); free(tmp); free(scratch);
     }
 }
 
