@@ -343,7 +343,7 @@ def main():
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts,
-                                              uniforms, scale)
+                                              uniforms, scale, acc_out)
     kv.close()
     print(json.dumps(result))
 
@@ -362,7 +362,7 @@ def pmc_traffic(config_id: int):
     return int(m.group(1)), str(path.relative_to(ROOT))
 
 
-def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, uniforms, scale):
+def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, uniforms, scale, decision):
     """The CPU oracle (a C port of the reference's host logic and of its attention
     semantics) timed on this host on bounded samples of the same workload, at every usable
     core and at one thread. A sample is the attention of layer 0 for the first S sequences,
@@ -370,7 +370,9 @@ def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, u
     drafts when the config has token histories). `value` is the all-cores figure; the
     one-thread figure uses a smaller sample of the same shape. The Go engine's own host
     loops (NGramDrafter.Draft and Verify, internal/engine/speculative.go:24-84) are also
-    timed at one thread per sequence."""
+    timed at one thread per sequence, and so is the return path of the device decision:
+    the one-hot LogitsPerPosition rows built from the step's (accepted, token) and the
+    engine's Verify + bonus Sample over them (serving.go:496-570), for the whole batch."""
     import numpy as np
 
     from oracle import oracle as ora
@@ -442,6 +444,21 @@ def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, u
     t0 = time.perf_counter()
     ora.accept_greedy(lg, drafts[:nv].cpu().numpy(), n_drafts[:nv].cpu().numpy())
     verify_us = (time.perf_counter() - t0) / nv * 1e6
+    # Return path: rows from the device decision of the bench step, then the engine's reads.
+    from gollmgo_amd.positions import LogitsPerPosition
+    dr_h, nd_h = drafts.cpu().numpy(), n_drafts.cpu().numpy()
+    acc_h, tok_h = decision[0].cpu().numpy(), decision[1].cpu().numpy()
+    lpp = LogitsPerPosition(int(logits.shape[-1]))
+    t0 = time.perf_counter()
+    pos = lpp.batch(dr_h, nd_h, acc_h, tok_h)
+    build_us = (time.perf_counter() - t0) * 1e6
+    T = cfg.temperature if cfg.accept == "rejection" else 0.0
+    ub = np.random.default_rng(0).random(len(pos))
+    tm = []
+    ea, et = ora.emit_positions(dr_h, nd_h, pos, T, cfg.top_p, ub, timer=tm)
+    emit_us = tm[0] * 1e6
+    return_ok = bool(np.array_equal(ea, acc_h) and np.array_equal(et, tok_h))
+    row_floats = int(sum(len(r) for rows in pos for r in rows))
     return {"value": all_cores["value"], "unit": "verified tokens/s", "cores": usable, "kind": "port",
             "sample": all_cores["sample"], "nproc": nproc, "usable_cpus": usable,
             "all_cores": all_cores, "one_thread": one_thread,
@@ -449,7 +466,13 @@ def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, u
                 "ngram_draft_us_per_seq": round(draft_us, 1),
                 "ngram_history_tokens": int(dh.shape[1]),
                 "verify_greedy_us_per_seq": round(verify_us, 1),
-                "verify_rows_x_vocab": [cfg.rows, int(logits.shape[-1])]}}
+                "verify_rows_x_vocab": [cfg.rows, int(logits.shape[-1])]},
+            "return_path_one_thread": {
+                "rows_build_us_per_step": round(build_us, 1),
+                "engine_verify_sample_us_per_step": round(emit_us, 1),
+                "row_floats_scanned": row_floats,
+                "sampler": f"T={T} top_p={cfg.top_p}",
+                "reproduces_device_decision": return_ok}}
 
 
 if __name__ == "__main__":

@@ -56,6 +56,7 @@ struct RowStats {
 
 constexpr int kCandCap = 4096;
 constexpr int kFindThreads = 1024;  // draw find: threads per sequence
+enum { kDrawPlain = 0, kDrawResidual = 1, kDrawNoDraft = 2 };  // what the final draw samples
 
 // The nucleus boundary of one row (top-p), from the coarse histogram: the boundary bin,
 // the mass of the bins before it and its own mass.
@@ -956,7 +957,9 @@ __global__ void __launch_bounds__(64) decide_kernel(const void* __restrict__ log
 
 // G (dense draft distributions only): per (sequence, segment) the residual weight sum of
 // the final row's segment, f_s * sum of rq, rq = e - min(e, floor(q * Zp / f_s)) over the
-// nucleus (the rejected draft's q row read once). Thread t of kSumThreads owns kSumRuns
+// nucleus less the rejected draft x itself (the rejected draft's q row read once). A
+// rejection with u < 1 means p(x) < q(x), so x's residual max(0, p - q) is exactly 0; it is
+// set to 0 rather than computed, so that rounding never gives it a unit. Thread t of kSumThreads owns kSumRuns
 // runs of eight logits, run r at offset (r * kSumThreads + t) * 8 of the segment.
 #ifndef GG_SUM_THREADS
 #define GG_SUM_THREADS 512
@@ -967,7 +970,8 @@ static_assert(kSumRuns * kSumThreads * 8 == kSegElems, "segment = runs of eight 
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
     const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
-    float inv_t, const float* __restrict__ seg_max, const SeqPlan* __restrict__ plan, SegSum* __restrict__ seg_sum) {
+    float inv_t, const int32_t* __restrict__ drafts, const float* __restrict__ seg_max,
+    const SeqPlan* __restrict__ plan, SegSum* __restrict__ seg_sum) {
     const int seg = blockIdx.x, b = blockIdx.y;
     const int R = K + 1;
     constexpr int kW = kSumThreads / 64;
@@ -978,6 +982,7 @@ __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
     const int row = b * R + d.row;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     const float* qrow = dprobs + ((size_t)b * K + d.row) * V;
+    const int xr = drafts[(size_t)b * K + d.row];
     float x[kSumRuns][8], q[kSumRuns][8];
 #pragma unroll
     for (int r = 0; r < kSumRuns; ++r) {
@@ -998,7 +1003,7 @@ __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
             const bool keep = f && nu.kept(x[r][k], i);  // (NaN past the row: never kept)
             const u64 e = keep ? gg_weight(x[r][k], ms, inv_t) : 0ull;
             const double qd = gg_clean_q(q[r][k]) * zpf;
-            s_res += (e && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
+            s_res += (e && i != xr && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
         }
     }
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1013,11 +1018,15 @@ __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
 }
 
 // H: per sequence, the draw. Wave 0 forms the final row's per-segment masses (lane s =
-// segment s): plain = f_s * (sum of kept e); residual = the dense sums above, or with
-// one-hot q the plain mass less the rejected draft's e - rq; picks the segment holding
-// floor(u * total) (the last segment with mass when none passes it, u >= 1). In that
-// segment thread k of 1024 owns the 8 consecutive elements [8k, 8k+8): their integer
-// weights (e, or rq) and a block scan find the element (or the last non-zero one).
+// segment s): plain = f_s * (sum of kept e); without the draft = plain less the rejected
+// draft x's f_s * e_x (the residual of one-hot q); residual = the dense sums above, or
+// the mass without the draft for one-hot q. The draw uses the residual; when it vanished
+// (dense q that is not a distribution), the row without the draft; when that vanished too,
+// the plain row. So a rejected draft is never drawn unless it holds the row's whole mass.
+// It picks the segment holding floor(u * total) (the last segment with mass when none
+// passes it, u >= 1). In that segment thread k of 1024 owns the 8 consecutive elements
+// [8k, 8k+8): their integer weights (e, or rq) and a block scan find the element (or the
+// last non-zero one).
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
     const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
@@ -1028,7 +1037,7 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
     const int b = blockIdx.x;
     const int R = K + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __shared__ int s_seg, s_use_res, s_found, s_last_mode;
+    __shared__ int s_seg, s_mode, s_found, s_last_mode;
     __shared__ u128 s_t;
     __shared__ u64 s_wsum[kFindThreads / 64];
     const SeqDecision d = plan[b].d;
@@ -1039,34 +1048,34 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
     const int xr = d.residual ? drafts[(size_t)b * K + d.row] : -1;
     const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
     if (wave == 0) {
-        u128 pl = 0, res = 0;
+        u128 pl = 0, ex = 0, res = 0;
         if (lane < nseg) {
             const float ms = seg_max[(size_t)row * nseg + lane];
             const u64 f = (finite_f(rv.m) && finite_f(ms)) ? seg_factor(ms, rv.m, inv_t) : 0ull;
             const u64 ek = use_topp ? seg_keep[(size_t)row * nseg + lane] : seg_e[(size_t)row * nseg + lane];
             pl = (u128)ek * f;
-            if (dense) {
-                res = seg_sum[(size_t)b * nseg + lane].res;
-            } else if (d.residual) {
-                res = pl;
-                if (xr >= 0 && xr < V && xr / kSegElems == lane && f) {
-                    const float l = ld<DT>(lp, xr);
-                    const u64 e = nu.kept(l, xr) ? gg_weight(l, ms, inv_t) : 0ull;
-                    const double zpf = gg_u128_to_double(rv.zp) / (double)f;
-                    const u64 rq = (e && (double)e > zpf) ? e - (u64)__builtin_floor(zpf) : 0ull;
-                    res -= (u128)(e - rq) * f;
-                }
+            ex = pl;
+            if (d.residual && xr >= 0 && xr < V && xr / kSegElems == lane && f) {
+                const float l = ld<DT>(lp, xr);
+                const u64 e = nu.kept(l, xr) ? gg_weight(l, ms, inv_t) : 0ull;
+                ex -= (u128)e * f;
             }
+            res = dense ? seg_sum[(size_t)b * nseg + lane].res : ex;
         }
-        u128 tot_res = res, tot_pl = pl;
+        u128 tot_res = res, tot_ex = ex, tot_pl = pl;
         for (int off = 32; off > 0; off >>= 1) {
             tot_res += shfl_xor_u128(tot_res, off);
+            tot_ex += shfl_xor_u128(tot_ex, off);
             tot_pl += shfl_xor_u128(tot_pl, off);
         }
-        // A vanished residual falls back to the target row itself.
-        const int use_res = (d.residual && tot_res > 0) ? 1 : 0;
-        const u128 tot = use_res ? tot_res : tot_pl;
-        const u128 v = use_res ? res : pl;
+        // kDrawPlain: the target row; kDrawResidual: the residual; kDrawNoDraft: the
+        // target row without the rejected draft.
+        const int mode = !d.residual ? kDrawPlain
+                         : tot_res > 0 ? kDrawResidual
+                         : tot_ex > 0  ? kDrawNoDraft
+                                       : kDrawPlain;
+        const u128 tot = mode == kDrawResidual ? tot_res : mode == kDrawNoDraft ? tot_ex : tot_pl;
+        const u128 v = mode == kDrawResidual ? res : mode == kDrawNoDraft ? ex : pl;
         int seg = -1, last_mode = 0;
         u128 tt = 0;
         if (tot > 0) {
@@ -1090,7 +1099,7 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
             }
         }
         if (lane == 0) {
-            s_use_res = use_res;
+            s_mode = mode;
             s_seg = seg;
             s_t = tt;
             s_last_mode = last_mode;
@@ -1103,8 +1112,8 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
         if (threadIdx.x == 0) out_tok[b] = 0;
         return;
     }
-    const bool use_res = s_use_res;
-    const float* qrow = (use_res && dense) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
+    const int mode = s_mode;
+    const float* qrow = (mode == kDrawResidual && dense) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
     const float ms = seg_max[(size_t)row * nseg + s_seg];
     // The chosen segment has mass, so its factor f is positive; its weights are f times
     // integers (e, or rq in units of e), so the element whose prefix passes the target
@@ -1129,9 +1138,10 @@ __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
         const int i = e0 + k;
         const u64 e = nu.kept(xl[k], i) ? gg_weight(xl[k], ms, inv_t) : 0ull;  // (NaN past the row)
         u64 w = e;
-        if (use_res) {
-            const double qv = qrow ? gg_clean_q(ql[k]) : (i == xr ? 1.0 : 0.0);
-            const double qd = qv * zpf;
+        if (mode != kDrawPlain && i == xr) {
+            w = 0;
+        } else if (qrow) {
+            const double qd = gg_clean_q(ql[k]) * zpf;
             w = (e && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
         }
         r[k] = w;
@@ -1270,8 +1280,8 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                               w.plan);                                                       \
     if (q)                                                                                                   \
         seg_residual_kernel<DTV><<<dim3(nseg, num_seqs), kSumThreads, 0, s>>>(logits, q, K, vocab, nseg,     \
-                                                                              vec_ok, inv_t, w.seg_max,      \
-                                                                              w.plan, w.seg_sum);            \
+                                                                              vec_ok, inv_t, drafts,         \
+                                                                              w.seg_max, w.plan, w.seg_sum); \
     seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(logits, q, K, vocab, nseg, vec_ok, inv_t,     \
                                                                use_topp, drafts, uniforms, w.seg_max,        \
                                                                w.seg_e, w.seg_keep, w.plan, w.seg_sum,       \

@@ -1,0 +1,383 @@
+//go:build rocm
+
+package rocm
+
+import (
+	"context"
+	"fmt"
+	"math"
+	"math/rand"
+	"unsafe"
+
+	"github.com/TensorGreed/gollmgo/internal/backend"
+)
+
+// Model is the part of a step that lives outside libgg_verify: embeddings, the
+// per-layer projections, norms, RoPE and MLP, and the LM head (the reference's
+// kernels/gollmgo_model.cu run_layer, minus its KV write and attention). It works on the
+// runner's [B][R] row layout: row j of sequence b is device row b*R+j, and padding rows
+// (j >= the sequence's token count) are computed and ignored. Every call is asynchronous
+// on the given stream.
+type Model interface {
+	NumLayers() int
+	NumQHeads() int
+	NumKVHeads() int
+	HeadDim() int
+	Vocab() int
+	// Embed loads the step's tokens (device int32 [B][R]) into the hidden state.
+	Embed(tokens unsafe.Pointer, B, R int, stream unsafe.Pointer) error
+	// QKV writes layer's q [B][R][Hq][D] and k, v [B][R][Hkv][D] (bf16, RoPE applied at
+	// positions, device int32 [B][R]).
+	QKV(layer int, positions, q, k, v unsafe.Pointer, stream unsafe.Pointer) error
+	// Post takes layer's attention output [B][R][Hq][D] (bf16) through the output
+	// projection, residual and MLP.
+	Post(layer int, attnOut unsafe.Pointer, stream unsafe.Pointer) error
+	// Logits writes every row's logits, device bf16 [B][R][V].
+	Logits(logits unsafe.Pointer, stream unsafe.Pointer) error
+	// Prefill runs a batch that holds prefill sequences on the model's own path.
+	Prefill(ctx context.Context, batch *backend.Batch) (*backend.StepOutput, error)
+}
+
+// Config fixes the pools and the acceptance rule.
+type Config struct {
+	NumBlocks   int
+	BlockSize   int
+	KVDtype     int // Dtype* of bridge.go
+	KVScales    int // Scale*: PerHead for FP8, PerBlock for INT8, None otherwise
+	MaxDrafts   int // K: rows per sequence are K+1
+	Temperature float32
+	TopP        float32
+	Rejection   bool // speculative sampling; false: greedy Verify + argmax
+	Seed        int64
+}
+
+// Runner implements backend.Runner (internal/backend/runner.go:84-93) and
+// backend.KVSwapper (runner.go:94-106) for decode steps with drafts. Per step the host
+// packs the batch (PackBatch), uploads it in one copy, runs the model with the verify
+// attention of every layer, the acceptance, and copies back 2*B int32s: the decision,
+// returned to the engine as one-hot LogitsPerPosition rows (OneHotRows).
+type Runner struct {
+	model  Model
+	cfg    Config
+	kv     *KVCache
+	stream unsafe.Pointer
+	rows   *OneHotRows
+	rng    *rand.Rand
+
+	maxB, maxR, maxBlocks int
+	hq, hkv, d, vocab     int
+
+	// Device buffers (allocated once at Warmup).
+	dIn                       unsafe.Pointer // the packed int32 inputs + float uniforms, one upload
+	dQ, dK, dV, dOut, dLogits unsafe.Pointer
+	dAttnWS, dAccWS, dDec     unsafe.Pointer
+	attnWS, accWS             uintptr
+	// Pinned host staging of the same layout, and of the decision.
+	hIn, hDec unsafe.Pointer
+	inBytes   uintptr
+}
+
+// New creates the pools; buffers follow at Warmup.
+func New(model Model, cfg Config) (*Runner, error) {
+	kv, err := NewKVCache(model.NumLayers(), cfg.NumBlocks, cfg.BlockSize, model.NumKVHeads(), model.HeadDim(),
+		cfg.KVDtype, cfg.KVScales)
+	if err != nil {
+		return nil, err
+	}
+	s, err := newStream()
+	if err != nil {
+		kv.Close()
+		return nil, err
+	}
+	return &Runner{
+		model: model, cfg: cfg, kv: kv, stream: s, rows: NewOneHotRows(model.Vocab()),
+		rng: rand.New(rand.NewSource(cfg.Seed)),
+		hq:  model.NumQHeads(), hkv: model.NumKVHeads(), d: model.HeadDim(), vocab: model.Vocab(),
+	}, nil
+}
+
+// Input layout of one step (int32 words): tokens, positions, slots [B*R]; ctx, rows,
+// n_drafts [B]; tables [B*maxBlocks]; drafts [B*K]; then float32 uniforms [B*R].
+type inLayout struct{ tokens, positions, slots, ctx, rows, tables, drafts, nDrafts, uniforms, words int }
+
+func layout(B, R, MB int) inLayout {
+	var l inLayout
+	off := 0
+	take := func(n int) int { o := off; off += n; return o }
+	l.tokens, l.positions, l.slots = take(B*R), take(B*R), take(B*R)
+	l.ctx, l.rows, l.nDrafts = take(B), take(B), take(B)
+	l.tables, l.drafts = take(B*MB), take(B*(R-1))
+	l.uniforms = take(B * R)
+	l.words = off
+	return l
+}
+
+func (r *Runner) Warmup(_ context.Context, p backend.WarmupProfile) error {
+	if p.BlockSize != 0 && p.BlockSize != r.cfg.BlockSize {
+		return fmt.Errorf("rocm: warm-up block size %d, pools use %d", p.BlockSize, r.cfg.BlockSize)
+	}
+	r.release()
+	r.maxB, r.maxR = p.MaxBatchSize, r.cfg.MaxDrafts+1
+	r.maxBlocks = (p.MaxSeqLen + r.cfg.BlockSize - 1) / r.cfg.BlockSize
+	B, R := r.maxB, r.maxR
+	r.inBytes = uintptr(layout(B, R, r.maxBlocks).words) * 4
+	r.attnWS = r.kv.AttentionWorkspace(B, R, r.hq, r.maxBlocks)
+	if r.cfg.Rejection {
+		r.accWS = AcceptRejectionWorkspace(B, R-1, r.vocab)
+	} else {
+		r.accWS = AcceptGreedyWorkspace(B, R-1, r.vocab)
+	}
+	rowBytes := uintptr(B*R) * 2
+	var err error
+	for _, a := range []struct {
+		p *unsafe.Pointer
+		n uintptr
+	}{
+		{&r.dIn, r.inBytes}, {&r.dQ, rowBytes * uintptr(r.hq*r.d)}, {&r.dOut, rowBytes * uintptr(r.hq*r.d)},
+		{&r.dK, rowBytes * uintptr(r.hkv*r.d)}, {&r.dV, rowBytes * uintptr(r.hkv*r.d)},
+		{&r.dLogits, rowBytes * uintptr(r.vocab)}, {&r.dAttnWS, r.attnWS}, {&r.dAccWS, r.accWS},
+		{&r.dDec, uintptr(2*B) * 4},
+	} {
+		if *a.p, err = deviceAlloc(a.n); err != nil {
+			r.release()
+			return err
+		}
+	}
+	if r.hIn, err = hostAlloc(r.inBytes); err == nil {
+		r.hDec, err = hostAlloc(uintptr(2*B) * 4)
+	}
+	if err != nil {
+		r.release()
+	}
+	return err
+}
+
+func i32(base unsafe.Pointer, word int, n int) []int32 {
+	return unsafe.Slice((*int32)(unsafe.Add(base, 4*word)), n)
+}
+
+func at(base unsafe.Pointer, word int) unsafe.Pointer { return unsafe.Add(base, 4*word) }
+
+func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepOutput, error) {
+	for _, p := range batch.IsPrefill {
+		if p {
+			return r.model.Prefill(ctx, batch)
+		}
+	}
+	if r.dIn == nil {
+		return nil, fmt.Errorf("rocm: Step before Warmup")
+	}
+	if len(batch.SequenceIDs) > r.maxB {
+		return nil, fmt.Errorf("rocm: batch of %d exceeds the warmed-up %d", len(batch.SequenceIDs), r.maxB)
+	}
+	in, err := PackBatch(batch, r.cfg.BlockSize, r.maxBlocks, r.maxR)
+	if err != nil {
+		return nil, err
+	}
+	B, R, MB, K := in.NumSeqs, in.RowsPerSeq, in.MaxBlocks, in.RowsPerSeq-1
+	l := layout(B, R, MB)
+	copy(i32(r.hIn, l.tokens, B*R), in.Tokens)
+	copy(i32(r.hIn, l.positions, B*R), in.Positions)
+	copy(i32(r.hIn, l.slots, B*R), in.Slots)
+	copy(i32(r.hIn, l.ctx, B), in.CtxLens)
+	copy(i32(r.hIn, l.rows, B), in.RowCounts)
+	copy(i32(r.hIn, l.nDrafts, B), in.NDrafts)
+	copy(i32(r.hIn, l.tables, B*MB), in.BlockTables)
+	copy(i32(r.hIn, l.drafts, B*K), in.Drafts)
+	u := unsafe.Slice((*float32)(at(r.hIn, l.uniforms)), B*R)
+	for i := range u {
+		u[i] = r.rng.Float32()
+	}
+	s := r.stream
+	if err := copyH2D(r.dIn, r.hIn, uintptr(l.words)*4, s); err != nil {
+		return nil, err
+	}
+	d := func(word int) unsafe.Pointer { return at(r.dIn, word) }
+	scale := float32(1.0 / math.Sqrt(float64(r.d))) // as gollmgo_model.cu
+	if err := r.model.Embed(d(l.tokens), B, R, s); err != nil {
+		return nil, err
+	}
+	if err := r.kv.Plan(d(l.ctx), d(l.rows), MB, B, R, r.hq, r.dAttnWS, r.attnWS, s); err != nil {
+		return nil, err
+	}
+	perBlock := r.cfg.KVScales == ScalePerBlock
+	for layer := 0; layer < r.model.NumLayers(); layer++ {
+		if err := r.model.QKV(layer, d(l.positions), r.dQ, r.dK, r.dV, s); err != nil {
+			return nil, err
+		}
+		if perBlock { // INT8 block scales are updated by gg_kv_append only
+			if err := r.kv.Append(layer, r.dK, r.dV, d(l.slots), B*R, s); err != nil {
+				return nil, err
+			}
+			err = r.kv.AttentionPlanned(layer, r.dQ, r.dOut, d(l.ctx), d(l.rows), d(l.tables), MB, B, R, r.hq,
+				scale, r.dAttnWS, r.attnWS, s)
+		} else {
+			err = r.kv.AppendAttention(layer, r.dK, r.dV, r.dQ, r.dOut, d(l.ctx), d(l.rows), d(l.tables), MB, B,
+				R, r.hq, scale, r.dAttnWS, r.attnWS, s)
+		}
+		if err != nil {
+			return nil, err
+		}
+		if err := r.model.Post(layer, r.dOut, s); err != nil {
+			return nil, err
+		}
+	}
+	if err := r.model.Logits(r.dLogits, s); err != nil {
+		return nil, err
+	}
+	acc, tok := r.dDec, unsafe.Add(r.dDec, 4*B)
+	if r.cfg.Rejection {
+		err = AcceptRejection(r.dLogits, DtypeBF16, nil, B, K, r.vocab, d(l.drafts), d(l.nDrafts), d(l.uniforms),
+			r.cfg.Temperature, r.cfg.TopP, acc, tok, r.dAccWS, r.accWS, s)
+	} else {
+		err = AcceptGreedy(r.dLogits, DtypeBF16, B, K, r.vocab, d(l.drafts), d(l.nDrafts), acc, tok, r.dAccWS,
+			r.accWS, s)
+	}
+	if err != nil {
+		return nil, err
+	}
+	if err := copyD2H(r.hDec, r.dDec, uintptr(2*B)*4, s); err != nil {
+		return nil, err
+	}
+	if err := syncStream(s); err != nil {
+		return nil, err
+	}
+	hAcc, hTok := i32(r.hDec, 0, B), i32(r.hDec, B, B)
+	out := &backend.StepOutput{
+		Logits:            make([][]float32, B),
+		LogitsPerPosition: make([][][]float32, B),
+	}
+	for i := 0; i < B; i++ {
+		n := int(in.NDrafts[i])
+		rows, err := r.rows.RowsFor(in.Drafts[i*K:i*K+n], int(hAcc[i]), hTok[i])
+		if err != nil {
+			return nil, fmt.Errorf("rocm: sequence %d: %w", i, err)
+		}
+		out.Logits[i] = rows[0]
+		if n > 0 {
+			out.LogitsPerPosition[i] = rows
+		}
+	}
+	return out, nil
+}
+
+func (r *Runner) Capabilities() backend.Capabilities {
+	return backend.Capabilities{
+		FP16: true, BF16: true, FP8: true, INT8: true,
+		PagedAttention:      true,
+		CUDAGraphs:          false, // the step is capture-safe; this runner does not capture yet
+		SpeculativeDecoding: true,  // K+1 rows per sequence in one Step
+		KVSwap:              true,
+	}
+}
+
+func (r *Runner) release() {
+	for _, p := range []*unsafe.Pointer{&r.dIn, &r.dQ, &r.dK, &r.dV, &r.dOut, &r.dLogits, &r.dAttnWS, &r.dAccWS,
+		&r.dDec} {
+		deviceFree(*p)
+		*p = nil
+	}
+	hostFree(r.hIn)
+	hostFree(r.hDec)
+	r.hIn, r.hDec = nil, nil
+}
+
+func (r *Runner) Close() error {
+	if r.kv == nil {
+		return nil
+	}
+	syncStream(r.stream)
+	r.release()
+	destroyStream(r.stream)
+	err := r.kv.Close()
+	r.kv, r.stream = nil, nil
+	return err
+}
+
+// Snapshot is a KV swap snapshot held in pinned host memory.
+type Snapshot struct {
+	host   unsafe.Pointer
+	bytes  uintptr
+	blocks int
+}
+
+func (s *Snapshot) NumBlocks() int     { return s.blocks }
+func (s *Snapshot) BytesOnHost() int64 { return int64(s.bytes) }
+func (s *Snapshot) Release() error {
+	hostFree(s.host)
+	s.host = nil
+	return nil
+}
+
+// swapIO uploads the block ids and allocates the device staging of one swap (a swap is
+// a preemption event, not a per-step call, so it may allocate).
+func (r *Runner) swapIO(blockIDs []int32) (ids, staging unsafe.Pointer, n uintptr, err error) {
+	n = r.kv.SnapshotBytes(len(blockIDs))
+	if ids, err = deviceAlloc(uintptr(4 * len(blockIDs))); err != nil {
+		return
+	}
+	if staging, err = deviceAlloc(n); err != nil {
+		deviceFree(ids)
+		return
+	}
+	if err = copyH2D(ids, unsafe.Pointer(&blockIDs[0]), uintptr(4*len(blockIDs)), r.stream); err == nil {
+		err = syncStream(r.stream) // blockIDs is Go memory: finish before returning
+	}
+	if err != nil {
+		deviceFree(ids)
+		deviceFree(staging)
+	}
+	return
+}
+
+func (r *Runner) SnapshotKV(_ context.Context, blockIDs []int32) (backend.KVSnapshot, error) {
+	if len(blockIDs) == 0 {
+		return &Snapshot{}, nil
+	}
+	ids, staging, n, err := r.swapIO(blockIDs)
+	if err != nil {
+		return nil, err
+	}
+	defer deviceFree(ids)
+	defer deviceFree(staging)
+	host, err := hostAlloc(n)
+	if err != nil {
+		return nil, err
+	}
+	if err = r.kv.Snapshot(ids, len(blockIDs), staging, n, host, r.stream); err == nil {
+		err = syncStream(r.stream)
+	}
+	if err != nil {
+		hostFree(host)
+		return nil, err
+	}
+	return &Snapshot{host: host, bytes: n, blocks: len(blockIDs)}, nil
+}
+
+func (r *Runner) RestoreKV(_ context.Context, snap backend.KVSnapshot, blockIDs []int32) error {
+	s, ok := snap.(*Snapshot)
+	if !ok {
+		return fmt.Errorf("rocm: snapshot of another backend")
+	}
+	if s.blocks != len(blockIDs) {
+		return fmt.Errorf("rocm: snapshot of %d blocks restored into %d", s.blocks, len(blockIDs))
+	}
+	if len(blockIDs) == 0 {
+		return nil
+	}
+	ids, staging, n, err := r.swapIO(blockIDs)
+	if err != nil {
+		return err
+	}
+	defer deviceFree(ids)
+	defer deviceFree(staging)
+	if err := r.kv.Restore(ids, len(blockIDs), staging, n, s.host, r.stream); err != nil {
+		return err
+	}
+	return syncStream(r.stream)
+}
+
+var (
+	_ backend.Runner    = (*Runner)(nil)
+	_ backend.KVSwapper = (*Runner)(nil)
+)

@@ -213,6 +213,62 @@ int ora_categorical_f64(const double* probs, int n, double u) {
     return 0;
 }
 
+/* Sampler.Sample (sampling.go:40-72) without top-k, the uniform supplied: temperature
+ * <= 1e-9 -> argmax; else logit * (1/T) in float64, softmax, top-p when 0 < p < 1, and
+ * the categorical draw. */
+int ora_sample_f64(const float* logits, int n, double temperature, double top_p, double u) {
+    if (n <= 0) return 0;
+    if (temperature <= 1e-9) return ora_argmax(logits, n);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)n);
+    double* pr = (double*)malloc(sizeof(double) * (size_t)n);
+    const double inv_t = 1.0 / temperature;
+    for (int i = 0; i < n; ++i) sc[i] = (double)logits[i] * inv_t;
+    ora_softmax_f64(sc, n, pr);
+    if (top_p > 0 && top_p < 1.0) {
+        ora_top_p_filter_f64(pr, n, top_p, sc);
+        memcpy(pr, sc, sizeof(double) * (size_t)n);
+    }
+    const int t = ora_categorical_f64(pr, n, u);
+    free(sc);
+    free(pr);
+    return t;
+}
+
+/* emitSpeculative's use of StepOutput.LogitsPerPosition (serving.go:496-570) over ragged
+ * rows, as Go slices: sequence b owns counts[b] rows, taken in order from rows / lens.
+ * Verify over the first min(count, n) rows; on a rejection the corrected token; on full
+ * acceptance Sample(rows[n]) when a row is there, else -1 (no token). n = 0 reduces to
+ * the standard path's Sample over the one row. uniforms[b] feeds the sample. */
+void ora_emit_positions(int B, int K, const int32_t* drafts, const int32_t* n_drafts,
+                        const float* const* rows, const int32_t* lens, const int32_t* counts,
+                        double temperature, double top_p, const double* uniforms, int32_t* out_acc,
+                        int32_t* out_tok) {
+    size_t r0 = 0;
+    for (int b = 0; b < B; ++b) {
+        int n = n_drafts[b];
+        if (n < 0) n = 0;
+        if (n > K) n = K;
+        const int cnt = counts[b];
+        const float* const* rw = rows + r0;
+        const int32_t* ln = lens + r0;
+        r0 += (size_t)cnt;
+        const int nv = cnt < n ? cnt : n;
+        const int32_t* d = drafts + (size_t)b * K;
+        int acc = n, cor = -1;
+        for (int i = 0; i < nv; ++i) { /* Verify, speculative.go:68-84 (fewer rows: all accepted) */
+            const int c = ora_argmax(rw[i], ln[i]);
+            if (c != d[i]) {
+                acc = i;
+                cor = c;
+                break;
+            }
+        }
+        out_acc[b] = acc;
+        if (acc < n) out_tok[b] = cor;
+        else out_tok[b] = cnt > n ? ora_sample_f64(rw[n], ln[n], temperature, top_p, uniforms[b]) : -1;
+    }
+}
+
 /* ------------------------------------------------------------ n-gram drafter */
 
 /* NGramDrafter.Draft (speculative.go:12-62) with an explicit hash map whose
@@ -407,8 +463,9 @@ static u128 row_weights(const float* row, int V, float inv_t, float top_p, u128*
  *   first rejection at row a: draw from r_i = f_s * (e_i - min(e_i, floor(q_i * Zp_a / f_s)))
  *     (the residual max(0, W_i - q_i * Zp) rounded in the segment's units of e; the
  *     quotient Zp / f_s and the product are doubles; q is one-hot at the draft when no
- *     draft distribution is given; r_i = 0 where f_s = 0); if every r_i is 0, draw from
- *     W of row a itself;
+ *     draft distribution is given; r_i = 0 where f_s = 0 and at the rejected draft x,
+ *     whose exact residual is 0 since u < 1 rejects only when p(x) < q(x)); if every r_i
+ *     is 0, draw from W of row a without x, and if that is 0 too, from W of row a;
  *   all accepted: draw from W of row n;
  *   draw(u, r): t = floor(u * sum r); first i with inclusive prefix > t; else the
  *     last i with r_i > 0; else 0.
@@ -448,12 +505,13 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
         const double zpd = u128_to_double(zp);
         u128 tot = 0;
         int residual = a < n;
+        const int xr = residual ? drafts[(size_t)b * K + a] : -1;
         if (residual) {
-            int xr = drafts[(size_t)b * K + a];
             for (int i = 0; i < V; ++i) {
                 const uint64_t fs = f[i / ORA_SEG];
                 r[i] = 0;
-                if (fs == 0 || e[i] == 0) continue;
+                /* a rejection (u < 1) means p(x) < q(x): the draft's residual is 0 */
+                if (fs == 0 || e[i] == 0 || i == xr) continue;
                 const double qv = dprobs ? clean_q(dprobs[((size_t)b * K + a) * V + i]) : (i == xr ? 1.0 : 0.0);
                 const double qd = qv * (zpd / (double)fs);
                 const uint64_t rq = (double)e[i] > qd ? e[i] - (uint64_t)floor(qd) : 0;
@@ -461,13 +519,18 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
                 tot += r[i];
             }
         }
-        if (!residual || tot == 0) {
-            tot = 0;
+        /* A vanished residual (dense q that is not a distribution) draws from the target
+         * row without the rejected draft, and that vanishing too, from the whole row. */
+        if (residual && tot == 0)
+            for (int i = 0; i < V; ++i) {
+                r[i] = i == xr ? 0 : w[i];
+                tot += r[i];
+            }
+        if (tot == 0)
             for (int i = 0; i < V; ++i) {
                 r[i] = w[i];
                 tot += r[i];
             }
-        }
         int tok = 0;
         if (tot > 0) {
             double u = (double)uniforms[(size_t)b * (K + 1) + K];

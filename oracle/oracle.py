@@ -8,6 +8,7 @@ Every function here calls the C restatement or does plain numpy bookkeeping
 from __future__ import annotations
 
 import ctypes as C
+import time
 import subprocess
 from pathlib import Path
 
@@ -192,6 +193,42 @@ def categorical_f64(p, u: float) -> int:
     f = lib().ora_categorical_f64
     f.argtypes = [C.c_void_p, C.c_int, C.c_double]
     return int(f(_p(p), len(p), float(u)))
+
+
+def sample_f64(logits, temperature: float, top_p: float, u: float) -> int:
+    """Sampler.Sample (sampling.go:40-72, no top-k) with the uniform supplied."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    f = lib().ora_sample_f64
+    f.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_double, C.c_double]
+    return int(f(_p(x), len(x), float(temperature), float(top_p), float(u)))
+
+
+def emit_positions(drafts, n_drafts, positions, temperature: float = 0.0, top_p: float = 1.0,
+                   uniforms=None, timer=None):
+    """What emitSpeculative (serving.go:496-570) takes from LogitsPerPosition: per sequence
+    (accepted, token), token -1 when every draft is accepted and no further row is given.
+    positions[b] is a list of 1-D float32 rows (ragged, as Go slices). timer: a list that
+    receives the seconds spent in the C routine alone."""
+    d = np.ascontiguousarray(drafts, dtype=np.int32)
+    B = len(positions)
+    K = d.shape[1] if d.ndim == 2 else 0
+    nd = np.ascontiguousarray(n_drafts, dtype=np.int32)
+    flat = [np.ascontiguousarray(r, dtype=np.float32) for rows in positions for r in rows]
+    ptrs = (C.c_void_p * max(1, len(flat)))(*[r.ctypes.data for r in flat])
+    lens = np.array([len(r) for r in flat] or [0], np.int32)
+    counts = np.array([len(rows) for rows in positions], np.int32)
+    u = np.ascontiguousarray(uniforms if uniforms is not None else np.zeros(B), dtype=np.float64)
+    acc = np.empty(B, np.int32)
+    tok = np.empty(B, np.int32)
+    f = lib().ora_emit_positions
+    f.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                  C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p]
+    t0 = time.perf_counter()
+    f(B, K, _p(d) if d.size else None, _p(nd), ptrs, _p(lens), _p(counts), float(temperature),
+      float(top_p), _p(u), _p(acc), _p(tok))
+    if timer is not None:
+        timer.append(time.perf_counter() - t0)
+    return acc, tok
 
 
 def draw_parity(logits_f32, temperature: float, top_p: float, uniforms, threads: int = 0):

@@ -157,3 +157,20 @@ def per_head_amax_scales(x: np.ndarray) -> np.ndarray:
 
 
 __all__ = ["PoolMirror", "rel_err_per_vector", "append_rows", "glibc_rand_uniform", "TOL", "say", "math"]
+
+
+def check_positions(drafts, n, acc, tok, vocab: int, temperature: float, top_p: float, seed: int) -> None:
+    """The engine's own Verify + Sample over the one-hot LogitsPerPosition rows built from a
+    device decision must give that decision back, and a rejected draft is never the token."""
+    from gollmgo_amd.positions import LogitsPerPosition
+
+    drafts, n, acc, tok = (np.asarray(x) for x in (drafts, n, acc, tok))
+    K = drafts.shape[1] if drafts.ndim == 2 else 0
+    for b in range(len(acc)):
+        nb = min(max(int(n[b]), 0), K)
+        if acc[b] < nb:
+            assert tok[b] != drafts[b, acc[b]], f"sequence {b}: the token after a rejection is the draft"
+    pos = LogitsPerPosition(vocab).batch(drafts, n, acc, tok)
+    u = np.random.default_rng(seed).random(len(acc))
+    ea, et = ora.emit_positions(drafts, n, pos, temperature, top_p, u)
+    assert np.array_equal(ea, acc) and np.array_equal(et, tok)

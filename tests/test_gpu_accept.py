@@ -4,7 +4,7 @@ import pytest
 import torch
 
 import gollmgo_amd.verify as gv
-from helpers import say
+from helpers import check_positions, say
 from oracle import oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -238,12 +238,14 @@ def test_acceptance_random_cases(gpu, seed):
     torch.cuda.synchronize()
     ea, et = ora.accept_greedy(host, drafts, n)
     assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et)
+    check_positions(drafts, n, acc.cpu().numpy(), tok.cpu().numpy(), V, 0.0, 1.0, seed)
     acc, tok = gv.accept_rejection(lg.cuda(), d_t, n_t, u_t, T, top_p,
                                    draft_probs=torch.from_numpy(q).cuda() if q is not None else None)
     torch.cuda.synchronize()
     ea, et = ora.accept_rejection(host, drafts, n, u, T, top_p, q)
     assert np.array_equal(acc.cpu().numpy(), ea)
     assert np.array_equal(tok.cpu().numpy(), et)
+    check_positions(drafts, n, acc.cpu().numpy(), tok.cpu().numpy(), V, T, top_p, seed)
 
 
 @pytest.mark.parametrize("cid", [2, 3, 4, 5])
@@ -280,3 +282,6 @@ def test_acceptance_full_size_configs(gpu, cid):
     print(f"  accepted {int(a.sum())} of {int(n.sum())} drafts")
     assert np.array_equal(a, ea)
     assert np.array_equal(t, et)
+    # The decision handed back as the engine's LogitsPerPosition (one-hot rows).
+    T = cfg.temperature if cfg.accept != "greedy" else 0.0
+    check_positions(drafts.cpu().numpy(), n.cpu().numpy(), a, t, V, T, cfg.top_p, cid)
