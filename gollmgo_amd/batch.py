@@ -123,4 +123,25 @@ def pack_batch(batch: Batch, block_size: int, max_blocks: int = 0, rows_per_seq:
         rows[i] = c
         drafts[i, :c - 1] = d
         nd[i] = c - 1
+    check_block_runs(slots, block_size)
     return StepInputs(B, R, MB, tokens, positions, slots, ctx, rows, tables, drafts, nd)
+
+
+def check_block_runs(slots: np.ndarray, block_size: int) -> None:
+    """gg_kv_append's rule for PER_BLOCK pools: the rows of one block are adjacent in the
+    slot mapping (skipped rows, slot < 0, may sit between them) with increasing offsets. A
+    block that reappears after another block's rows would get two leaders on the device."""
+    seen: set = set()
+    cur, last_off = -1, -1
+    for s in np.asarray(slots).tolist():
+        if s < 0:
+            continue
+        blk, off = divmod(int(s), block_size)
+        if blk != cur:
+            if blk in seen:
+                raise BatchError(f"block {blk} appears in two separate runs of the slot mapping")
+            seen.add(blk)
+            cur, last_off = blk, -1
+        if off <= last_off:
+            raise BatchError(f"block {blk}: offsets not increasing in the slot mapping")
+        last_off = off

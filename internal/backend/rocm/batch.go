@@ -148,5 +148,35 @@ func PackBatch(batch *backend.Batch, bs, maxBlocks, rowsPerSeq int) (*StepInputs
 		copy(in.Drafts[i*K:i*K+c-1], d)
 		in.NDrafts[i] = int32(c - 1)
 	}
+	if err := CheckBlockRuns(in.Slots, bs); err != nil {
+		return nil, err
+	}
 	return in, nil
+}
+
+// CheckBlockRuns enforces gg_kv_append's rule for PER_BLOCK pools: the rows of one block
+// are adjacent in the slot mapping (skipped rows, slot < 0, may sit between them) with
+// increasing offsets. A block that reappears after another block's rows would get two
+// leaders on the device.
+func CheckBlockRuns(slots []int32, bs int) error {
+	seen := map[int]bool{}
+	cur, lastOff := -1, -1
+	for _, s := range slots {
+		if s < 0 {
+			continue
+		}
+		blk, off := int(s)/bs, int(s)%bs
+		if blk != cur {
+			if seen[blk] {
+				return fmt.Errorf("rocm: block %d appears in two separate runs of the slot mapping", blk)
+			}
+			seen[blk] = true
+			cur, lastOff = blk, -1
+		}
+		if off <= lastOff {
+			return fmt.Errorf("rocm: block %d: offsets not increasing in the slot mapping", blk)
+		}
+		lastOff = off
+	}
+	return nil
 }

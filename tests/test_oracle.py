@@ -305,6 +305,35 @@ def test_rejection_bonus_draw_hits_every_nucleus_token(ora):
         assert tok.tolist() == toks
 
 
+def test_rejection_never_returns_the_rejected_draft(ora):
+    """After a rejection at draft x the draw excludes x: max(0, p - q) is 0 at x, since
+    u < 1 rejects only when p(x) < q(x). Also when the residual vanishes (q not a
+    distribution: all ones), where the draw falls back to the row without x."""
+    rng = np.random.default_rng(21)
+    B, K, V = 300, 4, 400
+    for T, top_p, dense in [(0.8, 1.0, False), (1.0, 0.9, False), (0.8, 1.0, True), (1.2, 0.95, True)]:
+        lg = rng.normal(0, 1.5, (B, K + 1, V)).astype(np.float32)
+        q = None
+        if dense:
+            q = rng.dirichlet(np.ones(V) * 0.3, (B, K)).astype(np.float32)
+        drafts = lg[:, :K].argmax(-1).astype(np.int32)
+        mask = rng.random((B, K)) < 0.4
+        drafts[mask] = rng.integers(0, V, int(mask.sum()))
+        n = rng.integers(1, K + 1, B).astype(np.int32)
+        u = rng.random((B, K + 1)).astype(np.float32)
+        acc, tok = ora.accept_rejection(lg, drafts, n, u, T, top_p, q)
+        rej = acc < n
+        assert rej.sum() > 20
+        assert np.all(tok[rej] != drafts[rej, acc[rej]])
+    # q = 1 everywhere: every residual is 0, and the draw takes the row without the draft.
+    lg = rng.normal(0, 1.0, (50, 2, 30)).astype(np.float32)
+    drafts = lg[:, 0].argmax(-1).astype(np.int32)[:, None]
+    q = np.ones((50, 1, 30), np.float32)
+    u = np.full((50, 2), 0.9, np.float32)
+    acc, tok = ora.accept_rejection(lg, drafts, np.ones(50, np.int32), u, 1.0, 1.0, q)
+    assert np.all(acc == 0) and np.all(tok != drafts[:, 0])
+
+
 @pytest.mark.parametrize("T,top_p", [(0.8, 1.0), (1.0, 1.0), (0.8, 0.95), (1.0, 0.95)])
 def test_fixed_point_draw_vs_float64_sampler(ora, T, top_p):
     """The fixed-point draw against Sampler.Sample's float64 rule (sampling.go:40-72,

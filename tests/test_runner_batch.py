@@ -122,6 +122,15 @@ def test_pack_refuses_inconsistent_batches():
         pack_batch(Batch([], [], [], [], [], [], [], []), bs)
 
 
+def test_block_runs_rule():
+    from gollmgo_amd.batch import check_block_runs
+    check_block_runs(np.array([32, 33, -1, 34, 16, 17, 48]), 16)  # runs of blocks 2, 1, 3
+    with pytest.raises(BatchError, match="two separate runs"):
+        check_block_runs(np.array([32, 33, 16, 34]), 16)
+    with pytest.raises(BatchError, match="not increasing"):
+        check_block_runs(np.array([33, 32]), 16)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dt", ["bf16", "fp8", "int8"])
 def test_packed_step_through_the_abi(gpu, dt):
