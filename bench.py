@@ -39,9 +39,10 @@ def parse():
     ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU baseline sample")
     ap.add_argument("--partition", type=int, default=-1, help="override split-K partition tokens")
     ap.add_argument("--layers", type=int, default=0, help="override layer count (0 = config)")
-    ap.add_argument("--append-in-call", action="store_true",
-                    help="append the draft KV through gg_verify_append_attention_planned (one call per "
-                         "layer) instead of gg_kv_append + gg_verify_attention_planned")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="append the draft KV with gg_kv_append before gg_verify_attention_planned instead of "
+                         "inside the attention call (gg_verify_append_attention_planned, the default where "
+                         "the pool allows it)")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches for `value` instead of replays of the captured step graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -162,10 +163,10 @@ def main():
     # The attention schedule depends only on the context lengths, shared by all layers of
     # a step: computed once per step (gg_verify_attention_plan), used by every layer.
     use_plan = cfg.partition == 0
-    # --append-in-call: the draft rows' KV append through the attention entry point
+    # The draft rows' KV append goes through the attention entry point
     # (gg_verify_append_attention_planned; not for PER_BLOCK INT8, whose block scales need
     # gg_kv_append).
-    fused = use_plan and cfg.kv_dtype != "int8" and args.append_in_call
+    fused = use_plan and cfg.kv_dtype != "int8" and not args.separate_append
 
     def step(record: bool):
         if hist is not None:
@@ -187,7 +188,8 @@ def main():
         for layer in range(L):
             if record:
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-                e0.record()
+                if not fused:
+                    e0.record()
             if not fused:
                 kv.append(layer, k_new[layer], v_new[layer], append_slots)
             if record:
@@ -199,7 +201,8 @@ def main():
                              workspace=ws_attn, planned=use_plan)
             if record:
                 e2.record()
-                ev["append"].append((e0, e1))
+                if not fused:  # (fused: the append is inside the attention call)
+                    ev["append"].append((e0, e1))
                 ev["attn"].append((e1, e2))
         if record:
             a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -293,8 +296,8 @@ def main():
     elif cfg.partition:
         attn_kernels = "attn_mfma_kernel + attn_combine_kernel (partition grid)"
     elif fused:
-        attn_kernels = ("gg_verify_append_attention_planned: draft-KV append launch + "
-                        "the library's automatic schedule (LPT pieces or stream-K) + merge")
+        attn_kernels = ("gg_verify_append_attention_planned: the library's automatic schedule (LPT pieces or "
+                        "stream-K), each piece appending its draft rows, + merge")
     else:
         attn_kernels = "gg_verify_attention_planned: the library's automatic schedule (LPT pieces or stream-K) + merge"
     traffic, traffic_src = pmc_traffic(args.config)

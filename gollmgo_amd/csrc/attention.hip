@@ -277,12 +277,15 @@ size_t attn_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_head
 gg_status_t launch_verify_attention(const AttnArgs& a, hipStream_t s) {
     const KV* kv = a.kv;
     KVView view = make_kv_view(kv, a.layer);
-    if (a.k_new) {
+    const bool mfma = a.sched != ATTN_SCHED_GRID || (attn_mfma_supported(kv, a.rows, a.num_q_heads) &&
+                                                     a.partition % 64 == 0 && a.partition <= kMfmaMaxPartition);
+    // Draft rows of the call: the MFMA kernels append them piece by piece (start_piece);
+    // the generic path takes a launch of its own first.
+    if (a.k_new && !mfma) {
         const gg_status_t st = launch_append_from_tables(a, view, s);
         if (st != GG_OK) return st;
     }
-    if (a.sched != ATTN_SCHED_GRID || (attn_mfma_supported(kv, a.rows, a.num_q_heads) && a.partition % 64 == 0 &&
-                                       a.partition <= kMfmaMaxPartition)) {
+    if (mfma) {
         // Stream-K and LPT launch their own merge over their record layout.
         gg_status_t st = launch_attn_mfma(a, view, s);
         if (st != GG_OK) return st;

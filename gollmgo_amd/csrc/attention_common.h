@@ -130,73 +130,116 @@ gg_status_t launch_append_from_tables(const AttnArgs& a, const KVView& kv, hipSt
 #ifdef __HIPCC__
 // The draft-KV rows of item (b, kvh): row b*rows + j, j < the sequence's row count, goes to
 // key position ctx - row_count + j, ctx as the attention clamps it to the table row (slot
-// from the block table; entries outside the pool are skipped). Same conversions as gg_kv_append: rounding to the pool type, FP8 as
-// E4M3-satfinite of x * (1 / per-head scale). Not for PER_BLOCK INT8 pools; head_dim a
-// multiple of 8 and 16-byte aligned rows (checked by the entry point). Run by a whole
-// workgroup; launched before the attention that reads those rows.
-__device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView& kv, int b, int kvh) {
+// from the block table; entries outside the pool are skipped). Same conversions as
+// gg_kv_append: rounding to the pool type, FP8 as E4M3-satfinite of x * (1 / per-head
+// scale). Not for PER_BLOCK INT8 pools; head_dim a multiple of 8 and 16-byte aligned rows
+// (checked by the entry point).
+//
+// Work item i of rows [j0, j1) is row j0 + i / (D/8), dims [8*(i % (D/8)), +8): K is one
+// contiguous run of the row, V eight columns of the dim-major tile. Split in two so that a
+// caller can issue the loads early and store later: append_load (block id, source words,
+// scales) and append_store (conversion and stores).
+struct AppendItem {
+    uint4 k[2], v[2];  // source words: f32 sources fill both, 16-bit sources k[0] / v[0]
+    size_t ki, vi;     // destination element indices in the K and V pools
+    float kinv, vinv;  // FP8: 1 / per-head scale
+    bool live;
+};
+__device__ __forceinline__ AppendItem append_load(const AttnArgs& a, const KVView& kv, int b, int kvh, int ctx,
+                                                  int nrows, int j0, int i) {
+    AppendItem it;
+    const int D = kv.D, bs = kv.bs, groups = D / 8;
+    const int j = j0 + i / groups, d0 = (i % groups) * 8;
+    const int pos = ctx - nrows + j;
+    const int blk = a.block_tables[(size_t)b * a.max_blocks + pos / bs];
+    it.live = blk >= 0 && blk < kv.num_blocks;
+    const int off = pos % bs;
+    const int bsafe = it.live ? blk : 0;
+    it.ki = kv.tile0(bsafe, kvh) + (size_t)off * D + d0;
+    it.vi = kv.tile0(bsafe, kvh) + (size_t)d0 * bs + off;
+    it.kinv = kv.dt == GG_DTYPE_FP8_E4M3 ? kv.k_head_scale[kv.Hkv + kvh] : 1.f;
+    it.vinv = kv.dt == GG_DTYPE_FP8_E4M3 ? kv.v_head_scale[kv.Hkv + kvh] : 1.f;
+    const size_t src = (((size_t)b * a.rows + j) * kv.Hkv + kvh) * D + d0;
+    if (dtype_bytes(a.new_dtype) == 4) {
+        const uint4* kp = (const uint4*)((const float*)a.k_new + src);
+        const uint4* vp = (const uint4*)((const float*)a.v_new + src);
+        it.k[0] = kp[0]; it.k[1] = kp[1]; it.v[0] = vp[0]; it.v[1] = vp[1];
+    } else {
+        it.k[0] = *(const uint4*)((const uint16_t*)a.k_new + src);
+        it.v[0] = *(const uint4*)((const uint16_t*)a.v_new + src);
+        it.k[1] = it.v[1] = make_uint4(0, 0, 0, 0);
+    }
+    return it;
+}
+__device__ __forceinline__ void append_store(const AttnArgs& a, const KVView& kv, const AppendItem& it) {
+    if (!it.live) return;
+    const int bs = kv.bs;
+    uint8_t* kc = const_cast<uint8_t*>(kv.kc);
+    uint8_t* vc = const_cast<uint8_t*>(kv.vc);
+    float kx[8], vx[8];
+    if (dtype_bytes(a.new_dtype) == 4) {
+        const uint32_t ku[8] = {it.k[0].x, it.k[0].y, it.k[0].z, it.k[0].w, it.k[1].x, it.k[1].y, it.k[1].z, it.k[1].w};
+        const uint32_t vu[8] = {it.v[0].x, it.v[0].y, it.v[0].z, it.v[0].w, it.v[1].x, it.v[1].y, it.v[1].z, it.v[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            kx[e] = __uint_as_float(ku[e]);
+            vx[e] = __uint_as_float(vu[e]);
+        }
+    } else {
+        const uint32_t ku[4] = {it.k[0].x, it.k[0].y, it.k[0].z, it.k[0].w};
+        const uint32_t vu[4] = {it.v[0].x, it.v[0].y, it.v[0].z, it.v[0].w};
+        const bool bf = a.new_dtype == GG_DTYPE_BF16;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t kh = (uint16_t)(ku[e >> 1] >> (16 * (e & 1)));
+            const uint16_t vh = (uint16_t)(vu[e >> 1] >> (16 * (e & 1)));
+            kx[e] = bf ? bf16_bits_to_f32(kh) : f16_bits_to_f32(kh);
+            vx[e] = bf ? bf16_bits_to_f32(vh) : f16_bits_to_f32(vh);
+        }
+    }
+    if (kv.dt == GG_DTYPE_FP8_E4M3) {
+        uint32_t w[2];
+#pragma unroll
+        for (int e = 0; e < 8; e += 4)
+            w[e >> 2] = f32x2_to_fp8e4m3_sat(kx[e] * it.kinv, kx[e + 1] * it.kinv) |
+                        (f32x2_to_fp8e4m3_sat(kx[e + 2] * it.kinv, kx[e + 3] * it.kinv) << 16);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t vw = f32x2_to_fp8e4m3_sat(vx[e] * it.vinv, vx[e + 1] * it.vinv);
+            vc[it.vi + (size_t)e * bs] = (uint8_t)vw;
+            vc[it.vi + (size_t)(e + 1) * bs] = (uint8_t)(vw >> 8);
+        }
+        *(uint2*)(kc + it.ki) = make_uint2(w[0], w[1]);
+    } else if (kv.dt == GG_DTYPE_F32) {
+        *(float4*)((float*)kc + it.ki) = make_float4(kx[0], kx[1], kx[2], kx[3]);
+        *(float4*)((float*)kc + it.ki + 4) = make_float4(kx[4], kx[5], kx[6], kx[7]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ((float*)vc)[it.vi + (size_t)e * bs] = vx[e];
+    } else {
+        // 16-bit pools: the K run as one 16-byte store, V column by column.
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint16_t lo = kv.dt == GG_DTYPE_BF16 ? f32_to_bf16_bits(kx[e]) : f32_to_f16_bits(kx[e]);
+            const uint16_t hi = kv.dt == GG_DTYPE_BF16 ? f32_to_bf16_bits(kx[e + 1]) : f32_to_f16_bits(kx[e + 1]);
+            w[e >> 1] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *(uint4*)((uint16_t*)kc + it.ki) = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) store_from_f32(vc, kv.dt, it.vi + (size_t)e * bs, vx[e]);
+    }
+}
+// Rows [j0, j1) of item (b, kvh) (clamped to the sequence's rows), by a whole workgroup,
+// before anything reads them.
+__device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView& kv, int b, int kvh, int j0 = 0,
+                                                 int j1 = 1 << 30) {
     const int ctx = seq_keys(a, b, kv.bs);
     const int nrows = seq_rows(a, b);
     if (ctx <= 0 || nrows <= 0 || nrows > ctx) return;
-    const int D = kv.D, bs = kv.bs;
-    const int32_t* bt = a.block_tables + (size_t)b * a.max_blocks;
-    uint8_t* kc = const_cast<uint8_t*>(kv.kc);
-    uint8_t* vc = const_cast<uint8_t*>(kv.vc);
-    const float kinv = kv.dt == GG_DTYPE_FP8_E4M3 ? kv.k_head_scale[kv.Hkv + kvh] : 1.f;
-    const float vinv = kv.dt == GG_DTYPE_FP8_E4M3 ? kv.v_head_scale[kv.Hkv + kvh] : 1.f;
-    // Eight consecutive dims per thread (one row's K run is contiguous, its V run strided).
-    const int groups = D / 8;
-    const int esz = (int)dtype_bytes(a.new_dtype);
-    for (int i = threadIdx.x; i < nrows * groups; i += blockDim.x) {
-        const int j = i / groups, d0 = (i % groups) * 8;
-        const int pos = ctx - nrows + j;
-        const int blk = bt[pos / bs];
-        if (blk < 0 || blk >= kv.num_blocks) continue;
-        const int off = pos % bs;
-        const size_t src = (((size_t)b * a.rows + j) * kv.Hkv + kvh) * D + d0;
-        float kx[8], vx[8];
-        if (esz == 4) {
-            const float4* kp = (const float4*)((const float*)a.k_new + src);
-            const float4* vp = (const float4*)((const float*)a.v_new + src);
-            const float4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
-            kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w; kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
-            vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w; vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
-        } else {
-            const uint4 kw = *(const uint4*)((const uint16_t*)a.k_new + src);
-            const uint4 vw = *(const uint4*)((const uint16_t*)a.v_new + src);
-            const uint32_t ku[4] = {kw.x, kw.y, kw.z, kw.w}, vu[4] = {vw.x, vw.y, vw.z, vw.w};
-            const bool bf = a.new_dtype == GG_DTYPE_BF16;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t kh = (uint16_t)(ku[e >> 1] >> (16 * (e & 1)));
-                const uint16_t vh = (uint16_t)(vu[e >> 1] >> (16 * (e & 1)));
-                kx[e] = bf ? bf16_bits_to_f32(kh) : f16_bits_to_f32(kh);
-                vx[e] = bf ? bf16_bits_to_f32(vh) : f16_bits_to_f32(vh);
-            }
-        }
-        const size_t ki = kv.tile0(blk, kvh) + (size_t)off * D + d0;
-        const size_t vi = kv.tile0(blk, kvh) + (size_t)d0 * bs + off;
-        if (kv.dt == GG_DTYPE_FP8_E4M3) {
-            uint32_t w[2];
-#pragma unroll
-            for (int e = 0; e < 8; e += 4)
-                w[e >> 2] = f32x2_to_fp8e4m3_sat(kx[e] * kinv, kx[e + 1] * kinv) |
-                            (f32x2_to_fp8e4m3_sat(kx[e + 2] * kinv, kx[e + 3] * kinv) << 16);
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const uint32_t vw = f32x2_to_fp8e4m3_sat(vx[e] * vinv, vx[e + 1] * vinv);
-                vc[vi + (size_t)e * bs] = (uint8_t)vw;
-                vc[vi + (size_t)(e + 1) * bs] = (uint8_t)(vw >> 8);
-            }
-            *(uint2*)(kc + ki) = make_uint2(w[0], w[1]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                store_from_f32(kc, kv.dt, ki + e, kx[e]);
-                store_from_f32(vc, kv.dt, vi + (size_t)e * bs, vx[e]);
-            }
-        }
-    }
+    j0 = j0 < 0 ? 0 : j0;
+    j1 = j1 > nrows ? nrows : j1;
+    for (int i = threadIdx.x; i < (j1 - j0) * (kv.D / 8); i += blockDim.x)
+        append_store(a, kv, append_load(a, kv, b, kvh, ctx, nrows, j0, i));
 }
 #endif
 

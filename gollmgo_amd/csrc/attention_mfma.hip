@@ -318,6 +318,49 @@ struct PieceIO {
     }
 };
 
+// Start piece d (PieceIO::start) and, when the call carries draft rows (a.k_new:
+// gg_verify_append_attention_planned on the MFMA path), append the rows whose key
+// positions lie in the piece. A key position belongs to exactly one piece, and only that
+// piece reads it, so no other workgroup waits for these stores; chunks are multiples of 16
+// tokens, so a block's tokens (its K rows and its V columns) are all read by one chunk.
+// The piece's own reads of those positions must follow a workgroup barrier (within a
+// workgroup a barrier orders global stores before loads: same CU, write-through L1):
+//   - rows inside the first chunks that `start` issues: appended, barrier, then `start`;
+//   - otherwise (the usual case: the rows are the item's last positions) the rows' loads
+//     are issued here, after `start`, into `ap` (one work item per thread), and attn_piece
+//     stores them before its Q-staging barrier, which precedes every later chunk's loads,
+//     so their latency overlaps the first chunk's and the Q loads'. More rows than
+//     threads, or no `ap` (the stream-K loop over pieces, whose registers are full), are
+//     appended here at once instead.
+template <gg_dtype_t DT>
+__device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
+                                            PieceIn<DT>& in, AppendItem* ap) {
+    constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
+    if (ap) ap->live = false;
+    // (PER_BLOCK INT8 pools never carry rows here: their scale update needs gg_kv_append.)
+    if (DT != GG_DTYPE_INT8 && a.k_new) {
+        const int ctx = seq_keys(a, d.b, kBS), nrows = seq_rows(a, d.b);
+        const int first = ctx - nrows;
+        const int j0 = max(0, d.t0 - first), j1 = min(nrows, d.t_end - first);
+        if (nrows > 0 && nrows <= ctx && j0 < j1) {
+            const int items = (j1 - j0) * (kD / 8);
+            if (first + j0 < d.t0 + kWaves * kTok) {
+                append_item_rows(a, kv, d.b, d.kvh, j0, j1);
+                __syncthreads();
+                PieceIO<DT>::start(a, kv, d, in);
+            } else if (ap && items <= (int)blockDim.x) {
+                PieceIO<DT>::start(a, kv, d, in);
+                if ((int)threadIdx.x < items) *ap = append_load(a, kv, d.b, d.kvh, ctx, nrows, j0, threadIdx.x);
+            } else {
+                PieceIO<DT>::start(a, kv, d, in);
+                append_item_rows(a, kv, d.b, d.kvh, j0, j1);
+            }
+            return;
+        }
+    }
+    PieceIO<DT>::start(a, kv, d, in);
+}
+
 // One piece of work: tokens [t0, t_end) of sequence b against kv head kvh. The result
 // goes to the output (part < 0 && rec < 0), to partition slot `part` of the fixed
 // partition grid, or to stream-K record `rec`. Must be reached by the whole workgroup.
@@ -325,7 +368,7 @@ struct PieceIO {
 // `in` holds the piece's first chunk, already issued (PieceIO::start).
 template <gg_dtype_t DT, int NT>
 __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, const PieceDesc pd,
-                                           PieceIn<DT>& in) {
+                                           PieceIn<DT>& in, const AppendItem* ap) {
     const int b = pd.b, kvh = pd.kvh, t0 = pd.t0, t_end = pd.t_end, part = pd.part, rec = pd.rec;
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
@@ -444,6 +487,8 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             s_q[rt][mm][lane] = qvalid[rt] ? op[rt] : zero4();
             if constexpr (kIsBf16) s_qlo[rt][mm][lane] = qvalid[rt] ? opl[rt] : zero4();
         }
+        if constexpr (DT != GG_DTYPE_INT8)
+            if (ap) append_store(a, kv, *ap);  // draft rows loaded by start_piece
         __syncthreads();
     }
 
@@ -718,8 +763,9 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(Attn
     if (part >= nparts) return;
     const PieceDesc d{b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1};
     PieceIn<DT> in;
-    PieceIO<DT>::start(a, kv, d, in);
-    attn_piece<DT, NT>(a, kv, d, in);
+    AppendItem ap;
+    start_piece<DT>(a, kv, d, in, &ap);
+    attn_piece<DT, NT>(a, kv, d, in, &ap);
 }
 
 // Chunks of work of sequence b (0 when it has nothing to compute).
@@ -817,8 +863,8 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
     PieceDesc d;
     while (next_piece(d)) {
         PieceIn<DT> in;
-        PieceIO<DT>::start(a, kv, d, in);
-        attn_piece<DT, NT>(a, kv, d, in);
+        start_piece<DT>(a, kv, d, in, nullptr);
+        attn_piece<DT, NT>(a, kv, d, in, nullptr);
     }
 }
 
@@ -919,8 +965,9 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     const int kvh = e.y & 0xffff, np = e.y >> 16;
     const PieceDesc d{b, kvh, e.z, e.w, -1, np > 1 ? p : -1};
     PieceIn<DT> in;
-    PieceIO<DT>::start(a, kv, d, in);
-    attn_piece<DT, NT>(a, kv, d, in);
+    AppendItem ap;
+    start_piece<DT>(a, kv, d, in, &ap);
+    attn_piece<DT, NT>(a, kv, d, in, &ap);
 #ifdef GG_TRACE
     if (threadIdx.x == 0) {
         g_trace[4 * p + 0] = tr_t0;

@@ -89,7 +89,8 @@ struct AttnArgs {
     int sk_min_chunks;    // least chunks a stream-K workgroup takes
     // Draft-KV rows appended by the same call (gg_verify_append_attention_planned): row
     // b*rows + j (j < the sequence's row count) is key position ctx - row_count + j, its
-    // slot taken from the block table; a launch of their own precedes the attention.
+    // slot taken from the block table. The MFMA kernels append each piece's rows before
+    // reading them; the generic path runs a launch of its own first.
     const void* k_new;
     const void* v_new;
     gg_dtype_t new_dtype;

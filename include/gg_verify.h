@@ -217,9 +217,10 @@ gg_status_t gg_verify_attention_planned(gg_kv_t kv, int layer, const void* q, gg
  *                  conversions, before the attention reads it. Rows past the row count
  *                  are ignored.
  * Then as gg_verify_attention_planned. The result (pool contents and out) equals
- * gg_kv_append with those slots followed by gg_verify_attention_planned (the append is
- * a launch of its own, one workgroup per (sequence, kv head), on the same stream; no
- * slot mapping needs to be built). PER_BLOCK INT8 pools are rejected (GG_ERR_INVALID):
+ * gg_kv_append with those slots followed by gg_verify_attention_planned. No slot mapping
+ * needs to be built, and on the MFMA path there is no extra launch: each attention
+ * workgroup writes the rows of its own key range before it reads them (other shapes run
+ * the append as a launch of its own first). PER_BLOCK INT8 pools are rejected (GG_ERR_INVALID):
  * their scale update needs gg_kv_append. */
 gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, const void* k_new, const void* v_new,
                                                gg_dtype_t new_dtype, const void* q, gg_dtype_t q_dtype,
