@@ -171,11 +171,17 @@ __device__ __forceinline__ AppendItem append_load(const AttnArgs& a, const KVVie
     }
     return it;
 }
-__device__ __forceinline__ void append_store(const AttnArgs& a, const KVView& kv, const AppendItem& it) {
-    if (!it.live) return;
-    const int bs = kv.bs;
-    uint8_t* kc = const_cast<uint8_t*>(kv.kc);
-    uint8_t* vc = const_cast<uint8_t*>(kv.vc);
+// A work item in the pool's format, ready to store: K as one run of 8 elements, V as 8
+// columns (element e at column e). FP8 pools use the low 8 bytes of k[0] and v[0], 16-bit
+// pools k[0] and v[0], f32 pools both words.
+struct AppendBytes {
+    uint4 k[2], v[2];
+    size_t ki, vi;  // destination element indices; ki == ~0: nothing to store
+};
+__device__ __forceinline__ AppendBytes append_encode(const AttnArgs& a, const KVView& kv, const AppendItem& it) {
+    AppendBytes o;
+    o.ki = it.live ? it.ki : ~(size_t)0;
+    o.vi = it.vi;
     float kx[8], vx[8];
     if (dtype_bytes(a.new_dtype) == 4) {
         const uint32_t ku[8] = {it.k[0].x, it.k[0].y, it.k[0].z, it.k[0].w, it.k[1].x, it.k[1].y, it.k[1].z, it.k[1].w};
@@ -197,37 +203,63 @@ __device__ __forceinline__ void append_store(const AttnArgs& a, const KVView& kv
             vx[e] = bf ? bf16_bits_to_f32(vh) : f16_bits_to_f32(vh);
         }
     }
+    o.k[1] = o.v[1] = make_uint4(0, 0, 0, 0);
     if (kv.dt == GG_DTYPE_FP8_E4M3) {
-        uint32_t w[2];
+        uint32_t w[2], u[2];
 #pragma unroll
-        for (int e = 0; e < 8; e += 4)
+        for (int e = 0; e < 8; e += 4) {
             w[e >> 2] = f32x2_to_fp8e4m3_sat(kx[e] * it.kinv, kx[e + 1] * it.kinv) |
                         (f32x2_to_fp8e4m3_sat(kx[e + 2] * it.kinv, kx[e + 3] * it.kinv) << 16);
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            const uint32_t vw = f32x2_to_fp8e4m3_sat(vx[e] * it.vinv, vx[e + 1] * it.vinv);
-            vc[it.vi + (size_t)e * bs] = (uint8_t)vw;
-            vc[it.vi + (size_t)(e + 1) * bs] = (uint8_t)(vw >> 8);
+            u[e >> 2] = f32x2_to_fp8e4m3_sat(vx[e] * it.vinv, vx[e + 1] * it.vinv) |
+                        (f32x2_to_fp8e4m3_sat(vx[e + 2] * it.vinv, vx[e + 3] * it.vinv) << 16);
         }
-        *(uint2*)(kc + it.ki) = make_uint2(w[0], w[1]);
+        o.k[0] = make_uint4(w[0], w[1], 0, 0);
+        o.v[0] = make_uint4(u[0], u[1], 0, 0);
     } else if (kv.dt == GG_DTYPE_F32) {
-        *(float4*)((float*)kc + it.ki) = make_float4(kx[0], kx[1], kx[2], kx[3]);
-        *(float4*)((float*)kc + it.ki + 4) = make_float4(kx[4], kx[5], kx[6], kx[7]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ((float*)vc)[it.vi + (size_t)e * bs] = vx[e];
+        o.k[0] = make_uint4(__float_as_uint(kx[0]), __float_as_uint(kx[1]), __float_as_uint(kx[2]), __float_as_uint(kx[3]));
+        o.k[1] = make_uint4(__float_as_uint(kx[4]), __float_as_uint(kx[5]), __float_as_uint(kx[6]), __float_as_uint(kx[7]));
+        o.v[0] = make_uint4(__float_as_uint(vx[0]), __float_as_uint(vx[1]), __float_as_uint(vx[2]), __float_as_uint(vx[3]));
+        o.v[1] = make_uint4(__float_as_uint(vx[4]), __float_as_uint(vx[5]), __float_as_uint(vx[6]), __float_as_uint(vx[7]));
     } else {
-        // 16-bit pools: the K run as one 16-byte store, V column by column.
-        uint32_t w[4];
+        uint32_t w[4], u[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            const uint16_t lo = kv.dt == GG_DTYPE_BF16 ? f32_to_bf16_bits(kx[e]) : f32_to_f16_bits(kx[e]);
-            const uint16_t hi = kv.dt == GG_DTYPE_BF16 ? f32_to_bf16_bits(kx[e + 1]) : f32_to_f16_bits(kx[e + 1]);
-            w[e >> 1] = (uint32_t)lo | ((uint32_t)hi << 16);
+            const bool bf = kv.dt == GG_DTYPE_BF16;
+            w[e >> 1] = (uint32_t)(bf ? f32_to_bf16_bits(kx[e]) : f32_to_f16_bits(kx[e])) |
+                        ((uint32_t)(bf ? f32_to_bf16_bits(kx[e + 1]) : f32_to_f16_bits(kx[e + 1])) << 16);
+            u[e >> 1] = (uint32_t)(bf ? f32_to_bf16_bits(vx[e]) : f32_to_f16_bits(vx[e])) |
+                        ((uint32_t)(bf ? f32_to_bf16_bits(vx[e + 1]) : f32_to_f16_bits(vx[e + 1])) << 16);
         }
-        *(uint4*)((uint16_t*)kc + it.ki) = make_uint4(w[0], w[1], w[2], w[3]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) store_from_f32(vc, kv.dt, it.vi + (size_t)e * bs, vx[e]);
+        o.k[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        o.v[0] = make_uint4(u[0], u[1], u[2], u[3]);
     }
+    return o;
+}
+__device__ __forceinline__ void append_write(const KVView& kv, const AppendBytes& o) {
+    if (o.ki == ~(size_t)0) return;
+    const int bs = kv.bs;
+    uint8_t* kc = const_cast<uint8_t*>(kv.kc);
+    uint8_t* vc = const_cast<uint8_t*>(kv.vc);
+    if (kv.dt == GG_DTYPE_FP8_E4M3) {
+        *(uint2*)(kc + o.ki) = make_uint2(o.k[0].x, o.k[0].y);
+        const uint32_t u[2] = {o.v[0].x, o.v[0].y};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vc[o.vi + (size_t)e * bs] = (uint8_t)(u[e >> 2] >> (8 * (e & 3)));
+    } else if (kv.dt == GG_DTYPE_F32) {
+        *(uint4*)((float*)kc + o.ki) = o.k[0];
+        *(uint4*)((float*)kc + o.ki + 4) = o.k[1];
+        const uint32_t u[8] = {o.v[0].x, o.v[0].y, o.v[0].z, o.v[0].w, o.v[1].x, o.v[1].y, o.v[1].z, o.v[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ((uint32_t*)vc)[o.vi + (size_t)e * bs] = u[e];
+    } else {
+        *(uint4*)((uint16_t*)kc + o.ki) = o.k[0];
+        const uint32_t u[4] = {o.v[0].x, o.v[0].y, o.v[0].z, o.v[0].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ((uint16_t*)vc)[o.vi + (size_t)e * bs] = (uint16_t)(u[e >> 1] >> (16 * (e & 1)));
+    }
+}
+__device__ __forceinline__ void append_store(const AttnArgs& a, const KVView& kv, const AppendItem& it) {
+    if (it.live) append_write(kv, append_encode(a, kv, it));
 }
 // Rows [j0, j1) of item (b, kvh) (clamped to the sequence's rows), by a whole workgroup,
 // before anything reads them.

@@ -318,25 +318,36 @@ struct PieceIO {
     }
 };
 
-// Start piece d (PieceIO::start) and, when the call carries draft rows (a.k_new:
-// gg_verify_append_attention_planned on the MFMA path), append the rows whose key
-// positions lie in the piece. A key position belongs to exactly one piece, and only that
-// piece reads it, so no other workgroup waits for these stores; chunks are multiples of 16
-// tokens, so a block's tokens (its K rows and its V columns) are all read by one chunk.
-// The piece's own reads of those positions must follow a workgroup barrier (within a
-// workgroup a barrier orders global stores before loads: same CU, write-through L1):
-//   - rows inside the first chunks that `start` issues: appended, barrier, then `start`;
-//   - otherwise (the usual case: the rows are the item's last positions) the rows' loads
-//     are issued here, after `start`, into `ap` (one work item per thread), and attn_piece
-//     stores them before its Q-staging barrier, which precedes every later chunk's loads,
-//     so their latency overlaps the first chunk's and the Q loads'. More rows than
-//     threads, or no `ap` (the stream-K loop over pieces, whose registers are full), are
-//     appended here at once instead.
+// Draft rows a piece appends itself (gg_verify_append_attention_planned on the MFMA path):
+// rows [j0, j1) of its sequence (none when j0 == j1), and this thread's work item of them.
+struct DeferredRows {
+    AppendItem it;
+    int j0, j1;
+};
+// Most work items (rows x 16 dim groups) a piece stages in LDS: 8 draft rows.
+constexpr int kAppMax = 128;
+
+// Start piece d (PieceIO::start) and, when the call carries draft rows (a.k_new), take
+// care of the rows whose key positions lie in the piece. A key position belongs to exactly
+// one piece, and only that piece reads it, so no other workgroup waits for these stores;
+// chunks are multiples of 16 tokens, so a block's tokens (its K rows and its V columns)
+// are all read by one chunk, and so by one wave.
+//   - Rows inside the first chunks that `start` issues (short pieces), more rows than
+//     kAppMax, or no `ap` (the stream-K loop over pieces, whose registers are full):
+//     appended here by the whole workgroup, then a barrier orders the stores before the
+//     piece's loads (within a workgroup a barrier orders global stores before loads:
+//     same CU, write-through L1).
+//   - Otherwise (the usual case: the rows are the item's last positions) their loads are
+//     issued here, after `start`, one work item per thread; attn_piece converts them into
+//     LDS before its Q-staging barrier, and the wave that loads the chunk holding them
+//     stores them right before that chunk's loads (one wave: program order). Nothing
+//     then waits for those stores until the chunk itself is needed, while a store before
+//     the first chunk would hold up every wave's first wait on the outstanding stores.
 template <gg_dtype_t DT>
 __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
-                                            PieceIn<DT>& in, AppendItem* ap) {
+                                            PieceIn<DT>& in, DeferredRows* ap) {
     constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
-    if (ap) ap->live = false;
+    if (ap) ap->j0 = ap->j1 = 0;
     // (PER_BLOCK INT8 pools never carry rows here: their scale update needs gg_kv_append.)
     if (DT != GG_DTYPE_INT8 && a.k_new) {
         const int ctx = seq_keys(a, d.b, kBS), nrows = seq_rows(a, d.b);
@@ -344,16 +355,16 @@ __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv,
         const int j0 = max(0, d.t0 - first), j1 = min(nrows, d.t_end - first);
         if (nrows > 0 && nrows <= ctx && j0 < j1) {
             const int items = (j1 - j0) * (kD / 8);
-            if (first + j0 < d.t0 + kWaves * kTok) {
+            if (ap && items <= kAppMax && first + j0 >= d.t0 + kWaves * kTok) {
+                PieceIO<DT>::start(a, kv, d, in);
+                ap->j0 = j0;
+                ap->j1 = j1;
+                ap->it.live = false;
+                if ((int)threadIdx.x < items) ap->it = append_load(a, kv, d.b, d.kvh, ctx, nrows, j0, threadIdx.x);
+            } else {
                 append_item_rows(a, kv, d.b, d.kvh, j0, j1);
                 __syncthreads();
                 PieceIO<DT>::start(a, kv, d, in);
-            } else if (ap && items <= (int)blockDim.x) {
-                PieceIO<DT>::start(a, kv, d, in);
-                if ((int)threadIdx.x < items) *ap = append_load(a, kv, d.b, d.kvh, ctx, nrows, j0, threadIdx.x);
-            } else {
-                PieceIO<DT>::start(a, kv, d, in);
-                append_item_rows(a, kv, d.b, d.kvh, j0, j1);
             }
             return;
         }
@@ -368,7 +379,7 @@ __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv,
 // `in` holds the piece's first chunk, already issued (PieceIO::start).
 template <gg_dtype_t DT, int NT>
 __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, const PieceDesc pd,
-                                           PieceIn<DT>& in, const AppendItem* ap) {
+                                           PieceIn<DT>& in, const DeferredRows* ap) {
     const int b = pd.b, kvh = pd.kvh, t0 = pd.t0, t_end = pd.t_end, part = pd.part, rec = pd.rec;
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
@@ -401,6 +412,21 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     if constexpr (DT == GG_DTYPE_FP8_E4M3) {
         sscale *= kv.k_head_scale[kvh];
         vfold = kv.v_head_scale[kvh];
+    }
+
+    // Draft rows loaded by start_piece: converted into LDS here (the Q-staging barrier
+    // below publishes them), stored by the wave that loads their chunk (see the loop).
+    __shared__ AppendBytes s_app[kAppMax];
+    int app_lo = 0, app_hi = 0;  // their key positions [app_lo, app_hi)
+    if constexpr (DT != GG_DTYPE_INT8) {
+        if (ap) {
+            const int j0 = __builtin_amdgcn_readfirstlane(ap->j0), j1 = __builtin_amdgcn_readfirstlane(ap->j1);
+            if (j0 < j1) {
+                if ((int)threadIdx.x < (j1 - j0) * (kD / 8)) s_app[threadIdx.x] = append_encode(a, kv, ap->it);
+                app_lo = first_masked + j0;
+                app_hi = first_masked + j1;
+            }
+        }
     }
 
     // ---- Q operands: B[k = 8*g4+i][n = c16] <- Q[row rt*16+c16][32*g4 + 8*mm + i] ----
@@ -487,8 +513,6 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             s_q[rt][mm][lane] = qvalid[rt] ? op[rt] : zero4();
             if constexpr (kIsBf16) s_qlo[rt][mm][lane] = qvalid[rt] ? opl[rt] : zero4();
         }
-        if constexpr (DT != GG_DTYPE_INT8)
-            if (ap) append_store(a, kv, *ap);  // draft rows loaded by start_piece
         __syncthreads();
     }
 
@@ -564,6 +588,16 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 #pragma unroll
                         for (int rt = 0; rt < NT; ++rt) sacc[rt][s] = mfma(cur.k[s][mm], qop[rt], sacc[rt][s], true);
                 }
+            }
+        }
+        // Draft rows of the next chunk of this wave, stored before its loads (same wave:
+        // the loads see them).
+        if constexpr (DT != GG_DTYPE_INT8) {
+            const int nt0 = t0 + (ch + kWaves) * kTok;
+            if (app_lo < app_hi && nt0 < app_hi && nt0 + kTok > app_lo) {
+                const int i0 = (max(app_lo, nt0) - app_lo) * (kD / 8);
+                const int i1 = (min(app_hi, nt0 + kTok) - app_lo) * (kD / 8);
+                for (int i = i0 + lane; i < i1; i += 64) append_write(kv, s_app[i]);
             }
         }
         // Next chunk's K rows stream in while this chunk finishes.
@@ -763,7 +797,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(Attn
     if (part >= nparts) return;
     const PieceDesc d{b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1};
     PieceIn<DT> in;
-    AppendItem ap;
+    DeferredRows ap;
     start_piece<DT>(a, kv, d, in, &ap);
     attn_piece<DT, NT>(a, kv, d, in, &ap);
 }
@@ -965,7 +999,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     const int kvh = e.y & 0xffff, np = e.y >> 16;
     const PieceDesc d{b, kvh, e.z, e.w, -1, np > 1 ? p : -1};
     PieceIn<DT> in;
-    AppendItem ap;
+    DeferredRows ap;
     start_piece<DT>(a, kv, d, in, &ap);
     attn_piece<DT, NT>(a, kv, d, in, &ap);
 #ifdef GG_TRACE

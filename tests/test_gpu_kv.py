@@ -694,6 +694,12 @@ def _derived_slots(lay, rows, bs, row_counts=None):
     (5, "bf16", 64, ("uniform", 300, 2100), True),    # LPT, ragged row counts
     (2, "f16", 6, ("uniform", 512, 3000), False),     # stream-K: append launch, then attention
     (1, "f32", 4, ("list", 64, 128, 192, 256), True),  # generic path
+    # Draft rows straddling chunk boundaries (64-token chunks for FP8, 32 for bf16), rows in
+    # a piece's first chunks (short contexts), and long items that LPT splits.
+    (3, "fp8", 64, ("list", *[64 * (1 + (i * 37) % 128) + (59, 60, 61, 62, 63, 0, 1, 30)[i % 8] for i in range(64)]),
+     False),
+    (5, "bf16", 64, ("list", *[32 * (1 + (i * 13) % 64) + (27, 28, 29, 30, 31, 0, 1, 16)[i % 8] for i in range(64)]),
+     True),
 ])
 def test_append_attention_fused_equals_separate(gpu, cid, dt, B, ctx, rc):
     """gg_verify_append_attention_planned == gg_kv_append (slots from the block tables)
