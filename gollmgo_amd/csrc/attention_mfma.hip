@@ -912,14 +912,27 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
 // last piece to finish needs device-scope fences, which write back / invalidate a whole
 // L2 here and cost more than the separate launch.)
 //
-// Plan layout (ints, in the workspace after the records), R = record bound:
+// Plan layout (ints, in the workspace after the records), R = record bound, B = sequences:
 //   [0]                       number of pieces
+//   [1]                       number of split sequences (pieces per kv head > 1)
 //   [16 + 4p ..]              piece p: (sequence, kv head | pieces per kv head << 16,
 //                             first token, end token); sequence -1 past the last piece
 //   [16 + 4R + 2b ..]         sequence b: (first piece, pieces per kv head)
+//   [16 + 4R + 2B' + 4i ..]   i-th split sequence (2B' = 2B rounded up to 4), in sequence order: (sequence, first
+//                             piece, pieces per kv head, 0)
 // Pieces of sequence b are first + j*Hkv + kvh.
 __device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
 __device__ __forceinline__ int* lpt_seq(int* plan, int recs) { return plan + 16 + 4 * recs; }
+__device__ __forceinline__ int4* lpt_split(int* plan, int recs, int B) {
+    return (int4*)(plan + 16 + 4 * recs + ((2 * B + 3) & ~3));  // 16-byte aligned
+}
+// Most sequences an LPT plan can split: a split sequence has more than T chunks per kv
+// head, T >= C * kLptPieceNum / (slots * kLptPieceDen) for C chunks in all, so fewer than
+// slots * kLptPieceDen / (kLptPieceNum * Hkv) of them fit in C. Sizes the merge grid.
+__host__ __device__ constexpr int lpt_max_split(int slots, int num_seqs, int num_kv_heads) {
+    const int m = slots * kLptPieceDen / (kLptPieceNum * num_kv_heads) + 1;
+    return m < num_seqs ? m : num_seqs;
+}
 
 // Sum over a 1024-thread workgroup (wave sums, then the 16 wave totals).
 __device__ __forceinline__ long long block_sum_1024(long long v, long long* s_w) {
@@ -955,12 +968,17 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
         s_cnt[b] = b < B ? cnt : 0;
     }
     const long long total = block_sum_1024(cnt, s_w);  // (its barriers also publish s_key / s_cnt)
+    const long long nsplit = block_sum_1024(np > 1 ? 1 : 0, s_w);
     int* plan = a.plan;
-    if (b == 0) plan[0] = (int)total;
+    if (b == 0) {
+        plan[0] = (int)total;
+        plan[1] = (int)nsplit;
+    }
     if (b >= B) return;
     // Pieces ahead of this sequence's: larger pieces, then equal pieces of lower sequences.
     // Eight sequences per step from 16-byte LDS reads (independent adds, no serial chain).
-    int pos = 0;
+    // Also the split sequences before this one (cnt > Hkv: more than one piece per head).
+    int pos = 0, split_rank = 0;
     for (int t0 = 0; t0 < B; t0 += 8) {
         const int4 k0 = *(const int4*)&s_key[t0], k1 = *(const int4*)&s_key[t0 + 4];
         const int4 n0 = *(const int4*)&s_cnt[t0], n1 = *(const int4*)&s_cnt[t0 + 4];
@@ -970,8 +988,10 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
         for (int e = 0; e < 8; ++e) {
             const int t = t0 + e;
             pos += (kk[e] > key || (kk[e] == key && t < b)) ? nn[e] : 0;
+            split_rank += (t < b && nn[e] > Hkv) ? 1 : 0;
         }
     }
+    if (np > 1) lpt_split(plan, recs, B)[split_rank] = make_int4(b, pos, np, 0);
     int* seq = lpt_seq(plan, recs) + 2 * b;
     seq[0] = pos;
     seq[1] = np;
@@ -1011,25 +1031,25 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
 #endif
 }
 
-// Merge the pieces of split items; workgroup (item, y) takes rows 4y .. 4y+3.
+// Merge the pieces of split items: workgroup (i, y) takes kv head i % Hkv of the
+// (i / Hkv)-th split sequence (the grid covers lpt_max_split sequences; the rest exit),
+// rows 4y .. 4y+3 (32 threads x 4 dims per row), so every record is requested at once.
 __global__ void __launch_bounds__(128) attn_lpt_combine_kernel(AttnArgs a, int Hkv, int tok, int recs) {
-    const int item = blockIdx.x;
-    const int b = item / Hkv, kvh = item % Hkv;
-    const int* seq = lpt_seq(a.plan, recs) + 2 * b;
-    const int first = seq[0], np = seq[1];  // (np == 0: no keys, no pieces)
-    if (np <= 1) return;
+    const int si = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv;
+    // (The count and the entry are requested together; entries past the count are stale.)
+    const int nsplit = a.plan[1];
+    const int4 e = lpt_split(a.plan, recs, a.num_seqs)[si];
+    if (si >= nsplit) return;
+    const int b = e.x, first = e.y, np = e.z;
     const int G = a.num_q_heads / Hkv;
     const int r = blockIdx.y * 4 + (threadIdx.x >> 5);
     const int d4 = threadIdx.x & 31;
     const int RW = G * a.rows;
-    if (r >= RW) return;
-    // Rows past row_counts[b] hold no records: their results are not stored below. The
-    // first two pieces' records are requested together (every split item has two or more).
+    if (r >= G * seq_rows(a, b)) return;  // rows past row_counts[b] hold no records
+    // The first two pieces' records are requested together (a split item has two or more).
     const size_t q0 = (size_t)(first + kvh) * RW + r, q1 = q0 + (size_t)Hkv * RW;
     const float2 ml0 = *(const float2*)(a.ws_ml + q0 * 2), ml1 = *(const float2*)(a.ws_ml + q1 * 2);
     const float4 v0 = ((const float4*)(a.ws_acc + q0 * kD))[d4], v1 = ((const float4*)(a.ws_acc + q1 * kD))[d4];
-    const int nrows = seq_rows(a, b);
-    if (r >= G * nrows) return;
     float M = -1e30f, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j = 0; j < np; ++j) {
@@ -1173,7 +1193,8 @@ gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s)
     const dim3 cgrid(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4);
     if (a.sched == ATTN_SCHED_STREAMK) attn_streamk_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, a.sk_grid);
     if (a.sched == ATTN_SCHED_LPT)
-        attn_lpt_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, lpt_records(a.sk_grid, a.num_seqs, kv.Hkv));
+        attn_lpt_combine_kernel<<<dim3(lpt_max_split(a.sk_grid, a.num_seqs, kv.Hkv) * kv.Hkv, cgrid.y), 128, 0, s>>>(
+            a, kv.Hkv, tok, lpt_records(a.sk_grid, a.num_seqs, kv.Hkv));
     return GG_OK;
 }
 
@@ -1203,7 +1224,7 @@ size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int nu
     const size_t rw = (size_t)(num_q_heads / kv->num_kv_heads) * rows;
     const size_t n_ml = records * rw * 2;
     const size_t n_acc = records * rw * kD;
-    const size_t plan_ints = 16 + 4 * records + 2 * (size_t)num_seqs;
+    const size_t plan_ints = 16 + 4 * records + 6 * (size_t)num_seqs + 4;
     if (ml_elems) *ml_elems = n_ml;
     if (acc_elems) *acc_elems = n_acc;
     return (((n_ml + 63) / 64) * 64 + n_acc) * sizeof(float) + plan_ints * sizeof(int);
