@@ -258,6 +258,19 @@ __device__ __forceinline__ void append_write(const KVView& kv, const AppendBytes
         for (int e = 0; e < 8; ++e) ((uint16_t*)vc)[o.vi + (size_t)e * bs] = (uint16_t)(u[e >> 1] >> (16 * (e & 1)));
     }
 }
+// The K run of a work item only.
+__device__ __forceinline__ void append_write_k(const KVView& kv, const AppendBytes& o) {
+    if (o.ki == ~(size_t)0) return;
+    uint8_t* kc = const_cast<uint8_t*>(kv.kc);
+    if (kv.dt == GG_DTYPE_FP8_E4M3) {
+        *(uint2*)(kc + o.ki) = make_uint2(o.k[0].x, o.k[0].y);
+    } else if (kv.dt == GG_DTYPE_F32) {
+        *(uint4*)((float*)kc + o.ki) = o.k[0];
+        *(uint4*)((float*)kc + o.ki + 4) = o.k[1];
+    } else {
+        *(uint4*)((uint16_t*)kc + o.ki) = o.k[0];
+    }
+}
 __device__ __forceinline__ void append_store(const AttnArgs& a, const KVView& kv, const AppendItem& it) {
     if (it.live) append_write(kv, append_encode(a, kv, it));
 }

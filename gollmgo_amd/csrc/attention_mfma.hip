@@ -43,6 +43,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef unsigned __int128 u128;
 
 constexpr int kD = 128;
 constexpr int kBS = 16;
@@ -415,14 +416,34 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
     }
 
     // Draft rows loaded by start_piece: converted into LDS here (the Q-staging barrier
-    // below publishes them), stored by the wave that loads their chunk (see the loop).
+    // below publishes them). The chunk that holds them reads stale pool bytes at their
+    // positions; the wave that owns that chunk patches its registers from LDS (see the
+    // loop), and the rows go to the pool after the loop, where nothing waits for the
+    // stores (on gfx950 stores count in vmcnt, so a store ahead of a chunk's loads would
+    // hold up the wait for that chunk). s_app keeps each work item (row, 8 dims) in the
+    // pool's format; s_vt the same V values by dim: element r of s_vt[d] is row r's V[d].
     __shared__ AppendBytes s_app[kAppMax];
+    __shared__ uint4 s_vt[kD];
     int app_lo = 0, app_hi = 0;  // their key positions [app_lo, app_hi)
     if constexpr (DT != GG_DTYPE_INT8) {
         if (ap) {
             const int j0 = __builtin_amdgcn_readfirstlane(ap->j0), j1 = __builtin_amdgcn_readfirstlane(ap->j1);
             if (j0 < j1) {
-                if ((int)threadIdx.x < (j1 - j0) * (kD / 8)) s_app[threadIdx.x] = append_encode(a, kv, ap->it);
+                const int i = threadIdx.x;
+                if (i < (j1 - j0) * (kD / 8)) {
+                    const AppendBytes o = append_encode(a, kv, ap->it);
+                    s_app[i] = o;
+                    const int r = i / (kD / 8), d0 = (i % (kD / 8)) * 8;
+                    if constexpr (kEB == 1) {
+                        const uint32_t u[2] = {o.v[0].x, o.v[0].y};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ((uint8_t*)&s_vt[d0 + e])[r] = (uint8_t)(u[e >> 2] >> (8 * (e & 3)));
+                    } else {
+                        const uint32_t u[4] = {o.v[0].x, o.v[0].y, o.v[0].z, o.v[0].w};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ((uint16_t*)&s_vt[d0 + e])[r] = (uint16_t)(u[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
                 app_lo = first_masked + j0;
                 app_hi = first_masked + j1;
             }
@@ -550,6 +571,30 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         const float kblk_scale = DT == GG_DTYPE_INT8 ? (cur.ksc > 0.f ? cur.ksc : 1.f) : 1.f;
         const float vblk_scale = DT == GG_DTYPE_INT8 ? cur.vsc : 1.f;
 
+        // Draft rows in this chunk: their K rows replace the stale pool bytes just read.
+        const bool app_here = DT != GG_DTYPE_INT8 && app_lo < app_hi && tc < app_hi && tc + kTok > app_lo;
+        if constexpr (DT != GG_DTYPE_INT8) {
+            if (app_here) {
+                const int kq = c16 >> 2;
+#pragma unroll
+                for (int s = 0; s < kNS; ++s) {
+                    const int r = tc + 16 * Geom::bq(kq) + Geom::ob(kq) + 4 * s + (c16 & 3) - app_lo;
+                    if (r >= 0 && r < app_hi - app_lo) {
+#pragma unroll
+                        for (int v = 0; v < Geom::kKVec; ++v) {
+                            if constexpr (kEB == 1) {
+                                const int g = 4 * g4 + 2 * v;
+                                const uint4 A = s_app[r * (kD / 8) + g].k[0], B = s_app[r * (kD / 8) + g + 1].k[0];
+                                cur.k[s][v] = make_uint4(A.x, A.y, B.x, B.y);
+                            } else {
+                                cur.k[s][v] = s_app[r * (kD / 8) + 4 * g4 + v].k[0];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+
         // ---- S^T = K . Q^T for kTok tokens x all row tiles; each K tile decoded once ----
         // The Q index is opaque to the optimiser so that the LDS reads stay in the loop
         // instead of being hoisted into registers for the whole piece.
@@ -588,16 +633,6 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 #pragma unroll
                         for (int rt = 0; rt < NT; ++rt) sacc[rt][s] = mfma(cur.k[s][mm], qop[rt], sacc[rt][s], true);
                 }
-            }
-        }
-        // Draft rows of the next chunk of this wave, stored before its loads (same wave:
-        // the loads see them).
-        if constexpr (DT != GG_DTYPE_INT8) {
-            const int nt0 = t0 + (ch + kWaves) * kTok;
-            if (app_lo < app_hi && nt0 < app_hi && nt0 + kTok > app_lo) {
-                const int i0 = (max(app_lo, nt0) - app_lo) * (kD / 8);
-                const int i1 = (min(app_hi, nt0 + kTok) - app_lo) * (kD / 8);
-                for (int i = i0 + lane; i < i1; i += 64) append_write(kv, s_app[i]);
             }
         }
         // Next chunk's K rows stream in while this chunk finishes.
@@ -691,6 +726,45 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         const typename IO::RawBlocks raw_after = IO::fetch_blocks(a, b, t0, ch + 2 * kWaves);
 
         // ---- O += P . V; each V dim tile decoded once for all row tiles ----
+        // Draft rows in this chunk: their V columns replace the stale pool bytes. The lane's
+        // run is offsets ob(g4) .. of its block, rows base + offset of the staged rows.
+        // Lanes whose block holds draft rows then write their runs back to the pool: the
+        // runs of a block cover its whole dim-major V tile, so these are full-line stores
+        // (the draft rows alone would be 1- or 2-byte pieces of every line, each a partial
+        // write to memory); the other offsets are written back with the bytes just read.
+        if constexpr (DT != GG_DTYPE_INT8) {
+            if (app_here) {
+                const int blk0 = tc + 16 * Geom::bq(g4) - app_lo;  // staged row of the block's offset 0
+                const int base = blk0 + Geom::ob(g4);
+                const int nr = app_hi - app_lo;
+                constexpr int kE = 8 * kEB;  // bits per element
+                constexpr int kRun = 16 / kEB;  // elements per 16-byte run
+                if (base < nr && base + kRun > 0) {
+                    // Element o of the run takes staged row base + o.
+                    const int lo_bits = (nr - (base > 0 ? base : 0)) * kE;
+                    u128 mask = lo_bits >= 128 ? ~(u128)0 : (((u128)1 << lo_bits) - 1);
+                    if (base < 0) mask <<= (-base) * kE;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) {
+                        const uint4 sv = s_vt[dt * 16 + c16];
+                        u128 nv = ((u128)sv.w << 96) | ((u128)sv.z << 64) | ((u128)sv.y << 32) | sv.x;
+                        if (kEB == 1) nv &= ((u128)1 << 64) - 1;  // 8 staged rows of one byte
+                        nv = base < 0 ? nv << ((-base) * kE) : nv >> (base * kE);
+                        const uint4 c = cur.v[dt];
+                        u128 cv = ((u128)c.w << 96) | ((u128)c.z << 64) | ((u128)c.y << 32) | c.x;
+                        cv = (cv & ~mask) | (nv & mask);
+                        cur.v[dt] = make_uint4((uint32_t)cv, (uint32_t)(cv >> 32), (uint32_t)(cv >> 64),
+                                               (uint32_t)(cv >> 96));
+                    }
+                }
+                if (blk_v >= 0 && blk0 < nr && blk0 + kBS > 0) {
+                    uint8_t* vbase = const_cast<uint8_t*>(kv.vc) +
+                                     (((size_t)blk_v * kv.Hkv + kvh) * (size_t)(2 * kBS * kD) + Geom::ob(g4)) * kEB;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) *(uint4*)(vbase + (size_t)(dt * 16 + c16) * kBS * kEB) = cur.v[dt];
+                }
+            }
+        }
         if (nvalid_v < kBS) {
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
@@ -720,6 +794,13 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         IO::load_v(kv, bl_next, kvh, cur);
         bl_cur = bl_next;
         bl_next = IO::lane_blocks(kv, raw_after, t_end);
+    }
+
+    // The draft rows' K to the pool (their V went back with the patched runs), now that no
+    // load of this piece waits behind the stores.
+    if constexpr (DT != GG_DTYPE_INT8) {
+        if (app_lo < app_hi)
+            for (int i = threadIdx.x; i < (app_hi - app_lo) * (kD / 8); i += blockDim.x) append_write_k(kv, s_app[i]);
     }
 
     // ---- merge the four waves' states through LDS ----
