@@ -68,6 +68,12 @@ func copyH2D(dst, src unsafe.Pointer, n uintptr, stream unsafe.Pointer) error {
 		C.hipStream_t(stream)))
 }
 
+// copyH2DSync copies from Go memory: synchronous, so C holds the Go pointer only during
+// the call, as cgo requires.
+func copyH2DSync(dst, src unsafe.Pointer, n uintptr) error {
+	return hipErr("hipMemcpy", C.hipMemcpy(dst, src, C.size_t(n), C.hipMemcpyHostToDevice))
+}
+
 func copyD2H(dst, src unsafe.Pointer, n uintptr, stream unsafe.Pointer) error {
 	return hipErr("hipMemcpyAsync", C.hipMemcpyAsync(dst, src, C.size_t(n), C.hipMemcpyDeviceToHost,
 		C.hipStream_t(stream)))

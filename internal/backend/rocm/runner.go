@@ -320,8 +320,8 @@ func (r *Runner) swapIO(blockIDs []int32) (ids, staging unsafe.Pointer, n uintpt
 		deviceFree(ids)
 		return
 	}
-	if err = copyH2D(ids, unsafe.Pointer(&blockIDs[0]), uintptr(4*len(blockIDs)), r.stream); err == nil {
-		err = syncStream(r.stream) // blockIDs is Go memory: finish before returning
+	if err = syncStream(r.stream); err == nil { // earlier work on the stream first
+		err = copyH2DSync(ids, unsafe.Pointer(&blockIDs[0]), uintptr(4*len(blockIDs)))
 	}
 	if err != nil {
 		deviceFree(ids)
