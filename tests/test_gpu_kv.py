@@ -705,9 +705,30 @@ def test_append_attention_fused_equals_separate(gpu, cid, dt, B, ctx, rc):
     """gg_verify_append_attention_planned == gg_kv_append (slots from the block tables)
     followed by gg_verify_attention_planned: pool bytes and outputs bit for bit."""
     say(f"fused append+attention config {cid} dt={dt} B={B} row_counts={rc}")
+    _fused_vs_separate(cid, dt, B, ctx, rc)
+
+
+@pytest.mark.parametrize("dt", ["fp8", "bf16"])
+def test_append_attention_fused_with_missing_blocks(gpu, dt):
+    """Block-table entries outside the pool (or negative) where draft rows land: both paths
+    skip those rows and mask those keys, so pools and outputs still agree bit for bit."""
+    say(f"fused append+attention with missing blocks dt={dt}")
+    _fused_vs_separate(3 if dt == "fp8" else 5, dt, 64, ("uniform", 300, 3000), False, corrupt=True)
+
+
+def _fused_vs_separate(cid, dt, B, ctx, rc, corrupt=False):
     cfg = scaled(CONFIGS[cid], num_seqs=B, ctx=ctx, layers=1, kv_dtype=dt)
     lay = build_layout(cfg)
     H, D, bs, R, Hq = cfg.num_kv_heads, cfg.head_dim, cfg.block_size, cfg.rows, cfg.num_q_heads
+    if corrupt:
+        # Every fifth sequence: the block holding its last draft row leaves the pool (odd
+        # sequences: past its end, even ones: negative). The context fill below still uses
+        # the layout's own slots.
+        tables = lay.block_tables.copy()
+        for b_ in range(0, B, 5):
+            pos = int(lay.keys[b_]) - 1
+            tables[b_, pos // bs] = lay.num_blocks + 3 if b_ % 2 else -2
+        lay = type(lay)(**{**lay.__dict__, "block_tables": tables})
     gen = torch.Generator(device="cuda").manual_seed(cfg.seed + 11)
     fill = torch.from_numpy(lay.fill_slots).cuda()
     kx = torch.randn(len(fill), H, D, device="cuda", dtype=torch.bfloat16, generator=gen)
@@ -719,7 +740,7 @@ def test_append_attention_fused_equals_separate(gpu, cid, dt, B, ctx, rc):
     if rc:
         row_counts = np.random.default_rng(cid).integers(1, R + 1, B).astype(np.int32)
     slots = _derived_slots(lay, R, bs, row_counts)
-    if row_counts is None:
+    if row_counts is None and not corrupt:
         np.testing.assert_array_equal(slots, lay.append_slots)  # the layout's own slots
     keys = torch.from_numpy(lay.keys).cuda()
     bt = torch.from_numpy(lay.block_tables).cuda()
