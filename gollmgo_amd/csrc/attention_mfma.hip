@@ -339,11 +339,12 @@ constexpr int kAppMax = 128;
 //     piece's loads (within a workgroup a barrier orders global stores before loads:
 //     same CU, write-through L1).
 //   - Otherwise (the usual case: the rows are the item's last positions) their loads are
-//     issued here, after `start`, one work item per thread; attn_piece converts them into
-//     LDS before its Q-staging barrier, and the wave that loads the chunk holding them
-//     stores them right before that chunk's loads (one wave: program order). Nothing
-//     then waits for those stores until the chunk itself is needed, while a store before
-//     the first chunk would hold up every wave's first wait on the outstanding stores.
+//     issued here, after `start`, one work item per thread. attn_piece converts them into
+//     LDS before its Q-staging barrier; the wave that reads the chunk holding them patches
+//     its registers from LDS (the pool still holds stale bytes there) and writes that
+//     block's V tile back whole, and the K rows are stored after the loop. No load waits
+//     behind these stores (gfx950 counts stores in vmcnt, so a store issued ahead of a
+//     chunk's loads would hold up the wait for that chunk).
 template <gg_dtype_t DT>
 __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
                                             PieceIn<DT>& in, DeferredRows* ap) {
