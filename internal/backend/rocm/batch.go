@@ -3,6 +3,8 @@
 // gollmgo tree. They are not compiled in this repository (its image has no Go
 // toolchain); gollmgo_amd/batch.py and gollmgo_amd/positions.py are the same functions in
 // Python, and tests/test_runner_batch.py and tests/test_positions.py run them.
+// batch_test.go and positions_test.go hold the Go side of those cases (positions_test.go
+// reads the rows with the engine's own Verify and Sampler).
 //
 // batch.go and positions.go are plain Go (no cgo, no build tag); bridge.go and runner.go
 // need the "rocm" build tag, cgo and the ROCm runtime.
