@@ -20,11 +20,13 @@
 //   top-p only: row_pick (per row, the segment histograms merged exactly into the row's
 //     and its boundary bin), decide_bounds (per sequence, every draft the bounds of the
 //     nucleus mass already decide, and the rows left open or holding the final draw
-//     flagged), seg_gather (flagged rows: each segment's kept sum above the boundary bin
-//     and that bin's elements), row_select (flagged rows: an LDS sort of those elements to
-//     the exact cut). A row whose boundary bin is crowded falls back to the exact
-//     single-block row kernel (three 11/11/10-bit radix levels on the order key and a
-//     9+9-bit index select of a tied cut).
+//     flagged and listed), seg_gather (listed rows: each segment's kept sum above the
+//     boundary bin and that bin's elements), row_select (listed rows: a sort of those
+//     elements to the exact cut). The later kernels are sized for about one listed row
+//     per sequence and loop over the list, so no block is launched for a row that needs
+//     nothing. A row whose boundary bin is crowded falls back to the exact single-block
+//     row passes (three 11/11/10-bit radix levels on the order key and a 9+9-bit index
+//     select of a tied cut).
 //   decide, one wave per sequence: the acceptance walk (accept iff u*q(x)*Zp < W(x)) and
 //     the view of the final row.
 //   seg_residual (dense draft distributions only), one block per (sequence, segment):
@@ -40,7 +42,7 @@
 namespace gg {
 namespace {
 
-constexpr int kThreads = 1024;
+constexpr int kThreads = 512;  // exact row passes: threads per row
 constexpr int kBins = 2048;
 typedef unsigned long long u64;
 typedef gg_u128 u128;
@@ -64,6 +66,7 @@ struct RowPick {
     u128 c_above;    // mass of the bins before the boundary bin
     u128 m_bin;      // mass of the boundary bin
     u128 tp;         // ceil(top_p * Z)
+    float m;         // the row's max finite logit (-inf when none)
     int cbin;        // boundary coarse bin (-1: no finite logit or Z == 0)
     int n_cand;      // elements of that bin gathered so far
 };
@@ -383,14 +386,18 @@ __device__ __forceinline__ int row_bin(float l, int cbm, float inv_t) {
 
 // B: per row, merge the segment histograms; the boundary bin, the mass above it and its
 // own mass. Thread t owns row bins t, t + 256, ...: row bin r gathers f_s * H_s[r - shift_s]
-// over the segments (the last row bin everything from there down), no atomics.
+// over the segments (the last row bin everything from there down), no atomics. A thread's
+// loads for a batch of segments are issued together. Block 0 also clears the counts of
+// the flagged-row list (decide_bounds_kernel) and the crowded-row list (row_select_kernel).
+constexpr int kPickBatch = 8;
 __global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, float inv_t, float top_p,
                                                                const int32_t* __restrict__ n_drafts,
                                                                const float* __restrict__ seg_max,
                                                                const u64* __restrict__ seg_e,
                                                                const u64* __restrict__ seg_hist,
-                                                               RowPick* __restrict__ pick) {
+                                                               RowPick* __restrict__ pick, int* __restrict__ n_flagged) {
     const int row = blockIdx.x;
+    if (row == 0 && threadIdx.x < 2) n_flagged[threadIdx.x] = 0;  // (flagged and crowded counts)
     const int R = K + 1;
     const int b = row / R, j = row % R;
     if (j > live_rows(n_drafts, b, K)) return;
@@ -402,36 +409,58 @@ __global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, 
     const float m = row_max_wave(seg_max, row, nseg);
     const u128 z = row_z_wave(seg_max, seg_e, row, nseg, m, inv_t);
     if (!finite_f(m) || z == 0) {
-        if (threadIdx.x == 0) pick[row] = RowPick{0, 0, 0, -1, 0};
+        if (threadIdx.x == 0) pick[row] = RowPick{0, 0, 0, m, -1, 0};
         return;
     }
     const int cbm = cb_abs(m, inv_t);
-    if (threadIdx.x < nseg) {
-        const float ms = seg_max[(size_t)row * nseg + threadIdx.x];
-        const u64 f = seg_factor(ms, m, inv_t);
+    if (threadIdx.x < 64) {
+        int sh = kRowBins;
+        u64 f = 0;
+        if (threadIdx.x < nseg) {
+            const float ms = seg_max[(size_t)row * nseg + threadIdx.x];
+            f = seg_factor(ms, m, inv_t);
+            if (f) sh = cbm - cb_abs(ms, inv_t);  // (no mass: no bins)
+        }
         s_f[threadIdx.x] = f;
-        s_shift[threadIdx.x] = f ? cbm - cb_abs(ms, inv_t) : kRowBins;  // (no mass: no bins)
+        s_shift[threadIdx.x] = sh;
     }
     __syncthreads();
     const u64* hrow = seg_hist + (size_t)row * nseg * kSegBins;
-    for (int r = threadIdx.x; r < kRowBins; r += kSegThreads) {
-        u128 acc = 0;
-        for (int sg = 0; sg < nseg; ++sg) {
-            const int lo = r - s_shift[sg];
-            if (lo >= kSegBins || lo < 0 && r < kRowBins - 1) continue;
-            const u64* hs = hrow + (size_t)sg * kSegBins;
-            u64 v = 0;
-            if (r < kRowBins - 1) {
-                v = hs[lo];
-                acc += (u128)v * s_f[sg];
-            } else {  // the last row bin: every segment bin from there down
-                u128 t = 0;
-                for (int bn = lo < 0 ? 0 : lo; bn < kSegBins; ++bn) t += hs[bn];
-                acc += t * s_f[sg];
+    constexpr int kPer = kRowBins / kSegThreads;
+    u128 acc[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) acc[k] = 0;
+    for (int sg0 = 0; sg0 < nseg; sg0 += kPickBatch) {
+        u64 v[kPer][kPickBatch];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int r = threadIdx.x + k * kSegThreads;
+#pragma unroll
+            for (int i = 0; i < kPickBatch; ++i) {
+                const int lo = r - s_shift[sg0 + i];  // (s_shift is kRowBins past nseg)
+                v[k][i] = (lo >= 0 && lo < kSegBins) ? hrow[(size_t)(sg0 + i) * kSegBins + lo] : 0ull;
             }
         }
-        hlo[r] = (u64)acc;
-        hhi[r] = (u64)(acc >> 64);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+#pragma unroll
+            for (int i = 0; i < kPickBatch; ++i) acc[k] += (u128)v[k][i] * s_f[sg0 + i];
+    }
+    // The last row bin also takes every segment bin below its own.
+    if (threadIdx.x == kSegThreads - 1) {
+        constexpr int r = kRowBins - 1;
+        for (int sg = 0; sg < nseg; ++sg) {
+            if (!s_f[sg]) continue;
+            u128 t = 0;
+            for (int bn = max(r - s_shift[sg] + 1, 0); bn < kSegBins; ++bn) t += hrow[(size_t)sg * kSegBins + bn];
+            acc[kPer - 1] += t * s_f[sg];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int r = threadIdx.x + k * kSegThreads;
+        hlo[r] = (u64)acc[k];
+        hhi[r] = (u64)(acc[k] >> 64);
     }
     const u128 tp = gg_u128_floor(ceil((double)top_p * gg_u128_to_double(z)));
     if (threadIdx.x == 0) s_bin = -1;
@@ -440,7 +469,7 @@ __global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, 
     __syncthreads();
     if (threadIdx.x == 0) {
         const int cb = s_bin;
-        pick[row] = RowPick{s_c, ((u128)hhi[cb] << 64) | hlo[cb], tp, cb, 0};
+        pick[row] = RowPick{s_c, ((u128)hhi[cb] << 64) | hlo[cb], tp, m, cb, 0};
     }
 }
 
@@ -465,7 +494,9 @@ __device__ __forceinline__ int bounds_test(const void* lp, const float* rsm, con
 
 // C: per sequence, one wave: the rows' bound outcomes; flags the rows that need the exact
 // nucleus (an open row and every row after it through the first certain rejection, or
-// just the row of the final draw when the bounds settle the walk).
+// just the row of the final draw when the bounds settle the walk) and appends them to the
+// flagged-row list (order free: each listed row is processed on its own). Lane j tests
+// draft j (max_drafts <= 64), so the rows' loads overlap.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restrict__ logits,
                                                            const float* __restrict__ dprobs, int K, int V, int nseg,
@@ -474,70 +505,89 @@ __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restric
                                                            const float* __restrict__ uniforms,
                                                            const float* __restrict__ seg_max,
                                                            const RowPick* __restrict__ pick,
-                                                           int* __restrict__ status, int* __restrict__ flag) {
+                                                           int* __restrict__ status, int* __restrict__ flag,
+                                                           int* __restrict__ n_flagged, int* __restrict__ flagged) {
     const int b = blockIdx.x;
     const int R = K + 1;
     const int n = live_rows(n_drafts, b, K);
     const int lane = threadIdx.x;
-    // The rows one after another (row_max_wave needs the whole wave on one row); lane 0
-    // tests each draft.
-    for (int j = 0; j < n; ++j) {
-        const int row = b * R + j;
-        const float m = row_max_wave(seg_max, row, nseg);
-        if (lane == 0) {
-            const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-            const int x = drafts[(size_t)b * K + j];
-            const double q = (dprobs && x >= 0 && x < V) ? gg_clean_q(dprobs[((size_t)b * K + j) * V + x]) : 1.0;
-            const double u = (double)uniforms[(size_t)b * R + j];
-            status[row] = bounds_test<DT>(lp, seg_max + (size_t)row * nseg, pick[row], m, inv_t, x, V, u, q);
-        }
+    int st = kRowAccept;
+    if (lane < n) {
+        const int row = b * R + lane;
+        const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+        const int x = drafts[(size_t)b * K + lane];
+        const double q = (dprobs && x >= 0 && x < V) ? gg_clean_q(dprobs[((size_t)b * K + lane) * V + x]) : 1.0;
+        const double u = (double)uniforms[(size_t)b * R + lane];
+        const RowPick pk = pick[row];
+        st = bounds_test<DT>(lp, seg_max + (size_t)row * nseg, pk, pk.m, inv_t, x, V, u, q);
+        status[row] = st;
     }
-    if (lane == 0) {
-        // Walk: the first row that is not a certain acceptance.
-        int j0 = n;
-        for (int j = 0; j < n; ++j)
-            if (status[b * R + j] != kRowAccept) {
-                j0 = j;
-                break;
-            }
-        int jend = j0;  // flag rows j0 .. jend
-        if (j0 < n && status[b * R + j0] == kRowUnsure) {
-            jend = n;
-            for (int j = j0 + 1; j < n; ++j)
-                if (status[b * R + j] == kRowReject) {
-                    jend = j;
-                    break;
-                }
-        }
-        for (int j = 0; j <= n; ++j) flag[b * R + j] = (j >= j0 && j <= jend) ? 1 : 0;
+    // Walk: the first row that is not a certain acceptance, then (if it is open) every
+    // row through the first certain rejection after it.
+    const unsigned long long not_acc = __ballot(lane < n && st != kRowAccept);
+    const int j0 = not_acc ? __ffsll((long long)not_acc) - 1 : n;
+    int jend = j0;  // flag rows j0 .. jend
+    if (j0 < n && __shfl(st, j0) == kRowUnsure) {
+        const unsigned long long rej = __ballot(lane > j0 && lane < n && st == kRowReject);
+        jend = rej ? __ffsll((long long)rej) - 1 : n;
     }
+    // Rows 0 .. n (n <= 64): lane j writes row j, lane 0 also row 64.
+    int mine = 0, mine64 = 0;
+    if (lane <= n) {
+        mine = lane >= j0 && lane <= jend;
+        flag[b * R + lane] = mine;
+    }
+    if (lane == 0 && n == 64) {
+        mine64 = jend >= 64;
+        flag[b * R + 64] = mine64;
+    }
+    const unsigned long long fl = __ballot(mine);
+    const int cnt = __popcll(fl) + __shfl(mine64, 0);
+    int base = 0;
+    if (lane == 0) base = atomicAdd(n_flagged, cnt);
+    base = __shfl(base, 0);
+    if (mine) flagged[base + __popcll(fl & ((1ull << lane) - 1))] = b * R + lane;
+    if (mine64) flagged[base + cnt - 1] = b * R + 64;
 }
 
 // D: per (flagged row, segment): the sum of e over the elements above the boundary bin
-// (all in the nucleus), and the boundary bin's elements gathered for the cut.
+// (all in the nucleus), and the boundary bin's elements gathered for the cut. Block
+// (seg, y) takes the listed rows y, y + gridDim.y, ... (the grid is sized for about one
+// flagged row per sequence, so no block is launched for an unflagged row).
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __restrict__ logits, int K, int V,
+__device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, int V, int nseg, int vec_ok,
+                                               float inv_t, int seg, int row, const float* __restrict__ seg_max,
+                                               RowPick* __restrict__ pick, uint2* __restrict__ cand,
+                                               u64* __restrict__ seg_keep);
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(8))) seg_gather_kernel(const void* __restrict__ logits, int V,
                                                                  int nseg, int vec_ok, float inv_t,
-                                                                 const int32_t* __restrict__ n_drafts,
-                                                                 const int* __restrict__ flag,
+                                                                 const int* __restrict__ n_flagged,
+                                                                 const int* __restrict__ flagged,
                                                                  const float* __restrict__ seg_max,
                                                                  RowPick* __restrict__ pick,
                                                                  uint2* __restrict__ cand, u64* __restrict__ seg_keep) {
-    const int seg = blockIdx.x, row = blockIdx.y;
-    const int R = K + 1;
-    const int b = row / R, j = row % R;
-    if (j > live_rows(n_drafts, b, K) || !flag[row]) return;
+    const int nf = *n_flagged;
+    for (int li = blockIdx.y; li < nf; li += gridDim.y)
+        seg_gather_row<DT>(logits, V, nseg, vec_ok, inv_t, blockIdx.x, flagged[li], seg_max, pick, cand, seg_keep);
+}
+template <gg_dtype_t DT>
+__device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, int V, int nseg, int vec_ok,
+                                               float inv_t, int seg, int row, const float* __restrict__ seg_max,
+                                               RowPick* __restrict__ pick, uint2* __restrict__ cand,
+                                               u64* __restrict__ seg_keep) {
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
     int idx[32];
     load_seg<DT>(lp, V, seg, vec_ok, x, idx);
     __shared__ u64 red[kSegThreads / 64];
+    __shared__ int s_hits[kSegThreads / 64];
+    __shared__ int s_base;
     const int cbin = pick[row].cbin;
-    const float m = row_max_wave(seg_max, row, nseg);
+    const float m = pick[row].m;
     const float ms = seg_max[(size_t)row * nseg + seg];
     const int cbm = cb_abs(m, inv_t);
-    // Above the boundary bin: kept; in it: gathered (a bit mask first, then one counter
-    // update per lane that has any and its candidates written in order).
+    // Above the boundary bin: kept; in it: gathered (a bit mask per thread).
     u64 keep = 0;
     uint32_t hits = 0;
     if (cbin >= 0 && finite_f(ms)) {
@@ -549,18 +599,34 @@ __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __r
             hits |= (uint32_t)(rb == cbin) << k;
         }
     }
-    keep = seg_block_sum(keep, red);
-    if (threadIdx.x == 0) seg_keep[(size_t)row * nseg + seg] = keep;
+    // The candidates' slots: an exclusive scan of the per-thread counts within the block
+    // and one counter update per block.
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nh = __popc(hits);
+    int incl = nh;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) s_hits[wv] = incl;
+    keep = seg_block_sum(keep, red);  // (its barriers also publish s_hits)
+    if (threadIdx.x == 0) {
+        seg_keep[(size_t)row * nseg + seg] = keep;
+        int tot = 0;
+        for (int i = 0; i < kSegThreads / 64; ++i) tot += s_hits[i];
+        s_base = tot ? atomicAdd(&pick[row].n_cand, tot) : 0;
+    }
+    __syncthreads();
     if (hits) {
-        int slot = atomicAdd(&pick[row].n_cand, __popc(hits));
+        int slot = s_base + incl - nh;
+        for (int i = 0; i < wv; ++i) slot += s_hits[i];
         while (hits) {
             const int k = __ffs(hits) - 1;
             hits &= hits - 1;
-            float xv = 0.f;
-            int iv = 0;
-#pragma unroll
-            for (int kk = 0; kk < 32; ++kk)
-                if (kk == k) xv = x[kk], iv = idx[kk];
+            // (load_seg's element order; the logit read again, from cache, so that the
+            // loaded values need not stay live)
+            const int iv = seg * kSegElems + (k >> 3) * 2048 + 8 * (int)threadIdx.x + (k & 7);
+            const float xv = ld<DT>(lp, iv);
             if (slot < kCandCap) cand[(size_t)row * kCandCap + slot] = make_uint2(__float_as_uint(xv), (unsigned)iv);
             ++slot;
         }
@@ -572,158 +638,18 @@ __device__ __forceinline__ float logit_of_key(unsigned int key) {
     return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
-// E: per flagged row, sort the boundary bin's elements by (key desc, index asc) and cut;
-// the row's exact statistics, and the kept elements' e added to their segments' sums.
-// A crowded bin (more than kCandCap elements) flags the row for the exact row kernel.
+// Exact per-row nucleus statistics by one 1024-thread block (passes over the whole row),
+// for a row whose boundary bin is crowded (more than kCandCap elements); also rewrites the
+// row's per-segment sums of kept e. Uses the segment maxima and sums of seg_pass_kernel.
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict__ logits, int K, int V,
-                                                          int nseg, float inv_t,
-                                                          const int32_t* __restrict__ drafts,
-                                                          const int32_t* __restrict__ n_drafts,
-                                                          const int* __restrict__ flag,
-                                                          const float* __restrict__ seg_max,
-                                                          const RowPick* __restrict__ pick,
-                                                          const uint2* __restrict__ cand,
-                                                          RowStats* __restrict__ stats, u64* __restrict__ seg_keep,
-                                                          int* __restrict__ crowded) {
-    const int row = blockIdx.x;
+__device__ void row_stats_exact(const void* __restrict__ logits, int K, int V, int nseg,
+                                const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
+                                float inv_t, float top_p, const float* __restrict__ seg_max,
+                                const u64* __restrict__ seg_e, RowStats* __restrict__ stats,
+                                u64* __restrict__ seg_keep, int row) {
     const int R = K + 1;
     const int b = row / R, j = row % R;
     const int n = live_rows(n_drafts, b, K);
-    if (j > n || !flag[row]) return;
-    __shared__ u64 s_key[kCandCap];    // order key << 32 | (~index): descending = the nucleus order
-    __shared__ u128 red[1024 / 64];
-    __shared__ u64 s_segk[64];
-    __shared__ int s_last;
-    const RowPick pk = pick[row];
-    const float m = row_max_wave(seg_max, row, nseg);
-    if (pk.cbin < 0) {  // no finite logit or Z == 0: no nucleus
-        if (threadIdx.x == 0) {
-            stats[row] = RowStats{0, 0, m, 0x7fffffff, 0u, 1};
-            crowded[row] = 0;
-        }
-        return;
-    }
-    const int nc = pk.n_cand;
-    if (nc > kCandCap) {
-        if (threadIdx.x == 0) crowded[row] = 1;
-        return;
-    }
-    int np2 = 1;
-    while (np2 < nc) np2 <<= 1;
-    for (int i = threadIdx.x; i < np2; i += 1024) {
-        if (i < nc) {
-            const uint2 c = cand[(size_t)row * kCandCap + i];
-            s_key[i] = ((u64)gg_order_key(__uint_as_float(c.x)) << 32) | (u64)(~c.y);
-        } else {
-            s_key[i] = 0;  // sorts last
-        }
-    }
-    if (threadIdx.x < 64) s_segk[threadIdx.x] = 0;
-    __syncthreads();
-    // Bitonic sort, descending.
-    for (int k = 2; k <= np2; k <<= 1) {
-        for (int jj = k >> 1; jj > 0; jj >>= 1) {
-            for (int i = threadIdx.x; i < np2; i += 1024) {
-                const int ix = i ^ jj;
-                if (ix > i) {
-                    const u64 a = s_key[i], c = s_key[ix];
-                    const bool desc = (i & k) == 0;
-                    if (desc ? (a < c) : (a > c)) {
-                        s_key[i] = c;
-                        s_key[ix] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // Weights in that order (logit from the order key, segment max from the index).
-    // Thread t owns positions [4t, 4t+4): an exclusive block scan of the thread sums gives
-    // each element's mass before it; the kept elements are a prefix (that mass never
-    // drops), so the cut is the largest kept position. Candidates span at most
-    // kCandCap = 4 * 1024 positions.
-    const int p0 = 4 * (int)threadIdx.x;
-    u128 w[4];
-    u64 ev[4];
-    int sv[4];
-    u128 tsum = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        w[k] = 0;
-        ev[k] = 0;
-        sv[k] = 0;
-        if (p0 + k < nc) {
-            const u64 key = s_key[p0 + k];
-            const int i = (int)(~(unsigned int)(key & 0xffffffffu));
-            sv[k] = i / kSegElems;
-            const float ms = seg_max[(size_t)row * nseg + sv[k]];
-            ev[k] = gg_weight(logit_of_key((unsigned int)(key >> 32)), ms, inv_t);
-            w[k] = (u128)ev[k] * seg_factor(ms, m, inv_t);
-        }
-        tsum += w[k];
-    }
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    u128 incl = tsum;
-    for (int o = 1; o < 64; o <<= 1) {
-        const u128 t = shfl_up_u128(incl, o);
-        if (lane >= o) incl += t;
-    }
-    if (lane == 63) red[wv] = incl;
-    __syncthreads();
-    u128 before = pk.c_above + incl - tsum;
-    for (int i = 0; i < wv; ++i) before += red[i];
-    int last = -1;
-    u128 zp = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        if (p0 + k < nc && (before < pk.tp || before == 0)) {
-            last = p0 + k;
-            zp = before + w[k];
-            if (ev[k]) atomicAdd(&s_segk[sv[k]], ev[k]);
-        }
-        before += w[k];
-    }
-    if (threadIdx.x == 0) s_last = -1;
-    __syncthreads();
-    if (last >= 0) atomicMax(&s_last, last);
-    __syncthreads();
-    // The kept candidates' e into their segments' sums (seg_gather_kernel wrote the part
-    // above the boundary bin).
-    if (threadIdx.x < nseg && s_segk[threadIdx.x]) seg_keep[(size_t)row * nseg + threadIdx.x] += s_segk[threadIdx.x];
-    if (last >= 0 && last == s_last) {  // the owner of the cut (position 0 always qualifies)
-        const unsigned int lam = (unsigned int)(s_key[last] >> 32);
-        // Ties at the boundary key kept for index <= idx_cut; every index when all are.
-        const bool all_ties = last + 1 >= nc || (unsigned int)(s_key[last + 1] >> 32) != lam;
-        const int idx_cut = all_ties ? 0x7fffffff : (int)(~(unsigned int)(s_key[last] & 0xffffffffu));
-        RowStats st{zp, 0, m, idx_cut, lam, 1};
-        if (j < n) {
-            const int x = drafts[(size_t)b * K + j];
-            if (x >= 0 && x < V) {
-                const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-                Nucleus nu{m, inv_t, lam, idx_cut};
-                st.wx = nu.weight(ld<DT>(lp, x), x, seg_max[(size_t)row * nseg + x / kSegElems]);
-            }
-        }
-        stats[row] = st;
-        crowded[row] = 0;
-    }
-}
-
-// Exact per-row nucleus statistics in one 1024-thread block (passes over the whole row),
-// for the rows row_select_kernel found crowded; also rewrites the row's per-segment sums
-// of kept e. Uses the segment maxima and sums of seg_pass_kernel.
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
-    const void* __restrict__ logits, int K, int V, int nseg, const int32_t* __restrict__ drafts,
-    const int32_t* __restrict__ n_drafts, float inv_t, float top_p, const int* __restrict__ flag,
-    const int* __restrict__ crowded, const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
-    RowStats* __restrict__ stats, u64* __restrict__ seg_keep) {
-    const int row = blockIdx.x;
-    const int R = K + 1;
-    const int b = row / R, j = row % R;
-    const int n = live_rows(n_drafts, b, K);
-    if (j > n || !flag[row] || crowded[row] == 0) return;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     const float* rms = seg_max + (size_t)row * nseg;
 
@@ -857,6 +783,217 @@ __global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
             if (x >= 0 && x < V) st.wx = nu.weight(ld<DT>(lp, x), x, rms[x / kSegElems]);
         }
         stats[row] = st;
+    }
+}
+
+// Bitonic sort of s[0, np2) into descending order (np2 a power of two <= 4 * 1024, 1024
+// threads). Element i = t + 1024 * r is held by thread t as v[r] while the compare
+// distance is below 64: its partner i ^ jj is then in the same wave, reached by a
+// shuffle with no barrier. Longer distances go through LDS, a barrier per step.
+__device__ __forceinline__ void sort_desc_1024(u64* s, int np2) {
+    const int t = threadIdx.x;
+    const int nr = (np2 + 1023) >> 10;
+    u64 v[4];
+    auto in_wave = [&](int k, int jj0) {
+        for (int jj = jj0; jj > 0; jj >>= 1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (r >= nr) break;
+                const int i = t + (r << 10);
+                const u64 c = shfl_xor_u64(v[r], jj);
+                const bool keep_max = ((i & k) == 0) == ((i & jj) == 0);
+                v[r] = keep_max ? (v[r] > c ? v[r] : c) : (v[r] < c ? v[r] : c);
+            }
+        }
+    };
+    auto load = [&]() {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = t + (r << 10);
+            v[r] = (r < nr && i < np2) ? s[i] : 0ull;
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = t + (r << 10);
+            if (r < nr && i < np2) s[i] = v[r];
+        }
+    };
+    load();
+    for (int k = 2; k <= np2 && k <= 64; k <<= 1) in_wave(k, k >> 1);
+    for (int k = 128; k <= np2; k <<= 1) {
+        store();
+        __syncthreads();
+        for (int jj = k >> 1; jj >= 64; jj >>= 1) {
+            for (int i = t; i < np2; i += 1024) {
+                const int ix = i ^ jj;
+                if (ix > i) {
+                    const u64 a = s[i], c = s[ix];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? (a < c) : (a > c)) {
+                        s[i] = c;
+                        s[ix] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        load();
+        in_wave(k, 32);
+    }
+    store();
+    __syncthreads();
+}
+
+// E: per flagged row, sort the boundary bin's elements by (key desc, index asc) and cut;
+// the row's exact statistics, and the kept elements' e added to their segments' sums.
+// A crowded bin (more than kCandCap elements) is left to rejection_row_stats_kernel.
+template <gg_dtype_t DT>
+__device__ void row_select_row(const void* __restrict__ logits, int K, int V, int nseg, float inv_t, float top_p,
+                               const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
+                               const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
+                               const RowPick* __restrict__ pick, const uint2* __restrict__ cand,
+                               RowStats* __restrict__ stats, u64* __restrict__ seg_keep, int* __restrict__ n_crowded,
+                               int* __restrict__ crowded, int row) {
+    const int R = K + 1;
+    const int b = row / R, j = row % R;
+    const int n = live_rows(n_drafts, b, K);
+    __shared__ u64 s_key[kCandCap];    // order key << 32 | (~index): descending = the nucleus order
+    __shared__ u128 red[1024 / 64];
+    __shared__ u64 s_segk[64];
+    __shared__ int s_last;
+    const RowPick pk = pick[row];
+    const float m = pk.m;
+    if (pk.cbin < 0) {  // no finite logit or Z == 0: no nucleus
+        if (threadIdx.x == 0) stats[row] = RowStats{0, 0, m, 0x7fffffff, 0u, 1};
+        return;
+    }
+    const int nc = pk.n_cand;
+    if (nc > kCandCap) {  // rejection_row_stats_kernel takes it
+        if (threadIdx.x == 0) crowded[atomicAdd(n_crowded, 1)] = row;
+        return;
+    }
+    int np2 = 1;
+    while (np2 < nc) np2 <<= 1;
+    for (int i = threadIdx.x; i < np2; i += 1024) {
+        if (i < nc) {
+            const uint2 c = cand[(size_t)row * kCandCap + i];
+            s_key[i] = ((u64)gg_order_key(__uint_as_float(c.x)) << 32) | (u64)(~c.y);
+        } else {
+            s_key[i] = 0;  // sorts last
+        }
+    }
+    if (threadIdx.x < 64) s_segk[threadIdx.x] = 0;
+    __syncthreads();
+    sort_desc_1024(s_key, np2);
+    // Weights in that order (logit from the order key, segment max from the index).
+    // Thread t owns positions [4t, 4t+4): an exclusive block scan of the thread sums gives
+    // each element's mass before it; the kept elements are a prefix (that mass never
+    // drops), so the cut is the largest kept position. Candidates span at most
+    // kCandCap = 4 * 1024 positions.
+    const int p0 = 4 * (int)threadIdx.x;
+    u128 w[4];
+    u64 ev[4];
+    int sv[4];
+    u128 tsum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        w[k] = 0;
+        ev[k] = 0;
+        sv[k] = 0;
+        if (p0 + k < nc) {
+            const u64 key = s_key[p0 + k];
+            const int i = (int)(~(unsigned int)(key & 0xffffffffu));
+            sv[k] = i / kSegElems;
+            const float ms = seg_max[(size_t)row * nseg + sv[k]];
+            ev[k] = gg_weight(logit_of_key((unsigned int)(key >> 32)), ms, inv_t);
+            w[k] = (u128)ev[k] * seg_factor(ms, m, inv_t);
+        }
+        tsum += w[k];
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    u128 incl = tsum;
+    for (int o = 1; o < 64; o <<= 1) {
+        const u128 t = shfl_up_u128(incl, o);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) red[wv] = incl;
+    __syncthreads();
+    u128 before = pk.c_above + incl - tsum;
+    for (int i = 0; i < wv; ++i) before += red[i];
+    int last = -1;
+    u128 zp = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (p0 + k < nc && (before < pk.tp || before == 0)) {
+            last = p0 + k;
+            zp = before + w[k];
+            if (ev[k]) atomicAdd(&s_segk[sv[k]], ev[k]);
+        }
+        before += w[k];
+    }
+    if (threadIdx.x == 0) s_last = -1;
+    __syncthreads();
+    if (last >= 0) atomicMax(&s_last, last);
+    __syncthreads();
+    // The kept candidates' e into their segments' sums (seg_gather_kernel wrote the part
+    // above the boundary bin).
+    if (threadIdx.x < nseg && s_segk[threadIdx.x]) seg_keep[(size_t)row * nseg + threadIdx.x] += s_segk[threadIdx.x];
+    if (last >= 0 && last == s_last) {  // the owner of the cut (position 0 always qualifies)
+        const unsigned int lam = (unsigned int)(s_key[last] >> 32);
+        // Ties at the boundary key kept for index <= idx_cut; every index when all are.
+        const bool all_ties = last + 1 >= nc || (unsigned int)(s_key[last + 1] >> 32) != lam;
+        const int idx_cut = all_ties ? 0x7fffffff : (int)(~(unsigned int)(s_key[last] & 0xffffffffu));
+        RowStats st{zp, 0, m, idx_cut, lam, 1};
+        if (j < n) {
+            const int x = drafts[(size_t)b * K + j];
+            if (x >= 0 && x < V) {
+                const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
+                Nucleus nu{m, inv_t, lam, idx_cut};
+                st.wx = nu.weight(ld<DT>(lp, x), x, seg_max[(size_t)row * nseg + x / kSegElems]);
+            }
+        }
+        stats[row] = st;
+    }
+}
+
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict__ logits, int K, int V,
+                                                          int nseg, float inv_t, float top_p,
+                                                          const int32_t* __restrict__ drafts,
+                                                          const int32_t* __restrict__ n_drafts,
+                                                          const int* __restrict__ n_flagged,
+                                                          const int* __restrict__ flagged,
+                                                          const float* __restrict__ seg_max,
+                                                          const u64* __restrict__ seg_e,
+                                                          const RowPick* __restrict__ pick,
+                                                          const uint2* __restrict__ cand,
+                                                          RowStats* __restrict__ stats, u64* __restrict__ seg_keep,
+                                                          int* __restrict__ n_crowded, int* __restrict__ crowded) {
+    const int nf = *n_flagged;
+    for (int li = blockIdx.x; li < nf; li += gridDim.x) {
+        row_select_row<DT>(logits, K, V, nseg, inv_t, top_p, drafts, n_drafts, seg_max, seg_e, pick, cand, stats,
+                           seg_keep, n_crowded, crowded, flagged[li]);
+        __syncthreads();  // (the next row reuses the shared arrays)
+    }
+}
+
+// The rows whose boundary bin is crowded (listed by row_select_kernel), by a few blocks:
+// such rows are rare, and with none the kernel only reads the list's count.
+constexpr int kRowStatsBlocks = 8;
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
+    const void* __restrict__ logits, int K, int V, int nseg, const int32_t* __restrict__ drafts,
+    const int32_t* __restrict__ n_drafts, float inv_t, float top_p, const int* __restrict__ n_crowded,
+    const int* __restrict__ crowded, const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
+    RowStats* __restrict__ stats, u64* __restrict__ seg_keep) {
+    const int nc = *n_crowded;
+    for (int li = blockIdx.x; li < nc; li += gridDim.x) {
+        const int row = crowded[li];
+        row_stats_exact<DT>(logits, K, V, nseg, drafts, n_drafts, inv_t, top_p, seg_max, seg_e, stats, seg_keep,
+                            row);
+        __syncthreads();
     }
 }
 
@@ -1196,7 +1333,9 @@ struct RejWs {
     RowPick* pick;
     int* status;       // top-p: bound outcome per row
     int* flag;         // top-p: row needs the exact nucleus
-    int* crowded;      // top-p: row needs the exact row kernel
+    int* n_flagged;    // top-p: lengths of the flagged-row and crowded-row lists
+    int* crowded;      // top-p: flagged rows whose boundary bin is crowded
+    int* flagged;      // top-p: the rows that need the exact nucleus
     uint2* cand;       // top-p: boundary-bin elements per row (logit bits, index)
     u64* seg_keep;     // top-p: per (row, segment) sum of kept e
     size_t bytes;
@@ -1224,7 +1363,9 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
         w.pick = (RowPick*)take(rows * sizeof(RowPick));
         w.status = (int*)take(rows * sizeof(int));
         w.flag = (int*)take(rows * sizeof(int));
+        w.n_flagged = (int*)take(2 * sizeof(int));
         w.crowded = (int*)take(rows * sizeof(int));
+        w.flagged = (int*)take(rows * sizeof(int));
         w.cand = (uint2*)take(rows * kCandCap * sizeof(uint2));
         w.seg_keep = (u64*)take(rows * nseg * sizeof(u64));
     }
@@ -1257,19 +1398,21 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                                                             inv_t, n_drafts, w.seg_max,      \
                                                                             w.seg_e, w.seg_hist);            \
         row_pick_kernel<<<rows, kSegThreads, 0, s>>>(K, nseg, inv_t, top_p, n_drafts, w.seg_max, w.seg_e,    \
-                                                     w.seg_hist, w.pick);                                    \
+                                                     w.seg_hist, w.pick, w.n_flagged);                       \
         decide_bounds_kernel<DTV><<<num_seqs, 64, 0, s>>>(logits, q, K, vocab, nseg, inv_t, drafts,          \
                                                           n_drafts, uniforms, w.seg_max, w.pick, w.status,   \
-                                                          w.flag);                                           \
-        seg_gather_kernel<DTV><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,      \
-                                                                        inv_t, n_drafts, w.flag, w.seg_max,  \
-                                                                        w.pick, w.cand, w.seg_keep);         \
-        row_select_kernel<DTV><<<rows, 1024, 0, s>>>(logits, K, vocab, nseg, inv_t, drafts, n_drafts,        \
-                                                     w.flag, w.seg_max, w.pick, w.cand, w.stats, w.seg_keep, \
-                                                     w.crowded);                                             \
-        rejection_row_stats_kernel<DTV><<<rows, kThreads, 0, s>>>(logits, K, vocab, nseg, drafts, n_drafts,  \
-                                                                  inv_t, top_p, w.flag, w.crowded,           \
-                                                                  w.seg_max, w.seg_e, w.stats, w.seg_keep);  \
+                                                          w.flag, w.n_flagged, w.flagged);                   \
+        seg_gather_kernel<DTV><<<dim3(nseg, num_seqs), kSegThreads, 0, s>>>(logits, vocab, nseg, vec_ok,     \
+                                                                            inv_t, w.n_flagged, w.flagged,   \
+                                                                            w.seg_max, w.pick, w.cand,       \
+                                                                            w.seg_keep);                     \
+        row_select_kernel<DTV><<<num_seqs, 1024, 0, s>>>(logits, K, vocab, nseg, inv_t, top_p, drafts,       \
+                                                         n_drafts, w.n_flagged, w.flagged, w.seg_max,        \
+                                                         w.seg_e, w.pick, w.cand, w.stats, w.seg_keep,       \
+                                                         w.n_flagged + 1, w.crowded);                        \
+        rejection_row_stats_kernel<DTV><<<kRowStatsBlocks, kThreads, 0, s>>>(                                \
+            logits, K, vocab, nseg, drafts, n_drafts, inv_t, top_p, w.n_flagged + 1, w.crowded, w.seg_max,   \
+            w.seg_e, w.stats, w.seg_keep);                                                                   \
     } else {                                                                                                 \
         seg_pass_kernel<DTV, false><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, \
                                                                              inv_t, n_drafts, w.seg_max,     \
