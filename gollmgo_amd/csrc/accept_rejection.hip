@@ -187,11 +187,13 @@ static_assert(kSegElems == kSegThreads * 32, "segment = 32 logits per thread");
 // logit's bin relative to a maximum a is cb(a) - cb(l). Both terms are integers, so a bin
 // relative to a segment max turns into the bin relative to the row max by adding
 // cb(m) - cb(m_s): the segments' histograms merge exactly. cb is monotone, so the bins
-// follow the nucleus order.
+// follow the nucleus order. (l * (16/T) is the same float as l/T * 16 outside the
+// subnormal range, the power-of-two factor being exact; the loop-invariant 16/T leaves
+// one multiply per logit.)
 constexpr int kSegBins = 400;   // per segment: e > 0 needs (m_s - l)/T < 24.3 nats (389 bins)
 constexpr int kRowBins = 1024;  // per row (the last bin takes everything further down)
 __device__ __forceinline__ int cb_abs(float l, float inv_t) {
-    const float y = fminf(fmaxf(l * inv_t * 16.0f, -1.0e9f), 1.0e9f);
+    const float y = fminf(fmaxf(l * (inv_t * 16.0f), -1.0e9f), 1.0e9f);
     return (int)__builtin_floorf(y);
 }
 
@@ -335,17 +337,20 @@ __global__ void __launch_bounds__(kSegThreads) seg_pass_kernel(const void* __res
     if constexpr (kTopP) {
         for (int i = threadIdx.x; i < kSegBins; i += kSegThreads) h[i] = 0;
     }
+    // Non-finite logits become -inf: no effect on the max, and weight 0 (gg_weight
+    // clamps x = -inf to -80), so neither loop branches per element.
     float ms = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 32; ++k)
-        if (finite_f(x[k])) ms = fmaxf(ms, x[k]);
+    for (int k = 0; k < 32; ++k) {
+        x[k] = finite_f(x[k]) ? x[k] : -INFINITY;
+        ms = fmaxf(ms, x[k]);
+    }
     ms = seg_block_max(ms, redf);  // (its barriers also publish the cleared histogram)
     u64 e = 0;
     if (finite_f(ms)) {
         const int cbm = kTopP ? cb_abs(ms, inv_t) : 0;
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
-            if (!finite_f(x[k])) continue;
             const u64 w = gg_weight(x[k], ms, inv_t);
             e += w;
             if constexpr (kTopP) {

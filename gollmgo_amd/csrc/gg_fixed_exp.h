@@ -16,13 +16,18 @@
 #define GG_HD static inline
 #endif
 
-#define GG_FIX_SCALE 34359738368.0f /* 2^35 */
 
-GG_HD float gg_expf_fixed(float x_in) {
-    // e^-80 < 2^-115: weight 0 (also for NaN). Written with selects rather than an early
-    // return, so that vector code evaluates it without branching per element.
-    const bool live = x_in >= -80.0f;
-    const float x = live ? (x_in > 0.0f ? 0.0f : x_in) : 0.0f;  // callers pass x <= 0
+// Fixed-point weight w = floor(e^x * 2^35) of logit l given the row max m and 1/T, x =
+// (l - m)/T (callers pass x <= 0; x > 0 counts as 0). e^x is p * 2^k with k in [-116, 0]
+// and p from the polynomial below; w = floor(p * 2^(k+35)), the power-of-two scaling
+// exact. Below x = -80 the weight is 0 (e^-80 * 2^35 < 2^-80), which clamping x to -80
+// also gives, so there is no per-element branch or select on the result (a NaN x is
+// clamped too). The floor and the conversion to 64 bits are two 32-bit conversions: the
+// high word floor(v * 2^-32) (at most 15) and the low word v - hi * 2^32, exact in float
+// (v has 24 significant bits and is at least hi * 2^32), truncated.
+GG_HD unsigned long long gg_weight(float l, float m, float inv_t) {
+    float x = (l - m) * inv_t;
+    x = x >= -80.0f ? (x > 0.0f ? 0.0f : x) : -80.0f;
     const float kf = __builtin_floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
     float r = __builtin_fmaf(kf, -0.693145751953125f, x);
     r = __builtin_fmaf(kf, -1.42860682030941723212e-6f, r);
@@ -39,17 +44,13 @@ GG_HD float gg_expf_fixed(float x_in) {
         unsigned int u;
         float f;
     } s;
-    s.u = (unsigned int)(k + 127) << 23;
-    return live ? p * s.f : 0.0f;
+    s.u = (unsigned int)(k + 127 + 35) << 23;
+    const float v = p * s.f;  // e^x * 2^35
+    const float hf = __builtin_floorf(v * 2.3283064365386963e-10f);  // 2^-32
+    const unsigned int hi = (unsigned int)hf;
+    const unsigned int lo = (unsigned int)__builtin_fmaf(hf, -4294967296.0f, v);
+    return ((unsigned long long)hi << 32) | lo;
 }
-
-// Fixed-point weight of logit l given the row max m and 1/T (all finite).
-GG_HD unsigned long long gg_weight(float l, float m, float inv_t) {
-    const float x = (l - m) * inv_t;
-    const float e = gg_expf_fixed(x);
-    return (unsigned long long)__builtin_floorf(e * GG_FIX_SCALE);
-}
-
 // Monotone order key of a finite logit (larger logit -> larger key; -0 == +0).
 GG_HD unsigned int gg_order_key(float l) {
     union {
