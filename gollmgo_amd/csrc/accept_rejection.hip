@@ -346,19 +346,21 @@ __global__ void __launch_bounds__(kSegThreads) seg_pass_kernel(const void* __res
         ms = fmaxf(ms, x[k]);
     }
     ms = seg_block_max(ms, redf);  // (its barriers also publish the cleared histogram)
-    u64 e = 0;
+    // The thread's 32 weights (integers below 2^36, held in floats) summed exactly in a
+    // double.
+    double ed = 0.0;
     if (finite_f(ms)) {
         const int cbm = kTopP ? cb_abs(ms, inv_t) : 0;
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
-            const u64 w = gg_weight(x[k], ms, inv_t);
-            e += w;
+            const float w = gg_weight_f(x[k], ms, inv_t);
+            ed += (double)w;
             if constexpr (kTopP) {
-                if (w) atomicAdd(&h[min(cbm - cb_abs(x[k], inv_t), kSegBins - 1)], w);
+                if (w != 0.0f) atomicAdd(&h[min(cbm - cb_abs(x[k], inv_t), kSegBins - 1)], gg_weight_u64(w));
             }
         }
     }
-    e = seg_block_sum(e, red);  // (its barriers also complete the histogram)
+    const u64 e = seg_block_sum((u64)ed, red);  // (its barriers also complete the histogram)
     if (threadIdx.x == 0) {
         seg_max[(size_t)row * nseg + seg] = ms;
         seg_e[(size_t)row * nseg + seg] = e;
@@ -565,7 +567,7 @@ __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, 
                                                RowPick* __restrict__ pick, uint2* __restrict__ cand,
                                                u64* __restrict__ seg_keep);
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(8))) seg_gather_kernel(const void* __restrict__ logits, int V,
+__global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __restrict__ logits, int V,
                                                                  int nseg, int vec_ok, float inv_t,
                                                                  const int* __restrict__ n_flagged,
                                                                  const int* __restrict__ flagged,
@@ -592,18 +594,23 @@ __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, 
     const float m = pick[row].m;
     const float ms = seg_max[(size_t)row * nseg + seg];
     const int cbm = cb_abs(m, inv_t);
-    // Above the boundary bin: kept; in it: gathered (a bit mask per thread).
-    u64 keep = 0;
+    // Above the boundary bin: kept (weights summed exactly in a double); in it: gathered
+    // (a bit mask per thread). No per-element branch: the weight is computed for every
+    // element and selected.
+    double kd = 0.0;
     uint32_t hits = 0;
     if (cbin >= 0 && finite_f(ms)) {
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
-            if (!finite_f(x[k])) continue;
-            const int rb = row_bin(x[k], cbm, inv_t);
-            if (rb < cbin) keep += gg_weight(x[k], ms, inv_t);
-            hits |= (uint32_t)(rb == cbin) << k;
+            const bool fin = finite_f(x[k]);
+            const float xv = fin ? x[k] : -INFINITY;
+            const int rb = row_bin(xv, cbm, inv_t);
+            const float w = gg_weight_f(xv, ms, inv_t);
+            kd += rb < cbin ? (double)w : 0.0;
+            hits |= (uint32_t)(fin && rb == cbin) << k;
         }
     }
+    u64 keep = (u64)kd;
     // The candidates' slots: an exclusive scan of the per-thread counts within the block
     // and one counter update per block.
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1136,18 +1143,21 @@ __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
     const float ms = seg_max[(size_t)row * nseg + seg];
     const u64 f = (finite_f(rv.m) && finite_f(ms)) ? seg_factor(ms, rv.m, inv_t) : 0ull;
     const double zpf = f ? gg_u128_to_double(rv.zp) / (double)f : 0.0;
-    u64 s_res = 0;
+    // Each residual is an integer below 2^36 (e - floor(qd) with floor(qd) < e), so the
+    // thread's sum is exact in a double.
+    double rd = 0.0;
 #pragma unroll
     for (int r = 0; r < kSumRuns; ++r) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int i = seg * kSegElems + (r * kSumThreads + (int)threadIdx.x) * 8 + k;
             const bool keep = f && nu.kept(x[r][k], i);  // (NaN past the row: never kept)
-            const u64 e = keep ? gg_weight(x[r][k], ms, inv_t) : 0ull;
+            const double e = keep ? (double)gg_weight_f(x[r][k], ms, inv_t) : 0.0;
             const double qd = gg_clean_q(q[r][k]) * zpf;
-            s_res += (e && i != xr && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
+            rd += (i != xr && e > qd) ? e - __builtin_floor(qd) : 0.0;  // (qd >= 0: e = 0 adds 0)
         }
     }
+    u64 s_res = (u64)rd;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     for (int o = 32; o > 0; o >>= 1) s_res += shfl_xor_u64(s_res, o);
     if (lane == 0) red64[wv] = s_res;

@@ -18,16 +18,15 @@
 
 
 // Fixed-point weight w = floor(e^x * 2^35) of logit l given the row max m and 1/T, x =
-// (l - m)/T (callers pass x <= 0; x > 0 counts as 0). e^x is p * 2^k with k in [-116, 0]
-// and p from the polynomial below; w = floor(p * 2^(k+35)), the power-of-two scaling
-// exact. Below x = -80 the weight is 0 (e^-80 * 2^35 < 2^-80), which clamping x to -80
-// also gives, so there is no per-element branch or select on the result (a NaN x is
-// clamped too). The floor and the conversion to 64 bits are two 32-bit conversions: the
-// high word floor(v * 2^-32) (at most 15) and the low word v - hi * 2^32, exact in float
-// (v has 24 significant bits and is at least hi * 2^32), truncated.
-GG_HD unsigned long long gg_weight(float l, float m, float inv_t) {
-    float x = (l - m) * inv_t;
-    x = x >= -80.0f ? (x > 0.0f ? 0.0f : x) : -80.0f;
+// (l - m)/T (callers pass x <= 0; x > 0 counts as 0), returned as a float holding that
+// integer exactly. e^x is p * 2^k with k in [-116, 0] and p from the polynomial below;
+// w = floor(p * 2^(k+35)), the power-of-two scaling exact. Below x = -80 the weight is
+// 0 (e^-80 * 2^35 < 2^-80), which clamping x to -80 also gives, so there is no branch or
+// select on the result (a NaN x is clamped too). w < 2^36, so sums of up to 2^17 weights
+// are exact in double.
+GG_HD float gg_weight_f(float l, float m, float inv_t) {
+    const float y = (l - m) * inv_t;
+    const float x = __builtin_fminf(y >= -80.0f ? y : -80.0f, 0.0f);  // (the compare maps NaN to -80)
     const float kf = __builtin_floorf(__builtin_fmaf(x, 1.44269504088896341f, 0.5f));
     float r = __builtin_fmaf(kf, -0.693145751953125f, x);
     r = __builtin_fmaf(kf, -1.42860682030941723212e-6f, r);
@@ -45,12 +44,18 @@ GG_HD unsigned long long gg_weight(float l, float m, float inv_t) {
         float f;
     } s;
     s.u = (unsigned int)(k + 127 + 35) << 23;
-    const float v = p * s.f;  // e^x * 2^35
-    const float hf = __builtin_floorf(v * 2.3283064365386963e-10f);  // 2^-32
+    return __builtin_floorf(p * s.f);  // floor(e^x * 2^35)
+}
+// The same weight as a 64-bit integer: two 32-bit conversions, the high word
+// floor(w * 2^-32) (at most 15) and the low word w - hi * 2^32 (exact in float: w has 24
+// significant bits and is at least hi * 2^32).
+GG_HD unsigned long long gg_weight_u64(float w) {
+    const float hf = __builtin_floorf(w * 2.3283064365386963e-10f);  // 2^-32
     const unsigned int hi = (unsigned int)hf;
-    const unsigned int lo = (unsigned int)__builtin_fmaf(hf, -4294967296.0f, v);
+    const unsigned int lo = (unsigned int)__builtin_fmaf(hf, -4294967296.0f, w);
     return ((unsigned long long)hi << 32) | lo;
 }
+GG_HD unsigned long long gg_weight(float l, float m, float inv_t) { return gg_weight_u64(gg_weight_f(l, m, inv_t)); }
 // Monotone order key of a finite logit (larger logit -> larger key; -0 == +0).
 GG_HD unsigned int gg_order_key(float l) {
     union {
