@@ -287,6 +287,17 @@ def main():
     if fused:  # the draft rows' K/V read (bf16) and written to the pool by the same call
         attn_bytes += B * R * H * D * 2 * (k_new.element_size() + eb)
     achieved = attn_bytes / (t_attn * 1e-6) / 1e9
+    # The same with every pool block counted once: sequences that share prefix blocks read
+    # them once each in the algorithmic count, but HBM serves a shared block once when its
+    # readers meet in cache. A block counts with the most tokens any reader uses of it.
+    used = {}
+    for i in range(B):
+        n_tok = int(keys_np[i])
+        for blk in range((n_tok + bs - 1) // bs):
+            pid = int(lay.block_tables[i, blk])
+            used[pid] = max(used.get(pid, 0), min(bs, n_tok - blk * bs))
+    unique_bytes = attn_bytes - kv_bytes + sum(used.values()) * H * D * eb * 2
+    achieved_unique = unique_bytes / (t_attn * 1e-6) / 1e9
     # One gg_verify_attention call: a single-piece plan (no workspace) is one launch of the
     # MFMA kernel; otherwise stream-K (or an explicit partition grid) plus its merge.
     from gollmgo_amd._lib import lib as _gglib
@@ -338,7 +349,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": attn_kernels, "algorithmic_bytes_per_launch": attn_bytes,
-                     "traffic_source": traffic_src},
+                     "traffic_source": traffic_src, "unique_block_bytes_per_launch": unique_bytes,
+                     "achieved_unique_block_bytes": round(achieved_unique, 1),
+                     "frac_unique_block_bytes": round(achieved_unique / HBM_PEAK_GBS, 4)},
         "accept_roofline": {"achieved": round(acc_bytes / (t_acc * 1e-6) / 1e9, 1), "unit": "GB/s",
                             "algorithmic_bytes_per_launch": acc_bytes},
         "setup_s": round(setup_s, 1),
