@@ -379,6 +379,17 @@ __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv,
 // partition grid, or to stream-K record `rec`. Must be reached by the whole workgroup.
 //
 // `in` holds the piece's first chunk, already issued (PieceIO::start).
+// Partial records go through device-scope (agent) relaxed atomic stores and loads: they
+// bypass the per-XCD caches' stale copies, so a workgroup on another XCD reads what was
+// written. Ordering before the merge counter comes from waiting for the stores to
+// complete (every record store of the workgroup) before the counter's atomic add.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <gg_dtype_t DT, int NT>
 __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, const PieceDesc pd,
                                            PieceIn<DT>& in, const DeferredRows* ap) {
@@ -858,10 +869,12 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             } else {
                 const size_t pidx = rec >= 0 ? (size_t)rec * (size_t)(G * R) + (size_t)r
                                              : (z * Hq + h) * a.max_parts + part;
-                a.ws_acc[pidx * kD + d] = acc * vfold;
+                // Device-scope stores: they reach the point every XCD reads from, so the
+                // last piece of an LPT item can merge the records in the same launch.
+                store_agent(a.ws_acc + pidx * kD + d, acc * vfold);
                 if (d == 0) {
-                    a.ws_ml[pidx * 2 + 0] = mx > -1e29f ? mx * kLn2 : -1e30f;
-                    a.ws_ml[pidx * 2 + 1] = L;
+                    store_agent(a.ws_ml + pidx * 2 + 0, mx > -1e29f ? mx * kLn2 : -1e30f);
+                    store_agent(a.ws_ml + pidx * 2 + 1, L);
                 }
             }
         }
@@ -990,31 +1003,23 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
 // at most T chunks. attn_lpt_plan_kernel orders the pieces by size, descending (ties:
 // sequence, then piece, then kv head), and workgroup p of the main launch runs piece p:
 // dispatched in order, the longest pieces start first and the shortest fill the tail.
-// attn_lpt_combine_kernel merges the partial records of split items. (Merging in the
-// last piece to finish needs device-scope fences, which write back / invalidate a whole
-// L2 here and cost more than the separate launch.)
+// The last piece of a split item to finish merges the item's partial records
+// (lpt_merge_if_last), so the schedule is one launch. Its records are written and read
+// with device-scope stores and loads; a device-scope fence instead would write back or
+// invalidate a whole L2 here, which costs more than a separate merge launch.
 //
 // Plan layout (ints, in the workspace after the records), R = record bound, B = sequences:
 //   [0]                       number of pieces
-//   [1]                       number of split sequences (pieces per kv head > 1)
 //   [16 + 4p ..]              piece p: (sequence, kv head | pieces per kv head << 16,
 //                             first token, end token); sequence -1 past the last piece
 //   [16 + 4R + 2b ..]         sequence b: (first piece, pieces per kv head)
-//   [16 + 4R + 2B' + 4i ..]   i-th split sequence (2B' = 2B rounded up to 4), in sequence order: (sequence, first
-//                             piece, pieces per kv head, 0)
+//   [16 + 4R + 2B + b*Hkv + h]  merge counter of (sequence b, kv head h)
 // Pieces of sequence b are first + j*Hkv + kvh.
 __device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
 __device__ __forceinline__ int* lpt_seq(int* plan, int recs) { return plan + 16 + 4 * recs; }
-__device__ __forceinline__ int4* lpt_split(int* plan, int recs, int B) {
-    return (int4*)(plan + 16 + 4 * recs + ((2 * B + 3) & ~3));  // 16-byte aligned
-}
-// Most sequences an LPT plan can split: a split sequence has more than T chunks per kv
-// head, T >= C * kLptPieceNum / (slots * kLptPieceDen) for C chunks in all, so fewer than
-// slots * kLptPieceDen / (kLptPieceNum * Hkv) of them fit in C. Sizes the merge grid.
-__host__ __device__ constexpr int lpt_max_split(int slots, int num_seqs, int num_kv_heads) {
-    const int m = slots * kLptPieceDen / (kLptPieceNum * num_kv_heads) + 1;
-    return m < num_seqs ? m : num_seqs;
-}
+// Merge counters, one per (sequence, kv head): pieces of a split item that have written
+// their records. The plan clears them; the piece that merges an item clears its counter.
+__device__ __forceinline__ int* lpt_count(int* plan, int recs, int B) { return lpt_seq(plan, recs) + 2 * B; }
 
 // Sum over a 1024-thread workgroup (wave sums, then the 16 wave totals).
 __device__ __forceinline__ long long block_sum_1024(long long v, long long* s_w) {
@@ -1050,17 +1055,12 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
         s_cnt[b] = b < B ? cnt : 0;
     }
     const long long total = block_sum_1024(cnt, s_w);  // (its barriers also publish s_key / s_cnt)
-    const long long nsplit = block_sum_1024(np > 1 ? 1 : 0, s_w);
     int* plan = a.plan;
-    if (b == 0) {
-        plan[0] = (int)total;
-        plan[1] = (int)nsplit;
-    }
+    if (b == 0) plan[0] = (int)total;
     if (b >= B) return;
     // Pieces ahead of this sequence's: larger pieces, then equal pieces of lower sequences.
     // Eight sequences per step from 16-byte LDS reads (independent adds, no serial chain).
-    // Also the split sequences before this one (cnt > Hkv: more than one piece per head).
-    int pos = 0, split_rank = 0;
+    int pos = 0;
     for (int t0 = 0; t0 < B; t0 += 8) {
         const int4 k0 = *(const int4*)&s_key[t0], k1 = *(const int4*)&s_key[t0 + 4];
         const int4 n0 = *(const int4*)&s_cnt[t0], n1 = *(const int4*)&s_cnt[t0 + 4];
@@ -1070,13 +1070,12 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
         for (int e = 0; e < 8; ++e) {
             const int t = t0 + e;
             pos += (kk[e] > key || (kk[e] == key && t < b)) ? nn[e] : 0;
-            split_rank += (t < b && nn[e] > Hkv) ? 1 : 0;
         }
     }
-    if (np > 1) lpt_split(plan, recs, B)[split_rank] = make_int4(b, pos, np, 0);
     int* seq = lpt_seq(plan, recs) + 2 * b;
     seq[0] = pos;
     seq[1] = np;
+    for (int h = 0; h < Hkv; ++h) lpt_count(plan, recs, B)[b * Hkv + h] = 0;
     int4* table = (int4*)lpt_table(plan);
     for (int j = 0; j < np; ++j) {
         const int c0 = (int)((long long)j * nch / np), c1 = (int)((long long)(j + 1) * nch / np);
@@ -1087,7 +1086,58 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     for (int q = (int)total + b; q < recs; q += B) table[q] = make_int4(-1, 0, 0, 0);
 }
 
-// Workgroup p computes piece p of the plan (exits past the last piece).
+// The piece of a split item that finishes last merges the item's records: the online
+// log-sum-exp over its pieces in piece order, as a merge launch of its own would. Each
+// piece waits until its record stores have completed, then counts itself in the item's
+// counter (a device-scope atomic, no fence: the records were written with device-scope
+// stores, and the merging workgroup reads them with device-scope loads). No workgroup
+// waits for another, so there is no spinning; the merge costs the last piece a read of
+// the item's records.
+__device__ void lpt_merge_if_last(const AttnArgs& a, int Hkv, int b, int kvh, int np) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's record stores are done
+    __syncthreads();
+    const int recs = lpt_records(a.sk_grid, a.num_seqs, Hkv);
+    int* cnt = lpt_count(a.plan, recs, a.num_seqs) + b * Hkv + kvh;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+    __syncthreads();
+    if (!s_last) return;
+    const int first = lpt_seq(a.plan, recs)[2 * b];
+    const int G = a.num_q_heads / Hkv;
+    const int RW = G * a.rows;
+    const int nrows = seq_rows(a, b), ctx = seq_keys(a, b, kBS);
+    if (nrows > 0 && nrows <= ctx) {
+        // Thread pairs (row, 4 dims): 32 threads per row.
+        for (int e = threadIdx.x; e < G * nrows * (kD / 4); e += blockDim.x) {
+            const int r = e / (kD / 4), d4 = e % (kD / 4);
+            float M = -1e30f, L = 0.f;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < np; ++j) {
+                const size_t q = (size_t)(first + j * Hkv + kvh) * RW + r;
+                const float mx = load_agent(a.ws_ml + q * 2), ly = load_agent(a.ws_ml + q * 2 + 1);
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = load_agent(a.ws_acc + q * kD + 4 * d4 + i);
+                const float mn = fmaxf(M, mx);
+                const float fo = __expf(M - mn), fn = __expf(mx - mn);
+                M = mn;
+                L = L * fo + ly * fn;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = acc[i] * fo + v[i] * fn;
+            }
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            const int j = r / G, g = r % G;
+            const size_t obase = (((size_t)b * a.rows + j) * a.num_q_heads + (size_t)kvh * G + g) * kD + 4 * d4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) store_from_f32(a.out, a.out_dtype, obase + i, acc[i] * inv);
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next layer
+}
+
+// Workgroup p computes piece p of the plan (exits past the last piece); the last piece of a
+// split item to finish merges it.
 template <gg_dtype_t DT, int NT>
 __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
     const int p = blockIdx.x;
@@ -1104,6 +1154,7 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     DeferredRows ap;
     start_piece<DT>(a, kv, d, in, &ap);
     attn_piece<DT, NT>(a, kv, d, in, &ap);
+    if (np > 1) lpt_merge_if_last(a, kv.Hkv, b, kvh, np);
 #ifdef GG_TRACE
     if (threadIdx.x == 0) {
         g_trace[4 * p + 0] = tr_t0;
@@ -1111,49 +1162,6 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
         g_trace[4 * p + 2] = (long long)__smid() | (1LL << 32);
     }
 #endif
-}
-
-// Merge the pieces of split items: workgroup (i, y) takes kv head i % Hkv of the
-// (i / Hkv)-th split sequence (the grid covers lpt_max_split sequences; the rest exit),
-// rows 4y .. 4y+3 (32 threads x 4 dims per row), so every record is requested at once.
-__global__ void __launch_bounds__(128) attn_lpt_combine_kernel(AttnArgs a, int Hkv, int tok, int recs) {
-    const int si = blockIdx.x / Hkv, kvh = blockIdx.x % Hkv;
-    // (The count and the entry are requested together; entries past the count are stale.)
-    const int nsplit = a.plan[1];
-    const int4 e = lpt_split(a.plan, recs, a.num_seqs)[si];
-    if (si >= nsplit) return;
-    const int b = e.x, first = e.y, np = e.z;
-    const int G = a.num_q_heads / Hkv;
-    const int r = blockIdx.y * 4 + (threadIdx.x >> 5);
-    const int d4 = threadIdx.x & 31;
-    const int RW = G * a.rows;
-    if (r >= G * seq_rows(a, b)) return;  // rows past row_counts[b] hold no records
-    // The first two pieces' records are requested together (a split item has two or more).
-    const size_t q0 = (size_t)(first + kvh) * RW + r, q1 = q0 + (size_t)Hkv * RW;
-    const float2 ml0 = *(const float2*)(a.ws_ml + q0 * 2), ml1 = *(const float2*)(a.ws_ml + q1 * 2);
-    const float4 v0 = ((const float4*)(a.ws_acc + q0 * kD))[d4], v1 = ((const float4*)(a.ws_acc + q1 * kD))[d4];
-    float M = -1e30f, L = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < np; ++j) {
-        const size_t q = (size_t)(first + j * Hkv + kvh) * RW + r;
-        const float2 ml = j == 0 ? ml0 : j == 1 ? ml1 : *(const float2*)(a.ws_ml + q * 2);
-        const float4 v = j == 0 ? v0 : j == 1 ? v1 : ((const float4*)(a.ws_acc + q * kD))[d4];
-        const float mn = fmaxf(M, ml.x);
-        const float fo = __expf(M - mn), fn = __expf(ml.x - mn);
-        M = mn;
-        L = L * fo + ml.y * fn;
-        acc.x = acc.x * fo + v.x * fn;
-        acc.y = acc.y * fo + v.y * fn;
-        acc.z = acc.z * fo + v.z * fn;
-        acc.w = acc.w * fo + v.w * fn;
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const int j = r / G, g = r % G;
-    const size_t obase = (((size_t)b * a.rows + j) * a.num_q_heads + (size_t)kvh * G + g) * kD + 4 * d4;
-    store_from_f32(a.out, a.out_dtype, obase + 0, acc.x * inv);
-    store_from_f32(a.out, a.out_dtype, obase + 1, acc.y * inv);
-    store_from_f32(a.out, a.out_dtype, obase + 2, acc.z * inv);
-    store_from_f32(a.out, a.out_dtype, obase + 3, acc.w * inv);
 }
 
 template <gg_dtype_t DT>
@@ -1274,9 +1282,7 @@ gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s)
     if (st != GG_OK) return st;
     const dim3 cgrid(a.num_seqs * kv.Hkv, (G * a.rows + 3) / 4);
     if (a.sched == ATTN_SCHED_STREAMK) attn_streamk_combine_kernel<<<cgrid, 128, 0, s>>>(a, kv.Hkv, tok, a.sk_grid);
-    if (a.sched == ATTN_SCHED_LPT)
-        attn_lpt_combine_kernel<<<dim3(lpt_max_split(a.sk_grid, a.num_seqs, kv.Hkv) * kv.Hkv, cgrid.y), 128, 0, s>>>(
-            a, kv.Hkv, tok, lpt_records(a.sk_grid, a.num_seqs, kv.Hkv));
+    // (LPT: the split items are merged inside the main launch, lpt_merge_if_last.)
     return GG_OK;
 }
 
@@ -1306,7 +1312,7 @@ size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int nu
     const size_t rw = (size_t)(num_q_heads / kv->num_kv_heads) * rows;
     const size_t n_ml = records * rw * 2;
     const size_t n_acc = records * rw * kD;
-    const size_t plan_ints = 16 + 4 * records + 6 * (size_t)num_seqs + 4;
+    const size_t plan_ints = 16 + 4 * records + 2 * (size_t)num_seqs + items;  // (items: merge counters)
     if (ml_elems) *ml_elems = n_ml;
     if (acc_elems) *acc_elems = n_acc;
     return (((n_ml + 63) / 64) * 64 + n_acc) * sizeof(float) + plan_ints * sizeof(int);
