@@ -245,20 +245,21 @@ AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int ma
         part = part < 64 ? 64 : (part > 512 ? 512 : part);
         return {ATTN_SCHED_GRID, (int)part};
     }
-    // Measured on MI355X: while the (sequence, kv head) items fill at least half the
-    // resident workgroup slots, longest-first pieces (LPT: items longer than the mean slot
-    // load cut in equal pieces, dispatched longest first) balance ragged contexts best;
-    // beyond the sequences an LPT workgroup can rank, one workgroup per item (no split, no
-    // merge) when the items fill the slots. Otherwise stream-K splits evenly.
+    // Measured on MI355X: while the (sequence, kv head) items fill at least a quarter of
+    // the resident workgroup slots, longest-first pieces (LPT: long items cut in equal
+    // pieces, dispatched longest first, split items merged inside the launch) balance
+    // ragged contexts best; beyond the sequences an LPT workgroup can rank, one workgroup
+    // per item (no split, no merge) when the items fill the slots. Otherwise stream-K
+    // splits evenly.
     const int G = num_q_heads / kv->num_kv_heads;
     const int nt = (G * rows + 15) / 16;
     const long long max_keys = (long long)max_blocks * kv->block_size;
     const long long items = (long long)num_seqs * kv->num_kv_heads;
     const long long slots = (long long)device_cu_count() * attn_occupancy(nt);
-    // (At half the slots LPT gives about two pieces per item, cut inside items only; with
-    // fewer, longer items stream-K's even split wins: config 2 63 vs 66 µs, config 4 164
-    // vs 117 µs.)
-    if (2 * items >= slots && num_seqs <= kLptMaxSeqs) return {ATTN_SCHED_LPT, 0};
+    // (With a merge launch of its own, LPT lost to stream-K at a quarter of the slots,
+    // config 4: 164 vs 117 µs. With the merge inside the launch and pieces of 4/3 of the
+    // mean slot load it wins there: 110.3 vs 112.7 µs, same box.)
+    if (4 * items >= slots && num_seqs <= kLptMaxSeqs) return {ATTN_SCHED_LPT, 0};
     if (items >= slots && max_keys <= kMfmaMaxPartition)
         return {ATTN_SCHED_GRID, (int)((max_keys + 63) / 64 * 64)};
     return {ATTN_SCHED_STREAMK, 0};

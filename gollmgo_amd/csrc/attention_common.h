@@ -107,19 +107,25 @@ struct AttnPlan {
 
 // LPT schedule: most sequences the plan kernel ranks (one per thread).
 constexpr int kLptMaxSeqs = 1024;
-// LPT piece length: at most T = ceil(C * kLptPieceNum / (slots * kLptPieceDen)) chunks
-// for C chunks of work over `slots` resident workgroups. 1.5 times the mean slot load,
-// measured on MI355X (attention µs at factors 1 / 4/3 / 3/2 / 7/4 / 2): config 3
-// 129.7 / 125.9 / 122.0 / 126.5 / 126.6, config 2 73.6 / 69.5 / 71.6 / 76.4 / 78.6,
-// config 5 unchanged. Fewer items are split (fewer merges and partial records) while the
-// longest-first order still balances the slots.
-constexpr int kLptPieceNum = 3;
-constexpr int kLptPieceDen = 2;
+// LPT piece length: at most T = ceil(C * num / (slots * den)) chunks for C chunks of work
+// over `slots` resident workgroups, num/den = 3/2 of the mean slot load when the
+// (sequence, kv head) items fill the slots and 4/3 when they are fewer. Measured on MI355X
+// (attention µs at factors 1 / 4/3 / 3/2 / 7/4, the merge inside the main launch):
+// config 3 (items = slots) 136.5 / 133.4 / 126.9 / 129.2; config 2 (items = slots / 2)
+// 81.8 / 73.3 / 76.6 / 77.2; config 5 (items = 2 slots) within 0.3 µs at every factor.
+// Longer pieces split fewer items; with fewer items than slots the long items must be cut
+// finer to occupy every slot.
+constexpr int kLptPieceNum = 3, kLptPieceDen = 2;            // items >= slots
+constexpr int kLptPieceNumFew = 4, kLptPieceDenFew = 3;      // items < slots
+__host__ __device__ constexpr bool lpt_few_items(int slots, int num_seqs, int num_kv_heads) {
+    return num_seqs * num_kv_heads < slots;
+}
 // Bound on the number of LPT pieces (= main-grid workgroups and partial records): the
-// cuts of every item at T chunks give at most C/T + items pieces. (Stream-K needs
-// grid + items records, which is more: the workspace holds the larger of the two.)
+// cuts of every item at T chunks give at most C/T + items pieces, C/T <= slots * den / num
+// (the smaller factor, 4/3, gives the larger bound). (Stream-K needs grid + items records,
+// which is more: the workspace holds the larger of the two.)
 __host__ __device__ constexpr int lpt_records(int slots, int num_seqs, int num_kv_heads) {
-    return (slots * kLptPieceDen + kLptPieceNum - 1) / kLptPieceNum + num_seqs * num_kv_heads;
+    return (slots * kLptPieceDenFew + kLptPieceNumFew - 1) / kLptPieceNumFew + num_seqs * num_kv_heads;
 }
 AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int max_blocks,
                    int partition_tokens);

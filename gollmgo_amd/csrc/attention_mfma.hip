@@ -1044,8 +1044,10 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     const int nch = b < B ? seq_chunks(a, b, tok) : 0;
     const int ctx = b < B ? seq_keys(a, b, kBS) : 0;
     const long long C = block_sum_1024((long long)Hkv * nch, s_w);
-    const long long den = (long long)slots * kLptPieceDen;
-    const int T = (int)max((C * kLptPieceNum + den - 1) / den, (long long)kStreamKMinChunks);
+    const bool few = lpt_few_items(slots, B, Hkv);
+    const long long den = (long long)slots * (few ? kLptPieceDenFew : kLptPieceDen);
+    const long long num = few ? kLptPieceNumFew : kLptPieceNum;
+    const int T = (int)max((C * num + den - 1) / den, (long long)kStreamKMinChunks);
     const int np = nch ? (nch + T - 1) / T : 0;
     const int key = np ? (nch + np - 1) / np : 0;
     const int cnt = np * Hkv;
