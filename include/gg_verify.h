@@ -170,8 +170,11 @@ gg_status_t gg_kv_append(gg_kv_t kv, int layer, const void* k, const void* v,
  *   block_tables: device int32[num_seqs][max_blocks_per_seq] of physical blocks
  *   scale       : softmax scale (1/sqrt(head_dim) in the reference)
  *   partition_tokens: split-K partition length, a multiple of 64. 0 = automatic:
- *                 one workgroup per (sequence, kv head) when those items fill the
- *                 device, else a stream-K split over a fixed grid (same results).
+ *                 longest-first pieces (long items cut, split items merged in the
+ *                 same launch) when the (sequence, kv head) items fill at least a
+ *                 quarter of the device's workgroup slots; one workgroup per item
+ *                 past 1024 sequences; else a stream-K split over a fixed grid
+ *                 (results equal to textbook attention in every case).
  * workspace must hold gg_verify_attention_workspace_size(...) bytes (may be 0). */
 size_t gg_verify_attention_workspace_size(gg_kv_t kv, int num_seqs, int rows_per_seq,
                                           int num_q_heads, int max_blocks_per_seq,
