@@ -147,6 +147,31 @@ def test_rejection_crowded_boundary_bin(gpu):
         assert np.array_equal(tok.cpu().numpy(), et), top_p
 
 
+def test_rejection_more_listed_rows_than_workgroups(gpu):
+    """Rows that need the exact nucleus are listed and the later kernels loop over the
+    list with grids sized by sequence (and 8 workgroups for crowded rows). Two-level tied
+    logits make every row's boundary bin crowded and its bounds open, so up to B*(K+1) =
+    18 rows are listed for 2 sequences, and more crowded rows than row-pass workgroups."""
+    say("rejection listed rows > workgroups")
+    rng = np.random.default_rng(41)
+    B, K, V = 2, 8, 20000
+    host = rng.integers(0, 2, (B, K + 1, V)).astype(np.float32)
+    lg = torch.from_numpy(host).to(torch.bfloat16)
+    host = lg.float().numpy()
+    drafts = np.argmax(host[:, :K], axis=-1).astype(np.int32)  # in the top level: often accepted
+    drafts[1, 3] = int(np.argmin(host[1, 3]))                  # one draft outside the nucleus
+    n = np.array([K, K - 2], np.int32)
+    for seed in range(4):
+        u = np.random.default_rng(seed).random((B, K + 1)).astype(np.float32) * 3e-4  # p(x) ~ 1/4000 inside
+        for top_p in (0.4, 0.95):
+            acc, tok = gv.accept_rejection(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(),
+                                           torch.from_numpy(u).cuda(), 1.0, top_p)
+            torch.cuda.synchronize()
+            ea, et = ora.accept_rejection(host, drafts, n, u, 1.0, top_p)
+            assert np.array_equal(acc.cpu().numpy(), ea), (seed, top_p)
+            assert np.array_equal(tok.cpu().numpy(), et), (seed, top_p)
+
+
 def test_rejection_small_temperature_is_greedy(gpu):
     say("rejection T->0")
     lg, host, drafts, n = logits_case(5, 3, 3000, "f32", seed=5)
