@@ -81,6 +81,7 @@ SIGNATURES = {
     "gg_accept_rejection": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp, _f, _f, _vp, _vp, _vp,
                                  _sz, _vp]),
     "gg_ngram_draft": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "gg_history_append_draft": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp]),
 }
 
 _lib: C.CDLL | None = None

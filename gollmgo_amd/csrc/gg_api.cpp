@@ -514,3 +514,20 @@ GG_API gg_status_t gg_ngram_draft(const int32_t* history, int hist_stride, const
     return launch_ngram_draft(history, hist_stride, hist_len, num_seqs, n, max_drafts, out_drafts,
                               out_n, (hipStream_t)stream);
 }
+
+GG_API gg_status_t gg_history_append_draft(int32_t* history, int hist_stride, int32_t* hist_len,
+                                           const int32_t* hist_rows, int num_seqs, const int32_t* drafts,
+                                           int drafts_per_seq, const int32_t* accepted, const int32_t* token,
+                                           int n, int max_drafts, int32_t* out_drafts, int32_t* out_n,
+                                           void* stream) {
+    clear_error();
+    if (n < 2) n = 2;
+    if (max_drafts < 1) max_drafts = 4;
+    GG_CHECK_ARG(n <= 9, "gg_history_append_draft: n must be <= 9 (the reference key holds 8 tokens)");
+    GG_CHECK_ARG(num_seqs > 0 && hist_stride >= 0 && max_drafts <= 64 && drafts_per_seq >= 0 && drafts_per_seq <= 64,
+                 "gg_history_append_draft: bad shape");
+    GG_CHECK_ARG(history && hist_len && accepted && token && out_drafts && out_n && (drafts || drafts_per_seq == 0),
+                 "gg_history_append_draft: NULL buffer");
+    return launch_history_append_draft(history, hist_stride, hist_len, hist_rows, num_seqs, drafts, drafts_per_seq,
+                                       accepted, token, n, max_drafts, out_drafts, out_n, (hipStream_t)stream);
+}

@@ -126,6 +126,10 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
 gg_status_t launch_ngram_draft(const int32_t* hist, int stride, const int32_t* hist_len, int num_seqs,
                                int n, int max_drafts, int32_t* out_drafts, int32_t* out_n,
                                hipStream_t s);
+gg_status_t launch_history_append_draft(int32_t* hist, int stride, int32_t* hist_len, const int32_t* rows,
+                                        int num_seqs, const int32_t* drafts, int k_in, const int32_t* accepted,
+                                        const int32_t* token, int n, int max_drafts, int32_t* out_drafts,
+                                        int32_t* out_n, hipStream_t s);
 
 }  // namespace gg
 

@@ -57,15 +57,12 @@ __device__ __forceinline__ int scan_resident(const int32_t* hs, int last, const 
     return m;
 }
 
-// KL = n - 1 key tokens (1..8), a compile-time constant for the resident scan.
+// The drafts of one sequence whose history is h[0, L): up to K chained lookups, written
+// to od[0..) and their count to *on. KL = n - 1 key tokens (1..8), a compile-time
+// constant for the resident scan. The whole workgroup calls it.
 template <int KL>
-__global__ void __launch_bounds__(kThreads) ngram_draft_kernel(
-    const int32_t* __restrict__ hist, int stride, const int32_t* __restrict__ hist_len, int n,
-    int K, int32_t* __restrict__ out_drafts, int32_t* __restrict__ out_n) {
-    const int b = blockIdx.x;
-    const int32_t* h = hist + (size_t)b * stride;
-    int L = hist_len[b];
-    if (L > stride) L = stride;
+__device__ __forceinline__ void draft_one(const int32_t* __restrict__ h, int L, int n, int K,
+                                          int32_t* __restrict__ od, int32_t* __restrict__ on) {
     const int kl = n - 1;
     // (A resident history may be read up to 8 + 32 tokens past its end: padding.)
     __shared__ __align__(16) int32_t tile[kResident + 48];
@@ -74,7 +71,7 @@ __global__ void __launch_bounds__(kThreads) ngram_draft_kernel(
     __shared__ int n_out;
     if (threadIdx.x == 0) n_out = 0;
     if (L < n) {
-        if (threadIdx.x == 0) out_n[b] = 0;
+        if (threadIdx.x == 0) *on = 0;
         return;
     }
     if (threadIdx.x < kl) key[threadIdx.x] = h[L - kl + threadIdx.x];
@@ -104,8 +101,8 @@ __global__ void __launch_bounds__(kThreads) ngram_draft_kernel(
             }
             __syncthreads();
         }
-        if ((int)threadIdx.x < step) out_drafts[(size_t)b * K + threadIdx.x] = drafts_s[threadIdx.x];
-        if (threadIdx.x == 0) out_n[b] = step;
+        if ((int)threadIdx.x < step) od[threadIdx.x] = drafts_s[threadIdx.x];
+        if (threadIdx.x == 0) *on = step;
         return;
     }
     for (int step = 0; step < K; ++step) {
@@ -134,7 +131,7 @@ __global__ void __launch_bounds__(kThreads) ngram_draft_kernel(
         const int next = h[best + kl];
         __syncthreads();
         if (threadIdx.x == 0) {
-            out_drafts[(size_t)b * K + step] = next;
+            od[step] = next;
             for (int k = 0; k + 1 < kl; ++k) key[k] = key[k + 1];
             key[kl - 1] = next;
             n_out = step + 1;
@@ -142,7 +139,53 @@ __global__ void __launch_bounds__(kThreads) ngram_draft_kernel(
         __syncthreads();
     }
     __syncthreads();
-    if (threadIdx.x == 0) out_n[b] = n_out;
+    if (threadIdx.x == 0) *on = n_out;
+}
+
+template <int KL>
+__global__ void __launch_bounds__(kThreads) ngram_draft_kernel(
+    const int32_t* __restrict__ hist, int stride, const int32_t* __restrict__ hist_len, int n,
+    int K, int32_t* __restrict__ out_drafts, int32_t* __restrict__ out_n) {
+    const int b = blockIdx.x;
+    const int L = min(hist_len[b], stride);
+    draft_one<KL>(hist + (size_t)b * stride, L, n, K, out_drafts + (size_t)b * K, out_n + b);
+}
+
+// The step's emitted tokens appended to each sequence's history, then its next drafts:
+// emitSpeculative (internal/engine/serving.go:541-566) emits the accepted drafts
+// drafts[b][0, accepted) and then the corrected or bonus token, and maybeDraft
+// (serving.go:608-620) drafts the next step from the whole history. Sequence b's history
+// is row rows[b] (b when rows is NULL). A history that the tokens would take past the
+// stride is left unchanged and its length set to -1 (no drafts from it until the caller
+// reseeds it); a negative length stays -1.
+template <int KL>
+__global__ void __launch_bounds__(kThreads) history_append_draft_kernel(
+    int32_t* __restrict__ hist, int stride, int32_t* __restrict__ hist_len, const int32_t* __restrict__ rows,
+    const int32_t* __restrict__ drafts, int k_in, const int32_t* __restrict__ accepted,
+    const int32_t* __restrict__ token, int n, int K, int32_t* __restrict__ out_drafts,
+    int32_t* __restrict__ out_n) {
+    const int b = blockIdx.x;
+    const int row = rows ? rows[b] : b;
+    int32_t* h = hist + (size_t)row * stride;
+    const int L = hist_len[row];
+    const int acc = min(max(accepted[b], 0), k_in);
+    const int tok = token[b];
+    const int cnt = acc + (tok >= 0 ? 1 : 0);
+    if (L < 0 || L + cnt > stride) {
+        if (threadIdx.x == 0) {
+            hist_len[row] = -1;
+            out_n[b] = 0;
+        }
+        return;
+    }
+    if ((int)threadIdx.x < cnt) h[L + threadIdx.x] = (int)threadIdx.x < acc ? drafts[(size_t)b * k_in + threadIdx.x] : tok;
+    // The appended tokens are read back by other threads of the workgroup (the key, the
+    // scans): workgroup-scope release and acquire around the barrier.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (threadIdx.x == 0) hist_len[row] = L + cnt;
+    draft_one<KL>(h, L + cnt, n, K, out_drafts + (size_t)b * K, out_n + b);
 }
 
 }  // namespace
@@ -158,6 +201,24 @@ gg_status_t launch_ngram_draft(const int32_t* hist, int stride, const int32_t* h
 #undef GG_NG
     }
     return check_hip(hipGetLastError(), "ngram_draft launch");
+}
+
+gg_status_t launch_history_append_draft(int32_t* hist, int stride, int32_t* hist_len, const int32_t* rows,
+                                        int num_seqs, const int32_t* drafts, int k_in, const int32_t* accepted,
+                                        const int32_t* token, int n, int max_drafts, int32_t* out_drafts,
+                                        int32_t* out_n, hipStream_t s) {
+    switch (n - 1) {
+#define GG_HA(KLV)                                                                                               \
+    case KLV:                                                                                                    \
+        history_append_draft_kernel<KLV><<<num_seqs, kThreads, 0, s>>>(hist, stride, hist_len, rows, drafts, k_in, \
+                                                                      accepted, token, n, max_drafts, out_drafts, \
+                                                                      out_n);                                     \
+        break;
+        GG_HA(1) GG_HA(2) GG_HA(3) GG_HA(4) GG_HA(5) GG_HA(6) GG_HA(7)
+        default: GG_HA(8)
+#undef GG_HA
+    }
+    return check_hip(hipGetLastError(), "history_append_draft launch");
 }
 
 }  // namespace gg

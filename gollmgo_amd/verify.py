@@ -312,3 +312,30 @@ def ngram_draft(history: torch.Tensor, hist_len: torch.Tensor, n: int, max_draft
                                _dev(d, "drafts", torch.int32), _dev(nn, "n_out", torch.int32),
                                _stream(stream)), "gg_ngram_draft")
     return d, nn
+
+
+def history_append_draft(history: torch.Tensor, hist_len: torch.Tensor, drafts: torch.Tensor,
+                         accepted: torch.Tensor, token: torch.Tensor, n: int, max_drafts: int,
+                         hist_rows: Optional[torch.Tensor] = None, out: Optional[tuple] = None,
+                         stream: Optional[torch.cuda.Stream] = None):
+    """Append each sequence's emitted tokens (drafts[b][:accepted[b]], then token[b]) to
+    its history row (hist_rows[b], or b) and draft the next step from it.
+    history [rows, stride] int32 and hist_len [rows] int32 are updated in place;
+    drafts [B, K_in] int32; accepted, token [B] int32 -> (next drafts [B, K'], n_out [B])."""
+    B = accepted.shape[0]
+    stride = history.shape[1]
+    if drafts.dim() != 2 or drafts.shape[0] != B or token.shape != (B,):
+        raise ValueError("drafts must be [num_seqs, drafts_per_seq], token [num_seqs]")
+    if hist_rows is not None and hist_rows.shape != (B,):
+        raise ValueError("hist_rows must be [num_seqs]")
+    K = max_drafts if max_drafts >= 1 else 4
+    d, nn = out if out is not None else (torch.zeros(B, K, dtype=torch.int32, device="cuda"),
+                                         torch.empty(B, dtype=torch.int32, device="cuda"))
+    check(lib().gg_history_append_draft(
+        _dev(history, "history", torch.int32), stride, _dev(hist_len, "hist_len", torch.int32),
+        _dev(hist_rows, "hist_rows", torch.int32) if hist_rows is not None else None, B,
+        _dev(drafts, "drafts", torch.int32) if drafts.numel() else None, drafts.shape[1],
+        _dev(accepted, "accepted", torch.int32),
+        _dev(token, "token", torch.int32), n, max_drafts, _dev(d, "drafts", torch.int32),
+        _dev(nn, "n_out", torch.int32), _stream(stream)), "gg_history_append_draft")
+    return d, nn

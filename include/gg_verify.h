@@ -313,6 +313,29 @@ gg_status_t gg_ngram_draft(const int32_t* history, int hist_stride, const int32_
                            int num_seqs, int n, int max_drafts, int32_t* out_drafts,
                            int32_t* out_n, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * The step's emitted tokens appended to device-resident histories, then the next
+ * drafts: one launch after the acceptance, so a runner can draft on the device
+ * without copying histories. Replaces, on the device, the history update of
+ * emitSpeculative (internal/engine/serving.go:541-566: accepted drafts, then the
+ * corrected or bonus token) followed by maybeDraft's NGramDrafter.Draft over the
+ * whole history (serving.go:608-620, speculative.go:24-62). Sequence b:
+ *   row       = hist_rows ? hist_rows[b] : b (history row of the sequence)
+ *   appends     drafts[b][0, accepted[b]) and then token[b] (if >= 0) at
+ *               history[row][hist_len[row] ..]; hist_len[row] grows by that count
+ *   then        out_drafts[b][0, out_n[b]) = gg_ngram_draft of the updated row
+ * A row whose tokens would pass hist_stride (or whose length is negative) is left
+ * unchanged with hist_len[row] = -1 and out_n[b] = 0: the caller reseeds it.
+ *   history  : device int32[rows][hist_stride]; hist_len: device int32[rows]
+ *   drafts   : device int32[num_seqs][drafts_per_seq] (the step's drafts)
+ *   accepted, token: device int32[num_seqs] (gg_accept_greedy / gg_accept_rejection)
+ *   n, max_drafts: as gg_ngram_draft */
+gg_status_t gg_history_append_draft(int32_t* history, int hist_stride, int32_t* hist_len,
+                                    const int32_t* hist_rows, int num_seqs, const int32_t* drafts,
+                                    int drafts_per_seq, const int32_t* accepted, const int32_t* token,
+                                    int n, int max_drafts, int32_t* out_drafts, int32_t* out_n,
+                                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

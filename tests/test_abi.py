@@ -61,6 +61,12 @@ def test_invalid_arguments_return_status():
     assert "vocab" in _lib.last_error()
     assert lib.gg_ngram_draft(None, 0, None, 1, 10, 4, None, None, None) == Status.ERR_INVALID
     assert "n must be <= 9" in _lib.last_error()
+    assert lib.gg_history_append_draft(None, 16, None, None, 1, None, 0, None, None, 3, 4, None, None,
+                                       None) == Status.ERR_INVALID
+    assert "NULL buffer" in _lib.last_error()
+    assert lib.gg_history_append_draft(None, 16, None, None, 1, None, 65, None, None, 3, 4, None, None,
+                                       None) == Status.ERR_INVALID
+    assert "bad shape" in _lib.last_error()
     assert lib.gg_kv_k_layer_ptr(None, 0) is None
 
 

@@ -95,3 +95,93 @@ def test_ngram_random_mixed(gpu, seed):
     got = [d[b, :nn[b]].tolist() for b in range(B)]
     want = [ora.ngram_draft(x, n, k) for x in hists]
     assert got == want
+
+
+# ------------------------------------------------- history append + next drafts (one launch)
+
+def _emit(drafts_b, acc, tok):
+    """emitSpeculative's emitted tokens (internal/engine/serving.go:541-566): the accepted
+    drafts, then the corrected or bonus token (none when the device had no mass, tok < 0)."""
+    return list(drafts_b[:acc]) + ([int(tok)] if tok >= 0 else [])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_history_append_draft_matches_host_drafter(gpu, seed):
+    """gg_history_append_draft against the host flow it replaces: the emitted tokens
+    appended to each sequence's history, then NGramDrafter.Draft over the whole history.
+    Histories live in rows of a larger pool (hist_rows maps sequences to rows, unused rows
+    untouched), lengths on both sides of the LDS-resident limit, some rows full enough to
+    overflow (left unchanged, length -1, no drafts), a negative length staying -1, and two
+    steps in a row, the second drafting from the first one's output."""
+    r = np.random.default_rng(1300 + seed)
+    n = int(r.integers(2, 6))
+    k_in = int(r.integers(0, 7))
+    k = int(r.integers(1, 7))
+    rows_total, B = 24, int(r.integers(1, 16))
+    alphabet = int(r.choice([3, 7, 50]))
+    stride = int(r.choice([64, 3000, 13000]))
+    pool = np.zeros((rows_total, stride), np.int32)
+    lens = np.zeros(rows_total, np.int32)
+    for row in range(rows_total):
+        L = int(r.integers(0, stride + 1))
+        if r.random() < 0.2:
+            L = stride - int(r.integers(0, 3))  # about to overflow
+        pool[row, :L] = r.integers(0, alphabet, L)
+        lens[row] = L
+    lens[int(r.integers(0, rows_total))] = -1
+    hist_rows = r.permutation(rows_total)[:B].astype(np.int32)
+    dev_pool, dev_lens = torch.from_numpy(pool).cuda(), torch.from_numpy(lens).cuda()
+    host = [pool[row, :max(lens[row], 0)].tolist() if lens[row] >= 0 else None for row in range(rows_total)]
+    drafts = r.integers(0, alphabet, (B, k_in)).astype(np.int32)
+    for step in range(2):
+        acc = np.array([int(r.integers(0, k_in + 1)) for _ in range(B)], np.int32)
+        tok = r.integers(-1, alphabet, B).astype(np.int32)
+        say(f"history append+draft seed {seed} step {step}: n={n} k_in={k_in} k={k} B={B} stride={stride}")
+        d, nn = gv.history_append_draft(dev_pool, dev_lens, torch.from_numpy(drafts).cuda(),
+                                        torch.from_numpy(acc).cuda(), torch.from_numpy(tok).cuda(), n, k,
+                                        hist_rows=torch.from_numpy(hist_rows).cuda())
+        torch.cuda.synchronize()
+        d, nn = d.cpu().numpy(), nn.cpu().numpy()
+        for b in range(B):
+            row = int(hist_rows[b])
+            emitted = _emit(drafts[b], int(acc[b]), int(tok[b]))
+            if host[row] is None or len(host[row]) + len(emitted) > stride:
+                host[row] = None
+                assert nn[b] == 0
+                continue
+            host[row] = host[row] + emitted
+            assert d[b, :nn[b]].tolist() == ora.ngram_draft(host[row], n, k), (b, row)
+        got_lens = dev_lens.cpu().numpy()
+        got_pool = dev_pool.cpu().numpy()
+        for row in range(rows_total):
+            if host[row] is None:
+                assert got_lens[row] == -1
+            else:
+                assert got_lens[row] == len(host[row])
+                assert got_pool[row, :len(host[row])].tolist() == host[row]
+        # The next step verifies this step's drafts (padded to k_in with zeros).
+        nd = np.zeros((B, k_in), np.int32)
+        for b in range(B):
+            m = min(int(nn[b]), k_in)
+            nd[b, :m] = d[b, :m]
+        drafts = nd
+
+
+def test_history_append_draft_identity_rows(gpu):
+    """hist_rows NULL: sequence b is row b; a sequence with nothing accepted and no token
+    appends nothing and drafts from its history as gg_ngram_draft does."""
+    say("history append+draft identity rows")
+    h = np.array([[1, 2, 3, 1, 2, 0, 0, 0], [5, 5, 5, 5, 0, 0, 0, 0]], np.int32)
+    ln = np.array([5, 4], np.int32)
+    drafts = np.array([[3, 9], [7, 7]], np.int32)
+    acc = np.array([1, 0], np.int32)
+    tok = np.array([1, -1], np.int32)
+    hp, lp = torch.from_numpy(h).cuda(), torch.from_numpy(ln).cuda()
+    d, nn = gv.history_append_draft(hp, lp, torch.from_numpy(drafts).cuda(), torch.from_numpy(acc).cuda(),
+                                    torch.from_numpy(tok).cuda(), 3, 4)
+    torch.cuda.synchronize()
+    assert lp.cpu().tolist() == [7, 4]
+    assert hp.cpu().numpy()[0, :7].tolist() == [1, 2, 3, 1, 2, 3, 1]
+    d, nn = d.cpu().numpy(), nn.cpu().numpy()
+    assert d[0, :nn[0]].tolist() == ora.ngram_draft([1, 2, 3, 1, 2, 3, 1], 3, 4)
+    assert d[1, :nn[1]].tolist() == ora.ngram_draft([5, 5, 5, 5], 3, 4)
