@@ -212,6 +212,19 @@ func NGramDraft(history unsafe.Pointer, stride int, histLen unsafe.Pointer, B, n
 	return ggErr("gg_ngram_draft", st)
 }
 
+// HistoryAppendDraft appends each sequence's emitted tokens (drafts[b][:accepted[b]],
+// then token[b]) to its device history row (rows[b], or b when rows is nil) and drafts
+// the next step from it: next device int32[B][K], nNext device int32[B]. A row the
+// tokens would overflow gets length -1 and no drafts.
+func HistoryAppendDraft(history unsafe.Pointer, stride int, histLen, rows unsafe.Pointer, B int,
+	drafts unsafe.Pointer, kIn int, accepted, token unsafe.Pointer, n, K int, next, nNext unsafe.Pointer,
+	stream unsafe.Pointer) error {
+	st := C.gg_history_append_draft((*C.int32_t)(history), C.int(stride), (*C.int32_t)(histLen),
+		(*C.int32_t)(rows), C.int(B), (*C.int32_t)(drafts), C.int(kIn), (*C.int32_t)(accepted),
+		(*C.int32_t)(token), C.int(n), C.int(K), (*C.int32_t)(next), (*C.int32_t)(nNext), stream)
+	return ggErr("gg_history_append_draft", st)
+}
+
 func AcceptGreedyWorkspace(B, K, V int) uintptr {
 	return uintptr(C.gg_accept_greedy_workspace_size(C.int(B), C.int(K), C.int(V)))
 }

@@ -49,6 +49,12 @@ type Config struct {
 	TopP        float32
 	Rejection   bool // speculative sampling; false: greedy Verify + argmax
 	Seed        int64
+	// Device drafting (drafts.go): each sequence's history kept on the device and the
+	// next step drafted there after the acceptance, served through Drafts.
+	DeviceDrafts  bool
+	NGramN        int // the engine's n-gram size (NewNGramDrafter)
+	HistoryStride int // longest history kept on the device (0: the warm-up MaxSeqLen)
+	HistoryRows   int // sequences with a device history (0: 4 x the warm-up batch)
 }
 
 // Runner implements backend.Runner (internal/backend/runner.go:84-93) and
@@ -66,6 +72,7 @@ type Runner struct {
 
 	maxB, maxR, maxBlocks int
 	hq, hkv, d, vocab     int
+	drafts                *deviceDrafts // nil without DeviceDrafts
 
 	// Device buffers (allocated once at Warmup).
 	dIn                       unsafe.Pointer // the packed int32 inputs + float uniforms, one upload
@@ -97,15 +104,18 @@ func New(model Model, cfg Config) (*Runner, error) {
 }
 
 // Input layout of one step (int32 words): tokens, positions, slots [B*R]; ctx, rows,
-// n_drafts [B]; tables [B*maxBlocks]; drafts [B*K]; then float32 uniforms [B*R].
-type inLayout struct{ tokens, positions, slots, ctx, rows, tables, drafts, nDrafts, uniforms, words int }
+// n_drafts, history rows [B]; tables [B*maxBlocks]; drafts [B*K]; then float32 uniforms
+// [B*R].
+type inLayout struct {
+	tokens, positions, slots, ctx, rows, tables, drafts, nDrafts, histRows, uniforms, words int
+}
 
 func layout(B, R, MB int) inLayout {
 	var l inLayout
 	off := 0
 	take := func(n int) int { o := off; off += n; return o }
 	l.tokens, l.positions, l.slots = take(B*R), take(B*R), take(B*R)
-	l.ctx, l.rows, l.nDrafts = take(B), take(B), take(B)
+	l.ctx, l.rows, l.nDrafts, l.histRows = take(B), take(B), take(B), take(B)
 	l.tables, l.drafts = take(B*MB), take(B*(R-1))
 	l.uniforms = take(B * R)
 	l.words = off
@@ -146,6 +156,16 @@ func (r *Runner) Warmup(_ context.Context, p backend.WarmupProfile) error {
 	if r.hIn, err = hostAlloc(r.inBytes); err == nil {
 		r.hDec, err = hostAlloc(uintptr(2*B) * 4)
 	}
+	if err == nil && r.cfg.DeviceDrafts {
+		stride, rows := r.cfg.HistoryStride, r.cfg.HistoryRows
+		if stride <= 0 {
+			stride = p.MaxSeqLen
+		}
+		if rows <= 0 {
+			rows = 4 * B
+		}
+		r.drafts, err = newDeviceDrafts(r.cfg.NGramN, r.cfg.MaxDrafts, stride, rows, B)
+	}
 	if err != nil {
 		r.release()
 	}
@@ -161,6 +181,9 @@ func at(base unsafe.Pointer, word int) unsafe.Pointer { return unsafe.Add(base, 
 func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepOutput, error) {
 	for _, p := range batch.IsPrefill {
 		if p {
+			if r.drafts != nil {
+				r.drafts.prefill(batch)
+			}
 			return r.model.Prefill(ctx, batch)
 		}
 	}
@@ -189,6 +212,12 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 		u[i] = r.rng.Float32()
 	}
 	s := r.stream
+	histRows := i32(r.hIn, l.histRows, B)
+	if r.drafts != nil { // the current tokens into the histories; rows seeded where needed
+		if err := r.drafts.prepare(in, batch.SequenceIDs, histRows, s); err != nil {
+			return nil, err
+		}
+	}
 	if err := copyH2D(r.dIn, r.hIn, uintptr(l.words)*4, s); err != nil {
 		return nil, err
 	}
@@ -236,6 +265,11 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 	if err != nil {
 		return nil, err
 	}
+	if r.drafts != nil { // emitted tokens appended on the device, next drafts computed there
+		if err := r.drafts.launch(d(l.histRows), d(l.drafts), B, K, acc, tok, s); err != nil {
+			return nil, err
+		}
+	}
 	if err := copyD2H(r.hDec, r.dDec, uintptr(2*B)*4, s); err != nil {
 		return nil, err
 	}
@@ -243,6 +277,9 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 		return nil, err
 	}
 	hAcc, hTok := i32(r.hDec, 0, B), i32(r.hDec, B, B)
+	if r.drafts != nil {
+		r.drafts.finish(in, batch.SequenceIDs, histRows, hAcc, hTok)
+	}
 	out := &backend.StepOutput{
 		Logits:            make([][]float32, B),
 		LogitsPerPosition: make([][][]float32, B),
@@ -280,6 +317,10 @@ func (r *Runner) release() {
 	hostFree(r.hIn)
 	hostFree(r.hDec)
 	r.hIn, r.hDec = nil, nil
+	if r.drafts != nil {
+		r.drafts.close()
+		r.drafts = nil
+	}
 }
 
 func (r *Runner) Close() error {

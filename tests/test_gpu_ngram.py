@@ -185,3 +185,63 @@ def test_history_append_draft_identity_rows(gpu):
     d, nn = d.cpu().numpy(), nn.cpu().numpy()
     assert d[0, :nn[0]].tolist() == ora.ngram_draft([1, 2, 3, 1, 2, 3, 1], 3, 4)
     assert d[1, :nn[1]].tolist() == ora.ngram_draft([5, 5, 5, 5], 3, 4)
+
+
+def test_device_drafter_serves_the_engine_drafts(gpu):
+    """The runner-side device drafting flow (gollmgo_amd/drafting.py, the twin of the Go
+    runner's drafts.go) driven by a simulated engine over many steps: prompts recorded at
+    prefill (one sequence chunked, one never seen), each step's current token, the device
+    decision's emitted tokens, fewer device rows than sequences (eviction and reseeding),
+    and a sequence rolled back by two tokens. Whenever the runner answers
+    Drafts(seq, len(history)), its drafts equal NGramDrafter.Draft over the engine's
+    history (the oracle's restatement); otherwise the engine drafts on the host."""
+    from gollmgo_amd.drafting import DeviceDrafter
+    say("device drafter flow")
+    r = np.random.default_rng(77)
+    n, K, alphabet = 3, 4, 6
+    S = 10
+    dd = DeviceDrafter(n, K, stride=600, rows=6, max_batch=S)
+    hist = {}
+    for sid in range(S):
+        prompt = r.integers(0, alphabet, int(r.integers(5, 60))).tolist()
+        hist[sid] = prompt
+        if sid == 9:
+            continue  # the runner never sees this prefill: host drafts only
+        if sid == 3:  # chunked prefill
+            h = len(prompt) // 2
+            dd.prefill([sid], [prompt[:h]], [list(range(h))])
+            dd.prefill([sid], [prompt[h:]], [list(range(h, len(prompt)))])
+        else:
+            dd.prefill([sid], [prompt], [list(range(len(prompt)))])
+        hist[sid].append(int(r.integers(0, alphabet)))  # the token sampled from the prefill logits
+    hist[9].append(int(r.integers(0, alphabet)))
+    device_answers = 0
+    for step in range(40):
+        active = sorted(r.choice(S, size=int(r.integers(3, 9)), replace=False).tolist())
+        if step == 20:
+            hist[active[0]] = hist[active[0]][:-2]  # a rollback: the runner's mirror diverges
+        drafts = np.zeros((len(active), K), np.int32)
+        nd = np.zeros(len(active), np.int32)
+        for b, sid in enumerate(active):
+            want = ora.ngram_draft(hist[sid], n, K)
+            got = dd.drafts(sid, len(hist[sid]))
+            if got is not None:
+                assert got == want, (step, sid)
+                device_answers += 1
+            d = got if got is not None else want
+            drafts[b, :len(d)] = d
+            nd[b] = len(d)
+        cur = [hist[sid][-1] for sid in active]
+        pos = [len(hist[sid]) - 1 for sid in active]
+        rows = dd.prepare(active, cur, pos)
+        acc = np.array([int(r.integers(0, nd[b] + 1)) for b in range(len(active))], np.int32)
+        tok = r.integers(0, alphabet, len(active)).astype(np.int32)
+        next_d, next_n = dd.launch(rows, torch.from_numpy(drafts).cuda(), torch.from_numpy(acc).cuda(),
+                                   torch.from_numpy(tok).cuda())
+        torch.cuda.synchronize()
+        dd.finish(active, rows, drafts, nd, acc, tok, next_d.cpu().numpy(), next_n.cpu().numpy())
+        for b, sid in enumerate(active):  # emitSpeculative
+            hist[sid] = hist[sid] + drafts[b, :acc[b]].tolist() + [int(tok[b])]
+    print(f"  device answers: {device_answers}")
+    assert device_answers > 40
+    assert dd.drafts(9, len(hist[9])) is None
