@@ -108,14 +108,19 @@ struct AttnPlan {
 // LPT schedule: most sequences the plan kernel ranks (one per thread).
 constexpr int kLptMaxSeqs = 1024;
 // LPT piece length: at most T = ceil(C * num / (slots * den)) chunks for C chunks of work
-// over `slots` resident workgroups, num/den = 3/2 of the mean slot load when the
+// over `slots` resident workgroups, num/den = 8/5 of the mean slot load when the
 // (sequence, kv head) items fill the slots and 4/3 when they are fewer. Measured on MI355X
-// (attention µs at factors 1 / 4/3 / 3/2 / 7/4, the merge inside the main launch):
-// config 3 (items = slots) 136.5 / 133.4 / 126.9 / 129.2; config 2 (items = slots / 2)
-// 81.8 / 73.3 / 76.6 / 77.2; config 5 (items = 2 slots) within 0.3 µs at every factor.
+// with the merge inside the launch, attention µs (the call with its append, one layer,
+// mean over eight seeded layouts of each config's context distribution):
+//   config-3 layouts (items = slots), f = 3/2 / 8/5 / 13/8 / 5/3 / 17/10:
+//     131.0 / 128.4 / 129.1 / 130.3 / 130.8 (8/5 the fastest on 7 of the 8 layouts);
+//   config-2 layouts (items = slots / 2), f = 6/5 / 5/4 / 4/3 / 7/5:
+//     70.6 / 67.3 / 64.3 / 64.1;
+//   config 5 (items = 2 slots) within 0.3 µs at every factor.
 // Longer pieces split fewer items; with fewer items than slots the long items must be cut
-// finer to occupy every slot.
-constexpr int kLptPieceNum = 3, kLptPieceDen = 2;            // items >= slots
+// finer to occupy every slot. The factor is a tuned constant; the time moves in steps as
+// items cross piece boundaries.
+constexpr int kLptPieceNum = 8, kLptPieceDen = 5;            // items >= slots
 constexpr int kLptPieceNumFew = 4, kLptPieceDenFew = 3;      // items < slots
 __host__ __device__ constexpr bool lpt_few_items(int slots, int num_seqs, int num_kv_heads) {
     return num_seqs * num_kv_heads < slots;
