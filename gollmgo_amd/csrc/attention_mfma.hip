@@ -999,10 +999,11 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
 
 // ---- LPT schedule: pieces of at most about the mean slot load, longest first ----
 //
-// Items longer than T = ceil(total chunks / resident slots) are cut into equal pieces of
-// at most T chunks. attn_lpt_plan_kernel orders the pieces by size, descending (ties:
-// sequence, then piece, then kv head), and workgroup p of the main launch runs piece p:
-// dispatched in order, the longest pieces start first and the shortest fill the tail.
+// Items longer than T = ceil(f * total chunks / resident slots) are cut into equal pieces
+// of at most T chunks. attn_lpt_plan_kernel orders the pieces by size, descending (ties:
+// sequence, then piece, then kv head), and the main launch runs them in that order (with
+// few items the first round pairs long and shorter pieces per CU, lpt_slot): dispatched in
+// order, the longest pieces start first and the shortest fill the tail.
 // The last piece of a split item to finish merges the item's partial records
 // (lpt_merge_if_last), so the schedule is one launch. Its records are written and read
 // with device-scope stores and loads; a device-scope fence instead would write back or
@@ -1016,6 +1017,19 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
 //   [16 + 4R + 2B + b*Hkv + h]  merge counter of (sequence b, kv head h)
 // Pieces of sequence b are first + j*Hkv + kvh.
 __device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
+// Workgroup of the piece of rank r (and, as an involution, rank of workgroup r). While the
+// (sequence, kv head) items do not outnumber the S slots: over the first W = min(S,
+// pieces) ranks, ranks [W/2, W) are reversed, so workgroups w and w + W/2 get ranks w and
+// W - 1 - w. Dispatched round-robin, those two land on one CU as its first two slots,
+// which then hold a long and a shorter piece instead of two long ones. Measured, same box:
+// config 2 (items = S/2) 73.3 -> 71.1 µs; over eight seeded config-3 layouts (items = S)
+// the mean 127.2 -> 126.1 µs and the worst layout 136.8 -> 129.4 µs; config 5 (items =
+// 2S) 128.3 -> 129.2 µs, so more items than slots keep the plain order. Records stay
+// indexed by rank.
+__device__ __forceinline__ int lpt_slot(int r, int S, int total, bool pair) {
+    const int W = min(S, total);
+    return (pair && r >= W / 2 && r < W) ? W / 2 + (W - 1 - r) : r;
+}
 __device__ __forceinline__ int* lpt_seq(int* plan, int recs) { return plan + 16 + 4 * recs; }
 // Merge counters, one per (sequence, kv head): pieces of a split item that have written
 // their records. The plan clears them; the piece that merges an item clears its counter.
@@ -1082,7 +1096,9 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     for (int j = 0; j < np; ++j) {
         const int c0 = (int)((long long)j * nch / np), c1 = (int)((long long)(j + 1) * nch / np);
         const int t0 = c0 * tok, t1 = min(c1 * tok, ctx);
-        for (int h = 0; h < Hkv; ++h) table[pos + j * Hkv + h] = make_int4(b, h | (np << 16), t0, t1);
+        for (int h = 0; h < Hkv; ++h)
+            table[lpt_slot(pos + j * Hkv + h, slots, (int)total, B * Hkv <= slots)] =
+                make_int4(b, h | (np << 16), t0, t1);
     }
     // Entries past the last piece tell their workgroups to exit.
     for (int q = (int)total + b; q < recs; q += B) table[q] = make_int4(-1, 0, 0, 0);
@@ -1138,8 +1154,8 @@ __device__ void lpt_merge_if_last(const AttnArgs& a, int Hkv, int b, int kvh, in
     if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next layer
 }
 
-// Workgroup p computes piece p of the plan (exits past the last piece); the last piece of a
-// split item to finish merges it.
+// Workgroup p computes the piece at table entry p (exits past the last piece); the last
+// piece of a split item to finish merges it.
 template <gg_dtype_t DT, int NT>
 __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
     const int p = blockIdx.x;
@@ -1151,7 +1167,8 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     const int b = e.x;
     if (b < 0) return;  // past the last piece
     const int kvh = e.y & 0xffff, np = e.y >> 16;
-    const PieceDesc d{b, kvh, e.z, e.w, -1, np > 1 ? p : -1};
+    const PieceDesc d{b, kvh, e.z, e.w, -1,
+                      np > 1 ? lpt_slot(p, a.sk_grid, a.plan[0], a.num_seqs * kv.Hkv <= a.sk_grid) : -1};
     PieceIn<DT> in;
     DeferredRows ap;
     start_piece<DT>(a, kv, d, in, &ap);
