@@ -584,9 +584,6 @@ __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, 
                                                RowPick* __restrict__ pick, uint2* __restrict__ cand,
                                                u64* __restrict__ seg_keep) {
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    float x[32];
-    int idx[32];
-    load_seg<DT>(lp, V, seg, vec_ok, x, idx);
     __shared__ u64 red[kSegThreads / 64];
     __shared__ int s_hits[kSegThreads / 64];
     __shared__ int s_base;
@@ -595,19 +592,28 @@ __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, 
     const float ms = seg_max[(size_t)row * nseg + seg];
     const int cbm = cb_abs(m, inv_t);
     // Above the boundary bin: kept (weights summed exactly in a double); in it: gathered
-    // (a bit mask per thread). No per-element branch: the weight is computed for every
-    // element and selected.
+    // (a bit mask per thread, bit k for load_seg's element k). No per-element branch: the
+    // weight is computed for every element and selected. The thread's 32 logits are taken
+    // in two halves of 16, so fewer registers are live and more waves fit per SIMD.
     double kd = 0.0;
     uint32_t hits = 0;
     if (cbin >= 0 && finite_f(ms)) {
+#pragma unroll 1
+        for (int half = 0; half < 2; ++half) {
+            float xa[8], xb[8];
+            const int e0 = seg * kSegElems + 2 * half * 2048 + 8 * (int)threadIdx.x;
+            load8<DT>(lp, V, e0, vec_ok, xa);
+            load8<DT>(lp, V, e0 + 2048, vec_ok, xb);
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            const bool fin = finite_f(x[k]);
-            const float xv = fin ? x[k] : -INFINITY;
-            const int rb = row_bin(xv, cbm, inv_t);
-            const float w = gg_weight_f(xv, ms, inv_t);
-            kd += rb < cbin ? (double)w : 0.0;
-            hits |= (uint32_t)(fin && rb == cbin) << k;
+            for (int k = 0; k < 16; ++k) {
+                const float xk = k < 8 ? xa[k] : xb[k - 8];
+                const bool fin = finite_f(xk);
+                const float xv = fin ? xk : -INFINITY;
+                const int rb = row_bin(xv, cbm, inv_t);
+                const float w = gg_weight_f(xv, ms, inv_t);
+                kd += rb < cbin ? (double)w : 0.0;
+                hits |= (uint32_t)(fin && rb == cbin) << (16 * half + k);
+            }
         }
     }
     u64 keep = (u64)kd;
