@@ -184,7 +184,7 @@ MFMA_SHAPES = [
     # (B, R, Hq, H, ctx) with D=128, bs=16 -> MFMA path (G*R <= 64)
     (3, 5, 24, 8, [40, 700, 1500]),          # 3B geometry, 1 row tile
     (4, 6, 32, 8, [100, 1030, 2047, 64]),    # 8B geometry, 2 row tiles
-    (2, 9, 32, 8, [5000, 777]),              # config-4 geometry, 3 row tiles (stream-K)
+    (2, 9, 32, 8, [5000, 777]),              # config-4 geometry, 3 row tiles (stream-K: few items)
     (32, 9, 32, 8, [37 * i % 700 + 20 for i in range(32)]),  # 3 row tiles, LPT pieces
     (2, 16, 16, 4, [300, 129]),              # 4 row tiles
     (2, 1, 8, 8, [31, 65]),                  # decode-only (R=1)
@@ -478,6 +478,22 @@ def test_attention_random_lpt_cases(gpu, seed):
     c = dict(dt=dt, B=B, R=R, Hq=H * G, H=H, D=128, bs=16, ctx=ctx, src="bf16", seed=seed, q_dt="bf16",
              row_counts=rows)
     say(f"attention random LPT case {seed}: dt={dt} B={B} R={R} G={G} rows={'ragged' if rows else 'all'}")
+    err = run_attention_case(**c)
+    print(f"  rel err {err:.2e}")
+    assert err <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt,long_ctx", [("fp8", 24000), ("bf16", 9000), ("int8", 16000)])
+def test_attention_lpt_item_split_many_ways(gpu, dt, long_ctx):
+    """LPT with one long sequence among short ones: its items are cut into many pieces
+    (tens), and the piece of each item that finishes last merges all of their records
+    inside the launch. Every sequence against the oracle."""
+    r = np.random.default_rng(3100 + long_ctx)
+    B = 40
+    ctx = [int(x) for x in r.integers(32, 300, B)]
+    ctx[int(r.integers(0, B))] = long_ctx
+    c = dict(dt=dt, B=B, R=6, Hq=32, H=8, D=128, bs=16, ctx=ctx, src="bf16", seed=long_ctx, q_dt="bf16")
+    say(f"attention LPT many-piece split: dt={dt} long context {long_ctx}")
     err = run_attention_case(**c)
     print(f"  rel err {err:.2e}")
     assert err <= TOL[dt]
