@@ -164,9 +164,8 @@ def main():
     # a step: computed once per step (gg_verify_attention_plan), used by every layer.
     use_plan = cfg.partition == 0
     # The draft rows' KV append goes through the attention entry point
-    # (gg_verify_append_attention_planned; not for PER_BLOCK INT8, whose block scales need
-    # gg_kv_append).
-    fused = use_plan and cfg.kv_dtype != "int8" and not args.separate_append
+    # (gg_verify_append_attention_planned; PER_BLOCK INT8 pools included).
+    fused = use_plan and not args.separate_append
 
     def step(record: bool):
         if hist is not None:

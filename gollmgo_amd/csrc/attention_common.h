@@ -285,8 +285,84 @@ __device__ __forceinline__ void append_write_k(const KVView& kv, const AppendByt
 __device__ __forceinline__ void append_store(const AttnArgs& a, const KVView& kv, const AppendItem& it) {
     if (it.live) append_write(kv, append_encode(a, kv, it));
 }
+// PER_BLOCK INT8: rows [jr0, jr1) of item (b, kvh), all landing in one block, by a whole
+// workgroup, with gg_kv_append's rule for a run of rows in one block (append_int8_block in
+// kv_append.hip): the amax of the rows' K and V over rows and dims, the block's new scale
+// max(old, fp16(amax / 127)) (old = 0 when the rows start the block), the rows quantised
+// with it, the rows already in the block re-quantised when the scale grew, the scale
+// published. A block outside the pool is skipped.
+__device__ __forceinline__ void append_int8_run(const AttnArgs& a, const KVView& kv, int b, int kvh, int ctx,
+                                                int nrows, int jr0, int jr1) {
+    __shared__ float s_red[2][16];
+    const int D = kv.D, bs = kv.bs;
+    const int pos0 = ctx - nrows + jr0;
+    const int blk = a.block_tables[(size_t)b * a.max_blocks + pos0 / bs];
+    if (blk < 0 || blk >= kv.num_blocks) return;  // (uniform)
+    const int lead_off = pos0 % bs;
+    const int nel = (jr1 - jr0) * D;
+    auto src_at = [&](int i) { return (((size_t)b * a.rows + jr0 + i / D) * kv.Hkv + kvh) * D + i % D; };
+    float mk = 0.f, mv = 0.f;
+    for (int i = threadIdx.x; i < nel; i += blockDim.x) {
+        const float kx = fabsf(load_as_f32(a.k_new, a.new_dtype, src_at(i)));
+        const float vx = fabsf(load_as_f32(a.v_new, a.new_dtype, src_at(i)));
+        mk = fmaxf(mk, kx == kx ? kx : 0.f);
+        mv = fmaxf(mv, vx == vx ? vx : 0.f);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        mk = fmaxf(mk, __shfl_xor(mk, o));
+        mv = fmaxf(mv, __shfl_xor(mv, o));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_red[0][threadIdx.x >> 6] = mk;
+        s_red[1][threadIdx.x >> 6] = mv;
+    }
+    __syncthreads();
+    mk = mv = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+        mk = fmaxf(mk, s_red[0][w]);
+        mv = fmaxf(mv, s_red[1][w]);
+    }
+    __syncthreads();  // (s_red is reused by the next run)
+    mk = fminf(mk, 3.0e38f);
+    mv = fminf(mv, 3.0e38f);
+    uint16_t* ksc = const_cast<uint16_t*>(kv.k_blk_scale);
+    uint16_t* vsc = const_cast<uint16_t*>(kv.v_blk_scale);
+    const size_t si = (size_t)blk * kv.Hkv + kvh;
+    const float k_old = lead_off == 0 ? 0.f : f16_bits_to_f32(ksc[si]);
+    const float v_old = lead_off == 0 ? 0.f : f16_bits_to_f32(vsc[si]);
+    const float k_new = fmaxf(k_old, f16_bits_to_f32(f32_to_f16_rne_bits(mk / 127.0f)));
+    const float v_new = fmaxf(v_old, f16_bits_to_f32(f32_to_f16_rne_bits(mv / 127.0f)));
+    const float k_inv = k_new > 0.f ? 1.0f / k_new : 0.f;
+    const float v_inv = v_new > 0.f ? 1.0f / v_new : 0.f;
+    int8_t* kc = (int8_t*)const_cast<uint8_t*>(kv.kc);
+    int8_t* vc = (int8_t*)const_cast<uint8_t*>(kv.vc);
+    const size_t t0 = kv.tile0(blk, kvh);
+    for (int i = threadIdx.x; i < nel; i += blockDim.x) {
+        const int off = lead_off + i / D, d = i % D;
+        kc[t0 + (size_t)off * D + d] = f32_to_i8_sat(load_as_f32(a.k_new, a.new_dtype, src_at(i)) * k_inv);
+        vc[t0 + (size_t)d * bs + off] = f32_to_i8_sat(load_as_f32(a.v_new, a.new_dtype, src_at(i)) * v_inv);
+    }
+    if (lead_off > 0 && (k_new != k_old || v_new != v_old)) {  // rows already in the block
+        for (int i = threadIdx.x; i < lead_off * D; i += blockDim.x) {
+            const int t = i / D, d = i % D;
+            if (k_new != k_old) {
+                const size_t ki = t0 + (size_t)t * D + d;
+                kc[ki] = f32_to_i8_sat(((float)kc[ki] * k_old) * k_inv);
+            }
+            if (v_new != v_old) {
+                const size_t vi = t0 + (size_t)d * bs + t;
+                vc[vi] = f32_to_i8_sat(((float)vc[vi] * v_old) * v_inv);
+            }
+        }
+    }
+    if (threadIdx.x == 0) {
+        ksc[si] = f32_to_f16_rne_bits(k_new);
+        vsc[si] = f32_to_f16_rne_bits(v_new);
+    }
+}
+
 // Rows [j0, j1) of item (b, kvh) (clamped to the sequence's rows), by a whole workgroup,
-// before anything reads them.
+// before anything reads them. PER_BLOCK INT8 pools go block by block (append_int8_run).
 __device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView& kv, int b, int kvh, int j0 = 0,
                                                  int j1 = 1 << 30) {
     const int ctx = seq_keys(a, b, kv.bs);
@@ -294,6 +370,15 @@ __device__ __forceinline__ void append_item_rows(const AttnArgs& a, const KVView
     if (ctx <= 0 || nrows <= 0 || nrows > ctx) return;
     j0 = j0 < 0 ? 0 : j0;
     j1 = j1 > nrows ? nrows : j1;
+    if (kv.dt == GG_DTYPE_INT8) {
+        for (int j = j0; j < j1;) {
+            const int pos = ctx - nrows + j;
+            const int je = min(j1, j + (kv.bs - pos % kv.bs));  // the rows in pos's block
+            append_int8_run(a, kv, b, kvh, ctx, nrows, j, je);
+            j = je;
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < (j1 - j0) * (kv.D / 8); i += blockDim.x)
         append_store(a, kv, append_load(a, kv, b, kvh, ctx, nrows, j0, i));
 }

@@ -334,10 +334,12 @@ constexpr int kAppMax = 128;
 // chunks are multiples of 16 tokens, so a block's tokens (its K rows and its V columns)
 // are all read by one chunk, and so by one wave.
 //   - Rows inside the first chunks that `start` issues (short pieces), more rows than
-//     kAppMax, or no `ap` (the stream-K loop over pieces, whose registers are full):
-//     appended here by the whole workgroup, then a barrier orders the stores before the
-//     piece's loads (within a workgroup a barrier orders global stores before loads:
-//     same CU, write-through L1).
+//     kAppMax, no `ap` (the stream-K loop over pieces, whose registers are full), or a
+//     PER_BLOCK INT8 pool (a block's new rows re-scale the whole block; a block lies in one
+//     piece, since pieces are whole chunks): appended here by the whole workgroup, then a
+//     barrier orders the stores before the piece's loads (within a workgroup a barrier
+//     orders global stores before loads: same CU, write-through L1; for INT8, with
+//     workgroup-scope release and acquire fences around it).
 //   - Otherwise (the usual case: the rows are the item's last positions) their loads are
 //     issued here, after `start`, one work item per thread. attn_piece converts them into
 //     LDS before its Q-staging barrier; the wave that reads the chunk holding them patches
@@ -350,19 +352,29 @@ __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv,
                                             PieceIn<DT>& in, DeferredRows* ap) {
     constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
     if (ap) ap->j0 = ap->j1 = 0;
-    // (PER_BLOCK INT8 pools never carry rows here: their scale update needs gg_kv_append.)
-    if (DT != GG_DTYPE_INT8 && a.k_new) {
+    if (a.k_new) {
         const int ctx = seq_keys(a, d.b, kBS), nrows = seq_rows(a, d.b);
         const int first = ctx - nrows;
         const int j0 = max(0, d.t0 - first), j1 = min(nrows, d.t_end - first);
         if (nrows > 0 && nrows <= ctx && j0 < j1) {
             const int items = (j1 - j0) * (kD / 8);
-            if (ap && items <= kAppMax && first + j0 >= d.t0 + kWaves * kTok) {
+            if (DT != GG_DTYPE_INT8 && ap && items <= kAppMax && first + j0 >= d.t0 + kWaves * kTok) {
                 PieceIO<DT>::start(a, kv, d, in);
                 ap->j0 = j0;
                 ap->j1 = j1;
                 ap->it.live = false;
                 if ((int)threadIdx.x < items) ap->it = append_load(a, kv, d.b, d.kvh, ctx, nrows, j0, threadIdx.x);
+            } else if (DT == GG_DTYPE_INT8) {
+                // Re-quantised rows and the block scales are read back by other waves:
+                // workgroup-scope release and acquire around the barrier. (Issuing the
+                // piece's first chunks before the block update, when the rows lie past
+                // them, was slower: 121.4 -> 130.7 µs per call at config 4. Loads retire
+                // in order, so the update's small loads waited behind the chunks.)
+                append_item_rows(a, kv, d.b, d.kvh, j0, j1);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __syncthreads();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                PieceIO<DT>::start(a, kv, d, in);
             } else {
                 append_item_rows(a, kv, d.b, d.kvh, j0, j1);
                 __syncthreads();

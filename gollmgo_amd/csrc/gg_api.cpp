@@ -368,8 +368,6 @@ GG_API gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, con
     GG_CHECK_ARG(kv != nullptr, "gg_verify_append_attention_planned: kv is NULL");
     GG_CHECK_ARG(k_new && v_new, "gg_verify_append_attention_planned: NULL buffer");
     GG_CHECK_ARG(is_float_io(new_dtype), "gg_verify_append_attention_planned: k/v dtype must be F32/F16/BF16");
-    GG_CHECK_ARG(kv->scale_mode != GG_SCALE_PER_BLOCK,
-                 "gg_verify_append_attention_planned: PER_BLOCK INT8 pools append with gg_kv_append");
     GG_CHECK_ARG(kv->head_dim % 8 == 0 && (uintptr_t)k_new % 16 == 0 && (uintptr_t)v_new % 16 == 0,
                  "gg_verify_append_attention_planned: needs head_dim % 8 == 0 and 16-byte aligned k_new/v_new");
     return verify_attention_impl(kv, layer, q, q_dtype, out, out_dtype, ctx_lens, row_counts, block_tables,

@@ -204,6 +204,11 @@ __device__ __forceinline__ uint32_t f32x2_to_fp8e4m3_sat(float a, float b) {
 
 __device__ __forceinline__ uint8_t f32_to_fp8e4m3_sat(float f) { return (uint8_t)f32x2_to_fp8e4m3_sat(f, 0.f); }
 
+// fp16 bits of f, round to nearest even (the PER_BLOCK INT8 scales are fp16).
+__device__ __forceinline__ uint16_t f32_to_f16_rne_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
 // Symmetric int8: round-half-even, clamp to +-127 (kernels/gollmgo_model.cu:258-268).
 __device__ __forceinline__ int8_t f32_to_i8_sat(float f) {
     float r = __builtin_rintf(f);

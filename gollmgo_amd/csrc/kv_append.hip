@@ -225,10 +225,6 @@ void launch_vec(const AppendArgs& a, gg_dtype_t dst, hipStream_t s) {
 // 127)), the run's rows quantised with it, the rows already in the block re-quantised
 // when the scale grew, and the scale published. No atomics, no staging.
 
-__device__ __forceinline__ uint16_t f32_to_f16_rne_bits(float f) {
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
 __device__ __forceinline__ bool slot_ok(int s, long long num_slots) { return s >= 0 && s < num_slots; }
 
 __global__ void __launch_bounds__(256) append_int8_block_kernel(AppendArgs a) {

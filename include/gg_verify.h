@@ -223,8 +223,9 @@ gg_status_t gg_verify_attention_planned(gg_kv_t kv, int layer, const void* q, gg
  * gg_kv_append with those slots followed by gg_verify_attention_planned. No slot mapping
  * needs to be built, and on the MFMA path there is no extra launch: each attention
  * workgroup writes the rows of its own key range before it reads them (other shapes run
- * the append as a launch of its own first). PER_BLOCK INT8 pools are rejected (GG_ERR_INVALID):
- * their scale update needs gg_kv_append. */
+ * the append as a launch of its own first). PER_BLOCK INT8 pools follow gg_kv_append's
+ * block rule: the workgroup that reads a block with new rows first re-scales the block
+ * (new scale, the new rows, the old rows re-quantised when the scale grew). */
 gg_status_t gg_verify_append_attention_planned(gg_kv_t kv, int layer, const void* k_new, const void* v_new,
                                                gg_dtype_t new_dtype, const void* q, gg_dtype_t q_dtype,
                                                void* out, gg_dtype_t out_dtype, const int32_t* ctx_lens,

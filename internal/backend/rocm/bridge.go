@@ -150,7 +150,7 @@ func (c *KVCache) AttentionPlanned(layer int, q, out, ctxLens, rowCounts, blockT
 // AppendAttention appends the step's K/V rows of one layer (device [B*R][Hkv][D] bf16,
 // row b*R+j = row j of sequence b) and runs the planned attention in one call: the rows go
 // to key positions ctxLens[b]-rowCounts[b]+j through the block table, so no slot mapping
-// is needed. Not for PER_BLOCK INT8 pools (use Append + AttentionPlanned there).
+// is needed. PER_BLOCK INT8 pools included.
 func (c *KVCache) AppendAttention(layer int, kNew, vNew, q, out, ctxLens, rowCounts, blockTables unsafe.Pointer,
 	maxBlocks, B, R, Hq int, scale float32, ws unsafe.Pointer, wsBytes uintptr, stream unsafe.Pointer) error {
 	st := C.gg_verify_append_attention_planned(c.h, C.int(layer), kNew, vNew, C.GG_DTYPE_BF16, q,

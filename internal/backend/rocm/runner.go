@@ -229,22 +229,14 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 	if err := r.kv.Plan(d(l.ctx), d(l.rows), MB, B, R, r.hq, r.dAttnWS, r.attnWS, s); err != nil {
 		return nil, err
 	}
-	perBlock := r.cfg.KVScales == ScalePerBlock
 	for layer := 0; layer < r.model.NumLayers(); layer++ {
 		if err := r.model.QKV(layer, d(l.positions), r.dQ, r.dK, r.dV, s); err != nil {
 			return nil, err
 		}
-		if perBlock { // INT8 block scales are updated by gg_kv_append only
-			if err := r.kv.Append(layer, r.dK, r.dV, d(l.slots), B*R, s); err != nil {
-				return nil, err
-			}
-			err = r.kv.AttentionPlanned(layer, r.dQ, r.dOut, d(l.ctx), d(l.rows), d(l.tables), MB, B, R, r.hq,
-				scale, r.dAttnWS, r.attnWS, s)
-		} else {
-			err = r.kv.AppendAttention(layer, r.dK, r.dV, r.dQ, r.dOut, d(l.ctx), d(l.rows), d(l.tables), MB, B,
-				R, r.hq, scale, r.dAttnWS, r.attnWS, s)
-		}
-		if err != nil {
+		// The rows' K/V are appended inside the attention call (PER_BLOCK INT8 pools
+		// included: the workgroup that reads a block with new rows re-scales it first).
+		if err := r.kv.AppendAttention(layer, r.dK, r.dV, r.dQ, r.dOut, d(l.ctx), d(l.rows), d(l.tables), MB, B,
+			R, r.hq, scale, r.dAttnWS, r.attnWS, s); err != nil {
 			return nil, err
 		}
 		if err := r.model.Post(layer, r.dOut, s); err != nil {

@@ -779,23 +779,31 @@ def _fused_vs_separate(cid, dt, B, ctx, rc, corrupt=False):
             kv.append(0, k_new, v_new, torch.from_numpy(slots).cuda())
             kv.attention(0, q, out, keys, bt, 1 / math.sqrt(D), row_counts=rc_t, workspace=ws, planned=True)
         torch.cuda.synchronize()
-        results.append((kv.k_pool(0).cpu().numpy(), kv.v_pool(0).cpu().numpy(), out.cpu().numpy()))
+        sc = kv.scales(0) if dt in ("fp8", "int8") else (torch.zeros(1), torch.zeros(1))
+        results.append((kv.k_pool(0).cpu().numpy(), kv.v_pool(0).cpu().numpy(), out.cpu().numpy(),
+                        tuple(t.float().cpu().numpy() for t in sc)))
         kv.close()
-    (fk, fv, fo), (sk, sv, so) = results
+    (fk, fv, fo, fsc), (sk, sv, so, ssc) = results
     np.testing.assert_array_equal(fk, sk)
     np.testing.assert_array_equal(fv, sv)
+    for a_, b_ in zip(fsc, ssc):  # PER_HEAD scales as set; PER_BLOCK scales as the appends left them
+        np.testing.assert_array_equal(a_, b_)
     if rc:  # rows past a sequence's row count are not computed
         for b in range(B):
             fo[b, row_counts[b]:] = so[b, row_counts[b]:] = 0
     np.testing.assert_array_equal(fo, so)
 
 
-def test_append_attention_rejects_per_block_int8(gpu):
-    kv = make_cache("int8", 2, 128, 16, 8)
-    z = torch.zeros(2, 2, 128, device="cuda", dtype=torch.bfloat16)
-    q = torch.zeros(1, 2, 2, 128, device="cuda", dtype=torch.bfloat16)
-    ws = kv.attention_workspace(1, 2, 2, 1, 0)
-    with pytest.raises(Exception, match="PER_BLOCK"):
-        kv.append_attention(0, z, z, q, torch.zeros_like(q), torch.tensor([4], dtype=torch.int32, device="cuda"),
-                            torch.zeros(1, 1, dtype=torch.int32, device="cuda"), 0.1, ws)
-    kv.close()
+@pytest.mark.parametrize("cid,B,ctx,rc", [
+    (4, 8, ("uniform", 16384, 32768), False),     # config 4 shape: LPT, one CU slot per workgroup
+    (4, 16, ("uniform", 100, 2000), True),        # ragged row counts, runs starting mid-block
+    (4, 3, ("list", 15, 16, 33), False),          # stream-K, rows filling and opening blocks
+    (4, 24, ("list", *[16 * i + (i % 5) for i in range(1, 25)]), False),  # runs straddling blocks
+])
+def test_append_attention_fused_per_block_int8(gpu, cid, B, ctx, rc):
+    """PER_BLOCK INT8: gg_verify_append_attention_planned equals gg_kv_append with the
+    derived slots followed by the planned attention: pool bytes, block scales and outputs
+    bit for bit (a block's new rows re-scale it, and the rows already in it are
+    re-quantised when its scale grows)."""
+    say(f"fused append int8 cid={cid} B={B} ctx={ctx} rc={rc}")
+    _fused_vs_separate(cid, "int8", B, ctx, rc)
