@@ -1023,32 +1023,52 @@ struct RowView {
     int idx_cut;
 };
 
-// A sequence's decision and the view of its final row, written by decide_kernel.
+// A sequence's decision and the view of its final row, decided by decide_seq.
 struct SeqPlan {
     RowView v;
     SeqDecision d;
 };
 
+// The inputs of decide_seq, as the kernels that run it (one wave of theirs) receive them.
+struct DecideIn {
+    const void* logits;
+    const float* dprobs;
+    int K, V, nseg;
+    float inv_t;
+    int use_topp;
+    const int32_t* drafts;
+    const int32_t* n_drafts;
+    const float* uniforms;
+    const RowStats* stats;
+    const int* status;
+    const int* flag;
+    const float* seg_max;
+    const u64* seg_e;
+};
 // F: per sequence, one wave: the acceptance walk and the view of the final row. Without
 // top-p every row's values come from the segment maxima and sums; with top-p a row the
 // bounds decided keeps that outcome and a flagged row is tested on its exact nucleus.
+// Run by all 64 lanes of one wave (lane = threadIdx.x & 63); the result is uniform.
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(64) decide_kernel(const void* __restrict__ logits, const float* __restrict__ dprobs,
-                                                    int K, int V, int nseg, float inv_t, int use_topp,
-                                                    const int32_t* __restrict__ drafts,
-                                                    const int32_t* __restrict__ n_drafts,
-                                                    const float* __restrict__ uniforms,
-                                                    const RowStats* __restrict__ stats,
-                                                    const int* __restrict__ status, const int* __restrict__ flag,
-                                                    const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
-                                                    SeqPlan* __restrict__ plan) {
-    const int b = blockIdx.x;
+__device__ SeqPlan decide_seq(const DecideIn& in, int b) {
+    const void* __restrict__ logits = in.logits;
+    const float* __restrict__ dprobs = in.dprobs;
+    const int K = in.K, V = in.V, nseg = in.nseg, use_topp = in.use_topp;
+    const float inv_t = in.inv_t;
+    const int32_t* __restrict__ drafts = in.drafts;
+    const int32_t* __restrict__ n_drafts = in.n_drafts;
+    const float* __restrict__ uniforms = in.uniforms;
+    const RowStats* __restrict__ stats = in.stats;
+    const int* __restrict__ status = in.status;
+    const int* __restrict__ flag = in.flag;
+    const float* __restrict__ seg_max = in.seg_max;
+    const u64* __restrict__ seg_e = in.seg_e;
     const int R = K + 1;
     const int n = live_rows(n_drafts, b, K);
     // The rows' tests do not depend on each other, so they run together: groups of
     // g = 2^ceil(log2 nseg) lanes take one row each (lane s of a group reads segment s),
     // 64/g rows per pass; the walk stops at the first failed row.
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     int g = 1;
     while (g < nseg) g <<= 1;
     const int per_pass = 64 / g;
@@ -1107,7 +1127,19 @@ __global__ void __launch_bounds__(64) decide_kernel(const void* __restrict__ log
         v.lam = 0;
         v.idx_cut = 0x7fffffff;
     }
-    if (threadIdx.x == 0) plan[b] = SeqPlan{v, SeqDecision{a, a, residual}};
+    return SeqPlan{v, SeqDecision{a, a, residual}};
+}
+
+// Wave 0 of the block decides sequence b; the plan is returned to every thread.
+template <gg_dtype_t DT>
+__device__ __forceinline__ SeqPlan decide_in_block(const DecideIn& in, int b) {
+    __shared__ SeqPlan s_plan;
+    if (threadIdx.x < 64) {
+        const SeqPlan p = decide_seq<DT>(in, b);
+        if (threadIdx.x == 0) s_plan = p;
+    }
+    __syncthreads();
+    return s_plan;
 }
 
 // G (dense draft distributions only): per (sequence, segment) the residual weight sum of
@@ -1122,18 +1154,26 @@ __global__ void __launch_bounds__(64) decide_kernel(const void* __restrict__ log
 constexpr int kSumThreads = GG_SUM_THREADS;
 constexpr int kSumRuns = kSegElems / (kSumThreads * 8);
 static_assert(kSumRuns * kSumThreads * 8 == kSegElems, "segment = runs of eight logits per thread");
+// Every block decides its sequence itself (decide_seq, one wave); block 0 of the
+// sequence stores the plan for the draw.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
-    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
-    float inv_t, const int32_t* __restrict__ drafts, const float* __restrict__ seg_max,
-    const SeqPlan* __restrict__ plan, SegSum* __restrict__ seg_sum) {
+    DecideIn din, int vec_ok, SeqPlan* __restrict__ plan, SegSum* __restrict__ seg_sum) {
     const int seg = blockIdx.x, b = blockIdx.y;
+    const void* __restrict__ logits = din.logits;
+    const float* __restrict__ dprobs = din.dprobs;
+    const int K = din.K, V = din.V, nseg = din.nseg;
+    const float inv_t = din.inv_t;
+    const int32_t* __restrict__ drafts = din.drafts;
+    const float* __restrict__ seg_max = din.seg_max;
     const int R = K + 1;
     constexpr int kW = kSumThreads / 64;
     __shared__ u64 red64[kW];
-    const SeqDecision d = plan[b].d;
+    const SeqPlan sp = decide_in_block<DT>(din, b);
+    if (seg == 0 && threadIdx.x == 0) plan[b] = sp;
+    const SeqDecision d = sp.d;
     if (!d.residual) return;  // the bonus draw needs no residual
-    const RowView rv = plan[b].v;
+    const RowView rv = sp.v;
     const int row = b * R + d.row;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     const float* qrow = dprobs + ((size_t)b * K + d.row) * V;
@@ -1185,21 +1225,29 @@ __global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
 // passes it, u >= 1). In that segment thread k of 1024 owns the 8 consecutive elements
 // [8k, 8k+8): their integer weights (e, or rq) and a block scan find the element (or the
 // last non-zero one).
+// Without dense draft distributions (no residual launch) the block decides its sequence
+// itself (decide_seq); otherwise it reads the plan the residual launch stored.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
-    const void* __restrict__ logits, const float* __restrict__ dprobs, int K, int V, int nseg, int vec_ok,
-    float inv_t, int use_topp, const int32_t* __restrict__ drafts, const float* __restrict__ uniforms,
-    const float* __restrict__ seg_max, const u64* __restrict__ seg_e, const u64* __restrict__ seg_keep,
-    const SeqPlan* __restrict__ plan, const SegSum* __restrict__ seg_sum, int32_t* __restrict__ out_acc,
-    int32_t* __restrict__ out_tok) {
+    DecideIn din, int vec_ok, const u64* __restrict__ seg_keep, const SeqPlan* __restrict__ plan,
+    const SegSum* __restrict__ seg_sum, int32_t* __restrict__ out_acc, int32_t* __restrict__ out_tok) {
     const int b = blockIdx.x;
+    const void* __restrict__ logits = din.logits;
+    const float* __restrict__ dprobs = din.dprobs;
+    const int K = din.K, V = din.V, nseg = din.nseg, use_topp = din.use_topp;
+    const float inv_t = din.inv_t;
+    const int32_t* __restrict__ drafts = din.drafts;
+    const float* __restrict__ uniforms = din.uniforms;
+    const float* __restrict__ seg_max = din.seg_max;
+    const u64* __restrict__ seg_e = din.seg_e;
     const int R = K + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __shared__ int s_seg, s_mode, s_found, s_last_mode;
     __shared__ u128 s_t;
     __shared__ u64 s_wsum[kFindThreads / 64];
-    const SeqDecision d = plan[b].d;
-    const RowView rv = plan[b].v;
+    const SeqPlan sp = dprobs ? plan[b] : decide_in_block<DT>(din, b);
+    const SeqDecision d = sp.d;
+    const RowView rv = sp.v;
     const int row = b * R + d.row;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     const bool dense = d.residual && dprobs;
@@ -1413,6 +1461,10 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     const int K = max_drafts;
     const size_t eb = dtype_bytes(dt);
     const int vec_ok = ((vocab * eb) % 16 == 0) && (((uintptr_t)logits) % 16 == 0);
+    // The acceptance walk of each sequence runs inside the residual launch (dense q) or
+    // the draw launch (one-hot q), not as a launch of its own.
+    const DecideIn din{logits, q, K, vocab, nseg, inv_t, use_topp, drafts, n_drafts, uniforms,
+                       w.stats, w.status, w.flag, w.seg_max, w.seg_e};
 #define GG_REJ(DTV)                                                                                          \
     if (use_topp) {                                                                                          \
         seg_pass_kernel<DTV, true><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,  \
@@ -1439,16 +1491,9 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                                                              inv_t, n_drafts, w.seg_max,     \
                                                                              w.seg_e, nullptr);              \
     }                                                                                                        \
-    decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(logits, q, K, vocab, nseg, inv_t, use_topp, drafts, n_drafts,  \
-                                              uniforms, w.stats, w.status, w.flag, w.seg_max, w.seg_e,       \
-                                              w.plan);                                                       \
     if (q)                                                                                                   \
-        seg_residual_kernel<DTV><<<dim3(nseg, num_seqs), kSumThreads, 0, s>>>(logits, q, K, vocab, nseg,     \
-                                                                              vec_ok, inv_t, drafts,         \
-                                                                              w.seg_max, w.plan, w.seg_sum); \
-    seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(logits, q, K, vocab, nseg, vec_ok, inv_t,     \
-                                                               use_topp, drafts, uniforms, w.seg_max,        \
-                                                               w.seg_e, w.seg_keep, w.plan, w.seg_sum,       \
+        seg_residual_kernel<DTV><<<dim3(nseg, num_seqs), kSumThreads, 0, s>>>(din, vec_ok, w.plan, w.seg_sum); \
+    seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(din, vec_ok, w.seg_keep, w.plan, w.seg_sum,   \
                                                                out_acc, out_tok);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
