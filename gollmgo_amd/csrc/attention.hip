@@ -255,10 +255,11 @@ AttnPlan attn_plan(const KV* kv, int num_seqs, int rows, int num_q_heads, int ma
     const int nt = (G * rows + 15) / 16;
     const long long max_keys = (long long)max_blocks * kv->block_size;
     const long long items = (long long)num_seqs * kv->num_kv_heads;
-    const long long slots = (long long)device_cu_count() * attn_occupancy(nt);
+    const long long slots = (long long)device_cu_count() * attn_occupancy((int)dtype_bytes(kv->dtype), nt);
     // (With a merge launch of its own, LPT lost to stream-K at a quarter of the slots,
     // config 4: 164 vs 117 µs. With the merge inside the launch and pieces of 4/3 of the
-    // mean slot load it wins there: 110.3 vs 112.7 µs, same box.)
+    // mean slot load it wins there: 110.3 vs 112.7 µs, same box. At an eighth of the slots
+    // it loses: config 4 with two workgroups per CU, 120.2 vs 117.4 µs.)
     if (4 * items >= slots && num_seqs <= kLptMaxSeqs) return {ATTN_SCHED_LPT, 0};
     if (items >= slots && max_keys <= kMfmaMaxPartition)
         return {ATTN_SCHED_GRID, (int)((max_keys + 63) / 64 * 64)};

@@ -94,10 +94,22 @@ inline bool attn_mfma_supported(const KV* kv, int rows, int num_q_heads) {
             kv->dtype == GG_DTYPE_FP8_E4M3 || kv->dtype == GG_DTYPE_INT8);
 }
 
-// MFMA kernel workgroups (of four waves) per CU for a row-tile count: two while one
-// wave's registers fit half the file, else one. Shared by the launch bounds, the stream-K
-// grid (one resident wave of workgroups) and the schedule choice.
-__host__ __device__ constexpr int attn_occupancy(int nt) { return nt <= 2 ? 2 : 1; }
+// MFMA kernel workgroups (of four waves) per CU for a pool's element size and row-tile
+// count: two while one wave's registers fit half the file (one or two row tiles; three
+// row tiles of a 1-byte pool in 32-token chunks, 217-248 VGPRs), else one. Shared by the
+// launch bounds, the stream-K grid (one resident wave of workgroups) and the schedule
+// choice.
+__host__ __device__ constexpr int attn_occupancy(int elem_bytes, int nt) {
+    return nt <= 2 || (elem_bytes == 1 && nt == 3) ? 2 : 1;
+}
+
+// Tokens per MFMA chunk for a pool's element size and row-tile count. At one or two row
+// tiles a lane moves 256 B of K and V per chunk: 64 tokens of a 1-byte pool, 32 of a
+// 2-byte one. From three row tiles on, 1-byte pools take 32-token chunks as well, which
+// halves the chunk's K/V, score and P registers next to the three or four O tiles.
+__host__ __device__ constexpr int attn_chunk_tokens(int elem_bytes, int nt) {
+    return elem_bytes == 1 && nt <= 2 ? 64 : 32;
+}
 
 // How one verify_attention call is scheduled.
 struct AttnPlan {

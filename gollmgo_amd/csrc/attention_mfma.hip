@@ -27,6 +27,7 @@
 #include "attention_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace gg {
 #ifdef GG_TRACE
@@ -161,6 +162,13 @@ __device__ __forceinline__ uint4 mask_bytes16(uint4 v, int nvalid) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 // Zero the 2-byte elements at offsets >= nvalid of an 8-offset run starting at `first`.
+// Bytes of an 8-byte run that starts at offset `first`: offsets >= nvalid cleared.
+__device__ __forceinline__ uint2 mask_bytes8(uint2 v, int nvalid, int first) {
+    const int n = nvalid - first;
+    const uint32_t m0 = n >= 4 ? 0xFFFFFFFFu : (n <= 0 ? 0u : 0xFFFFFFFFu >> (8 * (4 - n)));
+    const uint32_t m1 = n >= 8 ? 0xFFFFFFFFu : (n <= 4 ? 0u : 0xFFFFFFFFu >> (8 * (8 - n)));
+    return make_uint2(v.x & m0, v.y & m1);
+}
 __device__ __forceinline__ uint4 mask_halves8(uint4 v, int nvalid, int first) {
     uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -184,22 +192,23 @@ __device__ __forceinline__ uint4 mask_halves8(uint4 v, int nvalid, int first) {
 // lane's P values are the consecutive offsets ob(g4) .. ob(g4) + 4*NS - 1 of one block,
 // which is exactly the A operand of P.V (k = 8*g4 + i' -> offset ob(g4) + 8*pv + i') and
 // one contiguous run of the dim-major V block.
-template <int kEB>
+template <int kEB, int TOK>
 struct Geo {
-    static constexpr int kTok = kEB == 1 ? 64 : 32;
+    static constexpr int kTok = TOK;
     static constexpr int kNS = kTok / 16;                 // S tiles (and blocks) per chunk
     static constexpr int kNPV = kNS / 2;                  // P.V MFMAs per dim tile
     static constexpr int kKVec = 32 * kEB / 16;           // 16-byte loads per lane per K tile
-    static constexpr int kVBytes = 8 * kNPV * kEB;        // V bytes per lane per dim tile (16)
+    static constexpr int kVBytes = 8 * kNPV * kEB;        // V bytes per lane per dim tile (16, or 8)
+    using VReg = std::conditional_t<kVBytes == 16, uint4, uint2>;
     __device__ static __forceinline__ int bq(int q) { return kTok == 64 ? q : (q >> 1); }
     __device__ static __forceinline__ int ob(int q) { return kTok == 64 ? 0 : 8 * (q & 1); }
 };
 
-template <int kEB>
+template <int kEB, int TOK>
 struct ChunkRegs {
-    using G = Geo<kEB>;
+    using G = Geo<kEB, TOK>;
     uint4 k[G::kNS][G::kKVec];
-    uint4 v[8];
+    typename G::VReg v[8];
     float ksc, vsc;  // INT8 pools: scales of the lane's V block, fetched with its V
 };
 
@@ -215,9 +224,9 @@ struct LaneBlocks {
 
 // What a piece needs to start streaming: its first chunk's K/V in flight and the block
 // ids of its first two chunks (PieceIO::start).
-template <gg_dtype_t DT>
+template <gg_dtype_t DT, int TOK>
 struct PieceIn {
-    ChunkRegs<PoolTraits<DT>::kEB> cur;
+    ChunkRegs<PoolTraits<DT>::kEB, TOK> cur;
     LaneBlocks bl_cur, bl_next;
 };
 
@@ -227,10 +236,10 @@ struct PieceDesc {
     int b, kvh, t0, t_end, part, rec;
 };
 
-template <gg_dtype_t DT>
+template <gg_dtype_t DT, int TOK>
 struct PieceIO {
     static constexpr int kEB = PoolTraits<DT>::kEB;
-    using Geom = Geo<kEB>;
+    using Geom = Geo<kEB, TOK>;
     static constexpr int kNS = Geom::kNS;
     static constexpr int kTok = Geom::kTok;
 
@@ -275,7 +284,7 @@ struct PieceIO {
     // K rows: lane supplies M index c16 of every tile. Loads are unconditional (missing
     // blocks read block 0); such tokens are always masked in S.
     __device__ static __forceinline__ void load_k(const KVView& kv, const LaneBlocks bl, int kvh,
-                                                  ChunkRegs<kEB>& rg) {
+                                                  ChunkRegs<kEB, TOK>& rg) {
         const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4, kq = c16 >> 2;
         const int blk = bl.k;
         const uint8_t* base =
@@ -290,7 +299,7 @@ struct PieceIO {
     // V: lane owns block bq(g4), dim dt*16 + c16, offsets ob(g4) .. ob(g4)+16/kEB-1 (zeroed
     // later when the block is missing or partly past the keys).
     __device__ static __forceinline__ void load_v(const KVView& kv, const LaneBlocks bl, int kvh,
-                                                  ChunkRegs<kEB>& rg) {
+                                                  ChunkRegs<kEB, TOK>& rg) {
         const int lane = threadIdx.x & 63, c16 = lane & 15, g4 = lane >> 4;
         const int blk = bl.v;
         if constexpr (DT == GG_DTYPE_INT8) {
@@ -304,13 +313,13 @@ struct PieceIO {
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             const int d = dt * 16 + c16;
-            rg.v[dt] = *(const uint4*)(base + (size_t)d * kBS * kEB);
+            rg.v[dt] = *(const typename Geom::VReg*)(base + (size_t)d * kBS * kEB);
         }
     }
     // Issue the first chunk of piece d (this wave's first chunk is chunk `wave`): the block
     // ids of its first two chunks, then the first chunk's K rows and V columns.
     __device__ static __forceinline__ void start(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
-                                                 PieceIn<DT>& in) {
+                                                 PieceIn<DT, TOK>& in) {
         const int wave_u = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
         in.bl_cur = chunk_blocks(a, kv, d.b, d.t0, d.t_end, wave_u);
         in.bl_next = chunk_blocks(a, kv, d.b, d.t0, d.t_end, wave_u + kWaves);
@@ -347,10 +356,12 @@ constexpr int kAppMax = 128;
 //     block's V tile back whole, and the K rows are stored after the loop. No load waits
 //     behind these stores (gfx950 counts stores in vmcnt, so a store issued ahead of a
 //     chunk's loads would hold up the wait for that chunk).
-template <gg_dtype_t DT>
+template <gg_dtype_t DT, int TOK>
 __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv, const PieceDesc& d,
-                                            PieceIn<DT>& in, DeferredRows* ap) {
-    constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
+                                            PieceIn<DT, TOK>& in, DeferredRows* ap) {
+    constexpr int kTok = TOK;
+    // The in-register patch of the chunk holding the rows needs 16-byte V runs.
+    constexpr bool kDefer = DT != GG_DTYPE_INT8 && Geo<PoolTraits<DT>::kEB, TOK>::kVBytes == 16;
     if (ap) ap->j0 = ap->j1 = 0;
     if (a.k_new) {
         const int ctx = seq_keys(a, d.b, kBS), nrows = seq_rows(a, d.b);
@@ -358,8 +369,8 @@ __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv,
         const int j0 = max(0, d.t0 - first), j1 = min(nrows, d.t_end - first);
         if (nrows > 0 && nrows <= ctx && j0 < j1) {
             const int items = (j1 - j0) * (kD / 8);
-            if (DT != GG_DTYPE_INT8 && ap && items <= kAppMax && first + j0 >= d.t0 + kWaves * kTok) {
-                PieceIO<DT>::start(a, kv, d, in);
+            if (kDefer && ap && items <= kAppMax && first + j0 >= d.t0 + kWaves * kTok) {
+                PieceIO<DT, TOK>::start(a, kv, d, in);
                 ap->j0 = j0;
                 ap->j1 = j1;
                 ap->it.live = false;
@@ -374,16 +385,16 @@ __device__ __forceinline__ void start_piece(const AttnArgs& a, const KVView& kv,
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                 __syncthreads();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                PieceIO<DT>::start(a, kv, d, in);
+                PieceIO<DT, TOK>::start(a, kv, d, in);
             } else {
                 append_item_rows(a, kv, d.b, d.kvh, j0, j1);
                 __syncthreads();
-                PieceIO<DT>::start(a, kv, d, in);
+                PieceIO<DT, TOK>::start(a, kv, d, in);
             }
             return;
         }
     }
-    PieceIO<DT>::start(a, kv, d, in);
+    PieceIO<DT, TOK>::start(a, kv, d, in);
 }
 
 // One piece of work: tokens [t0, t_end) of sequence b against kv head kvh. The result
@@ -404,13 +415,15 @@ __device__ __forceinline__ float load_agent(const float* p) {
 
 template <gg_dtype_t DT, int NT>
 __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, const PieceDesc pd,
-                                           PieceIn<DT>& in, const DeferredRows* ap) {
+                                           PieceIn<DT, attn_chunk_tokens(PoolTraits<DT>::kEB, NT)>& in,
+                                           const DeferredRows* ap) {
     const int b = pd.b, kvh = pd.kvh, t0 = pd.t0, t_end = pd.t_end, part = pd.part, rec = pd.rec;
     using T = PoolTraits<DT>;
     constexpr bool kIsBf16 = T::kBf16;
     constexpr int kEB = T::kEB;
-    using Geom = Geo<kEB>;
-    using Regs = ChunkRegs<kEB>;
+    constexpr int TOK = attn_chunk_tokens(kEB, NT);
+    using Geom = Geo<kEB, TOK>;
+    using Regs = ChunkRegs<kEB, TOK>;
     constexpr int kTok = Geom::kTok;
     constexpr int kNS = Geom::kNS;
 
@@ -571,7 +584,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         for (int dt = 0; dt < 8; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    using IO = PieceIO<DT>;
+    using IO = PieceIO<DT, TOK>;
 
     Regs& cur = in.cur;
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -756,7 +769,7 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         // runs of a block cover its whole dim-major V tile, so these are full-line stores
         // (the draft rows alone would be 1- or 2-byte pieces of every line, each a partial
         // write to memory); the other offsets are written back with the bytes just read.
-        if constexpr (DT != GG_DTYPE_INT8) {
+        if constexpr (DT != GG_DTYPE_INT8 && Geom::kVBytes == 16) {
             if (app_here) {
                 const int blk0 = tc + 16 * Geom::bq(g4) - app_lo;  // staged row of the block's offset 0
                 const int base = blk0 + Geom::ob(g4);
@@ -792,8 +805,9 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
         if (nvalid_v < kBS) {
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
-                if constexpr (kEB == 1) cur.v[dt] = mask_bytes16(cur.v[dt], nvalid_v);
-                else cur.v[dt] = mask_halves8(cur.v[dt], nvalid_v, Geom::ob(g4));
+                if constexpr (kEB == 2) cur.v[dt] = mask_halves8(cur.v[dt], nvalid_v, Geom::ob(g4));
+                else if constexpr (Geom::kVBytes == 16) cur.v[dt] = mask_bytes16(cur.v[dt], nvalid_v);
+                else cur.v[dt] = mask_bytes8(cur.v[dt], nvalid_v, Geom::ob(g4));
             }
         }
 #pragma unroll
@@ -803,9 +817,11 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
                 uint4 vop;
                 if constexpr (kEB == 2) {
                     vop = cur.v[dt];
-                } else {
+                } else if constexpr (Geom::kVBytes == 16) {
                     const uint4 r = cur.v[dt];
                     vop = pv ? bytes8_to_f16x8<DT>(r.z, r.w) : bytes8_to_f16x8<DT>(r.x, r.y);
+                } else {
+                    vop = bytes8_to_f16x8<DT>(cur.v[dt].x, cur.v[dt].y);
                 }
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) {
@@ -896,16 +912,16 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
 
 // Fixed partition grid: workgroup (part, kvh, b) takes tokens [part*P, (part+1)*P).
 template <gg_dtype_t DT, int NT>
-__global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_kernel(AttnArgs a, KVView kv) {
+__global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) attn_mfma_kernel(AttnArgs a, KVView kv) {
     const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int ctx = seq_keys(a, b, kBS);
     const int P = a.partition;
     const int nparts = (ctx + P - 1) / P;
     if (part >= nparts) return;
     const PieceDesc d{b, kvh, part * P, min(part * P + P, ctx), nparts == 1 ? -1 : part, -1};
-    PieceIn<DT> in;
+    PieceIn<DT, attn_chunk_tokens(PoolTraits<DT>::kEB, NT)> in;
     DeferredRows ap;
-    start_piece<DT>(a, kv, d, in, &ap);
+    start_piece(a, kv, d, in, &ap);
     attn_piece<DT, NT>(a, kv, d, in, &ap);
 }
 
@@ -923,8 +939,8 @@ __device__ __forceinline__ int seq_chunks(const AttnArgs& a, int b, int tok) {
 // writes the output, any other piece writes record (workgroup + item), and
 // attn_streamk_combine_kernel merges the records of split items.
 template <gg_dtype_t DT, int NT>
-__global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_kernel(AttnArgs a, KVView kv) {
-    constexpr int kTok = Geo<PoolTraits<DT>::kEB>::kTok;
+__global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) attn_mfma_streamk_kernel(AttnArgs a, KVView kv) {
+    constexpr int kTok = attn_chunk_tokens(PoolTraits<DT>::kEB, NT);
     const int w = blockIdx.x;
     const int Hkv = kv.Hkv;
     __shared__ long long s_scan[256];
@@ -1003,8 +1019,8 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_streamk_ker
     };
     PieceDesc d;
     while (next_piece(d)) {
-        PieceIn<DT> in;
-        start_piece<DT>(a, kv, d, in, nullptr);
+        PieceIn<DT, attn_chunk_tokens(PoolTraits<DT>::kEB, NT)> in;
+        start_piece(a, kv, d, in, nullptr);
         attn_piece<DT, NT>(a, kv, d, in, nullptr);
     }
 }
@@ -1169,7 +1185,7 @@ __device__ void lpt_merge_if_last(const AttnArgs& a, int Hkv, int b, int kvh, in
 // Workgroup p computes the piece at table entry p (exits past the last piece); the last
 // piece of a split item to finish merges it.
 template <gg_dtype_t DT, int NT>
-__global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
+__global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) attn_mfma_lpt_kernel(AttnArgs a, KVView kv) {
     const int p = blockIdx.x;
 #ifdef GG_TRACE
     const long long tr_t0 = wall_clock64();
@@ -1181,9 +1197,9 @@ __global__ void __launch_bounds__(256, attn_occupancy(NT)) attn_mfma_lpt_kernel(
     const int kvh = e.y & 0xffff, np = e.y >> 16;
     const PieceDesc d{b, kvh, e.z, e.w, -1,
                       np > 1 ? lpt_slot(p, a.sk_grid, a.plan[0], a.num_seqs * kv.Hkv <= a.sk_grid) : -1};
-    PieceIn<DT> in;
+    PieceIn<DT, attn_chunk_tokens(PoolTraits<DT>::kEB, NT)> in;
     DeferredRows ap;
-    start_piece<DT>(a, kv, d, in, &ap);
+    start_piece(a, kv, d, in, &ap);
     attn_piece<DT, NT>(a, kv, d, in, &ap);
     if (np > 1) lpt_merge_if_last(a, kv.Hkv, b, kvh, np);
 #ifdef GG_TRACE
@@ -1297,7 +1313,7 @@ __global__ void __launch_bounds__(128) attn_streamk_combine_kernel(AttnArgs a, i
 gg_status_t launch_attn_mfma(const AttnArgs& a, const KVView& kv, hipStream_t s) {
     const int G = a.num_q_heads / kv.Hkv;
     const int nt = (G * a.rows + 15) / 16;
-    const int tok = (kv.dt == GG_DTYPE_FP8_E4M3 || kv.dt == GG_DTYPE_INT8) ? 64 : 32;
+    const int tok = attn_chunk_tokens(dtype_bytes(kv.dt), nt);
     if (a.sched == ATTN_SCHED_LPT && !a.plan_ready) {
         const gg_status_t st = launch_attn_plan(a, s);
         if (st != GG_OK) return st;
@@ -1321,8 +1337,8 @@ gg_status_t launch_attn_plan(const AttnArgs& a, hipStream_t s) {
     if (a.sched != ATTN_SCHED_LPT) return GG_OK;
     if (a.num_seqs > kLptMaxSeqs) return fail(GG_ERR_INTERNAL, "attention: LPT plan over too many sequences");
     const KV* kv = a.kv;
-    const int tok = (kv->dtype == GG_DTYPE_FP8_E4M3 || kv->dtype == GG_DTYPE_INT8) ? 64 : 32;
     const int Hkv = kv->num_kv_heads;
+    const int tok = attn_chunk_tokens(dtype_bytes(kv->dtype), (a.num_q_heads / Hkv * a.rows + 15) / 16);
     attn_lpt_plan_kernel<<<1, 1024, 0, s>>>(a, Hkv, tok, a.sk_grid, lpt_records(a.sk_grid, a.num_seqs, Hkv));
     return check_hip(hipGetLastError(), "verify_attention plan launch");
 }
@@ -1330,8 +1346,8 @@ gg_status_t launch_attn_plan(const AttnArgs& a, hipStream_t s) {
 int attn_streamk_grid(const KV* kv, int rows, int num_q_heads) {
     const int G = num_q_heads / kv->num_kv_heads;
     const int nt = (G * rows + 15) / 16;
-    // One resident wave of workgroups: each CU holds attn_occupancy(nt) of them.
-    return device_cu_count() * attn_occupancy(nt);
+    // One resident wave of workgroups: each CU holds attn_occupancy of them.
+    return device_cu_count() * attn_occupancy((int)dtype_bytes(kv->dtype), nt);
 }
 
 size_t attn_streamk_workspace_bytes(const KV* kv, int num_seqs, int rows, int num_q_heads, size_t* ml_elems,
