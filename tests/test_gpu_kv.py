@@ -719,6 +719,11 @@ def _derived_slots(lay, rows, bs, row_counts=None):
      True),
     # More sequences than the LPT plan ranks: one workgroup per (sequence, kv head).
     (3, "fp8", 1100, ("uniform", 20, 400), True),
+    # FP8 at three row tiles (32-token chunks, rows appended by the whole workgroup before
+    # the piece starts): stream-K with few items, and LPT with rows straddling chunks.
+    (4, "fp8", 8, ("uniform", 1000, 6000), True),
+    (4, "fp8", 64, ("list", *[32 * (1 + (i * 13) % 64) + (27, 28, 29, 30, 31, 0, 1, 16)[i % 8] for i in range(64)]),
+     False),
 ])
 def test_append_attention_fused_equals_separate(gpu, cid, dt, B, ctx, rc):
     """gg_verify_append_attention_planned == gg_kv_append (slots from the block tables)
