@@ -5,10 +5,10 @@
 // (internal/engine/serving.go:514-566). Two launches:
 //   1) segment argmax: grid (segments, rows); each block scans 4096 logits of one
 //      row with 16-byte loads and writes (value, index) of its first maximum;
-//   2) decide: one wave per sequence merges the segments of rows 0..n and walks the
-//      drafts in order: the first row whose argmax differs from its draft ends the
-//      accepted prefix and supplies the corrected token; if none differs, row n
-//      supplies the bonus token.
+//   2) decide: one block per sequence merges the segments of rows 0..n, every row at
+//      once (a lane group per row), then walks the drafts in order: the first row whose
+//      argmax differs from its draft ends the accepted prefix and supplies the corrected
+//      token; if none differs, row n supplies the bonus token.
 // Tie rule: first index of the maximum. NaN never wins; a NaN at element 0 makes
 // the row's argmax 0 (the reference scans with `>` from element 0).
 #include "gg_common.h"
@@ -104,7 +104,13 @@ __global__ void __launch_bounds__(kThreads) greedy_segment_kernel(
     }
 }
 
-__global__ void __launch_bounds__(64) greedy_decide_kernel(
+// Lane group of g = 2^ceil(log2 nseg) lanes per row (lane s of a group reads segment s,
+// and s + g, ... past 64), kDecideThreads / g rows per pass; each row's argmax lands in LDS
+// and thread 0 walks the rows. (Walking row by row, each row's loads waiting for the
+// previous row's decision, took 13 us for nine rows.)
+constexpr int kDecideThreads = 512;
+constexpr int kMaxRows = 65;  // rows per sequence: max_drafts + 1, max_drafts <= 64 (checked by the ABI)
+__global__ void __launch_bounds__(kDecideThreads) greedy_decide_kernel(
     const void* __restrict__ logits, gg_dtype_t dt, int K, int V, int nseg,
     const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
     const float2* __restrict__ ws, int32_t* __restrict__ out_acc, int32_t* __restrict__ out_tok) {
@@ -112,32 +118,45 @@ __global__ void __launch_bounds__(64) greedy_decide_kernel(
     const int R = K + 1;
     int n = n_drafts[b];
     n = n < 0 ? 0 : (n > K ? K : n);
-    int accepted = n, token = 0;
-    for (int j = 0; j <= n; ++j) {
-        const int row = b * R + j;
+    __shared__ int s_am[kMaxRows];
+    int g = 1;
+    while (g < nseg && g < 64) g <<= 1;
+    const int per_pass = kDecideThreads / g;
+    const int jl = threadIdx.x / g, sl = threadIdx.x % g;
+    for (int j0 = 0; j0 <= n; j0 += per_pass) {
+        const int j = j0 + jl;
+        const bool live = j <= n;
+        const int row = b * R + (live ? j : 0);
+        const float first = load_as_f32(logits, dt, (size_t)row * V);
         ArgBest best{-INFINITY, kNone};
-        for (int s = threadIdx.x; s < nseg; s += 64) {
-            float2 p = ws[(size_t)row * nseg + s];
-            int pi = __float_as_int(p.y);
+        for (int s = sl; s < nseg; s += g) {
+            const float2 p = ws[(size_t)row * nseg + s];
+            const int pi = __float_as_int(p.y);
             if (pi != kNone && (best.i == kNone || p.x > best.v || (p.x == best.v && pi < best.i))) {
                 best.v = p.x;
                 best.i = pi;
             }
         }
-        best = wave_best(best);
-        const float first = load_as_f32(logits, dt, (size_t)row * V);
-        int am = (first != first || best.i == kNone) ? 0 : best.i;
-        if (j == n) {
-            token = am;
-            break;
+        for (int o = g >> 1; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best.v, o);
+            const int oi = __shfl_xor(best.i, o);
+            if (oi != kNone && (best.i == kNone || ov > best.v || (ov == best.v && oi < best.i))) {
+                best.v = ov;
+                best.i = oi;
+            }
         }
-        if (am != drafts[(size_t)b * K + j]) {
-            accepted = j;
-            token = am;
-            break;
-        }
+        if (live && sl == 0) s_am[j] = (first != first || best.i == kNone) ? 0 : best.i;
     }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        int accepted = n, token = s_am[n];
+        for (int j = 0; j < n; ++j) {
+            if (s_am[j] != drafts[(size_t)b * K + j]) {
+                accepted = j;
+                token = s_am[j];
+                break;
+            }
+        }
         out_acc[b] = accepted;
         out_tok[b] = token;
     }
@@ -159,7 +178,8 @@ gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs
     const int vec_ok = ((vocab * eb) % 16 == 0) && (((uintptr_t)logits) % 16 == 0);
     greedy_segment_kernel<<<dim3(nseg, num_seqs * R), kThreads, 0, s>>>(logits, dt, R, vocab, nseg,
                                                                        vec_ok, n_drafts, (float2*)ws);
-    greedy_decide_kernel<<<num_seqs, 64, 0, s>>>(logits, dt, max_drafts, vocab, nseg, drafts,
+    if (R > kMaxRows) return fail(GG_ERR_INVALID, "accept_greedy: more than 64 drafts per sequence");
+    greedy_decide_kernel<<<num_seqs, kDecideThreads, 0, s>>>(logits, dt, max_drafts, vocab, nseg, drafts,
                                                  n_drafts, (const float2*)ws, out_acc, out_tok);
     return check_hip(hipGetLastError(), "accept_greedy launch");
 }

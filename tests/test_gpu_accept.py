@@ -40,6 +40,24 @@ def test_greedy_matches_oracle(gpu, dt, shape):
     assert np.array_equal(tok.cpu().numpy(), et)
 
 
+@pytest.mark.parametrize("shape", [(3, 40, 128256), (2, 64, 262144), (4, 17, 1000)])
+def test_greedy_many_drafts(gpu, shape):
+    """Rows past one pass of the decide block's lane groups (16 rows of 32 segments, 8 rows
+    of 64, or many rows of one segment), drafts matching the argmax with probability 0.97
+    so accepted lengths reach deep rows; every draft count from 0 to K."""
+    B, K, V = shape
+    say(f"greedy many drafts shape={shape}")
+    lg, host, drafts, n = logits_case(B, K, V, "bf16", seed=K * 31 + B, match_rate=0.97)
+    n[0] = K
+    if B > 2:
+        n[1] = 0
+    acc, tok = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
+    torch.cuda.synchronize()
+    ea, et = ora.accept_greedy(host, drafts, n)
+    assert np.array_equal(acc.cpu().numpy(), ea)
+    assert np.array_equal(tok.cpu().numpy(), et)
+
+
 def test_greedy_ties_nan_and_negative_zero(gpu):
     say("greedy ties/nan")
     V = 9000
