@@ -77,6 +77,9 @@ SIGNATURES = {
     "gg_verify_attention_noalloc": (_i, [_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     "gg_accept_greedy_workspace_size": (_sz, [_i, _i, _i]),
     "gg_accept_greedy": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gg_accept_greedy_sample_workspace_size": (_sz, [_i, _i, _i]),
+    "gg_accept_greedy_sample": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, C.c_double, _i, C.c_double, _vp, C.c_uint,
+                                     _vp, _vp, _vp, _sz, _vp]),
     "gg_accept_rejection_workspace_size": (_sz, [_i, _i, _i]),
     "gg_accept_rejection": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp, _f, _f, _vp, _vp, _vp,
                                  _sz, _vp]),

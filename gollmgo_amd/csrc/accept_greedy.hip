@@ -75,7 +75,8 @@ __global__ void __launch_bounds__(kThreads) greedy_segment_kernel(
     const int32_t* __restrict__ n_drafts, float2* __restrict__ ws) {
     const int row = blockIdx.y;  // b*R + j
     const int b = row / R, j = row % R;
-    if (j > n_drafts[b]) return;
+    const int nb = n_drafts[b];
+    if (j > (nb < 0 ? 0 : nb)) return;  // rows 0..n, n clamped as the decide kernel clamps it
     const int seg = blockIdx.x;
     const int base = seg * kSeg;
     ArgBest best{-INFINITY, kNone};

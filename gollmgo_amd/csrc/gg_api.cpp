@@ -465,6 +465,31 @@ GG_API gg_status_t gg_accept_greedy(const void* logits, gg_dtype_t logits_dtype,
                                 out_accepted, out_token, workspace, (hipStream_t)stream);
 }
 
+GG_API size_t gg_accept_greedy_sample_workspace_size(int num_seqs, int max_drafts, int vocab) {
+    if (!accept_shape_ok(num_seqs, max_drafts, vocab)) return 0;
+    return sample_workspace_bytes(num_seqs, max_drafts, vocab);
+}
+
+GG_API gg_status_t gg_accept_greedy_sample(const void* logits, gg_dtype_t logits_dtype, int num_seqs,
+                                           int max_drafts, int vocab, const int32_t* drafts,
+                                           const int32_t* n_drafts, double temperature, int top_k,
+                                           double top_p, const double* uniforms, unsigned flags,
+                                           int32_t* out_accepted, int32_t* out_token, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+    clear_error();
+    GG_CHECK_ARG(accept_shape_ok(num_seqs, max_drafts, vocab),
+                 "gg_accept_greedy_sample: bad shape (need num_seqs>0, 0<=max_drafts<=64, 0<vocab<=2^18)");
+    GG_CHECK_ARG(logits && n_drafts && uniforms && out_accepted && out_token && (drafts || max_drafts == 0),
+                 "gg_accept_greedy_sample: NULL buffer");
+    GG_CHECK_ARG(is_float_io(logits_dtype), "gg_accept_greedy_sample: logits dtype must be F32/F16/BF16");
+    GG_CHECK_ARG((flags & ~GG_SAMPLE_EXACT) == 0, "gg_accept_greedy_sample: unknown flags");
+    const size_t need = sample_workspace_bytes(num_seqs, max_drafts, vocab);
+    GG_CHECK_ARG(workspace && workspace_bytes >= need, "gg_accept_greedy_sample: workspace too small");
+    return launch_accept_greedy_sample(logits, logits_dtype, num_seqs, max_drafts, vocab, drafts, n_drafts,
+                                       temperature, top_k, top_p, uniforms, flags, out_accepted, out_token,
+                                       workspace, (hipStream_t)stream);
+}
+
 GG_API size_t gg_accept_rejection_workspace_size(int num_seqs, int max_drafts, int vocab) {
     if (!accept_shape_ok(num_seqs, max_drafts, vocab)) return 0;
     return rejection_workspace_bytes(num_seqs, max_drafts, vocab);

@@ -116,6 +116,12 @@ gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs
                                  int vocab, const int32_t* drafts, const int32_t* n_drafts,
                                  int32_t* out_acc, int32_t* out_tok, void* ws, hipStream_t s);
 
+size_t sample_workspace_bytes(int num_seqs, int max_drafts, int vocab);
+gg_status_t launch_accept_greedy_sample(const void* logits, gg_dtype_t dt, int num_seqs, int max_drafts, int vocab,
+                                        const int32_t* drafts, const int32_t* n_drafts, double temperature,
+                                        int top_k, double top_p, const double* uniforms, unsigned flags,
+                                        int32_t* out_acc, int32_t* out_tok, void* ws, hipStream_t s);
+
 size_t rejection_workspace_bytes(int num_seqs, int max_drafts, int vocab);
 gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const float* q, int num_seqs,
                                     int max_drafts, int vocab, const int32_t* drafts,

@@ -1,0 +1,45 @@
+// gg_exp64.h — the float64 exponential of the sampled draw.
+//
+// The sampler's softmax (internal/engine/sampling.go:112-136) calls math.Exp in float64.
+// A platform exp may differ in the last bit between host and device, so the library
+// carries its own: the method of fdlibm's e_exp.c (Sun Microsystems, 1993), which Go's
+// portable math.Exp (exp.go) also follows:
+//   k = int(x*log2e -+ 0.5) (truncated), hi = x - k*ln2hi, lo = k*ln2lo, r = hi - lo,
+//   c = r - r^2*(P1 + r^2*(P2 + ... P5)), y = 1 - ((lo - r*c/(2-c)) - hi), e^x = y*2^k.
+// Every operation rounds on its own (no fused multiply-add), the division is IEEE, and
+// the scaling by 2^k rounds once (ldexp), so the host C build and the gfx950 build give
+// the same bits. Within 1 ulp of glibc's exp.
+#pragma once
+
+#ifdef __HIPCC__
+#define GG_HD64 __host__ __device__ __forceinline__
+#else
+#include <math.h>
+#define GG_HD64 static inline
+#endif
+
+GG_HD64 double gg_exp64(double x) {
+#ifdef __clang__
+#pragma clang fp contract(off)
+#endif
+    const double ln2hi = 6.93147180369123816490e-01, ln2lo = 1.90821492927058770002e-10;
+    const double log2e = 1.44269504088896338700e+00;
+    const double P1 = 1.66666666666666019037e-01, P2 = -2.77777777770155933842e-03,
+                 P3 = 6.61375632143793436117e-05, P4 = -1.65339022054652515390e-06,
+                 P5 = 4.13813679705723846039e-08;
+    if (x != x) return x;                                      // NaN
+    if (x > 7.09782712893383973096e+02) return __builtin_inf();  // includes +inf
+    if (x < -7.45133219101941108420e+02) return 0.0;           // includes -inf
+    if (-3.7252902984619141e-09 < x && x < 3.7252902984619141e-09) return 1.0 + x;  // |x| < 2^-28
+    int k = 0;
+    if (x < 0) k = (int)(log2e * x - 0.5);
+    else if (x > 0) k = (int)(log2e * x + 0.5);
+    const double kd = (double)k;
+    const double hi = x - kd * ln2hi;
+    const double lo = kd * ln2lo;
+    const double r = hi - lo;
+    const double t = r * r;
+    const double c = r - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+    const double y = 1.0 - ((lo - (r * c) / (2.0 - c)) - hi);
+    return __builtin_ldexp(y, k);
+}

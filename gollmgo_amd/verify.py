@@ -9,6 +9,8 @@ of libgg_verify.so. Names follow the reference's domain:
   KVCache.attention  ~ gollmgo_kvcache_attention, for k+1 verify rows per sequence
   accept_greedy      ~ Verify + argmax as emitSpeculative drives them
                        (internal/engine/speculative.go:68-84, serving.go:514-566)
+  accept_greedy_sample ~ the same with the bonus token drawn by Sampler.Sample
+                       (internal/engine/sampling.go:40-72) at the engine's temperature/top-k/top-p
   accept_rejection   ~ speculative sampling with Sampler's temperature/top-p rules
   ngram_draft        ~ NGramDrafter.Draft (internal/engine/speculative.go:24-62)
 """
@@ -248,6 +250,11 @@ def greedy_workspace(num_seqs: int, max_drafts: int, vocab: int) -> torch.Tensor
     return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
 
 
+def sample_workspace(num_seqs: int, max_drafts: int, vocab: int) -> torch.Tensor:
+    n = lib().gg_accept_greedy_sample_workspace_size(num_seqs, max_drafts, vocab)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
+
+
 def rejection_workspace(num_seqs: int, max_drafts: int, vocab: int) -> torch.Tensor:
     n = lib().gg_accept_rejection_workspace_size(num_seqs, max_drafts, vocab)
     return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
@@ -270,6 +277,35 @@ def accept_greedy(logits: torch.Tensor, drafts: torch.Tensor, n_drafts: torch.Te
         drafts.data_ptr() if drafts.numel() else None, _dev(n_drafts, "n_drafts", torch.int32),
         _dev(acc, "accepted", torch.int32), _dev(tok, "token", torch.int32), workspace.data_ptr(),
         workspace.numel(), _stream(stream)), "gg_accept_greedy")
+    return acc, tok
+
+
+SAMPLE_EXACT = 1  # GG_SAMPLE_EXACT: every draw through the sequential path
+
+
+def accept_greedy_sample(logits: torch.Tensor, drafts: torch.Tensor, n_drafts: torch.Tensor,
+                         uniforms: torch.Tensor, temperature: float, top_k: int = 0, top_p: float = 0.0,
+                         flags: int = 0, workspace: Optional[torch.Tensor] = None, out: Optional[tuple] = None,
+                         stream: Optional[torch.cuda.Stream] = None):
+    """Greedy Verify; when every draft is accepted the bonus is Sampler.Sample(row n) with
+    (temperature, top_k, top_p) and uniforms[b] (float64) in place of rng.Float64().
+    logits [B, K+1, V]; drafts [B, K] int32; n_drafts [B] int32 -> (accepted [B], token [B])."""
+    B, R, V = logits.shape
+    K = R - 1
+    if drafts.shape != (B, K) and not (K == 0 and drafts.numel() == 0):
+        raise ValueError("drafts must be [num_seqs, max_drafts]")
+    if uniforms.shape != (B,):
+        raise ValueError("uniforms must be [num_seqs]")
+    if workspace is None:
+        workspace = sample_workspace(B, K, V)
+    acc, tok = out if out is not None else (torch.empty(B, dtype=torch.int32, device="cuda"),
+                                            torch.empty(B, dtype=torch.int32, device="cuda"))
+    check(lib().gg_accept_greedy_sample(
+        _dev(logits, "logits"), int(dtype_of(logits)), B, K, V,
+        drafts.data_ptr() if drafts.numel() else None, _dev(n_drafts, "n_drafts", torch.int32),
+        float(temperature), int(top_k), float(top_p), _dev(uniforms, "uniforms", torch.float64), int(flags),
+        _dev(acc, "accepted", torch.int32), _dev(tok, "token", torch.int32), workspace.data_ptr(),
+        workspace.numel(), _stream(stream)), "gg_accept_greedy_sample")
     return acc, tok
 
 

@@ -273,6 +273,35 @@ gg_status_t gg_accept_greedy(const void* logits, gg_dtype_t logits_dtype, int nu
                              void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Greedy acceptance with the reference's sampled bonus token.
+ * Replaces emitSpeculative at temperature > 0 (internal/engine/serving.go:514-566): the
+ * greedy Verify over the draft rows as gg_accept_greedy, and, when every draft is
+ * accepted, the bonus token Sampler.Sample(row n) (internal/engine/sampling.go:40-72) with
+ * the engine's SamplingParams (sampling.go:10-15) and the draw's uniform supplied:
+ *   temperature : SamplingParams.Temperature; <= 1e-9 gives gg_accept_greedy's result
+ *   top_k       : SamplingParams.TopK; active when 0 < top_k < vocab (topKFilter, :88-109)
+ *   top_p       : SamplingParams.TopP; active when 0 < top_p < 1 (topPFilter, :139-173)
+ *   uniforms    : device double[num_seqs], the value rng.Float64() gives the bonus draw of
+ *                 sequence b (categoricalSample, :176-192); unused for other sequences
+ *   flags       : 0, or GG_SAMPLE_EXACT to take every draw through the sequential path
+ * The token is the one the float64 rule gives: scaled = float64(l) * (1/T), the top-k
+ * filter, softmax (exp as fdlibm's method, the one Go's portable math.Exp uses), top-p
+ * and the first index whose cumulative probability exceeds u, every sum in the rule's
+ * order. Orders sort.Slice leaves open are fixed: value (or probability) descending, then
+ * index ascending, NaN last. Parallel sums decide whenever they clear the rule's boundary by
+ * more than their proven rounding bound; rows that do not (about 1 in 10^4, and rows holding
+ * NaN or +inf) are replayed sequentially on the device, about 3 ms per row.
+ * workspace: gg_accept_greedy_sample_workspace_size bytes. */
+#define GG_SAMPLE_EXACT 1u
+size_t gg_accept_greedy_sample_workspace_size(int num_seqs, int max_drafts, int vocab);
+gg_status_t gg_accept_greedy_sample(const void* logits, gg_dtype_t logits_dtype, int num_seqs,
+                                    int max_drafts, int vocab, const int32_t* drafts,
+                                    const int32_t* n_drafts, double temperature, int top_k,
+                                    double top_p, const double* uniforms, unsigned flags,
+                                    int32_t* out_accepted, int32_t* out_token, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Rejection-sampling acceptance (speculative sampling, Leviathan et al. 2023,
  * Alg. 1) with the reference sampler's temperature and top-p rules
  * (internal/engine/sampling.go:40-72,112-192). Not present in the reference.

@@ -148,7 +148,37 @@ void ora_accept_greedy(const float* logits, int B, int K, int V, const int32_t* 
     }
 }
 
-/* softmax (sampling.go:112-136) in float64, -inf -> 0. */
+/* exp in float64 as fdlibm's e_exp.c computes it (Sun Microsystems, 1993), the method of
+ * Go's portable math.Exp (exp.go, used where Go has no assembly version): special cases,
+ * k = int(x/ln2 -+ 0.5) truncated, r = (x - k*ln2hi) - k*ln2lo, the degree-5 minimax
+ * polynomial c(r) and 1 - ((lo - r*c/(2-c)) - hi) scaled by 2^k (ldexp rounds once). Every
+ * operation is rounded on its own (the library is built with -ffp-contract=off), as Go
+ * evaluates the expression on amd64. */
+double ora_exp64(double x) {
+    const double ln2hi = 6.93147180369123816490e-01, ln2lo = 1.90821492927058770002e-10;
+    const double log2e = 1.44269504088896338700e+00;
+    const double P1 = 1.66666666666666019037e-01, P2 = -2.77777777770155933842e-03,
+                 P3 = 6.61375632143793436117e-05, P4 = -1.65339022054652515390e-06,
+                 P5 = 4.13813679705723846039e-08;
+    if (isnan(x) || (isinf(x) && x > 0)) return x;
+    if (isinf(x)) return 0.0;
+    if (x > 7.09782712893383973096e+02) return INFINITY;
+    if (x < -7.45133219101941108420e+02) return 0.0;
+    if (-3.7252902984619141e-09 < x && x < 3.7252902984619141e-09) return 1.0 + x; /* |x| < 2^-28 */
+    int k = 0;
+    if (x < 0) k = (int)(log2e * x - 0.5);
+    else if (x > 0) k = (int)(log2e * x + 0.5);
+    const double hi = x - (double)k * ln2hi;
+    const double lo = (double)k * ln2lo;
+    const double r = hi - lo;
+    const double t = r * r;
+    const double c = r - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+    const double y = 1.0 - ((lo - (r * c) / (2.0 - c)) - hi);
+    return ldexp(y, k);
+}
+
+/* softmax (sampling.go:112-136) in float64: max by a `>` scan from element 0, -inf -> 0,
+ * the sum in index order, the division only when the sum is > 0. */
 void ora_softmax_f64(const double* in, int n, double* out) {
     double mx = in[0];
     for (int i = 1; i < n; ++i)
@@ -157,7 +187,7 @@ void ora_softmax_f64(const double* in, int n, double* out) {
     for (int i = 0; i < n; ++i) {
         if (isinf(in[i]) && in[i] < 0) out[i] = 0;
         else {
-            out[i] = exp(in[i] - mx);
+            out[i] = ora_exp64(in[i] - mx);
             sum += out[i];
         }
     }
@@ -170,16 +200,36 @@ typedef struct {
     double v;
 } ora_iv;
 
+/* The order of the reference's sort.Slice(... a.v > b.v) (sampling.go:97-99,148-150) with
+ * what it leaves open fixed: equal values (-0 == +0) by lower index first, NaN after every
+ * number. */
 static int cmp_desc_stable(const void* a, const void* b) {
     const ora_iv* x = (const ora_iv*)a;
     const ora_iv* y = (const ora_iv*)b;
-    if (x->v > y->v) return -1;
-    if (x->v < y->v) return 1;
+    const int xn = isnan(x->v), yn = isnan(y->v);
+    if (xn != yn) return xn - yn;
+    if (!xn) {
+        if (x->v > y->v) return -1;
+        if (x->v < y->v) return 1;
+    }
     return x->idx - y->idx;
 }
 
-/* topPFilter (sampling.go:139-173) with ties broken by lower index first (the
- * reference's sort.Slice leaves tie order unspecified). */
+/* topKFilter (sampling.go:88-109): the k largest values kept, the rest -inf. */
+void ora_top_k_filter_f64(const double* in, int n, int k, double* out) {
+    ora_iv* it = (ora_iv*)malloc(sizeof(ora_iv) * (size_t)n);
+    for (int i = 0; i < n; ++i) {
+        it[i].idx = i;
+        it[i].v = in[i];
+        out[i] = -INFINITY;
+    }
+    qsort(it, (size_t)n, sizeof(ora_iv), cmp_desc_stable);
+    for (int i = 0; i < k && i < n; ++i) out[it[i].idx] = it[i].v;
+    free(it);
+}
+
+/* topPFilter (sampling.go:139-173): walk in (prob desc, index asc) order, keep while
+ * !(cumulative >= p && cumulative > 0), then renormalise by the index-order sum. */
 void ora_top_p_filter_f64(const double* probs, int n, double p, double* out) {
     ora_iv* it = (ora_iv*)malloc(sizeof(ora_iv) * (size_t)n);
     for (int i = 0; i < n; ++i) {
@@ -213,25 +263,62 @@ int ora_categorical_f64(const double* probs, int n, double u) {
     return 0;
 }
 
-/* Sampler.Sample (sampling.go:40-72) without top-k, the uniform supplied: temperature
- * <= 1e-9 -> argmax; else logit * (1/T) in float64, softmax, top-p when 0 < p < 1, and
- * the categorical draw. */
-int ora_sample_f64(const float* logits, int n, double temperature, double top_p, double u) {
-    if (n <= 0) return 0;
-    if (temperature <= 1e-9) return ora_argmax(logits, n);
+/* The distribution Sampler.Sample (sampling.go:40-72) hands to categoricalSample, for
+ * temperature > 1e-9: scaled = float64(l) * (1/T), topKFilter when 0 < k < n, softmax,
+ * topPFilter when 0 < p < 1. out receives n probabilities. */
+void ora_sampler_probs_f64(const float* logits, int n, double temperature, int top_k, double top_p,
+                           double* out) {
     double* sc = (double*)malloc(sizeof(double) * (size_t)n);
-    double* pr = (double*)malloc(sizeof(double) * (size_t)n);
+    double* tk = (double*)malloc(sizeof(double) * (size_t)n);
     const double inv_t = 1.0 / temperature;
     for (int i = 0; i < n; ++i) sc[i] = (double)logits[i] * inv_t;
-    ora_softmax_f64(sc, n, pr);
-    if (top_p > 0 && top_p < 1.0) {
-        ora_top_p_filter_f64(pr, n, top_p, sc);
-        memcpy(pr, sc, sizeof(double) * (size_t)n);
+    if (top_k > 0 && top_k < n) {
+        ora_top_k_filter_f64(sc, n, top_k, tk);
+        memcpy(sc, tk, sizeof(double) * (size_t)n);
     }
-    const int t = ora_categorical_f64(pr, n, u);
+    ora_softmax_f64(sc, n, out);
+    if (top_p > 0 && top_p < 1.0) {
+        ora_top_p_filter_f64(out, n, top_p, tk);
+        memcpy(out, tk, sizeof(double) * (size_t)n);
+    }
     free(sc);
+    free(tk);
+}
+
+/* Sampler.Sample (sampling.go:40-72) with the uniform supplied in place of
+ * rng.Float64(): temperature <= 1e-9 -> argmax, else the categorical draw over
+ * ora_sampler_probs_f64. */
+int ora_sample_f64(const float* logits, int n, double temperature, int top_k, double top_p, double u) {
+    if (n <= 0) return 0;
+    if (temperature <= 1e-9) return ora_argmax(logits, n);
+    double* pr = (double*)malloc(sizeof(double) * (size_t)n);
+    ora_sampler_probs_f64(logits, n, temperature, top_k, top_p, pr);
+    const int t = ora_categorical_f64(pr, n, u);
     free(pr);
     return t;
+}
+
+/* gg_accept_greedy_sample's rule: ora_accept_greedy, except that the bonus token (every
+ * draft accepted) is Sampler.Sample(row n) with uniforms[b] (serving.go:552-566). */
+void ora_accept_greedy_sample(const float* logits, int B, int K, int V, const int32_t* drafts,
+                              const int32_t* n_drafts, double temperature, int top_k, double top_p,
+                              const double* uniforms, int32_t* out_acc, int32_t* out_tok, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#else
+    (void)threads;
+#endif
+    for (int b = 0; b < B; ++b) {
+        int n = n_drafts[b];
+        if (n < 0) n = 0;
+        if (n > K) n = K;
+        const float* rows = logits + (size_t)b * (K + 1) * V;
+        int acc, cor;
+        ora_verify(drafts + (size_t)b * K, n, rows, n, V, &acc, &cor);
+        out_acc[b] = acc;
+        out_tok[b] = acc < n ? cor : ora_sample_f64(rows + (size_t)n * V, V, temperature, top_k, top_p, uniforms[b]);
+    }
 }
 
 /* emitSpeculative's use of StepOutput.LogitsPerPosition (serving.go:496-570) over ragged
@@ -241,7 +328,7 @@ int ora_sample_f64(const float* logits, int n, double temperature, double top_p,
  * the standard path's Sample over the one row. uniforms[b] feeds the sample. */
 void ora_emit_positions(int B, int K, const int32_t* drafts, const int32_t* n_drafts,
                         const float* const* rows, const int32_t* lens, const int32_t* counts,
-                        double temperature, double top_p, const double* uniforms, int32_t* out_acc,
+                        double temperature, int top_k, double top_p, const double* uniforms, int32_t* out_acc,
                         int32_t* out_tok) {
     size_t r0 = 0;
     for (int b = 0; b < B; ++b) {
@@ -265,7 +352,7 @@ void ora_emit_positions(int B, int K, const int32_t* drafts, const int32_t* n_dr
         }
         out_acc[b] = acc;
         if (acc < n) out_tok[b] = cor;
-        else out_tok[b] = cnt > n ? ora_sample_f64(rw[n], ln[n], temperature, top_p, uniforms[b]) : -1;
+        else out_tok[b] = cnt > n ? ora_sample_f64(rw[n], ln[n], temperature, top_k, top_p, uniforms[b]) : -1;
     }
 }
 
@@ -787,7 +874,8 @@ static uint64_t desc_key_pos_f64(double x) { /* x >= 0 */
 
 /* For each of B rows of logits (V finite values) and U supplied uniforms per row, the
  * token of two samplers:
- *   tok_f64  : Sampler.Sample (sampling.go:40-72) in float64 without top-k: scaled =
+ *   tok_f64  : Sampler.Sample (sampling.go:40-72) in float64 without top-k (ora_exp64 as
+ *              math.Exp): scaled =
  *              float64(l) * (1/T) (:57-61), softmax (:112-136), topPFilter (:139-173;
  *              equal probabilities in index order, which sort.Slice leaves open),
  *              categoricalSample (:176-192) with the uniform in place of rng.Float64();
@@ -833,7 +921,7 @@ void ora_draw_parity(const float* logits, int B, int V, double temperature, doub
             if ((double)row[i] * inv_t64 > mx) mx = (double)row[i] * inv_t64;
         double sum = 0;
         for (int i = 0; i < V; ++i) {
-            pr[i] = exp((double)row[i] * inv_t64 - mx);
+            pr[i] = ora_exp64((double)row[i] * inv_t64 - mx);
             sum += pr[i];
         }
         for (int i = 0; i < V; ++i) pr[i] /= sum;
@@ -914,6 +1002,9 @@ void ora_int8_encode_n(const float* x, int8_t* out, long n) {
 }
 void ora_f16_round_n(const float* x, float* out, long n) {
     for (long i = 0; i < n; ++i) out[i] = ora_f16_round(x[i]);
+}
+void ora_exp64_n(const double* x, double* out, long n) {
+    for (long i = 0; i < n; ++i) out[i] = ora_exp64(x[i]);
 }
 void ora_expf_fixed_n(const float* x, float* out, long n) {
     for (long i = 0; i < n; ++i) out[i] = ora_expf_fixed(x[i]);

@@ -195,16 +195,63 @@ def categorical_f64(p, u: float) -> int:
     return int(f(_p(p), len(p), float(u)))
 
 
-def sample_f64(logits, temperature: float, top_p: float, u: float) -> int:
-    """Sampler.Sample (sampling.go:40-72, no top-k) with the uniform supplied."""
+def sample_f64(logits, temperature: float, top_p: float, u: float, top_k: int = 0) -> int:
+    """Sampler.Sample (sampling.go:40-72) with the uniform supplied."""
     x = np.ascontiguousarray(logits, dtype=np.float32)
     f = lib().ora_sample_f64
-    f.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_double, C.c_double]
-    return int(f(_p(x), len(x), float(temperature), float(top_p), float(u)))
+    f.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_int, C.c_double, C.c_double]
+    return int(f(_p(x), len(x), float(temperature), int(top_k), float(top_p), float(u)))
+
+
+def sampler_probs_f64(logits, temperature: float, top_k: int = 0, top_p: float = 1.0) -> np.ndarray:
+    """The distribution Sampler.Sample hands to categoricalSample (temperature > 1e-9)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.empty(len(x), np.float64)
+    f = lib().ora_sampler_probs_f64
+    f.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_int, C.c_double, C.c_void_p]
+    f(_p(x), len(x), float(temperature), int(top_k), float(top_p), _p(out))
+    return out
+
+
+def top_k_filter_f64(x, k: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty_like(x)
+    f = lib().ora_top_k_filter_f64
+    f.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+    f(_p(x), len(x), int(k), _p(out))
+    return out
+
+
+def exp64(x) -> np.ndarray:
+    """The float64 exponential of the sampler (fdlibm's method, as Go's portable math.Exp)."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty_like(x)
+    f = lib().ora_exp64_n
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_long]
+    f(_p(x), _p(out), x.size)
+    return out
+
+
+def accept_greedy_sample(logits_f32, drafts, n_drafts, temperature: float, top_k: int, top_p: float,
+                         uniforms, threads: int = 0):
+    """Greedy Verify with the bonus drawn by Sampler.Sample (gg_accept_greedy_sample's rule)."""
+    lg = np.ascontiguousarray(logits_f32, dtype=np.float32)
+    B, R, V = lg.shape
+    d = np.ascontiguousarray(drafts, dtype=np.int32).reshape(B, R - 1)
+    nd = np.ascontiguousarray(n_drafts, dtype=np.int32)
+    u = np.ascontiguousarray(uniforms, dtype=np.float64)
+    acc = np.empty(B, np.int32)
+    tok = np.empty(B, np.int32)
+    f = lib().ora_accept_greedy_sample
+    f.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_double, C.c_int,
+                  C.c_double, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+    f(_p(lg), B, R - 1, V, _p(d) if d.size else None, _p(nd), float(temperature), int(top_k), float(top_p),
+      _p(u), _p(acc), _p(tok), threads)
+    return acc, tok
 
 
 def emit_positions(drafts, n_drafts, positions, temperature: float = 0.0, top_p: float = 1.0,
-                   uniforms=None, timer=None):
+                   uniforms=None, timer=None, top_k: int = 0):
     """What emitSpeculative (serving.go:496-570) takes from LogitsPerPosition: per sequence
     (accepted, token), token -1 when every draft is accepted and no further row is given.
     positions[b] is a list of 1-D float32 rows (ragged, as Go slices). timer: a list that
@@ -222,10 +269,10 @@ def emit_positions(drafts, n_drafts, positions, temperature: float = 0.0, top_p:
     tok = np.empty(B, np.int32)
     f = lib().ora_emit_positions
     f.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-                  C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p]
+                  C.c_double, C.c_int, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p]
     t0 = time.perf_counter()
     f(B, K, _p(d) if d.size else None, _p(nd), ptrs, _p(lens), _p(counts), float(temperature),
-      float(top_p), _p(u), _p(acc), _p(tok))
+      int(top_k), float(top_p), _p(u), _p(acc), _p(tok))
     if timer is not None:
         timer.append(time.perf_counter() - t0)
     return acc, tok

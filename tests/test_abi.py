@@ -59,6 +59,9 @@ def test_invalid_arguments_return_status():
     assert lib.gg_accept_rejection(None, 0, None, 1, 4, 1 << 19, None, None, None, 0.8, 1.0, None, None, None, 0,
                                    None) == Status.ERR_INVALID
     assert "vocab" in _lib.last_error()
+    assert lib.gg_accept_greedy_sample(None, 0, 1, 4, 100, None, None, 0.8, 0, 0.9, None, 0, None, None, None, 0,
+                                       None) == Status.ERR_INVALID
+    assert "NULL buffer" in _lib.last_error()
     assert lib.gg_ngram_draft(None, 0, None, 1, 10, 4, None, None, None) == Status.ERR_INVALID
     assert "n must be <= 9" in _lib.last_error()
     assert lib.gg_history_append_draft(None, 16, None, None, 1, None, 0, None, None, 3, 4, None, None,

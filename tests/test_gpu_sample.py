@@ -1,0 +1,131 @@
+"""GPU parity: greedy Verify with the bonus token drawn by Sampler.Sample
+(gg_accept_greedy_sample), bit-exact against the oracle's float64 restatement of
+internal/engine/sampling.go:40-192 (ora_accept_greedy_sample / ora_emit_positions).
+
+Every case runs twice: the normal path (parallel float64 sums, sequential replay only for
+rows too close to a boundary) and GG_SAMPLE_EXACT (every draw replayed sequentially), so both
+device paths are pinned to the same oracle."""
+import numpy as np
+import pytest
+import torch
+
+import gollmgo_amd.verify as gv
+from helpers import say
+from oracle import oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+TD = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def case(B, K, V, dt, seed, sd=2.0, accept_all=0.8):
+    """Logits ~ N(0, sd) in dt; with probability accept_all a sequence's drafts are its rows'
+    argmaxes, so it reaches the bonus draw."""
+    rng = np.random.default_rng(seed)
+    lg = torch.from_numpy(rng.normal(0, sd, (B, K + 1, V)).astype(np.float32)).to(TD[dt])
+    host = lg.float().numpy()
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    for b in range(B):
+        if rng.random() < accept_all:
+            for j in range(K):
+                drafts[b, j] = ora.argmax(host[b, j])
+    n = rng.integers(0, K + 1, B).astype(np.int32)
+    u = rng.random(B)
+    return lg, host, drafts, n, u
+
+
+def run(lg, drafts, n, u, T, top_k, top_p, flags=0):
+    acc, tok = gv.accept_greedy_sample(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda(),
+                                       torch.from_numpy(np.ascontiguousarray(u, np.float64)).cuda(), T, top_k,
+                                       top_p, flags)
+    torch.cuda.synchronize()
+    return acc.cpu().numpy(), tok.cpu().numpy()
+
+
+def check(lg, host, drafts, n, u, T, top_k, top_p, label):
+    ea, et = ora.accept_greedy_sample(host, drafts, n, T, top_k, top_p, u, threads=16)
+    for flags in (0, gv.SAMPLE_EXACT):
+        say(f"{label} flags={flags}")
+        acc, tok = run(lg, drafts, n, u, T, top_k, top_p, flags)
+        bad = np.nonzero((acc != ea) | (tok != et))[0]
+        assert bad.size == 0, (label, flags, bad[:5], acc[bad[:5]], ea[bad[:5]], tok[bad[:5]], et[bad[:5]])
+    return ea, et
+
+
+@pytest.mark.parametrize("T,top_k,top_p", [(0.8, 0, 0.0), (0.8, 50, 0.0), (0.8, 0, 0.95), (1.3, 50, 0.9),
+                                           (0.6, 1, 0.5), (1.0, 4095, 0.99), (0.0, 50, 0.95)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_sample_small_vocab(gpu, dt, T, top_k, top_p):
+    lg, host, drafts, n, u = case(24, 3, 5003, dt, seed=int(T * 100) + top_k + int(top_p * 1000))
+    check(lg, host, drafts, n, u, T, top_k, top_p, f"small dt={dt} T={T} k={top_k} p={top_p}")
+
+
+@pytest.mark.parametrize("shape,dt", [((32, 4, 128256), "bf16"), ((8, 8, 128256), "bf16")])
+@pytest.mark.parametrize("top_k,top_p", [(0, 0.0), (50, 0.0), (0, 0.95), (50, 0.95)])
+def test_sample_config_shapes_via_emit_positions(gpu, shape, dt, top_k, top_p):
+    """Configs 2 and 4 at T = 0.8: the device decision equals what emitSpeculative would
+    compute from the full rows (ora_emit_positions reads them as Go slices)."""
+    B, K, V = shape
+    lg, host, drafts, n, u = case(B, K, V, dt, seed=B * 100 + K + top_k)
+    say(f"config shape={shape} k={top_k} p={top_p}")
+    ea, et = ora.emit_positions(drafts, n, [[host[b, j] for j in range(K + 1)] for b in range(B)], 0.8, top_p, u,
+                                top_k=top_k)
+    for flags in (0, gv.SAMPLE_EXACT):
+        acc, tok = run(lg, drafts, n, u, 0.8, top_k, top_p, flags)
+        assert np.array_equal(acc, ea) and np.array_equal(tok, et), (flags, acc, ea, tok, et)
+    assert (ea == np.clip(n, 0, K)).sum() >= B // 4  # enough bonus draws
+
+
+def test_sample_uniforms_on_cdf_boundaries(gpu):
+    """u placed exactly on, and one ulp below, float64 CDF boundaries of the rule: the
+    parallel sums cannot decide these, so the sequential replay must."""
+    B, K, V = 40, 0, 20011
+    rng = np.random.default_rng(5)
+    host = rng.normal(0, 2, (B, 1, V)).astype(np.float32)
+    lg = torch.from_numpy(host)
+    drafts = np.zeros((B, 0), np.int32)
+    n = np.zeros(B, np.int32)
+    for top_k, top_p in [(0, 0.0), (0, 0.9), (100, 0.0), (100, 0.8)]:
+        u = np.empty(B)
+        for b in range(B):
+            c = np.cumsum(ora.sampler_probs_f64(host[b, 0], 0.8, top_k, top_p))
+            nz = np.nonzero(np.diff(c) > 0)[0]
+            i = int(nz[rng.integers(0, len(nz))])
+            u[b] = c[i] if b % 2 == 0 else np.nextafter(c[i], 0.0)
+        check(lg, host, drafts, n, u, 0.8, top_k, top_p, f"boundaries k={top_k} p={top_p}")
+
+
+def test_sample_special_rows(gpu):
+    """Rows the fast path hands to the replay (NaN, +inf, all -inf, one bin holding every
+    element) and edges of the uniform and the filters."""
+    V = 9001
+    rng = np.random.default_rng(9)
+    rows = []
+    r = rng.normal(0, 2, V).astype(np.float32); r[17] = np.nan; rows.append(r)
+    r = rng.normal(0, 2, V).astype(np.float32); r[0] = np.nan; rows.append(r)
+    r = rng.normal(0, 2, V).astype(np.float32); r[4000] = np.inf; rows.append(r)
+    r = np.full(V, -np.inf, np.float32); rows.append(r)
+    r = np.full(V, -np.inf, np.float32); r[123] = 1.0; rows.append(r)
+    r = np.full(V, 0.5, np.float32); rows.append(r)                      # every element ties
+    r = np.where(rng.random(V) < 0.5, 0.0, -0.0).astype(np.float32); rows.append(r)  # +-0 ties
+    r = np.round(rng.normal(0, 2, V) * 4).astype(np.float32) / 4; rows.append(r)     # heavy ties
+    r = rng.normal(0, 2, V).astype(np.float32); r[:100] = -np.inf; rows.append(r)
+    r = (rng.normal(0, 1, V) * 1e-9).astype(np.float32); rows.append(r)  # tiny logits
+    host = np.stack(rows)[:, None, :]
+    B = host.shape[0]
+    lg = torch.from_numpy(host)
+    drafts = np.zeros((B, 0), np.int32)
+    n = np.zeros(B, np.int32)
+    for T, top_k, top_p in [(0.8, 0, 0.0), (0.8, 10, 0.0), (0.8, 0, 0.5), (2.0, 3000, 0.7), (1e30, 0, 0.0),
+                            (2e-9, 0, 0.0)]:
+        for u in (0.0, 0.5, 0.999999999, 1.0 - 2.0 ** -53):
+            check(lg, host, drafts, n, np.full(B, u), T, top_k, top_p, f"special T={T} k={top_k} p={top_p} u={u}")
+
+
+def test_sample_matches_greedy_at_zero_temperature(gpu):
+    lg, host, drafts, n, u = case(16, 5, 32000, "bf16", seed=77)
+    say("sample T=0 vs greedy")
+    acc, tok = run(lg, drafts, n, u, 0.0, 50, 0.9)
+    ga, gt = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(acc, ga.cpu().numpy()) and np.array_equal(tok, gt.cpu().numpy())
