@@ -58,7 +58,6 @@ struct RowStats {
 
 constexpr int kCandCap = 4096;
 constexpr int kFindThreads = 1024;  // draw find: threads per sequence
-enum { kDrawPlain = 0, kDrawResidual = 1, kDrawNoDraft = 2 };  // what the final draw samples
 
 // The nucleus boundary of one row (top-p), from the coarse histogram: the boundary bin,
 // the mass of the bins before it and its own mass.
@@ -197,11 +196,6 @@ __device__ __forceinline__ int cb_abs(float l, float inv_t) {
     return (int)__builtin_floorf(y);
 }
 
-// Residual weight sums of one segment of a sequence's final row (dense draft
-// distributions only), in units of W.
-struct SegSum {
-    u128 res;
-};
 
 // Per-row state of the top-p decision: certain outcome from the coarse bounds, or
 // resolved from the exact nucleus.
@@ -1116,276 +1110,21 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
             break;
         }
     }
-    const int row = b * R + a;
-    RowView v;
-    if (use_topp) {
-        const RowStats st = stats[row];
-        v = RowView{st.zp, st.m, st.lam, st.idx_cut};
-    } else {
-        v.m = row_max_wave(seg_max, row, nseg);
-        v.zp = row_z_wave(seg_max, seg_e, row, nseg, v.m, inv_t);
-        v.lam = 0;
-        v.idx_cut = 0x7fffffff;
-    }
-    return SeqPlan{v, SeqDecision{a, a, residual}};
+    return SeqPlan{RowView{}, SeqDecision{a, a, residual}};
 }
 
-// Wave 0 of the block decides sequence b; the plan is returned to every thread.
+// One wave per sequence: the acceptance walk, then what the final draw takes: the row
+// and, after a rejection, the rejected draft (the residual draw excludes it).
 template <gg_dtype_t DT>
-__device__ __forceinline__ SeqPlan decide_in_block(const DecideIn& in, int b) {
-    __shared__ SeqPlan s_plan;
-    if (threadIdx.x < 64) {
-        const SeqPlan p = decide_seq<DT>(in, b);
-        if (threadIdx.x == 0) s_plan = p;
-    }
-    __syncthreads();
-    return s_plan;
-}
-
-// G (dense draft distributions only): per (sequence, segment) the residual weight sum of
-// the final row's segment, f_s * sum of rq, rq = e - min(e, floor(q * Zp / f_s)) over the
-// nucleus less the rejected draft x itself (the rejected draft's q row read once). A
-// rejection with u < 1 means p(x) < q(x), so x's residual max(0, p - q) is exactly 0; it is
-// set to 0 rather than computed, so that rounding never gives it a unit. Thread t of kSumThreads owns kSumRuns
-// runs of eight logits, run r at offset (r * kSumThreads + t) * 8 of the segment.
-#ifndef GG_SUM_THREADS
-#define GG_SUM_THREADS 512
-#endif
-constexpr int kSumThreads = GG_SUM_THREADS;
-constexpr int kSumRuns = kSegElems / (kSumThreads * 8);
-static_assert(kSumRuns * kSumThreads * 8 == kSegElems, "segment = runs of eight logits per thread");
-// Every block decides its sequence itself (decide_seq, one wave); block 0 of the
-// sequence stores the plan for the draw.
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSumThreads) seg_residual_kernel(
-    DecideIn din, int vec_ok, SeqPlan* __restrict__ plan, SegSum* __restrict__ seg_sum) {
-    const int seg = blockIdx.x, b = blockIdx.y;
-    const void* __restrict__ logits = din.logits;
-    const float* __restrict__ dprobs = din.dprobs;
-    const int K = din.K, V = din.V, nseg = din.nseg;
-    const float inv_t = din.inv_t;
-    const int32_t* __restrict__ drafts = din.drafts;
-    const float* __restrict__ seg_max = din.seg_max;
-    const int R = K + 1;
-    constexpr int kW = kSumThreads / 64;
-    __shared__ u64 red64[kW];
-    const SeqPlan sp = decide_in_block<DT>(din, b);
-    if (seg == 0 && threadIdx.x == 0) plan[b] = sp;
-    const SeqDecision d = sp.d;
-    if (!d.residual) return;  // the bonus draw needs no residual
-    const RowView rv = sp.v;
-    const int row = b * R + d.row;
-    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    const float* qrow = dprobs + ((size_t)b * K + d.row) * V;
-    const int xr = drafts[(size_t)b * K + d.row];
-    float x[kSumRuns][8], q[kSumRuns][8];
-#pragma unroll
-    for (int r = 0; r < kSumRuns; ++r) {
-        const int e0 = seg * kSegElems + (r * kSumThreads + (int)threadIdx.x) * 8;
-        load8<DT>(lp, V, e0, vec_ok, x[r]);
-        load8<GG_DTYPE_F32>(qrow, V, e0, vec_ok && ((uintptr_t)qrow % 16) == 0, q[r]);
-    }
-    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
-    const float ms = seg_max[(size_t)row * nseg + seg];
-    const u64 f = (finite_f(rv.m) && finite_f(ms)) ? seg_factor(ms, rv.m, inv_t) : 0ull;
-    const double zpf = f ? gg_u128_to_double(rv.zp) / (double)f : 0.0;
-    // Each residual is an integer below 2^36 (e - floor(qd) with floor(qd) < e), so the
-    // thread's sum is exact in a double.
-    double rd = 0.0;
-#pragma unroll
-    for (int r = 0; r < kSumRuns; ++r) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i = seg * kSegElems + (r * kSumThreads + (int)threadIdx.x) * 8 + k;
-            const bool keep = f && nu.kept(x[r][k], i);  // (NaN past the row: never kept)
-            const double e = keep ? (double)gg_weight_f(x[r][k], ms, inv_t) : 0.0;
-            const double qd = gg_clean_q(q[r][k]) * zpf;
-            rd += (i != xr && e > qd) ? e - __builtin_floor(qd) : 0.0;  // (qd >= 0: e = 0 adds 0)
-        }
-    }
-    u64 s_res = (u64)rd;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    for (int o = 32; o > 0; o >>= 1) s_res += shfl_xor_u64(s_res, o);
-    if (lane == 0) red64[wv] = s_res;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        u64 tr = 0;
-        for (int w = 0; w < kW; ++w) tr += red64[w];
-        seg_sum[(size_t)b * nseg + seg] = SegSum{(u128)tr * f};
-    }
-}
-
-// H: per sequence, the draw. Wave 0 forms the final row's per-segment masses (lane s =
-// segment s): plain = f_s * (sum of kept e); without the draft = plain less the rejected
-// draft x's f_s * e_x (the residual of one-hot q); residual = the dense sums above, or
-// the mass without the draft for one-hot q. The draw uses the residual; when it vanished
-// (dense q that is not a distribution), the row without the draft; when that vanished too,
-// the plain row. So a rejected draft is never drawn unless it holds the row's whole mass.
-// It picks the segment holding floor(u * total) (the last segment with mass when none
-// passes it, u >= 1). In that segment thread k of 1024 owns the 8 consecutive elements
-// [8k, 8k+8): their integer weights (e, or rq) and a block scan find the element (or the
-// last non-zero one).
-// Without dense draft distributions (no residual launch) the block decides its sequence
-// itself (decide_seq); otherwise it reads the plan the residual launch stored.
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kFindThreads) seg_draw_find_kernel(
-    DecideIn din, int vec_ok, const u64* __restrict__ seg_keep, const SeqPlan* __restrict__ plan,
-    const SegSum* __restrict__ seg_sum, int32_t* __restrict__ out_acc, int32_t* __restrict__ out_tok) {
+__global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* __restrict__ out_acc,
+                                                        int* __restrict__ spec_row, int* __restrict__ spec_x) {
     const int b = blockIdx.x;
-    const void* __restrict__ logits = din.logits;
-    const float* __restrict__ dprobs = din.dprobs;
-    const int K = din.K, V = din.V, nseg = din.nseg, use_topp = din.use_topp;
-    const float inv_t = din.inv_t;
-    const int32_t* __restrict__ drafts = din.drafts;
-    const float* __restrict__ uniforms = din.uniforms;
-    const float* __restrict__ seg_max = din.seg_max;
-    const u64* __restrict__ seg_e = din.seg_e;
-    const int R = K + 1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __shared__ int s_seg, s_mode, s_found, s_last_mode;
-    __shared__ u128 s_t;
-    __shared__ u64 s_wsum[kFindThreads / 64];
-    const SeqPlan sp = dprobs ? plan[b] : decide_in_block<DT>(din, b);
-    const SeqDecision d = sp.d;
-    const RowView rv = sp.v;
-    const int row = b * R + d.row;
-    const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    const bool dense = d.residual && dprobs;
-    const int xr = d.residual ? drafts[(size_t)b * K + d.row] : -1;
-    const Nucleus nu{rv.m, inv_t, rv.lam, rv.idx_cut};
-    if (wave == 0) {
-        u128 pl = 0, ex = 0, res = 0;
-        if (lane < nseg) {
-            const float ms = seg_max[(size_t)row * nseg + lane];
-            const u64 f = (finite_f(rv.m) && finite_f(ms)) ? seg_factor(ms, rv.m, inv_t) : 0ull;
-            const u64 ek = use_topp ? seg_keep[(size_t)row * nseg + lane] : seg_e[(size_t)row * nseg + lane];
-            pl = (u128)ek * f;
-            ex = pl;
-            if (d.residual && xr >= 0 && xr < V && xr / kSegElems == lane && f) {
-                const float l = ld<DT>(lp, xr);
-                const u64 e = nu.kept(l, xr) ? gg_weight(l, ms, inv_t) : 0ull;
-                ex -= (u128)e * f;
-            }
-            res = dense ? seg_sum[(size_t)b * nseg + lane].res : ex;
-        }
-        u128 tot_res = res, tot_ex = ex, tot_pl = pl;
-        for (int off = 32; off > 0; off >>= 1) {
-            tot_res += shfl_xor_u128(tot_res, off);
-            tot_ex += shfl_xor_u128(tot_ex, off);
-            tot_pl += shfl_xor_u128(tot_pl, off);
-        }
-        // kDrawPlain: the target row; kDrawResidual: the residual; kDrawNoDraft: the
-        // target row without the rejected draft.
-        const int mode = !d.residual ? kDrawPlain
-                         : tot_res > 0 ? kDrawResidual
-                         : tot_ex > 0  ? kDrawNoDraft
-                                       : kDrawPlain;
-        const u128 tot = mode == kDrawResidual ? tot_res : mode == kDrawNoDraft ? tot_ex : tot_pl;
-        const u128 v = mode == kDrawResidual ? res : mode == kDrawNoDraft ? ex : pl;
-        int seg = -1, last_mode = 0;
-        u128 tt = 0;
-        if (tot > 0) {
-            const double u = (double)uniforms[(size_t)b * R + K];
-            const u128 t = gg_u128_floor(u * gg_u128_to_double(tot));
-            u128 incl = v;
-            for (int off = 1; off < 64; off <<= 1) {
-                const u128 y = shfl_up_u128(incl, off);
-                if (lane >= off) incl += y;
-            }
-            // First segment whose inclusive prefix passes t; none (u >= 1): the last
-            // segment with mass, searched for its last non-zero element.
-            const unsigned long long hit = __ballot(lane < nseg && incl > t);
-            if (hit) {
-                seg = __ffsll((long long)hit) - 1;
-                tt = t - shfl_u128(incl - v, seg);
-            } else {
-                const unsigned long long nz = __ballot(lane < nseg && v > 0);
-                seg = 63 - __clzll((long long)nz);
-                last_mode = 1;
-            }
-        }
-        if (lane == 0) {
-            s_mode = mode;
-            s_seg = seg;
-            s_t = tt;
-            s_last_mode = last_mode;
-            s_found = 0;
-            out_acc[b] = d.accepted;
-        }
+    const SeqPlan p = decide_seq<DT>(din, b);
+    if (threadIdx.x == 0) {
+        out_acc[b] = p.d.accepted;
+        spec_row[b] = p.d.row;
+        spec_x[b] = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
     }
-    __syncthreads();
-    if (s_seg < 0) {  // no mass at all
-        if (threadIdx.x == 0) out_tok[b] = 0;
-        return;
-    }
-    const int mode = s_mode;
-    const float* qrow = (mode == kDrawResidual && dense) ? dprobs + ((size_t)b * K + d.row) * V : nullptr;
-    const float ms = seg_max[(size_t)row * nseg + s_seg];
-    // The chosen segment has mass, so its factor f is positive; its weights are f times
-    // integers (e, or rq in units of e), so the element whose prefix passes the target
-    // tt is the one whose integer prefix passes tq = floor(tt / f).
-    const u64 f = seg_factor(ms, rv.m, inv_t);
-    const double zpf = f ? gg_u128_to_double(rv.zp) / (double)f : 0.0;
-    const u128 tt = s_t;
-    u64 tq = f ? (u64)(gg_u128_to_double(tt) / (double)f) : 0ull;  // within one of floor(tt / f)
-    while (f && (u128)tq * f > tt) --tq;
-    while (f && (u128)(tq + 1) * f <= tt) ++tq;
-    constexpr int kPer = kSegElems / kFindThreads;
-    static_assert(kPer == 8, "eight consecutive logits per thread");
-    const int e0 = s_seg * kSegElems + kPer * threadIdx.x;
-    float xl[kPer], ql[kPer];
-    load8<DT>(lp, V, e0, vec_ok, xl);
-    if (qrow) load8<GG_DTYPE_F32>(qrow, V, e0, vec_ok && ((uintptr_t)qrow % 16) == 0, ql);
-    u64 r[kPer];
-    u64 mine = 0;
-    int last_nz = -1;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int i = e0 + k;
-        const u64 e = nu.kept(xl[k], i) ? gg_weight(xl[k], ms, inv_t) : 0ull;  // (NaN past the row)
-        u64 w = e;
-        if (mode != kDrawPlain && i == xr) {
-            w = 0;
-        } else if (qrow) {
-            const double qd = gg_clean_q(ql[k]) * zpf;
-            w = (e && (double)e > qd) ? e - (u64)__builtin_floor(qd) : 0ull;
-        }
-        r[k] = w;
-        mine += w;
-        last_nz = w ? i : last_nz;
-    }
-    if (s_last_mode) {
-        for (int o = 32; o > 0; o >>= 1) last_nz = max(last_nz, __shfl_xor(last_nz, o));
-        if (lane == 0 && last_nz >= 0) atomicMax(&s_found, last_nz);
-        __syncthreads();
-        if (threadIdx.x == 0) out_tok[b] = s_found;
-        return;
-    }
-    // Exclusive block scan of the thread sums.
-    u64 incl = mine;
-    for (int off = 1; off < 64; off <<= 1) {
-        const u64 y = shfl_up_u64(incl, off);
-        if (lane >= off) incl += y;
-    }
-    if (lane == 63) s_wsum[wave] = incl;
-    __syncthreads();
-    u64 before = incl - mine;
-    for (int w = 0; w < wave; ++w) before += s_wsum[w];
-    if (before <= tq && before + mine > tq) {
-        u64 c = before;
-        int found = e0 + kPer - 1;
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            c += r[k];
-            if (c > tq) {
-                found = e0 + k;
-                break;
-            }
-        }
-        s_found = found;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) out_tok[b] = s_found;
 }
 
 }  // namespace
@@ -1395,8 +1134,9 @@ static int rej_nseg(int vocab) { return (vocab + kSegElems - 1) / kSegElems; }
 struct RejWs {
     float* seg_max;
     u64* seg_e;
-    SeqPlan* plan;
-    SegSum* seg_sum;   // dense draft distributions: residual sums per (sequence, segment)
+    int* spec_row;     // the final draw's row per sequence
+    int* spec_x;       // the rejected draft of a residual draw, -1 for a plain draw
+    void* draw;        // the final draw's own workspace (launch_final_draw)
     RowStats* stats;   // top-p: exact nucleus statistics of flagged rows
     u64* seg_hist;     // top-p: coarse histogram per (row, segment)
     RowPick* pick;
@@ -1424,8 +1164,9 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
     };
     w.seg_max = (float*)take(rows * nseg * sizeof(float));
     w.seg_e = (u64*)take(rows * nseg * sizeof(u64));
-    w.plan = (SeqPlan*)take((size_t)num_seqs * sizeof(SeqPlan));
-    w.seg_sum = (SegSum*)take((size_t)num_seqs * nseg * sizeof(SegSum));
+    w.spec_row = (int*)take((size_t)num_seqs * sizeof(int));
+    w.spec_x = (int*)take((size_t)num_seqs * sizeof(int));
+    w.draw = take(final_draw_workspace_bytes(num_seqs, vocab));
     if (topp) {
         w.stats = (RowStats*)take(rows * sizeof(RowStats));
         w.seg_hist = (u64*)take(rows * nseg * kSegBins * sizeof(u64));
@@ -1491,10 +1232,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                                                              inv_t, n_drafts, w.seg_max,     \
                                                                              w.seg_e, nullptr);              \
     }                                                                                                        \
-    if (q)                                                                                                   \
-        seg_residual_kernel<DTV><<<dim3(nseg, num_seqs), kSumThreads, 0, s>>>(din, vec_ok, w.plan, w.seg_sum); \
-    seg_draw_find_kernel<DTV><<<num_seqs, kFindThreads, 0, s>>>(din, vec_ok, w.seg_keep, w.plan, w.seg_sum,   \
-                                                               out_acc, out_tok);
+    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_REJ(GG_DTYPE_BF16) break;
@@ -1502,7 +1240,25 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
         default: return fail(GG_ERR_INVALID, "accept_rejection: logits dtype");
     }
 #undef GG_REJ
-    return check_hip(hipGetLastError(), "accept_rejection launch");
+    const gg_status_t st = check_hip(hipGetLastError(), "accept_rejection launch");
+    if (st != GG_OK) return st;
+    FinalDraw d{};
+    d.logits = logits;
+    d.dt = dt;
+    d.num_seqs = num_seqs;
+    d.max_drafts = K;
+    d.vocab = vocab;
+    d.temperature = (double)temperature;
+    d.top_k = 0;
+    d.top_p = (double)top_p;
+    d.uniforms_f32 = uniforms;
+    d.draft_probs = q;
+    d.spec_row = w.spec_row;
+    d.spec_x = w.spec_x;
+    d.seg_max = w.seg_max;
+    d.nseg_max = nseg;
+    d.out_tok = out_tok;
+    return launch_final_draw(d, w.draw, s);
 }
 
 }  // namespace gg

@@ -1,11 +1,14 @@
-// accept_sample.hip — greedy verify with the bonus token drawn as the reference samples it.
+// accept_sample.hip — the float64 token draw of the acceptance, as the reference samples.
 //
 // The reference's emitSpeculative (internal/engine/serving.go:514-566) runs the greedy
 // Verify over the draft rows, then, when every draft was accepted, draws the bonus token
 // with Sampler.Sample(posLogits[K]) (internal/engine/sampling.go:40-72): temperature,
 // top-k, softmax, top-p and a categorical draw, all in float64. This file adds that draw
 // to the greedy acceptance (accept_greedy.hip), with the uniform supplied in place of
-// rng.Float64().
+// rng.Float64(). The rejection acceptance (accept_rejection.hip) uses the same draw for its
+// final token: the bonus as above, or after a rejected draft x the residual
+// max(0, p - q) over tokens other than x, normalised, p being Sampler's distribution of
+// that row and q the draft distribution (one-hot at x for a deterministic drafter).
 //
 // The draw must give the token the float64 sequential rule gives, for every uniform. The
 // rule's sums run in index order (or in sorted order for top-p), one rounding per term, so
@@ -22,14 +25,15 @@
 // Orders the reference leaves open (sort.Slice is not stable) are fixed as value desc,
 // then index asc, NaN last; exp is gg_exp64 (gg_exp64.h), identical on host and device.
 //
-// Launches after the greedy pair (segment argmax, decide):
-//   prep   (B blocks)       : which sequences draw; row max from the greedy segments.
+// Launches after the acceptance has decided which row of each sequence is drawn from:
+//   prep   (B blocks)       : which sequences draw, from which row; the row max from the
+//                             acceptance's segment maxima.
 //   pass   (segments x B)   : e_i = exp(l_i/T - m) per element, segment sums, NaN/+inf
 //                             check, coarse histograms (count and mass per 4096 bins of
 //                             the value's order key) when top-k or top-p is on.
 //   select (B, top-k/p only): top-k threshold and nucleus cut from the histograms, the
 //                             crossing bin's items gathered and sorted in LDS.
-//   kept   (segments x B, top-k/p only): kept mass per segment.
+//   kept   (segments x B)   : the draw's weight per segment (kept e, or the residual).
 //   draw   (B)              : the segment and then the element where u * total falls.
 //   exact  (a few blocks)   : the literal rule for the rows flagged on the way.
 #include "gg_common.h"
@@ -53,8 +57,11 @@ constexpr int kNone = 0x7fffffff; // accept_greedy.hip's "no element" index
 enum : int { ST_NONE = 0, ST_DRAW = 1, ST_EXACT = 2 };
 
 struct RowInfo {
-    double m;                 // max scaled logit of the bonus row
+    double m;                 // max scaled logit of the drawn row
     unsigned long long cut;   // kept <=> comp_key >= cut (0 keeps every element)
+    double tot;               // the kept e summed (the nucleus mass with top-p)
+    int row;                  // row of the sequence drawn from
+    int x;                    // residual draw: the rejected draft (excluded); -1: plain draw
 };
 
 struct Ent {                  // exact path sort entry, ordered by (hi, lo) descending
@@ -62,17 +69,39 @@ struct Ent {                  // exact path sort entry, ordered by (hi, lo) desc
 };
 
 struct Layout {
-    size_t greedy, state, info, hcnt, hmass, segsum, segkept, exact, total;
+    size_t state, info, hcnt, hmass, segsum, segkept, exact, total;
     size_t slot_bytes, vpad, npow;
+};
+
+// Everything the draw launches share (passed by value).
+struct DrawParams {
+    const void* logits;       // [B][K+1][V]
+    gg_dtype_t dt;
+    int B, K, V, nseg;
+    double inv_t;
+    int top_k;
+    double top_p;
+    int use_k, use_p, filtered;
+    int vec;                  // rows allow 16-byte loads
+    double tau;
+    const double* ud;         // uniform of sequence b: ud[b], or else
+    const float* uf;          //   uf[b * (K + 1) + K]
+    const float* q;           // residual draws: dense draft distributions [B][K][V], or null
+    int* state;
+    RowInfo* info;
+    uint32_t* hcnt;
+    double* hmass;
+    double* segsum;
+    double* segkept;
+    int32_t* out_tok;
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-Layout layout(int B, int K, int V) {
+Layout layout(int B, int V) {
     Layout L{};
     const int nseg = (V + kSeg - 1) / kSeg;
-    size_t o = align256(greedy_workspace_bytes(B, K, V));
-    L.greedy = 0;
+    size_t o = 0;
     L.state = o;   o = align256(o + (size_t)B * sizeof(int));
     L.info = o;    o = align256(o + (size_t)B * sizeof(RowInfo));
     L.hcnt = o;    o = align256(o + (size_t)B * kBins * sizeof(uint32_t));
@@ -113,6 +142,69 @@ __device__ __forceinline__ double exp_term(float l, double inv_t, double m) {
     if (l == -INFINITY) return 0.0;
     const double v = (double)l * inv_t;
     return gg_exp64(v - m);
+}
+
+// The parallel path's exponential (gg_fast_exp64, gg_exp64.h): within 2e-14 relative of
+// gg_exp64; the margins count 1e-12. Nothing the rule decides depends on its bits, only sums
+// that clear a margin.
+constexpr double kFastExpErr = 1e-12;
+__device__ __forceinline__ double fast_exp64(double x) { return gg_fast_exp64(x); }
+__device__ __forceinline__ double fast_term(float l, double inv_t, double m) {
+    const double v = (double)l * inv_t;
+    return fast_exp64(v - m);  // -inf logits give -inf, hence 0
+}
+
+// Eight consecutive elements e0.. of a row as floats: one 16-byte load (two for f32) when
+// the row allows it, else element loads (past V: -inf).
+template <gg_dtype_t DT>
+__device__ __forceinline__ void load8(const void* row, int V, int e0, bool vec, float (&x)[8]) {
+    if (vec && e0 + 8 <= V) {
+        if constexpr (DT == GG_DTYPE_F32) {
+            const uint4 a = *(const uint4*)((const float*)row + e0);
+            const uint4 c = *(const uint4*)((const float*)row + e0 + 4);
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] = __uint_as_float(w[k]);
+        } else {
+            const uint4 a = *(const uint4*)((const uint16_t*)row + e0);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint16_t h = (uint16_t)(w[k >> 1] >> ((k & 1) * 16));
+                x[k] = DT == GG_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = e0 + k < V ? load_as_f32(row, DT, e0 + k) : -INFINITY;
+}
+
+__device__ __forceinline__ const void* drawn_row(const DrawParams& P, int b, int row) {
+    return (const uint8_t*)P.logits + ((size_t)b * (P.K + 1) + row) * P.V * dtype_bytes(P.dt);
+}
+__device__ __forceinline__ double uniform_of(const DrawParams& P, int b) {
+    return P.ud ? P.ud[b] : (double)P.uf[(size_t)b * (P.K + 1) + P.K];
+}
+__device__ __forceinline__ const float* q_row(const DrawParams& P, int b, const RowInfo& ri) {
+    return (P.q && ri.x >= 0) ? P.q + ((size_t)b * P.K + ri.row) * P.V : nullptr;
+}
+// A draft probability as the rule uses it: finite and in (0, 1], anything else 0.
+__device__ __forceinline__ double clean_q(float q) {
+    if (!(q > 0.0f) || !(q <= 3.402823466e38f)) return 0.0;
+    return q > 1.0f ? 1.0 : (double)q;
+}
+// The draw's weight of element e (logit l): its e if kept (plain draw, e units), or its
+// residual max(0, e/tot - q) (probability units; 0 at the rejected draft).
+__device__ __forceinline__ double draw_weight(const DrawParams& P, const RowInfo& ri, const float* qr, float l,
+                                              int e) {
+    if (comp_key(order_key(l), e) < ri.cut) return 0.0;
+    const double ev = fast_term(l, P.inv_t, ri.m);
+    if (ri.x < 0) return ev;
+    if (e == ri.x) return 0.0;
+    const double p = ev / ri.tot;
+    const double qv = qr ? clean_q(qr[e]) : 0.0;
+    return p > qv ? p - qv : 0.0;
 }
 
 __device__ __forceinline__ double lane_val(double x, int l) {
@@ -178,30 +270,48 @@ __device__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* sh, uint32_t* tota
 
 // ------------------------------------------------------------------------ prep
 
+// Sequence b draws from row spec_row[b] (-1: no draw), residual after draft spec_x[b]
+// (-1: plain) — or, for the greedy acceptance, from row n when all n drafts were accepted.
+// The row max comes from the acceptance's segment maxima: the greedy (value, index) pairs
+// of 4096-element segments (gws), or the rejection's finite maxima of 8192-element
+// segments (seg_max).
 __global__ void __launch_bounds__(256) sample_prep_kernel(
-    const float2* __restrict__ gws, int K, int nseg_g, const int32_t* __restrict__ n_drafts,
-    const int32_t* __restrict__ acc, double inv_t, int hist, int force_exact, uint32_t* __restrict__ hcnt,
-    double* __restrict__ hmass, int* __restrict__ state, RowInfo* __restrict__ info) {
+    DrawParams P, const float2* __restrict__ gws, const float* __restrict__ seg_max, int nseg_m,
+    const int32_t* __restrict__ n_drafts, const int32_t* __restrict__ acc, const int* __restrict__ spec_row,
+    const int* __restrict__ spec_x, int force_exact) {
     const int b = blockIdx.x;
-    const int R = K + 1;
-    const int n = clamp_n(n_drafts, b, K);
-    if (acc[b] != n) {
-        if (threadIdx.x == 0) state[b] = ST_NONE;
+    const int K = P.K, R = K + 1;
+    int row, x = -1;
+    if (gws) {
+        const int n = clamp_n(n_drafts, b, K);
+        row = acc[b] == n ? n : -1;
+    } else {
+        row = spec_row[b];
+        x = spec_x[b];
+    }
+    if (row < 0) {
+        if (threadIdx.x == 0) P.state[b] = ST_NONE;
         return;
     }
-    if (hist)
+    if (P.filtered)
         for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
-            hcnt[(size_t)b * kBins + i] = 0;
-            hmass[(size_t)b * kBins + i] = 0.0;
+            P.hcnt[(size_t)b * kBins + i] = 0;
+            P.hmass[(size_t)b * kBins + i] = 0.0;
         }
     if (threadIdx.x < 64) {
         float mx = -INFINITY;
         int any = 0;
-        for (int s = threadIdx.x; s < nseg_g; s += 64) {
-            const float2 p = gws[((size_t)b * R + n) * nseg_g + s];
-            if (__float_as_int(p.y) != kNone) {
-                any = 1;
-                mx = fmaxf(mx, p.x);
+        for (int s = threadIdx.x; s < nseg_m; s += 64) {
+            if (gws) {
+                const float2 p = gws[((size_t)b * R + row) * nseg_m + s];
+                if (__float_as_int(p.y) != kNone) {
+                    any = 1;
+                    mx = fmaxf(mx, p.x);
+                }
+            } else {
+                const float v = seg_max[((size_t)b * R + row) * nseg_m + s];
+                if (v > -INFINITY) any = 1;
+                mx = fmaxf(mx, v);
             }
         }
         for (int o = 32; o > 0; o >>= 1) {
@@ -209,34 +319,120 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             any |= __shfl_xor(any, o);
         }
         if (threadIdx.x == 0) {
-            const double m = (double)mx * inv_t;
+            const double m = (double)mx * P.inv_t;
             int st = ST_DRAW;
             // No finite maximum (all -inf / NaN, or +inf present), or a non-finite scale:
             // the literal rule decides.
             if (!any || !(mx > -INFINITY && mx < INFINITY) || !(m > -INFINITY && m < INFINITY) || force_exact)
                 st |= ST_EXACT;
-            info[b].m = m;
-            info[b].cut = 0;
-            state[b] = st;
+            RowInfo ri;
+            ri.m = m;
+            ri.cut = 0;
+            ri.tot = 0.0;
+            ri.row = row;
+            ri.x = x;
+            P.info[b] = ri;
+            P.state[b] = st;
         }
     }
 }
 
 // ------------------------------------------------------------------------ pass
 
-__global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(
-    const void* __restrict__ logits, gg_dtype_t dt, int K, int V, int nseg,
-    const int32_t* __restrict__ n_drafts, double inv_t, int want_cnt, int want_mass,
-    int* __restrict__ state, const RowInfo* __restrict__ info, uint32_t* __restrict__ hcnt,
-    double* __restrict__ hmass, double* __restrict__ segsum) {
+// The draw itself, by one block of kSegThreads: the segment where u * total falls (sums
+// per segment of the draw's weights), then the element inside it (16 per thread). A plain
+// draw's margins are tau * total (e units); a residual's tau * (1 + total) (probability
+// units: the parallel p carries up to tau of error summed over the row, whatever q is). A
+// residual total within a few margins of 0 may be 0 in the rule, whose fallbacks then
+// apply. Undecided: the row is left to the literal rule.
+template <gg_dtype_t DT>
+__device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, const double* sums) {
+    __shared__ double s_red[16];
+    __shared__ int s_seg, s_tok, s_bad;
+    __shared__ double s_base, s_tot;
+    const double tau = P.tau;
+    const double u = uniform_of(P, b);
+    const int nseg = P.nseg;
+    if (threadIdx.x == 0) {
+        double tot = 0.0;
+        for (int s = 0; s < nseg; ++s) tot += sums[s];
+        const double t = u * tot;
+        double run = 0.0;
+        int sel = -1;
+        for (int s = 0; s < nseg; ++s) {
+            if (run + sums[s] > t) {
+                sel = s;
+                break;
+            }
+            run += sums[s];
+        }
+        const double marg = ri.x < 0 ? tau * tot : tau * (1.0 + tot);
+        if (ri.x >= 0 && tot <= 8.0 * marg) sel = -1;
+        if (!(u >= tau && u < 1.0 - tau)) sel = -1;  // near 0, near or past 1, NaN
+        s_seg = sel;
+        s_base = run;
+        s_tot = tot;
+        s_tok = -1;
+        s_bad = 0;
+    }
+    __syncthreads();
+    const int seg = s_seg;
+    if (seg < 0) {
+        if (threadIdx.x == 0) atomicOr(&P.state[b], ST_EXACT);
+        return;
+    }
+    const double tot = s_tot, t = u * tot;
+    const double marg = ri.x < 0 ? tau * tot : tau * (1.0 + tot);
+    const void* row = drawn_row(P, b, ri.row);
+    const float* qr = q_row(P, b, ri);
+    constexpr int kPer = kSeg / kSegThreads;
+    static_assert(kPer == 16, "sixteen elements per thread");
+    const int e0 = seg * kSeg + threadIdx.x * kPer;
+    double ev[kPer];
+    double loc = 0.0;
+    float xl[2][8];
+    load8<DT>(row, P.V, e0, P.vec, xl[0]);
+    load8<DT>(row, P.V, e0 + 8, P.vec, xl[1]);
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int e = e0 + q;
+        ev[q] = e < P.V ? draw_weight(P, ri, qr, xl[q >> 3][q & 7], e) : 0.0;
+        loc += ev[q];
+    }
+    double btot;
+    double run = s_base + block_excl_scan(loc, s_red, &btot);
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const double nx = run + ev[q];
+        if (run <= t && nx > t) {
+            const bool ok = (t - run) > marg && (nx - t) > marg;
+            if (ok) s_tok = e0 + q;
+            else s_bad = 1;
+        }
+        run = nx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (s_tok >= 0 && !s_bad) P.out_tok[b] = s_tok;
+        else atomicOr(&P.state[b], ST_EXACT);
+    }
+}
+
+// Per (segment, sequence): e of every element (the parallel exponential), the segment's
+// sum, the NaN / +inf check, and with top-k / top-p the coarse histograms.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) {
     const int b = blockIdx.y, seg = blockIdx.x;
-    if (state[b] != ST_DRAW) return;
+    if (P.state[b] != ST_DRAW) return;
     __shared__ uint32_t s_cnt[kBins];
     __shared__ double s_mass[kBins];
     __shared__ double s_red[16];
-    const int n = clamp_n(n_drafts, b, K);
-    const void* row = (const uint8_t*)logits + ((size_t)b * (K + 1) + n) * V * dtype_bytes(dt);
-    const double m = info[b].m;
+    const int want_cnt = P.use_k, want_mass = P.filtered;
+    const int V = P.V;
+    const double inv_t = P.inv_t;
+    const RowInfo ri = P.info[b];
+    const void* row = drawn_row(P, b, ri.row);
+    const double m = ri.m;
     if (want_cnt || want_mass) {
         for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
             s_cnt[i] = 0;
@@ -246,111 +442,201 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(
     }
     double acc = 0.0;
     int bad = 0;
-    const int end = min(V, (seg + 1) * kSeg);
-    for (int e = seg * kSeg + threadIdx.x; e < end; e += blockDim.x) {
-        const float l = load_as_f32(row, dt, e);
-        if (l != l || l == INFINITY) {
-            bad = 1;
-            continue;
-        }
-        const double ev = exp_term(l, inv_t, m);
-        acc += ev;
-        if (want_cnt || want_mass) {
-            const int bin = (int)(order_key(l) >> 20);
-            if (want_cnt) atomicAdd(&s_cnt[bin], 1u);
-            if (want_mass && ev != 0.0) atomicAdd(&s_mass[bin], ev);
+    for (int c = threadIdx.x; c < kSeg / 8; c += blockDim.x) {
+        const int e0 = seg * kSeg + c * 8;
+        if (e0 >= V) break;
+        float x[8];
+        load8<DT>(row, V, e0, P.vec, x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float l = x[k];
+            if (l != l || l == INFINITY) bad = 1;
+            const double ev = (l != l || l == INFINITY) ? 0.0 : fast_term(l, inv_t, m);
+            acc += ev;
+            if ((want_cnt || want_mass) && e0 + k < V) {
+                const int bin = (int)(order_key(l) >> 20);
+                if (want_cnt) atomicAdd(&s_cnt[bin], 1u);
+                if (want_mass && ev != 0.0) atomicAdd(&s_mass[bin], ev);
+            }
         }
     }
     if (__syncthreads_or(bad)) {
-        if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
+        if (threadIdx.x == 0) atomicOr(&P.state[b], ST_EXACT);
         return;
     }
     const double tot = block_sum(acc, s_red);
-    if (threadIdx.x == 0) segsum[(size_t)b * nseg + seg] = tot;
+    if (threadIdx.x == 0) P.segsum[(size_t)b * P.nseg + seg] = tot;
     if (want_cnt || want_mass) {
         for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
-            if (want_cnt && s_cnt[i]) atomicAdd(&hcnt[(size_t)b * kBins + i], s_cnt[i]);
-            if (want_mass && s_mass[i] != 0.0) unsafeAtomicAdd(&hmass[(size_t)b * kBins + i], s_mass[i]);
+            if (want_cnt && s_cnt[i]) atomicAdd(&P.hcnt[(size_t)b * kBins + i], s_cnt[i]);
+            if (want_mass && s_mass[i] != 0.0) unsafeAtomicAdd(&P.hmass[(size_t)b * kBins + i], s_mass[i]);
         }
     }
 }
 
 // ---------------------------------------------------------------------- select
 
-// Bitonic sort of n_pad (a power of two, <= kCap) keys in LDS, descending.
-__device__ void lds_sort_desc(unsigned long long* a, int n_pad) {
-    for (int k = 2; k <= n_pad; k <<= 1)
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int p = threadIdx.x; p < n_pad / 2; p += blockDim.x) {
-                const int i = (p / j) * 2 * j + (p % j), l = i + j;
-                const unsigned long long x = a[i], y = a[l];
-                const bool desc = (i & k) == 0;
-                if (desc ? x < y : x > y) {
-                    a[i] = y;
-                    a[l] = x;
-                }
-            }
-            __syncthreads();
-        }
-}
-
-// Gather the elements of the row whose order key falls in bin `bin` into s_comp (sorted
-// descending, padded with 0) and their e into s_e. Returns the count, or -1 when the bin
-// holds more than kCap elements.
-__device__ int gather_bin(const void* row, gg_dtype_t dt, int V, int bin, double inv_t, double m,
+// Gather the elements of the row whose order key falls in bin `bin` into s_comp (in no
+// particular order) and their e into s_e. Returns the count, or -1 when the bin holds more
+// than kCap elements.
+template <gg_dtype_t DT>
+__device__ int gather_bin(const void* row, int V, bool vec, int bin, double inv_t, double m,
                           unsigned long long* s_comp, double* s_e, int* s_n) {
     if (threadIdx.x == 0) *s_n = 0;
     __syncthreads();
-    for (int e = threadIdx.x; e < V; e += blockDim.x) {
-        const float l = load_as_f32(row, dt, e);
-        const uint32_t key = order_key(l);
-        if ((int)(key >> 20) == bin) {
-            const int slot = atomicAdd(s_n, 1);
-            if (slot < kCap) s_comp[slot] = comp_key(key, e);
+    const int nch = (V + 7) / 8;
+    const int lane = threadIdx.x & 63;
+    for (int c0 = threadIdx.x; c0 - (int)threadIdx.x < nch; c0 += 4 * blockDim.x) {
+        float x[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = c0 + u * blockDim.x;
+            if (c < nch) load8<DT>(row, V, c * 8, vec, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = c0 + u * blockDim.x;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int e = c * 8 + k;
+                const uint32_t key = c < nch ? order_key(x[u][k]) : 0u;
+                const bool hit = c < nch && e < V && (int)(key >> 20) == bin;
+                // one LDS atomic per wave: the wave's hits take consecutive slots
+                const unsigned long long mask = __ballot(hit);
+                if (mask) {
+                    int base = 0;
+                    const int leader = __ffsll((long long)mask) - 1;
+                    if (lane == leader) base = atomicAdd(s_n, __popcll(mask));
+                    base = __shfl(base, leader);
+                    if (hit) {
+                        const int slot = base + __popcll(mask & ((1ull << lane) - 1ull));
+                        if (slot < kCap) s_comp[slot] = comp_key(key, e);
+                    }
+                }
+            }
         }
     }
     __syncthreads();
     const int ng = *s_n;
     __syncthreads();
     if (ng > kCap) return -1;
-    int np = 1;
-    while (np < ng) np <<= 1;
-    for (int i = ng + threadIdx.x; i < np; i += blockDim.x) s_comp[i] = 0ull;
-    __syncthreads();
-    lds_sort_desc(s_comp, np);
     for (int i = threadIdx.x; i < ng; i += blockDim.x)
         s_e[i] = exp_term(key_value((uint32_t)(s_comp[i] >> 32)), inv_t, m);
     __syncthreads();
     return ng;
 }
 
-__global__ void __launch_bounds__(kRowThreads) sample_select_kernel(
-    const void* __restrict__ logits, gg_dtype_t dt, int K, int V, int nseg,
-    const int32_t* __restrict__ n_drafts, double inv_t, int top_k, int use_p, double top_p, double tau,
-    int* __restrict__ state, RowInfo* __restrict__ info, const uint32_t* __restrict__ hcnt,
-    const double* __restrict__ hmass, const double* __restrict__ segsum) {
+// Among the ng gathered items (unique 64-bit keys, unordered), the first in descending key
+// order whose running total (of e with by_mass, else of 1) reaches `target`: a radix
+// descent over the low 52 key bits (the bin fixes the rest) in 8-bit digits, each a
+// 256-entry LDS histogram and a scan from the top digit. Returns the item's position in the
+// list (-1 if the total stays below target) and, through before, the total of the items
+// above it. The items are left in place.
+__device__ int select_desc(const unsigned long long* s_comp, const double* s_e, int ng, double target, bool by_mass,
+                           double* before, double* s_h, double* s_red, int* s_i) {
+    unsigned long long prefix = 0, pmask = 0;
+    double above = 0.0;
+    for (int shift = 44; shift >= -4; shift -= 8) {
+        const int sh = shift < 0 ? 0 : shift;
+        const int width = shift < 0 ? 4 : 8;
+        const unsigned long long dmask = ((1ull << width) - 1ull) << sh;
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) s_h[i] = 0.0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+            const unsigned long long c = s_comp[i];
+            if ((c & pmask) == prefix) atomicAdd(&s_h[(int)((c & dmask) >> sh)], by_mass ? s_e[i] : 1.0);
+        }
+        __syncthreads();
+        // digits from the top: thread t < 256 holds digit 255 - t
+        const int t = threadIdx.x;
+        const double hv = t < 256 ? s_h[255 - t] : 0.0;
+        double tot;
+        const double ex = block_excl_scan(hv, s_red, &tot);
+        if (t == 0) *s_i = -1;
+        __syncthreads();
+        // rounding may let two neighbouring digits both claim the crossing: the first in
+        // order (the larger digit) wins, and only its thread writes the total above it
+        const bool claim = t < 256 && hv > 0.0 && above + ex < target && above + ex + hv >= target;
+        if (claim) atomicMax(s_i, 255 - t);
+        __syncthreads();
+        if (claim && *s_i == 255 - t) s_h[256] = above + ex;
+        __syncthreads();
+        const int dgt = *s_i;
+        if (dgt < 0) {  // rounding between the histogram and the target: the caller's margin fails
+            __syncthreads();
+            return -1;
+        }
+        above = s_h[256];
+        prefix |= (unsigned long long)dgt << sh;
+        pmask |= dmask;
+        __syncthreads();
+    }
+    // prefix now names exactly one item (the low 52 bits are unique within the bin)
+    if (threadIdx.x == 0) *s_i = -1;
+    __syncthreads();
+    for (int i = threadIdx.x; i < ng; i += blockDim.x)
+        if ((s_comp[i] & pmask) == prefix) *s_i = i;
+    __syncthreads();
+    const int r = *s_i;
+    __syncthreads();
+    *before = above;
+    return r;
+}
+
+// The largest gathered key below `c` (0 if none): the next item in descending order.
+__device__ unsigned long long next_below(const unsigned long long* s_comp, int ng, unsigned long long c,
+                                         unsigned long long* s_u) {
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+        const unsigned long long v = s_comp[i];
+        if (v < c && v > best) best = v;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long v = __shfl_xor(best, o);
+        if (v > best) best = v;
+    }
+    if ((threadIdx.x & 63) == 0) s_u[threadIdx.x >> 6] = best;
+    __syncthreads();
+    unsigned long long r = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w)
+        if (s_u[w] > r) r = s_u[w];
+    __syncthreads();
+    return r;
+}
+
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kRowThreads) sample_select_kernel(DrawParams P) {
     const int b = blockIdx.x;
+    int* __restrict__ state = P.state;
     if (state[b] != ST_DRAW) return;
+    const int V = P.V, nseg = P.nseg, top_k = P.top_k, use_p = P.use_p;
+    const double inv_t = P.inv_t, top_p = P.top_p, tau = P.tau;
+    const gg_dtype_t dt = P.dt;
+    const uint32_t* __restrict__ hcnt = P.hcnt;
+    const double* __restrict__ hmass = P.hmass;
+    const double* __restrict__ segsum = P.segsum;
+    RowInfo* __restrict__ info = P.info;
     __shared__ double s_mass[kBins];
     __shared__ unsigned long long s_comp[kCap];
     __shared__ double s_e[kCap];
+    __shared__ double s_h[257];
     __shared__ double s_red[16];
     __shared__ uint32_t s_redu[16];
-    __shared__ int s_n, s_bin, s_flag;
+    __shared__ unsigned long long s_u[16];
+    __shared__ int s_n, s_bin, s_i;
     __shared__ double s_above;
     __shared__ uint32_t s_cabove;
-    const int n = clamp_n(n_drafts, b, K);
-    const void* row = (const uint8_t*)logits + ((size_t)b * (K + 1) + n) * V * dtype_bytes(dt);
+    const void* row = drawn_row(P, b, info[b].row);
     const double m = info[b].m;
-    const bool use_k = top_k > 0 && top_k < V;
+    const bool use_k = P.use_k;
     const int per = kBins / kRowThreads;  // bins per thread, positions counted from the top bin
-    for (int i = threadIdx.x; i < kBins; i += blockDim.x) s_mass[i] = hmass[(size_t)b * kBins + i];
-    if (threadIdx.x == 0) s_flag = 0;
+    if (P.filtered)
+        for (int i = threadIdx.x; i < kBins; i += blockDim.x) s_mass[i] = hmass[(size_t)b * kBins + i];
     __syncthreads();
 
-    unsigned long long cut = 0;
+    unsigned long long cut = 0, tk = 0;
     double S;
-    int kbin = -1, need = 0;
+    int kbin = -1, nk = 0;  // top-k: the threshold bin and its gathered items (in s_comp / s_e)
     if (use_k) {
         // The bin where the count from the top first reaches k.
         uint32_t c = 0;
@@ -378,15 +664,19 @@ __global__ void __launch_bounds__(kRowThreads) sample_select_kernel(
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
             return;
         }
-        need = top_k - (int)s_cabove;
-        const int ng = gather_bin(row, dt, V, kbin, inv_t, m, s_comp, s_e, &s_n);
-        if (ng < need) {  // more than kCap elements in the bin (or a count mismatch)
+        const int need = top_k - (int)s_cabove;
+        nk = gather_bin<DT>(row, V, P.vec, kbin, inv_t, m, s_comp, s_e, &s_n);
+        double dummy;
+        const int ck = nk < need ? -1 : select_desc(s_comp, s_e, nk, (double)need, false, &dummy, s_h, s_red, &s_i);
+        if (ck < 0) {  // more than kCap elements in the bin (or a count mismatch)
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
             return;
         }
-        cut = s_comp[need - 1];
+        tk = s_comp[ck];
+        cut = tk;
         double part = 0.0, above = 0.0;
-        for (int i = threadIdx.x; i < need; i += blockDim.x) part += s_e[i];
+        for (int i = threadIdx.x; i < nk; i += blockDim.x)
+            if (s_comp[i] >= tk) part += s_e[i];
         for (int i = kbin + 1 + threadIdx.x; i < kBins; i += blockDim.x) above += s_mass[i];
         part = block_sum(part, s_red);
         above = block_sum(above, s_red);
@@ -437,171 +727,83 @@ __global__ void __launch_bounds__(kRowThreads) sample_select_kernel(
             return;
         }
         const double above = s_above;
-        int nk;
-        if (use_k && pbin == kbin) {
-            nk = need;
-        } else {
-            nk = gather_bin(row, dt, V, pbin, inv_t, m, s_comp, s_e, &s_n);
-            if (nk < 0) {
+        int np = nk;
+        if (!(use_k && pbin == kbin)) {
+            np = gather_bin<DT>(row, V, P.vec, pbin, inv_t, m, s_comp, s_e, &s_n);
+            if (np < 0) {
                 if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
                 return;
             }
         }
-        // Inclusive prefix of e in (value desc, index asc) order; the cut is the first item
-        // whose inclusive mass reaches p * S.
-        const int q0 = threadIdx.x * (kCap / kRowThreads);
-        double loc = 0.0;
-        for (int q = 0; q < kCap / kRowThreads; ++q)
-            if (q0 + q < nk) loc += s_e[q0 + q];
-        double btot;
-        double irun = above + block_excl_scan(loc, s_red, &btot);
-        if (threadIdx.x == 0) s_n = 0x7fffffff;
-        __syncthreads();
-        int ic = -1;
-        double ic_above = 0.0;
-        for (int q = 0; q < kCap / kRowThreads; ++q) {
-            const int i = q0 + q;
-            if (i >= nk) break;
-            const double nx = irun + s_e[i];
-            if (irun < pS && nx >= pS) {
-                ic = i;
-                ic_above = irun;
-                break;
-            }
-            irun = nx;
-        }
-        if (ic >= 0) atomicMin(&s_n, ic);
-        __syncthreads();
-        if (ic >= 0 && ic == s_n) s_above = ic_above;
-        __syncthreads();
-        if (threadIdx.x == 0 && s_n == 0x7fffffff) s_n = -1;
-        __syncthreads();
-        const int ci = s_n;
+        // The cut: the first item (value desc, index asc) whose running mass reaches p * S.
+        double inbin = 0.0;
+        const int ci = select_desc(s_comp, s_e, np, pS - above, true, &inbin, s_h, s_red, &s_i);
         if (ci < 0) {
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
             return;
         }
+        const unsigned long long cc = s_comp[ci];
+        const unsigned long long nb = next_below(s_comp, np, cc, s_u);
         if (threadIdx.x == 0) {
-            const double A = s_above, ec = s_e[ci];
+            const double A = above + inbin, ec = s_e[ci];
             bool ok = (pS - A) > tau * S && (A + ec - pS) > tau * S;
+            if (use_k && cc < tk) ok = false;  // past the top-k set: only rounding gets here
             // An element after the cut with the same probability but another value would come
             // first in the rule's (probability desc, index asc) order if its index is lower.
-            if (ci + 1 < nk) {
-                if (s_e[ci + 1] == ec && (s_comp[ci + 1] >> 32) != (s_comp[ci] >> 32)) ok = false;
-            } else if (!(use_k && pbin == kbin) && pbin > 0) {
+            if (nb != 0 && !(use_k && nb < tk)) {
+                const double en = exp_term(key_value((uint32_t)(nb >> 32)), inv_t, m);
+                if (en == ec && (nb >> 32) != (cc >> 32)) ok = false;
+            } else if (nb == 0 && !(use_k && pbin == kbin) && pbin > 0) {
                 const double e_edge = exp_term(key_value(((uint32_t)pbin << 20) - 1u), inv_t, m);
                 if (e_edge >= ec) ok = false;
             }
             if (!ok) atomicOr(&state[b], ST_EXACT);
-            info[b].cut = s_comp[ci];
+            info[b].cut = cc;
+            info[b].tot = A + ec;
         }
         return;
     }
-    if (threadIdx.x == 0) info[b].cut = cut;
+    if (threadIdx.x == 0) {
+        info[b].cut = cut;
+        info[b].tot = S;
+    }
 }
 
 // ------------------------------------------------------------------------ kept
 
-__global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(
-    const void* __restrict__ logits, gg_dtype_t dt, int K, int V, int nseg,
-    const int32_t* __restrict__ n_drafts, double inv_t, const int* __restrict__ state,
-    const RowInfo* __restrict__ info, double* __restrict__ segkept) {
+// Per (segment, sequence): the draw's weights summed (kept e, or the residual).
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) {
     const int b = blockIdx.y, seg = blockIdx.x;
-    if (state[b] != ST_DRAW) return;
+    if (P.state[b] != ST_DRAW) return;
     __shared__ double s_red[16];
-    const int n = clamp_n(n_drafts, b, K);
-    const void* row = (const uint8_t*)logits + ((size_t)b * (K + 1) + n) * V * dtype_bytes(dt);
-    const double m = info[b].m;
-    const unsigned long long cut = info[b].cut;
+    const RowInfo ri = P.info[b];
+    const void* row = drawn_row(P, b, ri.row);
+    const float* qr = q_row(P, b, ri);
     double acc = 0.0;
-    const int end = min(V, (seg + 1) * kSeg);
-    for (int e = seg * kSeg + threadIdx.x; e < end; e += blockDim.x) {
-        const float l = load_as_f32(row, dt, e);
-        if (comp_key(order_key(l), e) >= cut) acc += exp_term(l, inv_t, m);
+    for (int c = threadIdx.x; c < kSeg / 8; c += blockDim.x) {
+        const int e0 = seg * kSeg + c * 8;
+        if (e0 >= P.V) break;
+        float x[8];
+        load8<DT>(row, P.V, e0, P.vec, x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (e0 + k < P.V) acc += draw_weight(P, ri, qr, x[k], e0 + k);
     }
     const double tot = block_sum(acc, s_red);
-    if (threadIdx.x == 0) segkept[(size_t)b * nseg + seg] = tot;
+    if (threadIdx.x == 0) P.segkept[(size_t)b * P.nseg + seg] = tot;
 }
 
 // ------------------------------------------------------------------------ draw
 
-__global__ void __launch_bounds__(kRowThreads) sample_draw_kernel(
-    const void* __restrict__ logits, gg_dtype_t dt, int K, int V, int nseg,
-    const int32_t* __restrict__ n_drafts, double inv_t, int filtered, const double* __restrict__ uniforms,
-    double tau, int* __restrict__ state, const RowInfo* __restrict__ info,
-    const double* __restrict__ segsum, const double* __restrict__ segkept, int32_t* __restrict__ out_tok) {
+// One block per sequence: the draw over the segment sums of the pass (a plain draw without
+// filters) or of the kept launch.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P, int use_segsum) {
     const int b = blockIdx.x;
-    if (state[b] != ST_DRAW) return;
-    __shared__ double s_red[16];
-    __shared__ int s_seg, s_tok, s_bad;
-    __shared__ double s_base, s_tot;
-    const double u = uniforms[b];
-    if (!(u >= tau && u < 1.0 - tau)) {  // near 0, near or past 1, NaN: the literal rule
-        if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-        return;
-    }
-    const double* sums = (filtered ? segkept : segsum) + (size_t)b * nseg;
-    if (threadIdx.x == 0) {
-        double tot = 0.0;
-        for (int s = 0; s < nseg; ++s) tot += sums[s];
-        const double t = u * tot;
-        double run = 0.0;
-        int sel = -1;
-        for (int s = 0; s < nseg; ++s) {
-            if (run + sums[s] > t) {
-                sel = s;
-                break;
-            }
-            run += sums[s];
-        }
-        s_seg = sel;
-        s_base = run;
-        s_tot = tot;
-        s_tok = -1;
-        s_bad = 0;
-    }
-    __syncthreads();
-    const int seg = s_seg;
-    if (seg < 0) {
-        if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-        return;
-    }
-    const double tot = s_tot, t = u * tot;
-    const int n = clamp_n(n_drafts, b, K);
-    const void* row = (const uint8_t*)logits + ((size_t)b * (K + 1) + n) * V * dtype_bytes(dt);
-    const double m = info[b].m;
-    const unsigned long long cut = info[b].cut;
-    constexpr int kPer = kSeg / kRowThreads;
-    const int e0 = seg * kSeg + threadIdx.x * kPer;
-    double ev[kPer];
-    double loc = 0.0;
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-        const int e = e0 + q;
-        ev[q] = 0.0;
-        if (e < V) {
-            const float l = load_as_f32(row, dt, e);
-            if (comp_key(order_key(l), e) >= cut) ev[q] = exp_term(l, inv_t, m);
-        }
-        loc += ev[q];
-    }
-    double btot;
-    double run = s_base + block_excl_scan(loc, s_red, &btot);
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-        const double nx = run + ev[q];
-        if (run <= t && nx > t) {
-            const bool ok = (t - run) > tau * tot && (nx - t) > tau * tot;
-            if (ok) s_tok = e0 + q;
-            else s_bad = 1;
-        }
-        run = nx;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        if (s_tok >= 0 && !s_bad) out_tok[b] = s_tok;
-        else atomicOr(&state[b], ST_EXACT);
-    }
+    if (P.state[b] != ST_DRAW) return;
+    const RowInfo ri = P.info[b];
+    draw_in_block<DT>(P, b, ri, (use_segsum ? P.segsum : P.segkept) + (size_t)b * P.nseg);
 }
 
 // ----------------------------------------------------------------------- exact
@@ -668,11 +870,26 @@ __device__ double wave_seq_sum(const double* a, int V) {
     return s;
 }
 
+// Sequential float64 sum of a[0, V) computed by wave 0, stored for the whole block.
+__device__ double block_seq_sum(const double* a, int V, double* s_red) {
+    if (threadIdx.x < 64) {
+        const double s = wave_seq_sum(a, V);
+        if (threadIdx.x == 0) s_red[0] = s;
+    }
+    __syncthreads();
+    const double s = s_red[0];
+    __syncthreads();
+    return s;
+}
+
 // The rule of Sampler.Sample for one row (temperature > 1e-9), literally:
-// internal/engine/sampling.go:57-71 and the helpers at :88-192.
+// internal/engine/sampling.go:57-71 and the helpers at :88-192. With x >= 0 the draw is the
+// residual one of the rejection acceptance: r_i = p_i - q_i where p_i > q_i, for i != x
+// (q_i the cleaned draft probability from qr, 0 without qr), r / sum(r); a zero sum falls
+// back to p without x, normalised, and that being 0 too, to p.
 __device__ int exact_draw(const void* row, gg_dtype_t dt, int V, double inv_t, int top_k, double top_p,
-                          double u, double* A, double* E, Ent* ent, int N, Ent* sh, double* s_red,
-                          int* s_i) {
+                          double u, int x, const float* qr, double* A, double* E, Ent* ent, int N, Ent* sh,
+                          double* s_red, int* s_i) {
     const int tid = threadIdx.x;
     // scaled[i] = float64(l) * invT (:57-61)
     for (int i = tid; i < V; i += blockDim.x) A[i] = (double)load_as_f32(row, dt, i) * inv_t;
@@ -779,6 +996,25 @@ __device__ int exact_draw(const void* row, gg_dtype_t dt, int V, double inv_t, i
         __syncthreads();
         fin = A;
     }
+    if (x >= 0) {
+        double* r = fin == A ? E : A;
+        for (int i = tid; i < V; i += blockDim.x) {
+            const double qv = qr ? clean_q(qr[i]) : 0.0;
+            r[i] = (i != x && fin[i] > qv) ? fin[i] - qv : 0.0;
+        }
+        __syncthreads();
+        double sr = block_seq_sum(r, V, s_red);
+        if (!(sr > 0)) {
+            for (int i = tid; i < V; i += blockDim.x) r[i] = i != x ? fin[i] : 0.0;
+            __syncthreads();
+            sr = block_seq_sum(r, V, s_red);
+        }
+        if (sr > 0) {
+            for (int i = tid; i < V; i += blockDim.x) r[i] = r[i] / sr;
+            __syncthreads();
+            fin = r;
+        }
+    }
     // categoricalSample (:176-192): first i with u < cumulative, else the last nonzero.
     if (tid < 64) {
         const int lane = tid;
@@ -818,10 +1054,8 @@ __device__ int exact_draw(const void* row, gg_dtype_t dt, int V, double inv_t, i
     return tok;
 }
 
-__global__ void __launch_bounds__(kRowThreads) sample_exact_kernel(
-    const void* __restrict__ logits, gg_dtype_t dt, int B, int K, int V, const int32_t* __restrict__ n_drafts,
-    double inv_t, int top_k, double top_p, const double* __restrict__ uniforms, const int* __restrict__ state,
-    uint8_t* __restrict__ scratch, size_t slot_bytes, size_t vpad, int npow, int32_t* __restrict__ out_tok) {
+__global__ void __launch_bounds__(kRowThreads) sample_exact_kernel(DrawParams P, uint8_t* __restrict__ scratch,
+                                                                    size_t slot_bytes, size_t vpad, int npow) {
     __shared__ Ent sh[kChunk];
     __shared__ double s_red[16];
     __shared__ int s_i;
@@ -829,61 +1063,112 @@ __global__ void __launch_bounds__(kRowThreads) sample_exact_kernel(
     double* A = (double*)slot;
     double* E = A + vpad;
     Ent* ent = (Ent*)(E + vpad);
-    for (int b = blockIdx.x; b < B; b += gridDim.x) {
-        if (!(state[b] & ST_EXACT)) continue;
-        const int n = clamp_n(n_drafts, b, K);
-        const void* row = (const uint8_t*)logits + ((size_t)b * (K + 1) + n) * V * dtype_bytes(dt);
-        const int tok = exact_draw(row, dt, V, inv_t, top_k, top_p, uniforms[b], A, E, ent, npow, sh, s_red, &s_i);
-        if (threadIdx.x == 0) out_tok[b] = tok;
+    for (int b = blockIdx.x; b < P.B; b += gridDim.x) {
+        if (!(P.state[b] & ST_EXACT)) continue;
+        const RowInfo ri = P.info[b];
+        const int tok = exact_draw(drawn_row(P, b, ri.row), P.dt, P.V, P.inv_t, P.top_k, P.top_p, uniform_of(P, b),
+                                   ri.x, q_row(P, b, ri), A, E, ent, npow, sh, s_red, &s_i);
+        if (threadIdx.x == 0) P.out_tok[b] = tok;
         __syncthreads();
     }
 }
 
 }  // namespace
 
+size_t final_draw_workspace_bytes(int num_seqs, int vocab) { return layout(num_seqs, vocab).total; }
+
+gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
+    const int B = d.num_seqs, K = d.max_drafts, V = d.vocab;
+    const Layout L = layout(B, V);
+    uint8_t* w = (uint8_t*)ws;
+    DrawParams P{};
+    P.logits = d.logits;
+    P.dt = d.dt;
+    P.B = B;
+    P.K = K;
+    P.V = V;
+    P.nseg = (V + kSeg - 1) / kSeg;
+    P.inv_t = 1.0 / d.temperature;
+    P.top_k = d.top_k;
+    P.top_p = d.top_p;
+    P.use_k = d.top_k > 0 && d.top_k < V;
+    P.use_p = d.top_p > 0 && d.top_p < 1.0;
+    P.filtered = P.use_k || P.use_p;
+    {
+        const size_t eb = dtype_bytes(d.dt);
+        P.vec = ((size_t)V * eb % 16 == 0) && ((uintptr_t)d.logits % 16 == 0);
+    }
+    // Bound on the rounding of a sequential or parallel float64 sum over the row (plus the
+    // 4096 histogram bins), relative to the sum: 8 * (V + 4096) * 2^-53, plus twice the
+    // parallel path's exponential error.
+    P.tau = 8.0 * ((double)V + 4096.0) * 0x1p-53 + 2.0 * kFastExpErr;
+    P.ud = d.uniforms_f64;
+    P.uf = d.uniforms_f32;
+    P.q = d.draft_probs;
+    P.state = (int*)(w + L.state);
+    P.info = (RowInfo*)(w + L.info);
+    P.hcnt = (uint32_t*)(w + L.hcnt);
+    P.hmass = (double*)(w + L.hmass);
+    P.segsum = (double*)(w + L.segsum);
+    P.segkept = (double*)(w + L.segkept);
+    P.out_tok = d.out_tok;
+    const int force = d.force_exact ? 1 : 0;
+    const int nseg_m = d.greedy_seg ? (V + kGreedySeg - 1) / kGreedySeg : d.nseg_max;
+    sample_prep_kernel<<<B, 256, 0, s>>>(P, d.greedy_seg, d.seg_max, nseg_m, d.n_drafts, d.accepted, d.spec_row,
+                                         d.spec_x, force);
+    // A plain draw without filters draws from the pass's segment sums; a filtered one needs
+    // the cut (select) and the kept sums per segment (kept), a residual one the kept total
+    // (select) and the residual sums (kept).
+    const bool residual = d.spec_row != nullptr;
+    const bool two_pass = P.filtered || residual;
+#define GG_DRAW(DTV)                                                                                 \
+    sample_pass_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                              \
+    if (two_pass) {                                                                                  \
+        sample_select_kernel<DTV><<<B, kRowThreads, 0, s>>>(P);                                      \
+        sample_kept_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                          \
+    }                                                                                                \
+    sample_draw_kernel<DTV><<<B, kSegThreads, 0, s>>>(P, two_pass ? 0 : 1);
+    switch (d.dt) {
+        case GG_DTYPE_F32: GG_DRAW(GG_DTYPE_F32) break;
+        case GG_DTYPE_BF16: GG_DRAW(GG_DTYPE_BF16) break;
+        case GG_DTYPE_F16: GG_DRAW(GG_DTYPE_F16) break;
+        default: return fail(GG_ERR_INVALID, "final draw: logits dtype");
+    }
+#undef GG_DRAW
+    const int slots = B < kExactSlots ? B : kExactSlots;
+    sample_exact_kernel<<<slots, kRowThreads, 0, s>>>(P, w + L.exact, L.slot_bytes, L.vpad, (int)L.npow);
+    return check_hip(hipGetLastError(), "final draw launch");
+}
+
 size_t sample_workspace_bytes(int num_seqs, int max_drafts, int vocab) {
-    return layout(num_seqs, max_drafts, vocab).total;
+    return ((greedy_workspace_bytes(num_seqs, max_drafts, vocab) + 255) & ~(size_t)255) +
+           final_draw_workspace_bytes(num_seqs, vocab);
 }
 
 gg_status_t launch_accept_greedy_sample(const void* logits, gg_dtype_t dt, int B, int K, int V,
                                         const int32_t* drafts, const int32_t* n_drafts, double temperature,
                                         int top_k, double top_p, const double* uniforms, unsigned flags,
                                         int32_t* out_acc, int32_t* out_tok, void* ws, hipStream_t s) {
-    const Layout L = layout(B, K, V);
     uint8_t* w = (uint8_t*)ws;
-    gg_status_t st = launch_accept_greedy(logits, dt, B, K, V, drafts, n_drafts, out_acc, out_tok, w + L.greedy, s);
+    gg_status_t st = launch_accept_greedy(logits, dt, B, K, V, drafts, n_drafts, out_acc, out_tok, w, s);
     if (st != GG_OK) return st;
     if (temperature <= 1e-9) return GG_OK;  // Sampler.Sample's greedy case (sampling.go:54-56)
-    const double inv_t = 1.0 / temperature;
-    const bool use_k = top_k > 0 && top_k < V;
-    const bool use_p = top_p > 0 && top_p < 1.0;
-    const bool filtered = use_k || use_p;
-    const int nseg = (V + kSeg - 1) / kSeg;
-    const int nseg_g = (V + kGreedySeg - 1) / kGreedySeg;
-    const double tau = 8.0 * ((double)V + 4096.0) * 0x1p-53;
-    int* state = (int*)(w + L.state);
-    RowInfo* info = (RowInfo*)(w + L.info);
-    uint32_t* hcnt = (uint32_t*)(w + L.hcnt);
-    double* hmass = (double*)(w + L.hmass);
-    double* segsum = (double*)(w + L.segsum);
-    double* segkept = (double*)(w + L.segkept);
-    const int force = (flags & GG_SAMPLE_EXACT) ? 1 : 0;
-    sample_prep_kernel<<<B, 256, 0, s>>>((const float2*)(w + L.greedy), K, nseg_g, n_drafts, out_acc, inv_t,
-                                         filtered ? 1 : 0, force, hcnt, hmass, state, info);
-    sample_pass_kernel<<<dim3(nseg, B), kSegThreads, 0, s>>>(logits, dt, K, V, nseg, n_drafts, inv_t, use_k ? 1 : 0,
-                                                             filtered ? 1 : 0, state, info, hcnt, hmass, segsum);
-    if (filtered) {
-        sample_select_kernel<<<B, kRowThreads, 0, s>>>(logits, dt, K, V, nseg, n_drafts, inv_t, top_k, use_p ? 1 : 0,
-                                                       top_p, tau, state, info, hcnt, hmass, segsum);
-        sample_kept_kernel<<<dim3(nseg, B), kSegThreads, 0, s>>>(logits, dt, K, V, nseg, n_drafts, inv_t, state, info,
-                                                                 segkept);
-    }
-    sample_draw_kernel<<<B, kRowThreads, 0, s>>>(logits, dt, K, V, nseg, n_drafts, inv_t, filtered ? 1 : 0, uniforms,
-                                                 tau, state, info, segsum, segkept, out_tok);
-    const int slots = B < kExactSlots ? B : kExactSlots;
-    sample_exact_kernel<<<slots, kRowThreads, 0, s>>>(logits, dt, B, K, V, n_drafts, inv_t, top_k, top_p, uniforms,
-                                                      state, w + L.exact, L.slot_bytes, L.vpad, (int)L.npow, out_tok);
-    return check_hip(hipGetLastError(), "accept_greedy_sample launch");
+    FinalDraw d{};
+    d.logits = logits;
+    d.dt = dt;
+    d.num_seqs = B;
+    d.max_drafts = K;
+    d.vocab = V;
+    d.temperature = temperature;
+    d.top_k = top_k;
+    d.top_p = top_p;
+    d.uniforms_f64 = uniforms;
+    d.n_drafts = n_drafts;
+    d.accepted = out_acc;
+    d.greedy_seg = (const float2*)w;
+    d.force_exact = (flags & GG_SAMPLE_EXACT) != 0;
+    d.out_tok = out_tok;
+    return launch_final_draw(d, w + ((greedy_workspace_bytes(B, K, V) + 255) & ~(size_t)255), s);
 }
 
 }  // namespace gg

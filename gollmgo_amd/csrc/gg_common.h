@@ -116,6 +116,36 @@ gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs
                                  int vocab, const int32_t* drafts, const int32_t* n_drafts,
                                  int32_t* out_acc, int32_t* out_tok, void* ws, hipStream_t s);
 
+// The float64 token draw shared by the greedy-with-sampled-bonus and the rejection
+// acceptance (accept_sample.hip): per sequence, a row drawn with Sampler.Sample's rule, or
+// after a rejected draft the residual of that row's distribution against the draft's.
+struct FinalDraw {
+    const void* logits;          // [num_seqs][max_drafts + 1][vocab]
+    gg_dtype_t dt;
+    int num_seqs, max_drafts, vocab;
+    double temperature;          // > 1e-9
+    int top_k;
+    double top_p;
+    const double* uniforms_f64;  // uniform of sequence b: uniforms_f64[b], or
+    const float* uniforms_f32;   //   uniforms_f32[b * (max_drafts + 1) + max_drafts]
+    const float* draft_probs;    // residual draws: [num_seqs][max_drafts][vocab], or null (one-hot)
+    // Which row: either greedy (row n_drafts[b] when accepted[b] == n_drafts[b], the row
+    // maxima from the greedy segment pairs greedy_seg), or given (spec_row[b], -1 = none;
+    // spec_x[b] the rejected draft of a residual draw, -1 = plain; the row maxima from
+    // seg_max [rows][nseg_max], finite maxima of 8192-element segments).
+    const int32_t* n_drafts;
+    const int32_t* accepted;
+    const float2* greedy_seg;
+    const int* spec_row;
+    const int* spec_x;
+    const float* seg_max;
+    int nseg_max;
+    bool force_exact;
+    int32_t* out_tok;
+};
+size_t final_draw_workspace_bytes(int num_seqs, int vocab);
+gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s);
+
 size_t sample_workspace_bytes(int num_seqs, int max_drafts, int vocab);
 gg_status_t launch_accept_greedy_sample(const void* logits, gg_dtype_t dt, int num_seqs, int max_drafts, int vocab,
                                         const int32_t* drafts, const int32_t* n_drafts, double temperature,

@@ -43,3 +43,27 @@ GG_HD64 double gg_exp64(double x) {
     const double y = 1.0 - ((lo - (r * c) / (2.0 - c)) - hi);
     return __builtin_ldexp(y, k);
 }
+
+// A cheaper float64 exponential for sums that only need to be close: x = k ln2 + r with
+// fused reductions, the degree-11 Taylor polynomial of e^r in Horner form (|r| <= 0.3466,
+// truncation below 7e-15) and 2^k. Within 2e-14 relative of gg_exp64 on [-745, 0]
+// (tests/test_sampler_oracle.py); 0 below -745.2 and for NaN.
+GG_HD64 double gg_fast_exp64(double x) {
+    if (!(x >= -745.2)) return 0.0;
+    const double kd = __builtin_rint(x * 1.4426950408889634);
+    double r = __builtin_fma(kd, -6.93147180369123816490e-01, x);
+    r = __builtin_fma(kd, -1.90821492927058770002e-10, r);
+    double p = 2.5052108385441720e-08;                // 1/11!
+    p = __builtin_fma(p, r, 2.7557319223985893e-07);  // 1/10!
+    p = __builtin_fma(p, r, 2.7557319223985888e-06);  // 1/9!
+    p = __builtin_fma(p, r, 2.4801587301587302e-05);  // 1/8!
+    p = __builtin_fma(p, r, 1.9841269841269841e-04);  // 1/7!
+    p = __builtin_fma(p, r, 1.3888888888888889e-03);  // 1/6!
+    p = __builtin_fma(p, r, 8.3333333333333332e-03);  // 1/5!
+    p = __builtin_fma(p, r, 4.1666666666666664e-02);  // 1/4!
+    p = __builtin_fma(p, r, 1.6666666666666666e-01);  // 1/3!
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    return __builtin_ldexp(p, (int)kd);
+}

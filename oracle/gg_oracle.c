@@ -544,18 +544,49 @@ static u128 row_weights(const float* row, int V, float inv_t, float top_p, u128*
     return row_weights_ef(row, V, inv_t, top_p, w_out, scratch, NULL, NULL);
 }
 
-/* Speculative sampling (Leviathan et al. 2023, Alg. 1) over the exact weights W:
+/* The final draw of the rejection acceptance in float64, with Sampler's rules: p =
+ * ora_sampler_probs_f64(row) (temperature, top-p; sampling.go:57-71). Plain (x < 0): the
+ * categorical draw over p, i.e. Sampler.Sample. Residual after the rejected draft x:
+ * r_i = p_i - q_i where p_i > q_i, for i != x (q_i = clean_q of the draft distribution,
+ * 0 without one: a one-hot q puts its mass on x alone), normalised by its index-order sum;
+ * a zero sum falls back to p without x, normalised, and that being zero too, to p. */
+int ora_final_draw_f64(const float* row, int V, double temperature, int top_k, double top_p, int x,
+                       const float* qrow, double u) {
+    double* p = (double*)malloc(sizeof(double) * (size_t)V);
+    double* r = (double*)malloc(sizeof(double) * (size_t)V);
+    ora_sampler_probs_f64(row, V, temperature, top_k, top_p, p);
+    const double* dist = p;
+    if (x >= 0) {
+        double s = 0;
+        for (int i = 0; i < V; ++i) {
+            const double q = qrow ? clean_q(qrow[i]) : 0.0;
+            r[i] = (i != x && p[i] > q) ? p[i] - q : 0.0;
+        }
+        for (int i = 0; i < V; ++i) s += r[i];
+        if (!(s > 0)) {
+            s = 0;
+            for (int i = 0; i < V; ++i) r[i] = i != x ? p[i] : 0.0;
+            for (int i = 0; i < V; ++i) s += r[i];
+        }
+        if (s > 0) {
+            for (int i = 0; i < V; ++i) r[i] /= s;
+            dist = r;
+        }
+    }
+    const int t = ora_categorical_f64(dist, V, u);
+    free(p);
+    free(r);
+    return t;
+}
+
+/* Speculative sampling (Leviathan et al. 2023, Alg. 1). The acceptance tests use the exact
+ * fixed-point weights W:
  *   accept draft j iff u_j * q_j(x_j) * Zp_j < W_j(x_j)   (doubles, left to right;
- *     q as clean_q; W and Zp through u128_to_double)
- *   first rejection at row a: draw from r_i = f_s * (e_i - min(e_i, floor(q_i * Zp_a / f_s)))
- *     (the residual max(0, W_i - q_i * Zp) rounded in the segment's units of e; the
- *     quotient Zp / f_s and the product are doubles; q is one-hot at the draft when no
- *     draft distribution is given; r_i = 0 where f_s = 0 and at the rejected draft x,
- *     whose exact residual is 0 since u < 1 rejects only when p(x) < q(x)); if every r_i
- *     is 0, draw from W of row a without x, and if that is 0 too, from W of row a;
- *   all accepted: draw from W of row n;
- *   draw(u, r): t = floor(u * sum r); first i with inclusive prefix > t; else the
- *     last i with r_i > 0; else 0.
+ *     q as clean_q; W and Zp through u128_to_double; q one-hot at the draft when no draft
+ *     distribution is given);
+ * the token is drawn in float64 by ora_final_draw_f64 with uniforms[b][K]: after the
+ * first rejection at row a, the residual of row a against q_a without the rejected draft;
+ * when every draft passes, the bonus from row n (Sampler.Sample).
  * logits [B][K+1][V] (fp32 values), dprobs [B][K][V] or NULL (one-hot q),
  * uniforms [B][K+1] (element K drives the final draw). */
 void ora_accept_rejection(const float* logits, int B, int K, int V, const float* dprobs,
@@ -563,9 +594,6 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
                           float temperature, float top_p, int32_t* out_acc, int32_t* out_tok) {
     const float inv_t = 1.0f / temperature;
     u128* w = (u128*)malloc(sizeof(u128) * (size_t)V);
-    u128* r = (u128*)malloc(sizeof(u128) * (size_t)V);
-    uint64_t* e = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
-    uint64_t* f = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)((V + ORA_SEG - 1) / ORA_SEG));
     ora_il* scratch = (ora_il*)malloc(sizeof(ora_il) * (size_t)V);
     for (int b = 0; b < B; ++b) {
         int n = n_drafts[b];
@@ -573,9 +601,8 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
         if (n > K) n = K;
         const float* lg = logits + (size_t)b * (K + 1) * V;
         int a = n;
-        u128 zp = 0;
         for (int j = 0; j < n; ++j) {
-            zp = row_weights(lg + (size_t)j * V, V, inv_t, top_p, w, scratch);
+            const u128 zp = row_weights(lg + (size_t)j * V, V, inv_t, top_p, w, scratch);
             int x = drafts[(size_t)b * K + j];
             int ok = 0;
             if (x >= 0 && x < V) {
@@ -588,64 +615,13 @@ void ora_accept_rejection(const float* logits, int B, int K, int V, const float*
                 break;
             }
         }
-        zp = row_weights_ef(lg + (size_t)a * V, V, inv_t, top_p, w, scratch, e, f);
-        const double zpd = u128_to_double(zp);
-        u128 tot = 0;
-        int residual = a < n;
-        const int xr = residual ? drafts[(size_t)b * K + a] : -1;
-        if (residual) {
-            for (int i = 0; i < V; ++i) {
-                const uint64_t fs = f[i / ORA_SEG];
-                r[i] = 0;
-                /* a rejection (u < 1) means p(x) < q(x): the draft's residual is 0 */
-                if (fs == 0 || e[i] == 0 || i == xr) continue;
-                const double qv = dprobs ? clean_q(dprobs[((size_t)b * K + a) * V + i]) : (i == xr ? 1.0 : 0.0);
-                const double qd = qv * (zpd / (double)fs);
-                const uint64_t rq = (double)e[i] > qd ? e[i] - (uint64_t)floor(qd) : 0;
-                r[i] = (u128)rq * fs;
-                tot += r[i];
-            }
-        }
-        /* A vanished residual (dense q that is not a distribution) draws from the target
-         * row without the rejected draft, and that vanishing too, from the whole row. */
-        if (residual && tot == 0)
-            for (int i = 0; i < V; ++i) {
-                r[i] = i == xr ? 0 : w[i];
-                tot += r[i];
-            }
-        if (tot == 0)
-            for (int i = 0; i < V; ++i) {
-                r[i] = w[i];
-                tot += r[i];
-            }
-        int tok = 0;
-        if (tot > 0) {
-            double u = (double)uniforms[(size_t)b * (K + 1) + K];
-            const u128 t = u128_floor(u * u128_to_double(tot));
-            u128 c = 0;
-            int found = -1;
-            for (int i = 0; i < V; ++i) {
-                c += r[i];
-                if (c > t) {
-                    found = i;
-                    break;
-                }
-            }
-            if (found < 0)
-                for (int i = V - 1; i >= 0; --i)
-                    if (r[i] > 0) {
-                        found = i;
-                        break;
-                    }
-            tok = found < 0 ? 0 : found;
-        }
+        const int x = a < n ? drafts[(size_t)b * K + a] : -1;
+        const float* qrow = (a < n && dprobs) ? dprobs + ((size_t)b * K + a) * V : NULL;
         out_acc[b] = a;
-        out_tok[b] = tok;
+        out_tok[b] = ora_final_draw_f64(lg + (size_t)a * V, V, (double)temperature, 0, (double)top_p, x, qrow,
+                                        (double)uniforms[(size_t)b * (K + 1) + K]);
     }
     free(w);
-    free(r);
-    free(e);
-    free(f);
     free(scratch);
 }
 
@@ -839,153 +815,6 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
         }
         free(sc);
         free(acc);
-    }
-}
-
-/* --------------------------------------------- sampler draw parity (test helper) */
-
-/* Stable LSD radix sort of idx[0..n) by key[idx] ascending, four 16-bit passes. */
-static void radix_sort_idx(const uint64_t* key, int n, int* idx, int* tmp) {
-    int* cnt = (int*)malloc(sizeof(int) * 65537);
-    for (int pass = 0; pass < 4; ++pass) {
-        const int sh = 16 * pass;
-        memset(cnt, 0, sizeof(int) * 65537);
-        for (int i = 0; i < n; ++i) cnt[((key[idx[i]] >> sh) & 0xffff) + 1]++;
-        for (int d = 0; d < 65536; ++d) cnt[d + 1] += cnt[d];
-        for (int i = 0; i < n; ++i) tmp[cnt[(key[idx[i]] >> sh) & 0xffff]++] = idx[i];
-        memcpy(idx, tmp, sizeof(int) * (size_t)n);
-    }
-    free(cnt);
-}
-
-/* Order key of a finite float, ascending in (value desc): -0 counts as +0. */
-static uint64_t desc_key_f32(float x) {
-    if (x == 0.0f) x = 0.0f;
-    uint32_t u;
-    memcpy(&u, &x, 4);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u); /* ascending order of values */
-    return (uint64_t)(~u);
-}
-static uint64_t desc_key_pos_f64(double x) { /* x >= 0 */
-    uint64_t u;
-    memcpy(&u, &x, 8);
-    return ~u;
-}
-
-/* For each of B rows of logits (V finite values) and U supplied uniforms per row, the
- * token of two samplers:
- *   tok_f64  : Sampler.Sample (sampling.go:40-72) in float64 without top-k (ora_exp64 as
- *              math.Exp): scaled =
- *              float64(l) * (1/T) (:57-61), softmax (:112-136), topPFilter (:139-173;
- *              equal probabilities in index order, which sort.Slice leaves open),
- *              categoricalSample (:176-192) with the uniform in place of rng.Float64();
- *   tok_fixed: the final draw of ora_accept_rejection for a row with no drafts: the
- *              fixed-point weights and nucleus of row_weights, then the first index
- *              whose inclusive prefix exceeds floor(u * total).
- * dist[row*U + k] is the distance of u from the nearer float64 CDF boundary of
- * tok_f64 (min(u - cum_before, cum_through - u)); nucleus_diff[row] counts the tokens
- * kept by one nucleus and not by the other. */
-void ora_draw_parity(const float* logits, int B, int V, double temperature, double top_p,
-                     const float* uniforms, int U, int32_t* tok_fixed, int32_t* tok_f64, double* dist,
-                     int32_t* nucleus_diff, int threads) {
-    const float inv_t = 1.0f / (float)temperature;
-    const double inv_t64 = 1.0 / temperature;
-    const int use_p = top_p > 0 && top_p < 1;
-#ifdef _OPENMP
-    if (threads > 0) omp_set_num_threads(threads);
-#pragma omp parallel for schedule(dynamic, 1)
-#else
-    (void)threads;
-#endif
-    for (int b = 0; b < B; ++b) {
-        const float* row = logits + (size_t)b * V;
-        u128* w = (u128*)malloc(sizeof(u128) * (size_t)V);
-        uint64_t* key = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
-        double* pr = (double*)malloc(sizeof(double) * (size_t)V);
-        double* kept = (double*)malloc(sizeof(double) * (size_t)V);
-        double* cdf = (double*)malloc(sizeof(double) * (size_t)V);
-        u128* pre = (u128*)malloc(sizeof(u128) * (size_t)V);
-        int* idx = (int*)malloc(sizeof(int) * (size_t)V);
-        int* tmp = (int*)malloc(sizeof(int) * (size_t)V);
-        ora_il* scratch = (ora_il*)malloc(sizeof(ora_il) * (size_t)V);
-        /* fixed point: the acceptance's own row weights and nucleus */
-        row_weights(row, V, inv_t, (float)top_p, w, scratch);
-        u128 tot = 0;
-        for (int i = 0; i < V; ++i) {
-            tot += w[i];
-            pre[i] = tot;
-        }
-        /* float64 sampler */
-        double mx = (double)row[0] * inv_t64;
-        for (int i = 1; i < V; ++i)
-            if ((double)row[i] * inv_t64 > mx) mx = (double)row[i] * inv_t64;
-        double sum = 0;
-        for (int i = 0; i < V; ++i) {
-            pr[i] = ora_exp64((double)row[i] * inv_t64 - mx);
-            sum += pr[i];
-        }
-        for (int i = 0; i < V; ++i) pr[i] /= sum;
-        for (int i = 0; i < V; ++i) kept[i] = use_p ? 0.0 : pr[i];
-        if (use_p) {
-            for (int i = 0; i < V; ++i) {
-                idx[i] = i;
-                key[i] = desc_key_pos_f64(pr[i]);
-            }
-            radix_sort_idx(key, V, idx, tmp);
-            double cum = 0;
-            for (int k = 0; k < V; ++k) {
-                if (cum >= top_p && cum > 0) break;
-                kept[idx[k]] = pr[idx[k]];
-                cum += pr[idx[k]];
-            }
-            double s2 = 0;
-            for (int i = 0; i < V; ++i) s2 += kept[i];
-            for (int i = 0; i < V; ++i) kept[i] /= s2;
-        }
-        double c = 0;
-        int nd = 0;
-        for (int i = 0; i < V; ++i) {
-            c += kept[i];
-            cdf[i] = c;
-            nd += (kept[i] > 0) != (w[i] > 0);
-        }
-        nucleus_diff[b] = nd;
-        for (int k = 0; k < U; ++k) {
-            const double u = (double)uniforms[(size_t)b * U + k];
-            /* first i with u < cdf[i] (cdf is non-decreasing) */
-            int lo = 0, hi = V;
-            while (lo < hi) {
-                const int mid = (lo + hi) / 2;
-                if (u < cdf[mid]) hi = mid;
-                else lo = mid + 1;
-            }
-            int tf = lo;
-            if (tf == V) { /* fallback: last nonzero */
-                tf = 0;
-                for (int i = V - 1; i >= 0; --i)
-                    if (kept[i] > 0) {
-                        tf = i;
-                        break;
-                    }
-            }
-            const double before = tf > 0 ? cdf[tf - 1] : 0.0;
-            const double d0 = u - before, d1 = cdf[tf] - u;
-            dist[(size_t)b * U + k] = d0 < d1 ? d0 : d1;
-            tok_f64[(size_t)b * U + k] = tf;
-            int tq = 0;
-            if (tot > 0) {
-                const u128 t = u128_floor(u * u128_to_double(tot));
-                int l2 = 0, h2 = V;
-                while (l2 < h2) {
-                    const int mid = (l2 + h2) / 2;
-                    if (pre[mid] > t) h2 = mid;
-                    else l2 = mid + 1;
-                }
-                tq = l2 < V ? l2 : 0;
-            }
-            tok_fixed[(size_t)b * U + k] = tq;
-        }
-        free(w); free(key); free(pr); free(kept); free(cdf); free(pre); free(idx); free(tmp); free(scratch);
     }
 }
 

@@ -278,24 +278,6 @@ def emit_positions(drafts, n_drafts, positions, temperature: float = 0.0, top_p:
     return acc, tok
 
 
-def draw_parity(logits_f32, temperature: float, top_p: float, uniforms, threads: int = 0):
-    """Per (row, uniform): (fixed-point token, float64 Sampler.Sample token, distance of u
-    from the nearer float64 CDF boundary); per row: nucleus membership differences."""
-    lg = np.ascontiguousarray(logits_f32, dtype=np.float32)
-    B, V = lg.shape
-    u = np.ascontiguousarray(uniforms, dtype=np.float32).reshape(B, -1)
-    U = u.shape[1]
-    tq = np.empty((B, U), np.int32)
-    tf = np.empty((B, U), np.int32)
-    dist = np.empty((B, U), np.float64)
-    nd = np.empty(B, np.int32)
-    f = lib().ora_draw_parity
-    f.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_double, C.c_double, C.c_void_p, C.c_int, C.c_void_p,
-                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
-    f(_p(lg), B, V, float(temperature), float(top_p), _p(u), U, _p(tq), _p(tf), _p(dist), _p(nd), threads)
-    return tq, tf, dist, nd
-
-
 # ---------------------------------------------------------------- KV cache
 
 DT_CODE = {"f32": 0, "f16": 1, "bf16": 2, "fp8": 3, "int8": 4}

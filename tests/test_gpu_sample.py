@@ -129,3 +129,79 @@ def test_sample_matches_greedy_at_zero_temperature(gpu):
     ga, gt = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
     torch.cuda.synchronize()
     assert np.array_equal(acc, ga.cpu().numpy()) and np.array_equal(tok, gt.cpu().numpy())
+
+
+def _residual_boundary_uniforms(host, drafts, acc, n, q, T, top_p, rng):
+    """For sequences that stop at a rejection, u on (and one ulp below) a float64 CDF
+    boundary of the residual draw; others keep a random u."""
+    B, R, V = host.shape
+    K = R - 1
+    u = rng.random(B)
+    for b in range(B):
+        a = int(acc[b])
+        if a >= n[b]:
+            continue
+        p = ora.sampler_probs_f64(host[b, a], T, 0, top_p)
+        qq = np.zeros(V) if q is None else np.where((q[b, a] > 0) & np.isfinite(q[b, a]), np.minimum(q[b, a], 1), 0)
+        r = np.where(p > qq, p - qq, 0.0)
+        r[int(drafts[b, a])] = 0.0
+        s = np.cumsum(r)[-1]
+        if not s > 0:
+            continue
+        c = np.cumsum(r / s)
+        nz = np.nonzero(np.diff(c) > 0)[0]
+        if len(nz):
+            i = int(nz[rng.integers(0, len(nz))])
+            u[b] = c[i] if b % 2 == 0 else np.nextafter(c[i], 0.0)
+    return u
+
+
+@pytest.mark.parametrize("dense,top_p", [(False, 1.0), (False, 0.9), (True, 1.0), (True, 0.8)])
+def test_rejection_draw_on_boundaries(gpu, dense, top_p):
+    """The rejection acceptance's final draw (float64, the sample module's residual mode)
+    with the draw's uniform on residual CDF boundaries: the parallel sums cannot decide
+    these, so the sequential replay does; the decisions stay equal to the oracle's."""
+    B, K, V, T = 48, 3, 6007, 0.8
+    rng = np.random.default_rng(31 + int(dense) + int(top_p * 10))
+    host = rng.normal(0, 2, (B, K + 1, V)).astype(np.float32)
+    q = rng.dirichlet(np.ones(V) * 0.3, (B, K)).astype(np.float32) if dense else None
+    drafts = host[:, :K].argmax(-1).astype(np.int32)
+    mask = rng.random((B, K)) < 0.5
+    drafts[mask] = rng.integers(0, V, int(mask.sum()))
+    n = np.full(B, K, np.int32)
+    u = rng.random((B, K + 1)).astype(np.float32)
+    acc, _ = ora.accept_rejection(host, drafts, n, u, T, top_p, q)
+    ufin = _residual_boundary_uniforms(host, drafts, acc, n, q, float(np.float32(T)), float(np.float32(top_p)), rng)
+    u[:, K] = ufin.astype(np.float32)  # rounded to float32: still on or next to a boundary
+    ea, et = ora.accept_rejection(host, drafts, n, u, T, top_p, q)
+    say(f"rejection boundaries dense={dense} top_p={top_p}")
+    ga, gt = gv.accept_rejection(torch.from_numpy(host).cuda(), torch.from_numpy(drafts).cuda(),
+                                 torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda(), T, top_p,
+                                 torch.from_numpy(q).cuda() if dense else None)
+    torch.cuda.synchronize()
+    assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et)
+    assert (ea < n).sum() > B // 4
+
+
+def test_rejection_special_final_rows(gpu):
+    """NaN / +inf in the final row and a draft distribution that is all ones (every residual
+    0: the fallback to the row without the draft)."""
+    B, K, V = 8, 1, 3001
+    rng = np.random.default_rng(41)
+    host = rng.normal(0, 2, (B, K + 1, V)).astype(np.float32)
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    host[0, 0, 5] = np.nan
+    host[1, 1, 7] = np.inf
+    host[2, 0, :] = -np.inf
+    host[2, 0, 3] = 0.0
+    q = np.ones((B, K, V), np.float32)
+    n = np.full(B, K, np.int32)
+    u = rng.random((B, K + 1)).astype(np.float32)
+    for dq in (None, q):
+        ea, et = ora.accept_rejection(host, drafts, n, u, 0.8, 0.9, dq)
+        say(f"rejection special rows dense={dq is not None}")
+        ga, gt = gv.accept_rejection(torch.from_numpy(host).cuda(), torch.from_numpy(drafts).cuda(),
+                                     torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda(), 0.8, 0.9,
+                                     torch.from_numpy(dq).cuda() if dq is not None else None)
+        torch.cuda.synchronize()
+        assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et)

@@ -34,19 +34,6 @@ def test_emit_positions_matches_dense_verify(ora):
     assert np.array_equal(acc, ea) and np.array_equal(tok, et)
 
 
-@pytest.mark.parametrize("T,top_p", [(0.8, 1.0), (1.0, 0.9), (0.5, 0.5)])
-def test_sample_f64_matches_draw_parity_sampler(ora, T, top_p):
-    """Two separate float64 restatements of Sampler.Sample agree (qsort nucleus here,
-    radix-sorted nucleus in the draw-parity routine)."""
-    rng = np.random.default_rng(11)
-    B, V = 40, 3000
-    lg = rng.normal(0, 2, (B, V)).astype(np.float32)
-    u = rng.random((B, 1)).astype(np.float32)
-    _, tf, dist, _ = ora.draw_parity(lg, T, top_p, u, threads=1)
-    for b in range(B):
-        assert ora.sample_f64(lg[b], T, top_p, float(u[b, 0])) == tf[b, 0]
-
-
 def random_decisions(rng, B, K, V):
     drafts = rng.integers(0, V, (B, K)).astype(np.int32)
     n = rng.integers(0, K + 1, B).astype(np.int32)

@@ -72,6 +72,36 @@ int main(int argc, char** argv) {
     assert same.all(), x[~same][:5]
 
 
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_fast_exp64_error_bound(ora, tmp_path):
+    """The device's parallel-path exponential stays within 2e-14 relative of ora_exp64 on
+    [-708, 0] (the draw's margins count 1e-12), and gives 0 below -745.2."""
+    src = tmp_path / "f.c"
+    src.write_text(r"""
+#include <stdio.h>
+#include "gg_exp64.h"
+int main(int argc, char** argv) {
+    FILE* f = fopen(argv[1], "rb"); FILE* g = fopen(argv[2], "wb"); double x;
+    while (fread(&x, 8, 1, f) == 1) { double y = gg_fast_exp64(x); fwrite(&y, 8, 1, g); }
+    fclose(f); fclose(g); return 0;
+}
+""")
+    exe = tmp_path / "f"
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-I", str(ROOT / "gollmgo_amd" / "csrc"), str(src), "-o",
+                    str(exe), "-lm"], check=True)
+    rng = np.random.default_rng(3)
+    x = np.concatenate([-rng.random(2_000_000) * 708, -rng.random(500_000) * 2, np.linspace(-708, 0, 200_001)])
+    (tmp_path / "x.bin").write_bytes(x.tobytes())
+    subprocess.run([str(exe), str(tmp_path / "x.bin"), str(tmp_path / "y.bin")], check=True)
+    got = np.frombuffer((tmp_path / "y.bin").read_bytes(), np.float64)
+    want = ora.exp64(x)
+    rel = np.abs(got - want) / want
+    assert rel.max() < 2e-14, rel.max()
+    (tmp_path / "x.bin").write_bytes(np.array([-745.3, -1000.0, np.nan, -np.inf]).tobytes())
+    subprocess.run([str(exe), str(tmp_path / "x.bin"), str(tmp_path / "y.bin")], check=True)
+    assert (np.frombuffer((tmp_path / "y.bin").read_bytes(), np.float64) == 0).all()
+
+
 def test_top_k_reference_case(ora, golden):
     """sampling_test.go:56-71: top-2 of {1,5,3,2,4} keeps indices 1 and 4."""
     f = ora.top_k_filter_f64(np.array([1.0, 5.0, 3.0, 2.0, 4.0]), 2)
