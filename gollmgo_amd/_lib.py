@@ -2,15 +2,19 @@
 
 The library is loaded from this package directory only. There is no fallback:
 if it is missing, every entry point raises, so a GPU run can never silently
-take another code path.
+take another code path. GG_VERIFY_TRACE=1 loads the timeline build instead
+(libgg_verify_trace.so, compiled with -DGG_TRACE by build.build_trace; same
+kernels, plus per-workgroup timestamps of the LPT attention kernel).
 """
 from __future__ import annotations
 
 import ctypes as C
 import enum
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libgg_verify.so"
+_TRACE = os.environ.get("GG_VERIFY_TRACE", "") == "1"
+LIB_PATH = Path(__file__).resolve().parent / ("libgg_verify_trace.so" if _TRACE else "libgg_verify.so")
 
 
 class Status(enum.IntEnum):
@@ -103,6 +107,9 @@ def lib() -> C.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+        if _TRACE:
+            handle.gg_debug_trace_ptr.restype = C.c_void_p
+            handle.gg_debug_trace_ptr.argtypes = []
         _lib = handle
     return _lib
 

@@ -48,14 +48,14 @@ def _headers() -> list[Path]:
     return sorted([*CSRC.glob("*.h"), *INCLUDE.glob("*.h")])
 
 
-def _compile(src: Path, force: bool) -> Path:
-    obj = OBJ / (src.name + ".o")
+def _compile(src: Path, force: bool, obj_dir: Path = OBJ, extra: tuple = ()) -> Path:
+    obj = obj_dir / (src.name + ".o")
     newest_dep = max([src.stat().st_mtime] + [h.stat().st_mtime for h in _headers()])
     if not force and obj.exists() and obj.stat().st_mtime >= newest_dep:
         return obj
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(INCLUDE), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-I", str(INCLUDE), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
-        cmd = [hipcc(), *HIPCC_FLAGS, "-x", "hip", "-I", str(INCLUDE), "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-x", "hip", "-I", str(INCLUDE), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
@@ -78,6 +78,21 @@ def build(force: bool = False, verbose: bool = False) -> Path:
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def build_trace(force: bool = False) -> Path:
+    """The timeline build: every source with -DGG_TRACE, linked to libgg_verify_trace.so
+    (loaded instead of the library when GG_VERIFY_TRACE=1). Diagnostics only."""
+    obj_dir = OBJ / "trace"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    out = PKG / "libgg_verify_trace.so"
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        objs = list(ex.map(lambda s: _compile(s, force, obj_dir, ("-DGG_TRACE",)), _sources()))
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(out), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    return out
 
 
 if __name__ == "__main__":
