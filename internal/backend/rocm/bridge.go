@@ -192,6 +192,18 @@ func AcceptGreedy(logits unsafe.Pointer, dt int, B, K, V int, drafts, nDrafts,
 	return ggErr("gg_accept_greedy", st)
 }
 
+// AcceptGreedySample: AcceptGreedy whose bonus token (every draft accepted) is drawn as the
+// engine's Sampler.Sample draws it, with temperature, topK and topP of the engine's
+// SamplingParams and uniforms (device float64 [B]) in place of rng.Float64().
+func AcceptGreedySample(logits unsafe.Pointer, dt int, B, K, V int, drafts, nDrafts unsafe.Pointer,
+	temperature float64, topK int, topP float64, uniforms, accepted, token, ws unsafe.Pointer, wsBytes uintptr,
+	stream unsafe.Pointer) error {
+	st := C.gg_accept_greedy_sample(logits, C.gg_dtype_t(dt), C.int(B), C.int(K), C.int(V), (*C.int32_t)(drafts),
+		(*C.int32_t)(nDrafts), C.double(temperature), C.int(topK), C.double(topP), (*C.double)(uniforms), 0,
+		(*C.int32_t)(accepted), (*C.int32_t)(token), ws, C.size_t(wsBytes), stream)
+	return ggErr("gg_accept_greedy_sample", st)
+}
+
 // AcceptRejection: as AcceptGreedy plus draftProbs (device float [B][K][V], or nil for
 // the one-hot n-gram drafter), uniforms (device float [B][K+1]), temperature, topP.
 func AcceptRejection(logits unsafe.Pointer, dt int, draftProbs unsafe.Pointer, B, K, V int,
@@ -227,6 +239,10 @@ func HistoryAppendDraft(history unsafe.Pointer, stride int, histLen, rows unsafe
 
 func AcceptGreedyWorkspace(B, K, V int) uintptr {
 	return uintptr(C.gg_accept_greedy_workspace_size(C.int(B), C.int(K), C.int(V)))
+}
+
+func AcceptGreedySampleWorkspace(B, K, V int) uintptr {
+	return uintptr(C.gg_accept_greedy_sample_workspace_size(C.int(B), C.int(K), C.int(V)))
 }
 
 func AcceptRejectionWorkspace(B, K, V int) uintptr {

@@ -10,6 +10,7 @@ import (
 	"unsafe"
 
 	"github.com/TensorGreed/gollmgo/internal/backend"
+	"github.com/TensorGreed/gollmgo/internal/engine"
 )
 
 // Model is the part of a step that lives outside libgg_verify: embeddings, the
@@ -38,17 +39,34 @@ type Model interface {
 	Prefill(ctx context.Context, batch *backend.Batch) (*backend.StepOutput, error)
 }
 
+// Acceptance selects how the device decides a step's drafts.
+type Acceptance int
+
+const (
+	// AcceptGreedy: the reference's Verify on the device; when every draft is accepted the
+	// bonus token is drawn on the device as the engine's Sampler.Sample would draw it, with
+	// Config.Sampling (the engine's own SamplingParams) and the runner's uniform stream.
+	AcceptGreedy Acceptance = iota
+	// AcceptBonusRow: Verify on the device; when every draft is accepted the bonus row's real
+	// logits are copied back, so the engine's Sampler (and its random stream) draws the
+	// bonus exactly as with the reference's runner. One D2H row per such sequence.
+	AcceptBonusRow
+	// AcceptRejection: speculative sampling at Sampling's temperature and top-p (no
+	// counterpart in the reference), one-hot draft distributions.
+	AcceptRejection
+)
+
 // Config fixes the pools and the acceptance rule.
 type Config struct {
-	NumBlocks   int
-	BlockSize   int
-	KVDtype     int // Dtype* of bridge.go
-	KVScales    int // Scale*: PerHead for FP8, PerBlock for INT8, None otherwise
-	MaxDrafts   int // K: rows per sequence are K+1
-	Temperature float32
-	TopP        float32
-	Rejection   bool // speculative sampling; false: greedy Verify + argmax
-	Seed        int64
+	NumBlocks  int
+	BlockSize  int
+	KVDtype    int // Dtype* of bridge.go
+	KVScales   int // Scale*: PerHead for FP8, PerBlock for INT8, None otherwise
+	MaxDrafts  int // K: rows per sequence are K+1
+	Acceptance Acceptance
+	// Sampling must be the SamplingParams the engine was built with
+	// (ServingEngineConfig.Sampling): the device draws with them.
+	Sampling engine.SamplingParams
 	// Device drafting (drafts.go): each sequence's history kept on the device and the
 	// next step drafted there after the acceptance, served through Drafts.
 	DeviceDrafts  bool
@@ -75,13 +93,14 @@ type Runner struct {
 	drafts                *deviceDrafts // nil without DeviceDrafts
 
 	// Device buffers (allocated once at Warmup).
-	dIn                       unsafe.Pointer // the packed int32 inputs + float uniforms, one upload
+	dIn                       unsafe.Pointer // the packed int32 inputs + uniforms, one upload
 	dQ, dK, dV, dOut, dLogits unsafe.Pointer
 	dAttnWS, dAccWS, dDec     unsafe.Pointer
 	attnWS, accWS             uintptr
-	// Pinned host staging of the same layout, and of the decision.
-	hIn, hDec unsafe.Pointer
-	inBytes   uintptr
+	// Pinned host staging of the same layout, of the decision and (AcceptBonusRow) of the
+	// bonus rows.
+	hIn, hDec, hBonus unsafe.Pointer
+	inBytes           uintptr
 }
 
 // New creates the pools; buffers follow at Warmup.
@@ -96,16 +115,20 @@ func New(model Model, cfg Config) (*Runner, error) {
 		kv.Close()
 		return nil, err
 	}
+	seed := int64(1)
+	if cfg.Sampling.Seed != nil {
+		seed = int64(*cfg.Sampling.Seed)
+	}
 	return &Runner{
 		model: model, cfg: cfg, kv: kv, stream: s, rows: NewOneHotRows(model.Vocab()),
-		rng: rand.New(rand.NewSource(cfg.Seed)),
+		rng: rand.New(rand.NewSource(seed)),
 		hq:  model.NumQHeads(), hkv: model.NumKVHeads(), d: model.HeadDim(), vocab: model.Vocab(),
 	}, nil
 }
 
 // Input layout of one step (int32 words): tokens, positions, slots [B*R]; ctx, rows,
-// n_drafts, history rows [B]; tables [B*maxBlocks]; drafts [B*K]; then float32 uniforms
-// [B*R].
+// n_drafts, history rows [B]; tables [B*maxBlocks]; drafts [B*K]; then the uniforms, at an
+// even word: float32 [B*R] (rejection) or float64 [B] (the bonus draw).
 type inLayout struct {
 	tokens, positions, slots, ctx, rows, tables, drafts, nDrafts, histRows, uniforms, words int
 }
@@ -117,7 +140,12 @@ func layout(B, R, MB int) inLayout {
 	l.tokens, l.positions, l.slots = take(B*R), take(B*R), take(B*R)
 	l.ctx, l.rows, l.nDrafts, l.histRows = take(B), take(B), take(B), take(B)
 	l.tables, l.drafts = take(B*MB), take(B*(R-1))
-	l.uniforms = take(B * R)
+	off += off & 1
+	uw := B * R
+	if uw < 2*B {
+		uw = 2 * B
+	}
+	l.uniforms = take(uw)
 	l.words = off
 	return l
 }
@@ -132,10 +160,10 @@ func (r *Runner) Warmup(_ context.Context, p backend.WarmupProfile) error {
 	B, R := r.maxB, r.maxR
 	r.inBytes = uintptr(layout(B, R, r.maxBlocks).words) * 4
 	r.attnWS = r.kv.AttentionWorkspace(B, R, r.hq, r.maxBlocks)
-	if r.cfg.Rejection {
+	if r.cfg.Acceptance == AcceptRejection {
 		r.accWS = AcceptRejectionWorkspace(B, R-1, r.vocab)
 	} else {
-		r.accWS = AcceptGreedyWorkspace(B, R-1, r.vocab)
+		r.accWS = AcceptGreedySampleWorkspace(B, R-1, r.vocab)
 	}
 	rowBytes := uintptr(B*R) * 2
 	var err error
@@ -155,6 +183,9 @@ func (r *Runner) Warmup(_ context.Context, p backend.WarmupProfile) error {
 	}
 	if r.hIn, err = hostAlloc(r.inBytes); err == nil {
 		r.hDec, err = hostAlloc(uintptr(2*B) * 4)
+	}
+	if err == nil && r.cfg.Acceptance == AcceptBonusRow {
+		r.hBonus, err = hostAlloc(uintptr(B*r.vocab) * 2)
 	}
 	if err == nil && r.cfg.DeviceDrafts {
 		stride, rows := r.cfg.HistoryStride, r.cfg.HistoryRows
@@ -207,9 +238,16 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 	copy(i32(r.hIn, l.nDrafts, B), in.NDrafts)
 	copy(i32(r.hIn, l.tables, B*MB), in.BlockTables)
 	copy(i32(r.hIn, l.drafts, B*K), in.Drafts)
-	u := unsafe.Slice((*float32)(at(r.hIn, l.uniforms)), B*R)
-	for i := range u {
-		u[i] = r.rng.Float32()
+	if r.cfg.Acceptance == AcceptRejection {
+		u := unsafe.Slice((*float32)(at(r.hIn, l.uniforms)), B*R)
+		for i := range u {
+			u[i] = r.rng.Float32()
+		}
+	} else {
+		u := unsafe.Slice((*float64)(at(r.hIn, l.uniforms)), B)
+		for i := range u {
+			u[i] = r.rng.Float64()
+		}
 	}
 	s := r.stream
 	histRows := i32(r.hIn, l.histRows, B)
@@ -247,12 +285,17 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 		return nil, err
 	}
 	acc, tok := r.dDec, unsafe.Add(r.dDec, 4*B)
-	if r.cfg.Rejection {
+	sp := r.cfg.Sampling
+	switch r.cfg.Acceptance {
+	case AcceptRejection:
 		err = AcceptRejection(r.dLogits, DtypeBF16, nil, B, K, r.vocab, d(l.drafts), d(l.nDrafts), d(l.uniforms),
-			r.cfg.Temperature, r.cfg.TopP, acc, tok, r.dAccWS, r.accWS, s)
-	} else {
+			float32(sp.Temperature), float32(sp.TopP), acc, tok, r.dAccWS, r.accWS, s)
+	case AcceptBonusRow:
 		err = AcceptGreedy(r.dLogits, DtypeBF16, B, K, r.vocab, d(l.drafts), d(l.nDrafts), acc, tok, r.dAccWS,
 			r.accWS, s)
+	default:
+		err = AcceptGreedySample(r.dLogits, DtypeBF16, B, K, r.vocab, d(l.drafts), d(l.nDrafts), sp.Temperature,
+			sp.TopK, sp.TopP, d(l.uniforms), acc, tok, r.dAccWS, r.accWS, s)
 	}
 	if err != nil {
 		return nil, err
@@ -269,6 +312,12 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 		return nil, err
 	}
 	hAcc, hTok := i32(r.hDec, 0, B), i32(r.hDec, B, B)
+	var bonus [][]float32
+	if r.cfg.Acceptance == AcceptBonusRow {
+		if bonus, err = r.bonusRows(in, hAcc, B, R); err != nil {
+			return nil, err
+		}
+	}
 	if r.drafts != nil {
 		r.drafts.finish(in, batch.SequenceIDs, histRows, hAcc, hTok)
 	}
@@ -282,10 +331,49 @@ func (r *Runner) Step(ctx context.Context, batch *backend.Batch) (*backend.StepO
 		if err != nil {
 			return nil, fmt.Errorf("rocm: sequence %d: %w", i, err)
 		}
+		if bonus != nil && bonus[i] != nil {
+			rows[len(rows)-1] = bonus[i] // the engine's Sampler draws the bonus
+		}
 		out.Logits[i] = rows[0]
 		if n > 0 {
 			out.LogitsPerPosition[i] = rows
 		}
+	}
+	return out, nil
+}
+
+// bonusRows copies back, for every sequence that accepted all its drafts, the logits of its
+// bonus row (bf16 on the device) as float32, as the reference's runner returns rows
+// (kernels/gollmgo_model.cu:1057-1060). Other sequences get nil.
+func (r *Runner) bonusRows(in *StepInputs, hAcc []int32, B, R int) ([][]float32, error) {
+	V := r.vocab
+	need := false
+	for i := 0; i < B; i++ {
+		if int(hAcc[i]) == int(in.NDrafts[i]) {
+			src := unsafe.Add(r.dLogits, uintptr((i*R+int(in.NDrafts[i]))*V)*2)
+			if err := copyD2H(unsafe.Add(r.hBonus, uintptr(i*V)*2), src, uintptr(V)*2, r.stream); err != nil {
+				return nil, err
+			}
+			need = true
+		}
+	}
+	if !need {
+		return nil, nil
+	}
+	if err := syncStream(r.stream); err != nil {
+		return nil, err
+	}
+	out := make([][]float32, B)
+	for i := 0; i < B; i++ {
+		if int(hAcc[i]) != int(in.NDrafts[i]) {
+			continue
+		}
+		h := unsafe.Slice((*uint16)(unsafe.Add(r.hBonus, uintptr(i*V)*2)), V)
+		row := make([]float32, V)
+		for j, b := range h {
+			row[j] = math.Float32frombits(uint32(b) << 16)
+		}
+		out[i] = row
 	}
 	return out, nil
 }
@@ -308,7 +396,8 @@ func (r *Runner) release() {
 	}
 	hostFree(r.hIn)
 	hostFree(r.hDec)
-	r.hIn, r.hDec = nil, nil
+	hostFree(r.hBonus)
+	r.hIn, r.hDec, r.hBonus = nil, nil, nil
 	if r.drafts != nil {
 		r.drafts.close()
 		r.drafts = nil
