@@ -531,16 +531,44 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             }
         };
         uint4 opl[NT];
+        // f16 operands (FP8 / INT8 / F16 pools) hold |q| < 65504. A bf16 or f32 query beyond
+        // 2^15 is scaled by 2^-k for the piece (k from the rows' largest |q|) and the score
+        // multiplier by 2^k: power-of-two scalings are exact, so in range nothing changes.
+        constexpr bool kF16Op = !kIsBf16;
+        __shared__ float s_qmax[4];
+        auto piece_q_shift = [&](float local_max) -> int {
+            for (int o = 32; o > 0; o >>= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, o));
+            if (lane == 0) s_qmax[wave] = local_max;
+            __syncthreads();
+            const float mx = fmaxf(fmaxf(s_qmax[0], s_qmax[1]), fmaxf(s_qmax[2], s_qmax[3]));
+            int e = 0;
+            (void)frexpf(mx, &e);  // mx = f * 2^e, f in [0.5, 1)
+            return (mx == mx && mx <= 3.402823466e38f && e > 15) ? e - 15 : 0;
+        };
         if (a.q_dtype == GG_DTYPE_F32) {
             float4 raw[NT][2];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
                 for (int h = 0; h < 2; ++h) raw[rt][h] = ((const float4*)((const float*)a.q + qb[rt]))[h];
+            float qs = 1.f;
+            if constexpr (kF16Op) {
+                float lm = 0.f;
+#pragma unroll
+                for (int rt = 0; rt < NT; ++rt)
+                    if (qvalid[rt])
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            lm = fmaxf(lm, fmaxf(fmaxf(fabsf(raw[rt][h].x), fabsf(raw[rt][h].y)),
+                                                 fmaxf(fabsf(raw[rt][h].z), fabsf(raw[rt][h].w))));
+                const int k = piece_q_shift(lm);
+                qs = ldexpf(1.f, -k);
+                sscale = ldexpf(sscale, k);
+            }
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt) {
-                const float f[8] = {raw[rt][0].x, raw[rt][0].y, raw[rt][0].z, raw[rt][0].w,
-                                    raw[rt][1].x, raw[rt][1].y, raw[rt][1].z, raw[rt][1].w};
+                const float f[8] = {raw[rt][0].x * qs, raw[rt][0].y * qs, raw[rt][0].z * qs, raw[rt][0].w * qs,
+                                    raw[rt][1].x * qs, raw[rt][1].y * qs, raw[rt][1].z * qs, raw[rt][1].w * qs};
                 pack8(f, op[rt], opl[rt]);
             }
         } else {
@@ -552,18 +580,34 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& a, const KVView& kv, 
             }
             // Convert when the Q type differs from the MFMA operand type.
             if (src_bf16 != kIsBf16) {
+                float f[NT][8];
+                float lm = 0.f;
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) {
                     const uint32_t w[4] = {op[rt].x, op[rt].y, op[rt].z, op[rt].w};
-                    float f[8];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const uint16_t lo = (uint16_t)w[k], hi = (uint16_t)(w[k] >> 16);
-                        f[2 * k] = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-                        f[2 * k + 1] = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                        f[rt][2 * k] = src_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                        f[rt][2 * k + 1] = src_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
                     }
-                    pack8(f, op[rt], opl[rt]);
+                    if (qvalid[rt])
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) lm = fmaxf(lm, fabsf(f[rt][k]));
                 }
+                if constexpr (kF16Op) {
+                    const int k = piece_q_shift(lm);
+                    if (k > 0) {
+                        const float qs = ldexpf(1.f, -k);
+#pragma unroll
+                        for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) f[rt][e] *= qs;
+                        sscale = ldexpf(sscale, k);
+                    }
+                }
+#pragma unroll
+                for (int rt = 0; rt < NT; ++rt) pack8(f[rt], op[rt], opl[rt]);
             }
         }
 #pragma unroll
@@ -1139,6 +1183,17 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
 // stores, and the merging workgroup reads them with device-scope loads). No workgroup
 // waits for another, so there is no spinning; the merge costs the last piece a read of
 // the item's records.
+// Ordering, on gfx950 (gg_kv_create refuses other devices): a device-scope relaxed store
+// is issued with the system-coherent bit, so it is written through the XCD's L2 to the
+// coherence point, and it counts in vmcnt until that write is acknowledged;
+// `s_waitcnt vmcnt(0)` therefore returns only once every record store of the thread is
+// visible at the coherence point. The barrier orders all threads' waits before thread 0's
+// counter add, which is performed at the coherence point. The merging piece sees the final
+// count in the add's return value and only then issues its record loads, which are
+// device-scope (system-coherent bit: served from the coherence point, never from a stale
+// line of its own XCD's L2). So every record load follows, in time, the completion of the
+// record's store. The language-level way (a release add and an acquire read) writes back
+// and invalidates the whole XCD L2 on this device and costs config 3 about 4 % (measured).
 __device__ void lpt_merge_if_last(const AttnArgs& a, int Hkv, int b, int kvh, int np) {
     __shared__ int s_last;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's record stores are done

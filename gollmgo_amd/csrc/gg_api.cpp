@@ -77,6 +77,19 @@ GG_API gg_status_t gg_kv_create(int num_layers, int num_blocks, int block_size, 
     } else {
         GG_CHECK_ARG(scale_mode == GG_SCALE_NONE, "gg_kv_create: float pools take GG_SCALE_NONE");
     }
+    {
+        // The code objects are gfx950 only, and the in-launch merge of split attention items
+        // relies on gfx950's ordering of device-scope stores, waits and atomics (the stores
+        // complete at the device's coherence point before the counter's add is issued), so
+        // a pool is only created on a gfx950 device.
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+            return fail(GG_ERR_HIP, "gg_kv_create: no HIP device");
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            return fail(GG_ERR_INVALID, std::string("gg_kv_create: the library is built for gfx950, device is ") +
+                                            prop.gcnArchName);
+    }
     gg_kv* kv = new gg_kv();
     kv->num_layers = num_layers;
     kv->num_blocks = num_blocks;

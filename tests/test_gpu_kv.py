@@ -135,7 +135,7 @@ def test_append_random_cases(gpu, seed):
 # ------------------------------------------------------------------ attention
 
 def run_attention_case(dt, B, R, Hq, H, D, bs, ctx, partition=0, src="f32", seed=0, q_dt="f32",
-                       row_counts=None, kv_sd=1.0):
+                       row_counts=None, kv_sd=1.0, q_sd=1.0, v_sd=None):
     rng = np.random.default_rng(seed)
     keys = np.asarray(ctx, np.int32) + R
     nbs = [(int(k) + bs - 1) // bs for k in keys]
@@ -151,14 +151,14 @@ def run_attention_case(dt, B, R, Hq, H, D, bs, ctx, partition=0, src="f32", seed
     mirror = PoolMirror(kv)
     slots = np.concatenate([bt[b, np.arange(keys[b]) // bs] * bs + np.arange(keys[b]) % bs for b in range(B)]).astype(np.int32)
     kk = rng.normal(0, kv_sd, (len(slots), H, D)).astype(np.float32)
-    vv = rng.normal(0, kv_sd, (len(slots), H, D)).astype(np.float32)
+    vv = rng.normal(0, kv_sd if v_sd is None else v_sd, (len(slots), H, D)).astype(np.float32)
     if dt == "fp8":
         ks, vs = per_head_amax_scales(kk), per_head_amax_scales(vv)
         kv.set_head_scales(0, ks, vs)
         mirror.set_head_scales(ks, vs)
     append_rows(kv, mirror, kk, vv, slots, src)
     mirror.sync_from_device()
-    q = rng.normal(0, 1, (B, R, Hq, D)).astype(np.float32)
+    q = rng.normal(0, q_sd, (B, R, Hq, D)).astype(np.float32)
     qt = torch.from_numpy(q).to({"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[q_dt]).cuda()
     qh = qt.float().cpu().numpy()
     out = torch.zeros(B, R, Hq, D, dtype=torch.float32, device="cuda")
@@ -200,6 +200,24 @@ def test_attention_mfma_path(gpu, dt, shape):
         err = run_attention_case(dt, B, R, Hq, H, 128, 16, ctx, partition=part, src="bf16", q_dt="bf16", seed=shape)
         print(f"  rel err {err:.2e}")
         assert err <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["f16", "fp8", "int8"])
+@pytest.mark.parametrize("q_sd", [3e4, 1e6])
+def test_attention_large_bf16_queries_on_f16_operand_pools(gpu, dt, q_sd):
+    """FP8 / INT8 / F16 pools take Q as f16 MFMA operands (|q| < 65504). bf16 queries far
+    beyond that (|q| up to ~1.4e5, and ~5e6) are scaled by a power of two for the piece,
+    with the score multiplier scaled back, so the result stays textbook attention. K is
+    drawn at 3/q_sd so that the scores stay O(1): with scores in the tens of thousands
+    the fp32 dot products themselves would decide the softmax, whatever the operands. V
+    keeps N(0, 1)."""
+    for shape in (0, 1, 3):
+        B, R, Hq, H, ctx = MFMA_SHAPES[shape]
+        for part in (0, 256):
+            say(f"attention large q dt={dt} q_sd={q_sd} shape={shape} partition={part}")
+            err = run_attention_case(dt, B, R, Hq, H, 128, 16, ctx, partition=part, src="bf16", q_dt="bf16",
+                                     seed=shape + 7, q_sd=q_sd, kv_sd=3.0 / q_sd, v_sd=1.0)
+            assert err <= TOL[dt], (dt, q_sd, shape, part, err)
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "fp8", "int8"])
