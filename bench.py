@@ -378,9 +378,10 @@ def pmc_traffic(config_id: int):
 
 
 def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, uniforms, scale, decision):
-    """The CPU oracle (a C port of the reference's host logic and of its attention
-    semantics) timed on this host on bounded samples of the same workload, at every usable
-    core and at one thread. A sample is the attention of layer 0 for the first S sequences,
+    """A C port of the reference's host logic and of its attention (the v1 kernel's loop,
+    kernels/gollmgo_paged_attn.cu:38-119, at its fp32 precision: ora_attention_ref_f32, not
+    the fp64 checker) timed on this host on bounded samples of the same workload, at every
+    usable core and at one thread. A sample is the attention of layer 0 for the first S sequences,
     scaled by L layers, plus the acceptance of the same S sequences (and their n-gram
     drafts when the config has token histories). `value` is the all-cores figure; the
     one-thread figure uses a smaller sample of the same shape. The Go engine's own host
@@ -414,8 +415,8 @@ def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, u
     def sample(S, threads):
         qh = q[0, :S].float().cpu().numpy()
         t0 = time.perf_counter()
-        ora.attention(qh, kc, vc, cfg.kv_dtype, cfg.num_kv_heads, cfg.head_dim, cfg.block_size, lay.keys[:S],
-                      lay.block_tables[:S], scale, ks, vs, threads=threads)
+        ora.attention_ref_f32(qh, kc, vc, cfg.kv_dtype, cfg.num_kv_heads, cfg.head_dim, cfg.block_size,
+                              lay.keys[:S], lay.block_tables[:S], scale, ks, vs, threads=threads)
         t_attn = time.perf_counter() - t0
         t_dr = 0.0
         if hist is not None:
@@ -433,7 +434,7 @@ def cpu_baseline(args, cfg, lay, kv, q, logits, draft_probs, drafts, n_drafts, u
             ora.accept_greedy(lg, dr, nd)
         t_acc = time.perf_counter() - t0
         step_s = cfg.layers * t_attn + t_acc + t_dr
-        desc = (f"{S} of {cfg.num_seqs} sequences: layer-0 attention ({t_attn:.2f} s, fp64, {threads} thread(s)) "
+        desc = (f"{S} of {cfg.num_seqs} sequences: layer-0 attention ({t_attn:.2f} s, the reference's v1 loop in fp32, {threads} thread(s)) "
                 f"x {cfg.layers} layers + {cfg.accept} acceptance ({t_acc:.2f} s, 1 thread)"
                 + (f" + n-gram drafts ({t_dr:.3f} s)" if hist is not None else ""))
         return {"value": round(S * cfg.rows / step_s, 2), "threads": threads, "sample": desc,

@@ -818,6 +818,70 @@ void ora_attention(const float* q, float* out, const uint8_t* kc, const uint8_t*
     }
 }
 
+/* The reference's v1 paged attention (kernels/gollmgo_paged_attn.cu:38-119) in fp32, as a
+ * host loop: per (sequence, verify row, query head) the dot products over the visible keys
+ * in fp32 (q * k, summed over d in order, then * scale), the max, expf(s - max) summed in
+ * key order, a reciprocal of the sum, and the fp32 weighted sum of V. Causal rows, block
+ * tables and the fp8 / int8 scales as ora_attention. This is the CPU baseline bench.py
+ * times (the reference semantics at the reference's precision); ora_attention, in fp64, is
+ * the checker. */
+void ora_attention_ref_f32(const float* q, float* out, const uint8_t* kc, const uint8_t* vc, int dt, int H,
+                           int D, int bs, const float* k_scale, const float* v_scale, const int32_t* ctx_lens,
+                           const int32_t* row_counts, const int32_t* block_tables, int max_blocks, int B, int R,
+                           int Hq, float scale, int threads, int num_blocks) {
+    const int G = Hq / H;
+    const long items = (long)B * R * Hq;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1)
+#else
+    (void)threads;
+#endif
+    for (long w = 0; w < items; ++w) {
+        const int b = (int)(w / ((long)R * Hq)), j = (int)((w / Hq) % R), hq = (int)(w % Hq);
+        int ctx = ctx_lens[b];
+        if (ctx < 0) ctx = 0;
+        if (ctx > max_blocks * bs) ctx = max_blocks * bs;
+        const int nr = row_counts ? row_counts[b] : R;
+        if (nr <= 0 || nr > ctx || j >= nr) continue;
+        const int pos = ctx - nr + j, n = pos + 1, h = hq / G;
+        float* sc = (float*)malloc(sizeof(float) * (size_t)n);
+        const float* qv = q + (((size_t)b * R + j) * Hq + hq) * D;
+        float mx = -1e30f;
+        for (int t = 0; t < n; ++t) {
+            const int blk = block_tables[(size_t)b * max_blocks + t / bs], o = t % bs;
+            if (blk < 0 || blk >= num_blocks) {
+                sc[t] = -INFINITY;
+                continue;
+            }
+            const float ks = dt == 3 ? k_scale[h] : dt == 4 ? k_scale[(size_t)blk * H + h] : 1.0f;
+            float dot = 0.0f;
+            for (int d = 0; d < D; ++d) dot += qv[d] * (raw_elem(kc, dt, k_off(blk, h, o, d, H, bs, D)) * ks);
+            sc[t] = dot * scale;
+            if (sc[t] > mx) mx = sc[t];
+        }
+        float sum = 0.0f;
+        for (int t = 0; t < n; ++t) {
+            sc[t] = expf(sc[t] - mx);
+            sum += sc[t];
+        }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (int t = 0; t < n; ++t) sc[t] *= inv;
+        float* ov = out + (((size_t)b * R + j) * Hq + hq) * D;
+        for (int d = 0; d < D; ++d) {
+            float acc = 0.0f;
+            for (int t = 0; t < n; ++t) {
+                if (sc[t] == 0.0f) continue;
+                const int blk = block_tables[(size_t)b * max_blocks + t / bs], o = t % bs;
+                const float vs = dt == 3 ? v_scale[h] : dt == 4 ? v_scale[(size_t)blk * H + h] : 1.0f;
+                acc += sc[t] * (raw_elem(vc, dt, v_off(blk, h, o, d, H, bs, D)) * vs);
+            }
+            ov[d] = acc;
+        }
+        free(sc);
+    }
+}
+
 /* ------------------------------------------------------- array helpers */
 
 void ora_fp8_encode_n(const float* x, uint8_t* out, long n) {

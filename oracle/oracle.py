@@ -300,7 +300,7 @@ def kv_append_q(kc: np.ndarray, vc: np.ndarray, dt: str, H: int, D: int, bs: int
 
 def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, dt: str, H: int, D: int, bs: int,
               ctx_lens: np.ndarray, block_tables: np.ndarray, scale: float, k_scale=None, v_scale=None,
-              row_counts=None, threads: int = 0) -> np.ndarray:
+              row_counts=None, threads: int = 0, fn: str = "ora_attention") -> np.ndarray:
     """fp64 textbook attention; q [B,R,Hq,D] fp32 values; pools as raw bytes (one
     layer, all blocks: the block count is taken from their size)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
@@ -316,9 +316,17 @@ def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, dt: str, H: int, D:
     vc = np.ascontiguousarray(vc)
     eb = {"f32": 4, "f16": 2, "bf16": 2, "fp8": 1, "int8": 1}[dt]
     num_blocks = kc.nbytes // (H * bs * D * eb)
-    f = lib().ora_attention
+    f = getattr(lib(), fn)
     f.argtypes = [C.c_void_p] * 4 + [C.c_int] * 4 + [C.c_void_p] * 5 + [C.c_int] * 4 + [C.c_float, C.c_int, C.c_int]
     f(_p(q), _p(out), _p(kc), _p(vc), DT_CODE[dt], H, D, bs,
       _p(ks) if ks is not None else None, _p(vs) if vs is not None else None, _p(cl),
       _p(rc) if rc is not None else None, _p(bt), bt.shape[1], B, R, Hq, float(scale), threads, int(num_blocks))
     return out
+
+
+def attention_ref_f32(q, kc, vc, dt, H, D, bs, ctx_lens, block_tables, scale, k_scale=None, v_scale=None,
+                      row_counts=None, threads: int = 0) -> np.ndarray:
+    """The reference's v1 attention semantics in fp32 (kernels/gollmgo_paged_attn.cu:38-119):
+    the timed CPU baseline of bench.py, not the checker (that is `attention`, fp64)."""
+    return attention(q, kc, vc, dt, H, D, bs, ctx_lens, block_tables, scale, k_scale, v_scale, row_counts, threads,
+                     fn="ora_attention_ref_f32")

@@ -542,3 +542,29 @@ def test_kv_append_int8_skipped_rows_inside_a_run(ora):
     # The block's scale is the amax of every row it holds over 127 (rounded to fp16).
     amax = np.abs(np.concatenate([first, rows])).max(axis=(0, 2))
     assert np.array_equal(pools[1][2][H:2 * H], ora.f16_round_c((amax / np.float32(127)).astype(np.float32)))
+
+
+def test_attention_ref_f32_is_the_same_rule(ora):
+    """The fp32 restatement of the reference's v1 loop (the timed CPU baseline) computes the
+    same attention as the fp64 checker, to fp32 rounding, on every pool type."""
+    rng = np.random.default_rng(41)
+    for dt in ("bf16", "fp8", "int8", "f32"):
+        q, kc, vc, kvals, vvals, keys, bt = _bf16_pool_case(ora, seed=3)
+        H, D, bs = 2, 32, 4
+        ks = vs = None
+        if dt != "bf16":
+            kf = ora.bf16_to_f32(kc.view(np.uint16)).reshape(-1, H, bs, D)
+            vf = ora.bf16_to_f32(vc.view(np.uint16)).reshape(-1, H, D, bs)
+            if dt == "f32":
+                kc, vc = kf.astype(np.float32).view(np.uint8).copy(), vf.astype(np.float32).view(np.uint8).copy()
+            elif dt == "fp8":
+                ks = vs = np.full(H, 1 / 64, np.float32)
+                kc, vc = ora.fp8_encode(kf * 64), ora.fp8_encode(vf * 64)
+            else:
+                nb = kf.shape[0]
+                ks = vs = np.full(nb * H, 1 / 32, np.float32)
+                kc = ora.int8_encode(kf * 32).view(np.uint8).copy()
+                vc = ora.int8_encode(vf * 32).view(np.uint8).copy()
+        a = ora.attention(q, kc, vc, dt, H, D, bs, keys, bt, 0.2, ks, vs)
+        b = ora.attention_ref_f32(q, kc, vc, dt, H, D, bs, keys, bt, 0.2, ks, vs)
+        assert np.abs(a - b).max() <= 1e-5 * max(1.0, np.abs(a).max()), dt
