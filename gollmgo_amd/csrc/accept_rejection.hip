@@ -1115,15 +1115,25 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
 
 // One wave per sequence: the acceptance walk, then what the final draw takes: the row
 // and, after a rejection, the rejected draft (the residual draw excludes it).
+// With top-p the row's exact fixed-point nucleus boundary key goes along (0: none): the
+// float64 cut almost always falls in the same coarse bin, which the draw then gathers in its
+// first pass.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* __restrict__ out_acc,
-                                                        int* __restrict__ spec_row, int* __restrict__ spec_x) {
+                                                        int* __restrict__ spec_row, int* __restrict__ spec_x,
+                                                        unsigned int* __restrict__ spec_key) {
     const int b = blockIdx.x;
     const SeqPlan p = decide_seq<DT>(din, b);
     if (threadIdx.x == 0) {
         out_acc[b] = p.d.accepted;
         spec_row[b] = p.d.row;
         spec_x[b] = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
+        unsigned int key = 0;
+        if (din.use_topp) {
+            const RowStats st = din.stats[(size_t)b * (din.K + 1) + p.d.row];
+            if (st.valid) key = st.lam;
+        }
+        spec_key[b] = key;
     }
 }
 
@@ -1136,6 +1146,7 @@ struct RejWs {
     u64* seg_e;
     int* spec_row;     // the final draw's row per sequence
     int* spec_x;       // the rejected draft of a residual draw, -1 for a plain draw
+    unsigned int* spec_key;  // top-p: the final row's fixed-point nucleus boundary key
     void* draw;        // the final draw's own workspace (launch_final_draw)
     RowStats* stats;   // top-p: exact nucleus statistics of flagged rows
     u64* seg_hist;     // top-p: coarse histogram per (row, segment)
@@ -1166,6 +1177,7 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
     w.seg_e = (u64*)take(rows * nseg * sizeof(u64));
     w.spec_row = (int*)take((size_t)num_seqs * sizeof(int));
     w.spec_x = (int*)take((size_t)num_seqs * sizeof(int));
+    w.spec_key = (unsigned int*)take((size_t)num_seqs * sizeof(unsigned int));
     w.draw = take(final_draw_workspace_bytes(num_seqs, vocab));
     if (topp) {
         w.stats = (RowStats*)take(rows * sizeof(RowStats));
@@ -1232,7 +1244,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                                                              inv_t, n_drafts, w.seg_max,     \
                                                                              w.seg_e, nullptr);              \
     }                                                                                                        \
-    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x);
+    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x, w.spec_key);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_REJ(GG_DTYPE_BF16) break;
@@ -1255,6 +1267,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     d.draft_probs = q;
     d.spec_row = w.spec_row;
     d.spec_x = w.spec_x;
+    d.spec_key = w.spec_key;
     d.seg_max = w.seg_max;
     d.nseg_max = nseg;
     d.out_tok = out_tok;

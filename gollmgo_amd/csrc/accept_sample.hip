@@ -62,6 +62,12 @@ struct RowInfo {
     double tot;               // the kept e summed (the nucleus mass with top-p)
     int row;                  // row of the sequence drawn from
     int x;                    // residual draw: the rejected draft (excluded); -1: plain draw
+    int cbin;                 // the coarse bin the gather launch collects (-1: none)
+    int need;                 // top-k: how many of that bin's elements the filter keeps
+    double above;             // histogram mass of the bins above cbin (top-p without top-k)
+    double S;                 // top-p without top-k: the row's e summed
+    int kept_pass;            // the kept launch computes the draw's segment sums
+    int pregather;            // cbin known before the pass (a hint), which gathers it
 };
 
 struct Ent {                  // exact path sort entry, ordered by (hi, lo) descending
@@ -69,7 +75,7 @@ struct Ent {                  // exact path sort entry, ordered by (hi, lo) desc
 };
 
 struct Layout {
-    size_t state, info, hcnt, hmass, segsum, segkept, exact, total;
+    size_t state, info, hcnt, hmass, segsum, segkept, segabove, ncand, cand, exact, total;
     size_t slot_bytes, vpad, npow;
 };
 
@@ -93,6 +99,9 @@ struct DrawParams {
     double* hmass;
     double* segsum;
     double* segkept;
+    double* segabove;         // per segment: e summed over the bins above cbin
+    int* ncand;               // per sequence: elements of cbin gathered
+    unsigned long long* cand; // per sequence: kCap gathered keys
     int32_t* out_tok;
 };
 
@@ -108,6 +117,9 @@ Layout layout(int B, int V) {
     L.hmass = o;   o = align256(o + (size_t)B * kBins * sizeof(double));
     L.segsum = o;  o = align256(o + (size_t)B * nseg * sizeof(double));
     L.segkept = o; o = align256(o + (size_t)B * nseg * sizeof(double));
+    L.segabove = o; o = align256(o + (size_t)B * nseg * sizeof(double));
+    L.ncand = o;   o = align256(o + (size_t)B * sizeof(int));
+    L.cand = o;    o = align256(o + (size_t)B * kCap * sizeof(unsigned long long));
     L.vpad = ((size_t)V + 63) & ~(size_t)63;
     size_t np = kChunk;
     while (np < (size_t)V) np <<= 1;
@@ -144,14 +156,18 @@ __device__ __forceinline__ double exp_term(float l, double inv_t, double m) {
     return gg_exp64(v - m);
 }
 
-// The parallel path's exponential (gg_fast_exp64, gg_exp64.h): within 2e-14 relative of
+// The parallel path's exponential (gg_fast_exp64_tab, gg_exp64.h): within 2e-14 relative of
 // gg_exp64; the margins count 1e-12. Nothing the rule decides depends on its bits, only sums
 // that clear a margin.
 constexpr double kFastExpErr = 1e-12;
-__device__ __forceinline__ double fast_exp64(double x) { return gg_fast_exp64(x); }
-__device__ __forceinline__ double fast_term(float l, double inv_t, double m) {
+__device__ __forceinline__ double fast_term(float l, double inv_t, double m, const double* tab) {
     const double v = (double)l * inv_t;
-    return fast_exp64(v - m);  // -inf logits give -inf, hence 0
+    return gg_fast_exp64_tab(v - m, tab);  // -inf logits give -inf, hence 0
+}
+// Each block's copy of the exponential's table (64 doubles in LDS).
+__device__ __forceinline__ void load_exp_table(double* s_tab) {
+    if (threadIdx.x < 64) s_tab[threadIdx.x] = gg_exp64((double)threadIdx.x * (6.93147180559945286227e-01 / 64.0));
+    __syncthreads();
 }
 
 // Eight consecutive elements e0.. of a row as floats: one 16-byte load (two for f32) when
@@ -197,9 +213,9 @@ __device__ __forceinline__ double clean_q(float q) {
 // The draw's weight of element e (logit l): its e if kept (plain draw, e units), or its
 // residual max(0, e/tot - q) (probability units; 0 at the rejected draft).
 __device__ __forceinline__ double draw_weight(const DrawParams& P, const RowInfo& ri, const float* qr, float l,
-                                              int e) {
+                                              int e, const double* tab) {
     if (comp_key(order_key(l), e) < ri.cut) return 0.0;
-    const double ev = fast_term(l, P.inv_t, ri.m);
+    const double ev = fast_term(l, P.inv_t, ri.m, tab);
     if (ri.x < 0) return ev;
     if (e == ri.x) return 0.0;
     const double p = ev / ri.tot;
@@ -278,7 +294,7 @@ __device__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* sh, uint32_t* tota
 __global__ void __launch_bounds__(256) sample_prep_kernel(
     DrawParams P, const float2* __restrict__ gws, const float* __restrict__ seg_max, int nseg_m,
     const int32_t* __restrict__ n_drafts, const int32_t* __restrict__ acc, const int* __restrict__ spec_row,
-    const int* __restrict__ spec_x, int force_exact) {
+    const int* __restrict__ spec_x, const unsigned int* __restrict__ spec_key, int force_exact) {
     const int b = blockIdx.x;
     const int K = P.K, R = K + 1;
     int row, x = -1;
@@ -293,7 +309,9 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
         if (threadIdx.x == 0) P.state[b] = ST_NONE;
         return;
     }
-    if (P.filtered)
+    // top-p alone with a hint of the cut's order key: the pass gathers that bin itself
+    const unsigned int hint = (P.use_p && !P.use_k && spec_key) ? spec_key[b] : 0u;
+    if (P.filtered && hint == 0)
         for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
             P.hcnt[(size_t)b * kBins + i] = 0;
             P.hmass[(size_t)b * kBins + i] = 0.0;
@@ -331,6 +349,16 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             ri.tot = 0.0;
             ri.row = row;
             ri.x = x;
+            ri.cbin = -1;
+            ri.need = 0;
+            ri.above = 0.0;
+            ri.S = 0.0;
+            ri.kept_pass = 0;
+            ri.pregather = hint != 0;
+            if (hint != 0) {
+                ri.cbin = (int)(hint >> 20);
+                P.ncand[b] = 0;
+            }
             P.info[b] = ri;
             P.state[b] = st;
         }
@@ -346,7 +374,8 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
 // residual total within a few margins of 0 may be 0 in the rule, whose fallbacks then
 // apply. Undecided: the row is left to the literal rule.
 template <gg_dtype_t DT>
-__device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, const double* sums) {
+__device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, const double* sums,
+                              const double* s_tab) {
     __shared__ double s_red[16];
     __shared__ int s_seg, s_tok, s_bad;
     __shared__ double s_base, s_tot;
@@ -396,7 +425,7 @@ __device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, con
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int e = e0 + q;
-        ev[q] = e < P.V ? draw_weight(P, ri, qr, xl[q >> 3][q & 7], e) : 0.0;
+        ev[q] = e < P.V ? draw_weight(P, ri, qr, xl[q >> 3][q & 7], e, s_tab) : 0.0;
         loc += ev[q];
     }
     double btot;
@@ -420,6 +449,38 @@ __device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, con
 
 // Per (segment, sequence): e of every element (the parallel exponential), the segment's
 // sum, the NaN / +inf check, and with top-k / top-p the coarse histograms.
+// Stage the elements of one coarse bin found by a block in LDS, one counter update per wave.
+constexpr int kBlockCap = 2048;  // a segment's hits staged in LDS; more: the row goes exact
+__device__ __forceinline__ void stage_hit(bool hit, unsigned long long comp, int* s_cnt, unsigned long long* s_buf) {
+    const int lane = threadIdx.x & 63;
+    const unsigned long long mask = __ballot(hit);
+    if (mask) {
+        int base = 0;
+        const int leader = __ffsll((long long)mask) - 1;
+        if (lane == leader) base = atomicAdd(s_cnt, __popcll(mask));
+        base = __shfl(base, leader);
+        if (hit) {
+            const int slot = base + __popcll(mask & ((1ull << lane) - 1ull));
+            if (slot < kBlockCap) s_buf[slot] = comp;
+        }
+    }
+}
+// The staged elements appended to the sequence's list (one global update per block; an
+// overflow forces the count past kCap, so the row goes exact).
+__device__ __forceinline__ void flush_hits(const DrawParams& P, int b, int* s_cnt, int* s_base,
+                                           const unsigned long long* s_buf) {
+    __syncthreads();
+    const int n = *s_cnt;
+    if (threadIdx.x == 0 && n > 0) *s_base = atomicAdd(&P.ncand[b], n > kBlockCap ? kCap + 1 : n);
+    __syncthreads();
+    if (n > 0 && n <= kBlockCap)
+        for (int i = threadIdx.x; i < n; i += blockDim.x)
+            if (*s_base + i < kCap) P.cand[(size_t)b * kCap + *s_base + i] = s_buf[i];
+}
+
+// Per (segment, sequence): e of every element (the parallel exponential), the segment's
+// sum, the NaN / +inf check, and with top-k / top-p the coarse histograms — or, when the
+// cut's bin is known beforehand, that bin's elements and the sum of e above it.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) {
     const int b = blockIdx.y, seg = blockIdx.x;
@@ -427,10 +488,15 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
     __shared__ uint32_t s_cnt[kBins];
     __shared__ double s_mass[kBins];
     __shared__ double s_red[16];
-    const int want_cnt = P.use_k, want_mass = P.filtered;
+    __shared__ double s_tab[64];
+    __shared__ int s_hits, s_base;
+    unsigned long long* s_buf = (unsigned long long*)s_mass;  // pregather: the staging buffer
+    load_exp_table(s_tab);
+    const RowInfo ri = P.info[b];
+    const bool pre = ri.pregather;
+    const int want_cnt = P.use_k && !pre, want_mass = P.filtered && !pre;
     const int V = P.V;
     const double inv_t = P.inv_t;
-    const RowInfo ri = P.info[b];
     const void* row = drawn_row(P, b, ri.row);
     const double m = ri.m;
     if (want_cnt || want_mass) {
@@ -438,23 +504,28 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
             s_cnt[i] = 0;
             s_mass[i] = 0.0;
         }
-        __syncthreads();
     }
-    double acc = 0.0;
+    if (threadIdx.x == 0) s_hits = 0;
+    __syncthreads();
+    double acc = 0.0, above = 0.0;
     int bad = 0;
-    for (int c = threadIdx.x; c < kSeg / 8; c += blockDim.x) {
-        const int e0 = seg * kSeg + c * 8;
-        if (e0 >= V) break;
+    for (int c0 = 0; c0 < kSeg / 8; c0 += blockDim.x) {
+        const int e0 = seg * kSeg + (c0 + threadIdx.x) * 8;
         float x[8];
         load8<DT>(row, V, e0, P.vec, x);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const float l = x[k];
-            if (l != l || l == INFINITY) bad = 1;
-            const double ev = (l != l || l == INFINITY) ? 0.0 : fast_term(l, inv_t, m);
+            const bool in = e0 + k < V;
+            if (in && (l != l || l == INFINITY)) bad = 1;
+            const double ev = (!in || l != l || l == INFINITY) ? 0.0 : fast_term(l, inv_t, m, s_tab);
             acc += ev;
-            if ((want_cnt || want_mass) && e0 + k < V) {
-                const int bin = (int)(order_key(l) >> 20);
+            const uint32_t key = order_key(l);
+            const int bin = (int)(key >> 20);
+            if (pre) {
+                if (in && bin > ri.cbin) above += ev;
+                stage_hit(in && bin == ri.cbin, comp_key(key, e0 + k), &s_hits, s_buf);
+            } else if ((want_cnt || want_mass) && in) {
                 if (want_cnt) atomicAdd(&s_cnt[bin], 1u);
                 if (want_mass && ev != 0.0) atomicAdd(&s_mass[bin], ev);
             }
@@ -466,6 +537,12 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
     }
     const double tot = block_sum(acc, s_red);
     if (threadIdx.x == 0) P.segsum[(size_t)b * P.nseg + seg] = tot;
+    if (pre) {
+        const double ab = block_sum(above, s_red);
+        if (threadIdx.x == 0) P.segabove[(size_t)b * P.nseg + seg] = ab;
+        flush_hits(P, b, &s_hits, &s_base, s_buf);
+        return;
+    }
     if (want_cnt || want_mass) {
         for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
             if (want_cnt && s_cnt[i]) atomicAdd(&P.hcnt[(size_t)b * kBins + i], s_cnt[i]);
@@ -604,53 +681,63 @@ __device__ unsigned long long next_below(const unsigned long long* s_comp, int n
     return r;
 }
 
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kRowThreads) sample_select_kernel(DrawParams P) {
+// Select, first part (one block per sequence): from the coarse histograms, the bin the
+// gather launch collects — the top-k threshold bin, or without top-k the nucleus cut's bin
+// and the histogram mass above it. Without filters (a residual draw) only the row's total.
+__global__ void __launch_bounds__(kRowThreads) sample_select1_kernel(DrawParams P) {
     const int b = blockIdx.x;
-    int* __restrict__ state = P.state;
-    if (state[b] != ST_DRAW) return;
-    const int V = P.V, nseg = P.nseg, top_k = P.top_k, use_p = P.use_p;
-    const double inv_t = P.inv_t, top_p = P.top_p, tau = P.tau;
-    const gg_dtype_t dt = P.dt;
-    const uint32_t* __restrict__ hcnt = P.hcnt;
-    const double* __restrict__ hmass = P.hmass;
-    const double* __restrict__ segsum = P.segsum;
-    RowInfo* __restrict__ info = P.info;
-    __shared__ double s_mass[kBins];
-    __shared__ unsigned long long s_comp[kCap];
-    __shared__ double s_e[kCap];
-    __shared__ double s_h[257];
+    if (P.state[b] != ST_DRAW) return;
     __shared__ double s_red[16];
     __shared__ uint32_t s_redu[16];
-    __shared__ unsigned long long s_u[16];
-    __shared__ int s_n, s_bin, s_i;
+    __shared__ int s_bin;
     __shared__ double s_above;
     __shared__ uint32_t s_cabove;
-    const void* row = drawn_row(P, b, info[b].row);
-    const double m = info[b].m;
-    const bool use_k = P.use_k;
     const int per = kBins / kRowThreads;  // bins per thread, positions counted from the top bin
-    if (P.filtered)
-        for (int i = threadIdx.x; i < kBins; i += blockDim.x) s_mass[i] = hmass[(size_t)b * kBins + i];
-    __syncthreads();
-
-    unsigned long long cut = 0, tk = 0;
-    double S;
-    int kbin = -1, nk = 0;  // top-k: the threshold bin and its gathered items (in s_comp / s_e)
-    if (use_k) {
+    const int nseg = P.nseg;
+    RowInfo* info = P.info;
+    if (info[b].pregather) {  // the pass gathered the hinted bin and summed e above it
+        double sv = 0.0, av = 0.0;
+        for (int i = threadIdx.x; i < nseg; i += blockDim.x) {
+            sv += P.segsum[(size_t)b * nseg + i];
+            av += P.segabove[(size_t)b * nseg + i];
+        }
+        const double S = block_sum(sv, s_red);
+        const double A = block_sum(av, s_red);
+        if (threadIdx.x == 0) {
+            info[b].S = S;
+            info[b].above = A;
+        }
+        return;
+    }
+    if (threadIdx.x == 0) P.ncand[b] = 0;
+    if (!P.filtered) {  // a residual draw without filters: the total of the pass
+        double sv = 0.0;
+        for (int i = threadIdx.x; i < nseg; i += blockDim.x) {
+            const double v = P.segsum[(size_t)b * nseg + i];
+            sv += v;
+            P.segkept[(size_t)b * nseg + i] = v;
+        }
+        const double S = block_sum(sv, s_red);
+        if (threadIdx.x == 0) {
+            info[b].tot = S;
+            info[b].kept_pass = P.q != nullptr;  // dense q: the residual needs its own sums
+        }
+        return;
+    }
+    if (P.use_k) {
         // The bin where the count from the top first reaches k.
         uint32_t c = 0;
-        for (int q = 0; q < per; ++q) c += hcnt[(size_t)b * kBins + (kBins - 1 - (threadIdx.x * per + q))];
+        for (int q = 0; q < per; ++q) c += P.hcnt[(size_t)b * kBins + (kBins - 1 - (threadIdx.x * per + q))];
         uint32_t tot;
-        uint32_t before = block_excl_scan_u32(c, s_redu, &tot);
+        const uint32_t before = block_excl_scan_u32(c, s_redu, &tot);
         if (threadIdx.x == 0) s_bin = -1;
         __syncthreads();
-        if (before < (uint32_t)top_k && before + c >= (uint32_t)top_k) {
+        if (before < (uint32_t)P.top_k && before + c >= (uint32_t)P.top_k) {
             uint32_t run = before;
             for (int q = 0; q < per; ++q) {
                 const int bin = kBins - 1 - (threadIdx.x * per + q);
-                const uint32_t cq = hcnt[(size_t)b * kBins + bin];
-                if (run + cq >= (uint32_t)top_k) {
+                const uint32_t cq = P.hcnt[(size_t)b * kBins + bin];
+                if (run + cq >= (uint32_t)P.top_k) {
                     s_bin = bin;
                     s_cabove = run;
                     break;
@@ -659,113 +746,249 @@ __global__ void __launch_bounds__(kRowThreads) sample_select_kernel(DrawParams P
             }
         }
         __syncthreads();
-        kbin = s_bin;
-        if (kbin < 0) {  // fewer counted elements than k: cannot happen for a clean row
-            if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-            return;
+        if (threadIdx.x == 0) {
+            if (s_bin < 0) atomicOr(&P.state[b], ST_EXACT);  // fewer counted elements than k
+            info[b].cbin = s_bin;
+            info[b].need = P.top_k - (int)s_cabove;
         }
-        const int need = top_k - (int)s_cabove;
-        nk = gather_bin<DT>(row, V, P.vec, kbin, inv_t, m, s_comp, s_e, &s_n);
+        return;
+    }
+    // top-p alone: the bin where the mass from the top first reaches p * S.
+    double sv = 0.0;
+    for (int i = threadIdx.x; i < nseg; i += blockDim.x) sv += P.segsum[(size_t)b * nseg + i];
+    const double S = block_sum(sv, s_red);
+    const double pS = P.top_p * S;
+    double c = 0.0;
+    for (int q = 0; q < per; ++q) c += P.hmass[(size_t)b * kBins + kBins - 1 - (threadIdx.x * per + q)];
+    double tot;
+    const double before = block_excl_scan(c, s_red, &tot);
+    // Rounding can let two neighbouring threads both see the crossing; the first in order
+    // wins (atomicMax on the bin) and only its owner writes the mass above it.
+    if (threadIdx.x == 0) s_bin = -1;
+    __syncthreads();
+    double run = before;
+    int mine = -1;
+    double mine_above = 0.0;
+    if (before < pS && before + c >= pS) {
+        for (int q = 0; q < per; ++q) {
+            const int bin = kBins - 1 - (threadIdx.x * per + q);
+            const double mq = P.hmass[(size_t)b * kBins + bin];
+            if (run + mq >= pS) {
+                mine = bin;
+                mine_above = run;
+                break;
+            }
+            run += mq;
+        }
+        if (mine >= 0) atomicMax(&s_bin, mine);
+    }
+    __syncthreads();
+    if (mine >= 0 && mine == s_bin) s_above = mine_above;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (s_bin < 0) atomicOr(&P.state[b], ST_EXACT);  // p * S at the very end: rounding decides
+        info[b].cbin = s_bin;
+        info[b].above = s_above;
+        info[b].S = S;
+    }
+}
+
+// Gather (per segment and sequence): the elements of bin cbin appended to the sequence's
+// list (one counter update per wave), and the e of the elements above that bin summed
+// per segment.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) sample_gather_kernel(DrawParams P) {
+    const int b = blockIdx.y, seg = blockIdx.x;
+    if (P.state[b] != ST_DRAW) return;
+    const RowInfo ri = P.info[b];
+    if (ri.cbin < 0 || ri.pregather) return;
+    __shared__ double s_red[16];
+    __shared__ unsigned long long s_buf[kBlockCap];
+    __shared__ int s_cnt, s_base;
+    __shared__ double s_tab[64];
+    load_exp_table(s_tab);
+    const void* row = drawn_row(P, b, ri.row);
+    if (threadIdx.x == 0) s_cnt = 0;
+    __syncthreads();
+    double acc = 0.0;
+    for (int c0 = 0; c0 < kSeg / 8; c0 += blockDim.x) {
+        const int e0 = seg * kSeg + (c0 + threadIdx.x) * 8;
+        float x[8];
+        load8<DT>(row, P.V, e0, P.vec, x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int e = e0 + k;
+            const uint32_t key = order_key(x[k]);
+            const int bin = (int)(key >> 20);
+            const bool in = e < P.V;
+            if (in && bin > ri.cbin) acc += fast_term(x[k], P.inv_t, ri.m, s_tab);
+            stage_hit(in && bin == ri.cbin, comp_key(key, e), &s_cnt, s_buf);
+        }
+    }
+    flush_hits(P, b, &s_cnt, &s_base, s_buf);
+    const double tot = block_sum(acc, s_red);
+    if (threadIdx.x == 0) P.segabove[(size_t)b * P.nseg + seg] = tot;
+}
+
+// Select, second part (one block per sequence): the gathered bin resolved in LDS — the
+// top-k threshold and/or the nucleus cut — with the margins, then the draw's segment sums
+// (the mass above the bin plus the bin's kept elements), unless the kept launch has to
+// compute them.
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams P) {
+    const int b = blockIdx.x;
+    int* __restrict__ state = P.state;
+    if (state[b] != ST_DRAW) return;
+    RowInfo ri = P.info[b];
+    if (ri.cbin < 0) return;
+    const int V = P.V, nseg = P.nseg;
+    const double inv_t = P.inv_t, tau = P.tau, m = ri.m;
+    __shared__ double s_mass[kBins];
+    __shared__ unsigned long long s_comp[kCap];
+    __shared__ double s_e[kCap];
+    __shared__ double s_h[257];
+    __shared__ double s_red[16];
+    __shared__ unsigned long long s_u[16];
+    __shared__ double s_segk[64];
+    __shared__ double s_tab[64];
+    __shared__ int s_n, s_bin, s_i, s_ok;
+    load_exp_table(s_tab);
+    __shared__ double s_above;
+    const void* row = drawn_row(P, b, ri.row);
+    const int per = kBins / kRowThreads;
+    int ng = P.ncand[b];
+    if (ng > kCap) {  // a crowded bin: the literal rule decides
+        if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
+        return;
+    }
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+        s_comp[i] = P.cand[(size_t)b * kCap + i];
+        s_e[i] = exp_term(key_value((uint32_t)(s_comp[i] >> 32)), inv_t, m);
+    }
+    if (threadIdx.x == 0) s_ok = 1;
+    __syncthreads();
+
+    unsigned long long cut = 0, tk = 0;
+    double tot = 0.0;
+    int cbin = ri.cbin;  // the bin whose kept elements complete the segment sums
+    if (P.use_k) {
         double dummy;
-        const int ck = nk < need ? -1 : select_desc(s_comp, s_e, nk, (double)need, false, &dummy, s_h, s_red, &s_i);
-        if (ck < 0) {  // more than kCap elements in the bin (or a count mismatch)
+        const int ck = ng < ri.need ? -1 : select_desc(s_comp, s_e, ng, (double)ri.need, false, &dummy, s_h, s_red, &s_i);
+        if (ck < 0) {
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
             return;
         }
         tk = s_comp[ck];
         cut = tk;
         double part = 0.0, above = 0.0;
-        for (int i = threadIdx.x; i < nk; i += blockDim.x)
+        for (int i = threadIdx.x; i < ng; i += blockDim.x)
             if (s_comp[i] >= tk) part += s_e[i];
-        for (int i = kbin + 1 + threadIdx.x; i < kBins; i += blockDim.x) above += s_mass[i];
+        for (int i = ri.cbin + 1 + threadIdx.x; i < kBins; i += blockDim.x) above += P.hmass[(size_t)b * kBins + i];
         part = block_sum(part, s_red);
         above = block_sum(above, s_red);
-        S = above + part;
-        // Kept mass per bin: bins above the threshold bin whole, that bin in part, none below.
-        for (int i = threadIdx.x; i < kbin; i += blockDim.x) s_mass[i] = 0.0;
-        if (threadIdx.x == 0) s_mass[kbin] = part;
-        __syncthreads();
-    } else {
-        double s = 0.0;
-        for (int i = threadIdx.x; i < nseg; i += blockDim.x) s += segsum[(size_t)b * nseg + i];
-        S = block_sum(s, s_red);
-    }
-
-    if (use_p) {
-        const double pS = top_p * S;
-        // The bin where the kept mass from the top first reaches p * S.
-        double c = 0.0;
-        for (int q = 0; q < per; ++q) c += s_mass[kBins - 1 - (threadIdx.x * per + q)];
-        double tot;
-        const double before = block_excl_scan(c, s_red, &tot);
-        // Rounding can let two neighbouring threads both see the crossing; the first in
-        // order wins (atomicMax on the bin) and only its owner writes the mass above it.
-        if (threadIdx.x == 0) s_bin = -1;
-        __syncthreads();
-        double run = before;
-        int mine = -1;
-        double mine_above = 0.0;
-        if (before < pS && before + c >= pS) {
-            for (int q = 0; q < per; ++q) {
-                const int bin = kBins - 1 - (threadIdx.x * per + q);
-                const double mq = s_mass[bin];
-                if (run + mq >= pS) {
-                    mine = bin;
-                    mine_above = run;
-                    break;
+        tot = above + part;
+        if (P.use_p) {
+            const double S = tot, pS = P.top_p * S;
+            // Kept mass per bin: bins above the threshold bin whole, that bin in part.
+            for (int i = threadIdx.x; i < kBins; i += blockDim.x)
+                s_mass[i] = i > ri.cbin ? P.hmass[(size_t)b * kBins + i] : (i == ri.cbin ? part : 0.0);
+            __syncthreads();
+            double c = 0.0;
+            for (int q = 0; q < per; ++q) c += s_mass[kBins - 1 - (threadIdx.x * per + q)];
+            double btot;
+            const double before = block_excl_scan(c, s_red, &btot);
+            if (threadIdx.x == 0) s_bin = -1;
+            __syncthreads();
+            double run = before;
+            int mine = -1;
+            double mine_above = 0.0;
+            if (before < pS && before + c >= pS) {
+                for (int q = 0; q < per; ++q) {
+                    const int bin = kBins - 1 - (threadIdx.x * per + q);
+                    const double mq = s_mass[bin];
+                    if (run + mq >= pS) {
+                        mine = bin;
+                        mine_above = run;
+                        break;
+                    }
+                    run += mq;
                 }
-                run += mq;
+                if (mine >= 0) atomicMax(&s_bin, mine);
             }
-            if (mine >= 0) atomicMax(&s_bin, mine);
-        }
-        __syncthreads();
-        if (mine >= 0 && mine == s_bin) s_above = mine_above;
-        __syncthreads();
-        const int pbin = s_bin;
-        if (pbin < 0) {  // p * S at the very end of the mass: the rounding decides
-            if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-            return;
-        }
-        const double above = s_above;
-        int np = nk;
-        if (!(use_k && pbin == kbin)) {
-            np = gather_bin<DT>(row, V, P.vec, pbin, inv_t, m, s_comp, s_e, &s_n);
-            if (np < 0) {
+            __syncthreads();
+            if (mine >= 0 && mine == s_bin) s_above = mine_above;
+            __syncthreads();
+            const int pbin = s_bin;
+            if (pbin < 0) {
                 if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
                 return;
             }
+            if (pbin != ri.cbin) {
+                // The cut lies above the threshold bin: that bin's elements (one block gathers
+                // them), and the kept launch computes the segment sums.
+                ng = gather_bin<DT>(row, V, P.vec, pbin, inv_t, m, s_comp, s_e, &s_n);
+                if (ng < 0) {
+                    if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
+                    return;
+                }
+                ri.kept_pass = 1;
+                cbin = pbin;
+            }
+            ri.above = s_above;
+            ri.S = S;
         }
+    }
+    if (P.use_p) {
+        const double S = ri.S, pS = P.top_p * S, above = ri.above;
         // The cut: the first item (value desc, index asc) whose running mass reaches p * S.
         double inbin = 0.0;
-        const int ci = select_desc(s_comp, s_e, np, pS - above, true, &inbin, s_h, s_red, &s_i);
+        const int ci = select_desc(s_comp, s_e, ng, pS - above, true, &inbin, s_h, s_red, &s_i);
         if (ci < 0) {
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
             return;
         }
         const unsigned long long cc = s_comp[ci];
-        const unsigned long long nb = next_below(s_comp, np, cc, s_u);
+        const unsigned long long nb = next_below(s_comp, ng, cc, s_u);
         if (threadIdx.x == 0) {
             const double A = above + inbin, ec = s_e[ci];
             bool ok = (pS - A) > tau * S && (A + ec - pS) > tau * S;
-            if (use_k && cc < tk) ok = false;  // past the top-k set: only rounding gets here
+            if (P.use_k && cc < tk) ok = false;  // past the top-k set: only rounding gets here
             // An element after the cut with the same probability but another value would come
             // first in the rule's (probability desc, index asc) order if its index is lower.
-            if (nb != 0 && !(use_k && nb < tk)) {
+            if (nb != 0 && !(P.use_k && nb < tk)) {
                 const double en = exp_term(key_value((uint32_t)(nb >> 32)), inv_t, m);
                 if (en == ec && (nb >> 32) != (cc >> 32)) ok = false;
-            } else if (nb == 0 && !(use_k && pbin == kbin) && pbin > 0) {
-                const double e_edge = exp_term(key_value(((uint32_t)pbin << 20) - 1u), inv_t, m);
+            } else if (nb == 0 && !(P.use_k && cbin == ri.cbin) && cbin > 0) {
+                const double e_edge = exp_term(key_value(((uint32_t)cbin << 20) - 1u), inv_t, m);
                 if (e_edge >= ec) ok = false;
             }
-            if (!ok) atomicOr(&state[b], ST_EXACT);
-            info[b].cut = cc;
-            info[b].tot = A + ec;
+            if (!ok) {
+                atomicOr(&state[b], ST_EXACT);
+                s_ok = 0;
+            }
+            s_above = A + ec;
         }
-        return;
+        __syncthreads();
+        cut = cc;
+        tot = s_above;
+    }
+    if (!s_ok) return;
+    if (P.q && ri.x >= 0) ri.kept_pass = 1;  // dense residual weights need the kept launch
+    if (!ri.kept_pass) {
+        // segment sums: the bins above cbin (gather launch) plus cbin's kept elements
+        for (int i = threadIdx.x; i < nseg; i += blockDim.x) s_segk[i] = P.segabove[(size_t)b * nseg + i];
+        __syncthreads();
+        for (int i = threadIdx.x; i < ng; i += blockDim.x)
+            if (s_comp[i] >= cut)
+                atomicAdd(&s_segk[comp_index(s_comp[i]) / kSeg],
+                          fast_term(key_value((uint32_t)(s_comp[i] >> 32)), inv_t, m, s_tab));
+        __syncthreads();
+        for (int i = threadIdx.x; i < nseg; i += blockDim.x) P.segkept[(size_t)b * nseg + i] = s_segk[i];
     }
     if (threadIdx.x == 0) {
-        info[b].cut = cut;
-        info[b].tot = S;
+        P.info[b].cut = cut;
+        P.info[b].tot = tot;
+        P.info[b].kept_pass = ri.kept_pass;
     }
 }
 
@@ -778,6 +1001,9 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
     if (P.state[b] != ST_DRAW) return;
     __shared__ double s_red[16];
     const RowInfo ri = P.info[b];
+    if (!ri.kept_pass) return;
+    __shared__ double s_tab[64];
+    load_exp_table(s_tab);
     const void* row = drawn_row(P, b, ri.row);
     const float* qr = q_row(P, b, ri);
     double acc = 0.0;
@@ -788,7 +1014,7 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
         load8<DT>(row, P.V, e0, P.vec, x);
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-            if (e0 + k < P.V) acc += draw_weight(P, ri, qr, x[k], e0 + k);
+            if (e0 + k < P.V) acc += draw_weight(P, ri, qr, x[k], e0 + k, s_tab);
     }
     const double tot = block_sum(acc, s_red);
     if (threadIdx.x == 0) P.segkept[(size_t)b * P.nseg + seg] = tot;
@@ -797,13 +1023,30 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
 // ------------------------------------------------------------------------ draw
 
 // One block per sequence: the draw over the segment sums of the pass (a plain draw without
-// filters) or of the kept launch.
+// filters) or of the kept e (select or the kept launch). A one-hot residual whose sums are
+// kept e takes them as (kept e - e of the rejected draft) / total, its weights r = e / total.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P, int use_segsum) {
     const int b = blockIdx.x;
     if (P.state[b] != ST_DRAW) return;
+    __shared__ double s_sums[64];
+    __shared__ double s_tab[64];
+    load_exp_table(s_tab);
     const RowInfo ri = P.info[b];
-    draw_in_block<DT>(P, b, ri, (use_segsum ? P.segsum : P.segkept) + (size_t)b * P.nseg);
+    const double* src = (use_segsum ? P.segsum : P.segkept) + (size_t)b * P.nseg;
+    if (ri.x >= 0 && !ri.kept_pass) {
+        if (threadIdx.x < P.nseg) {
+            double v = src[threadIdx.x];
+            if (ri.x < P.V && ri.x / kSeg == (int)threadIdx.x) {
+                const float lx = load_as_f32(drawn_row(P, b, ri.row), P.dt, ri.x);
+                if (comp_key(order_key(lx), ri.x) >= ri.cut) v -= fast_term(lx, P.inv_t, ri.m, s_tab);
+            }
+            s_sums[threadIdx.x] = v / ri.tot;
+        }
+        __syncthreads();
+        src = s_sums;
+    }
+    draw_in_block<DT>(P, b, ri, src, s_tab);
 }
 
 // ----------------------------------------------------------------------- exact
@@ -1111,21 +1354,30 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     P.hmass = (double*)(w + L.hmass);
     P.segsum = (double*)(w + L.segsum);
     P.segkept = (double*)(w + L.segkept);
+    P.segabove = (double*)(w + L.segabove);
+    P.ncand = (int*)(w + L.ncand);
+    P.cand = (unsigned long long*)(w + L.cand);
     P.out_tok = d.out_tok;
     const int force = d.force_exact ? 1 : 0;
     const int nseg_m = d.greedy_seg ? (V + kGreedySeg - 1) / kGreedySeg : d.nseg_max;
     sample_prep_kernel<<<B, 256, 0, s>>>(P, d.greedy_seg, d.seg_max, nseg_m, d.n_drafts, d.accepted, d.spec_row,
-                                         d.spec_x, force);
-    // A plain draw without filters draws from the pass's segment sums; a filtered one needs
-    // the cut (select) and the kept sums per segment (kept), a residual one the kept total
-    // (select) and the residual sums (kept).
+                                         d.spec_x, d.spec_key, force);
+    // A plain draw without filters draws from the pass's segment sums. With filters: the bin
+    // of the cut (select1), its elements and the sums above it (gather), the cut and the
+    // segment sums (select2); the kept launch only for dense residuals and for a nucleus cut
+    // above the top-k bin. A residual draw without filters takes the pass's total (select1).
     const bool residual = d.spec_row != nullptr;
     const bool two_pass = P.filtered || residual;
 #define GG_DRAW(DTV)                                                                                 \
     sample_pass_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                              \
     if (two_pass) {                                                                                  \
-        sample_select_kernel<DTV><<<B, kRowThreads, 0, s>>>(P);                                      \
-        sample_kept_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                          \
+        sample_select1_kernel<<<B, kRowThreads, 0, s>>>(P);                                          \
+        if (P.filtered) {                                                                            \
+            sample_gather_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                    \
+            sample_select2_kernel<DTV><<<B, kRowThreads, 0, s>>>(P);                                 \
+        }                                                                                            \
+        if (P.filtered || P.q)                                                                       \
+            sample_kept_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                      \
     }                                                                                                \
     sample_draw_kernel<DTV><<<B, kSegThreads, 0, s>>>(P, two_pass ? 0 : 1);
     switch (d.dt) {

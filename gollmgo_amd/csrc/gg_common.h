@@ -138,6 +138,7 @@ struct FinalDraw {
     const float2* greedy_seg;
     const int* spec_row;
     const int* spec_x;
+    const unsigned int* spec_key;  // given rows, top-p: an order key near the nucleus cut (0: none)
     const float* seg_max;
     int nseg_max;
     bool force_exact;

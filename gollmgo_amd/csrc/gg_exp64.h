@@ -67,3 +67,25 @@ GG_HD64 double gg_fast_exp64(double x) {
     p = __builtin_fma(p, r, 1.0);
     return __builtin_ldexp(p, (int)kd);
 }
+
+// The same, table-driven: x = n ln2/64 + r (|r| <= ln2/128), e^x = 2^(n>>6) * T[n&63] * p(r),
+// T[j] = gg_exp64(j ln2 / 64), p the degree-5 Taylor polynomial (truncation below 4e-17).
+// About half the operations of gg_fast_exp64; within 2e-14 relative of gg_exp64 on
+// [-745, 0] (tests/test_sampler_oracle.py). 0 below -745.2 and for NaN.
+GG_HD64 void gg_exp64_table(double* tab) {
+    for (int j = 0; j < 64; ++j) tab[j] = gg_exp64((double)j * (6.93147180559945286227e-01 / 64.0));
+}
+GG_HD64 double gg_fast_exp64_tab(double x, const double* tab) {
+    if (!(x >= -745.2)) return 0.0;
+    const double nd = __builtin_rint(x * (64.0 * 1.4426950408889634));
+    double r = __builtin_fma(nd, -6.93147180369123816490e-01 / 64.0, x);
+    r = __builtin_fma(nd, -1.90821492927058770002e-10 / 64.0, r);
+    const int n = (int)nd;
+    double p = 8.3333333333333332e-03;               // 1/5!
+    p = __builtin_fma(p, r, 4.1666666666666664e-02);  // 1/4!
+    p = __builtin_fma(p, r, 1.6666666666666666e-01);  // 1/3!
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    return __builtin_ldexp(tab[n & 63] * p, n >> 6);
+}

@@ -82,7 +82,12 @@ def test_fast_exp64_error_bound(ora, tmp_path):
 #include "gg_exp64.h"
 int main(int argc, char** argv) {
     FILE* f = fopen(argv[1], "rb"); FILE* g = fopen(argv[2], "wb"); double x;
-    while (fread(&x, 8, 1, f) == 1) { double y = gg_fast_exp64(x); fwrite(&y, 8, 1, g); }
+    double tab[64]; gg_exp64_table(tab);
+    int use_tab = argc > 3;
+    while (fread(&x, 8, 1, f) == 1) {
+        double y = use_tab ? gg_fast_exp64_tab(x, tab) : gg_fast_exp64(x);
+        fwrite(&y, 8, 1, g);
+    }
     fclose(f); fclose(g); return 0;
 }
 """)
@@ -91,15 +96,16 @@ int main(int argc, char** argv) {
                     str(exe), "-lm"], check=True)
     rng = np.random.default_rng(3)
     x = np.concatenate([-rng.random(2_000_000) * 708, -rng.random(500_000) * 2, np.linspace(-708, 0, 200_001)])
-    (tmp_path / "x.bin").write_bytes(x.tobytes())
-    subprocess.run([str(exe), str(tmp_path / "x.bin"), str(tmp_path / "y.bin")], check=True)
-    got = np.frombuffer((tmp_path / "y.bin").read_bytes(), np.float64)
     want = ora.exp64(x)
-    rel = np.abs(got - want) / want
-    assert rel.max() < 2e-14, rel.max()
-    (tmp_path / "x.bin").write_bytes(np.array([-745.3, -1000.0, np.nan, -np.inf]).tobytes())
-    subprocess.run([str(exe), str(tmp_path / "x.bin"), str(tmp_path / "y.bin")], check=True)
-    assert (np.frombuffer((tmp_path / "y.bin").read_bytes(), np.float64) == 0).all()
+    for extra in ([], ["tab"]):  # gg_fast_exp64, then the table-driven gg_fast_exp64_tab
+        (tmp_path / "x.bin").write_bytes(x.tobytes())
+        subprocess.run([str(exe), str(tmp_path / "x.bin"), str(tmp_path / "y.bin"), *extra], check=True)
+        got = np.frombuffer((tmp_path / "y.bin").read_bytes(), np.float64)
+        rel = np.abs(got - want) / want
+        assert rel.max() < 2e-14, (extra, rel.max())
+        (tmp_path / "x.bin").write_bytes(np.array([-745.3, -1000.0, np.nan, -np.inf]).tobytes())
+        subprocess.run([str(exe), str(tmp_path / "x.bin"), str(tmp_path / "y.bin"), *extra], check=True)
+        assert (np.frombuffer((tmp_path / "y.bin").read_bytes(), np.float64) == 0).all()
 
 
 def test_top_k_reference_case(ora, golden):
