@@ -174,12 +174,12 @@ gg_status_t launch_accept_greedy(const void* logits, gg_dtype_t dt, int num_seqs
                                  int vocab, const int32_t* drafts, const int32_t* n_drafts,
                                  int32_t* out_acc, int32_t* out_tok, void* ws, hipStream_t s) {
     const int R = max_drafts + 1;
+    if (R > kMaxRows) return fail(GG_ERR_INVALID, "accept_greedy: more than 64 drafts per sequence");
     const int nseg = (vocab + kSeg - 1) / kSeg;
     const size_t eb = dtype_bytes(dt);
     const int vec_ok = ((vocab * eb) % 16 == 0) && (((uintptr_t)logits) % 16 == 0);
     greedy_segment_kernel<<<dim3(nseg, num_seqs * R), kThreads, 0, s>>>(logits, dt, R, vocab, nseg,
                                                                        vec_ok, n_drafts, (float2*)ws);
-    if (R > kMaxRows) return fail(GG_ERR_INVALID, "accept_greedy: more than 64 drafts per sequence");
     greedy_decide_kernel<<<num_seqs, kDecideThreads, 0, s>>>(logits, dt, max_drafts, vocab, nseg, drafts,
                                                  n_drafts, (const float2*)ws, out_acc, out_tok);
     return check_hip(hipGetLastError(), "accept_greedy launch");
