@@ -1115,23 +1115,24 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
 
 // One wave per sequence: the acceptance walk, then what the final draw takes: the row
 // and, after a rejection, the rejected draft (the residual draw excludes it).
-// With top-p the row's exact fixed-point nucleus boundary key goes along (0: none): the
-// float64 cut almost always falls in the same coarse bin, which the draw then gathers in its
-// first pass.
+// With top-p the row's fixed-point nucleus cut goes along as (boundary key << 32 | ~idx_cut)
+// (0: none): the float64 cut is almost always that element, and otherwise almost always in
+// its coarse bin, which the draw gathers in its first pass.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* __restrict__ out_acc,
                                                         int* __restrict__ spec_row, int* __restrict__ spec_x,
-                                                        unsigned int* __restrict__ spec_key) {
+                                                        unsigned long long* __restrict__ spec_key) {
     const int b = blockIdx.x;
     const SeqPlan p = decide_seq<DT>(din, b);
     if (threadIdx.x == 0) {
         out_acc[b] = p.d.accepted;
         spec_row[b] = p.d.row;
         spec_x[b] = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
-        unsigned int key = 0;
+        unsigned long long key = 0;
         if (din.use_topp) {
             const RowStats st = din.stats[(size_t)b * (din.K + 1) + p.d.row];
-            if (st.valid) key = st.lam;
+            if (st.valid && st.lam != 0u)
+                key = ((unsigned long long)st.lam << 32) | (unsigned long long)(~(unsigned int)st.idx_cut);
         }
         spec_key[b] = key;
     }
@@ -1146,7 +1147,7 @@ struct RejWs {
     u64* seg_e;
     int* spec_row;     // the final draw's row per sequence
     int* spec_x;       // the rejected draft of a residual draw, -1 for a plain draw
-    unsigned int* spec_key;  // top-p: the final row's fixed-point nucleus boundary key
+    unsigned long long* spec_key;  // top-p: the final row's fixed-point nucleus cut element
     void* draw;        // the final draw's own workspace (launch_final_draw)
     RowStats* stats;   // top-p: exact nucleus statistics of flagged rows
     u64* seg_hist;     // top-p: coarse histogram per (row, segment)
@@ -1177,7 +1178,7 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
     w.seg_e = (u64*)take(rows * nseg * sizeof(u64));
     w.spec_row = (int*)take((size_t)num_seqs * sizeof(int));
     w.spec_x = (int*)take((size_t)num_seqs * sizeof(int));
-    w.spec_key = (unsigned int*)take((size_t)num_seqs * sizeof(unsigned int));
+    w.spec_key = (unsigned long long*)take((size_t)num_seqs * sizeof(unsigned long long));
     w.draw = take(final_draw_workspace_bytes(num_seqs, vocab));
     if (topp) {
         w.stats = (RowStats*)take(rows * sizeof(RowStats));

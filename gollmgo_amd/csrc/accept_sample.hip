@@ -68,6 +68,7 @@ struct RowInfo {
     double S;                 // top-p without top-k: the row's e summed
     int kept_pass;            // the kept launch computes the draw's segment sums
     int pregather;            // cbin known before the pass (a hint), which gathers it
+    unsigned long long hint;  // the hinted cut element's key (comp_key order), or 0
 };
 
 struct Ent {                  // exact path sort entry, ordered by (hi, lo) descending
@@ -88,7 +89,9 @@ struct DrawParams {
     int top_k;
     double top_p;
     int use_k, use_p, filtered;
+    int hint_mode;            // top-p alone with the caller's cut hints: select1 / gather not launched
     int vec;                  // rows allow 16-byte loads
+    int vec_q;                // so do the draft distributions' rows
     double tau;
     const double* ud;         // uniform of sequence b: ud[b], or else
     const float* uf;          //   uf[b * (K + 1) + K]
@@ -196,6 +199,24 @@ __device__ __forceinline__ void load8(const void* row, int V, int e0, bool vec, 
     for (int k = 0; k < 8; ++k) x[k] = e0 + k < V ? load_as_f32(row, DT, e0 + k) : -INFINITY;
 }
 
+// Eight draft probabilities e0.. of a row (0 past V, or with no row).
+__device__ __forceinline__ void load8q(const float* qr, int V, int e0, bool vec, float (&y)[8]) {
+    if (!qr) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) y[k] = 0.0f;
+        return;
+    }
+    if (vec && e0 + 8 <= V) {
+        const float4 a = *(const float4*)(qr + e0);
+        const float4 c = *(const float4*)(qr + e0 + 4);
+        y[0] = a.x; y[1] = a.y; y[2] = a.z; y[3] = a.w;
+        y[4] = c.x; y[5] = c.y; y[6] = c.z; y[7] = c.w;
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) y[k] = e0 + k < V ? qr[e0 + k] : 0.0f;
+}
+
 __device__ __forceinline__ const void* drawn_row(const DrawParams& P, int b, int row) {
     return (const uint8_t*)P.logits + ((size_t)b * (P.K + 1) + row) * P.V * dtype_bytes(P.dt);
 }
@@ -211,16 +232,25 @@ __device__ __forceinline__ double clean_q(float q) {
     return q > 1.0f ? 1.0 : (double)q;
 }
 // The draw's weight of element e (logit l): its e if kept (plain draw, e units), or its
-// residual max(0, e/tot - q) (probability units; 0 at the rejected draft).
-__device__ __forceinline__ double draw_weight(const DrawParams& P, const RowInfo& ri, const float* qr, float l,
-                                              int e, const double* tab) {
+// residual max(0, e/tot - q) (probability units; 0 at the rejected draft). inv_tot is
+// 1/tot: one more rounding per element, far inside the margins.
+__device__ __forceinline__ double draw_weight(const DrawParams& P, const RowInfo& ri, float q, float l,
+                                              int e, const double* tab, double inv_tot) {
     if (comp_key(order_key(l), e) < ri.cut) return 0.0;
     const double ev = fast_term(l, P.inv_t, ri.m, tab);
     if (ri.x < 0) return ev;
     if (e == ri.x) return 0.0;
-    const double p = ev / ri.tot;
-    const double qv = qr ? clean_q(qr[e]) : 0.0;
+    const double p = ev * inv_tot;
+    const double qv = clean_q(q);
     return p > qv ? p - qv : 0.0;
+}
+
+// The pass's segment sums added in segment order (the row's e total without filters); every
+// kernel that needs it adds them the same way.
+__device__ __forceinline__ double seg_total(const DrawParams& P, int b) {
+    double t = 0.0;
+    for (int s = 0; s < P.nseg; ++s) t += P.segsum[(size_t)b * P.nseg + s];
+    return t;
 }
 
 __device__ __forceinline__ double lane_val(double x, int l) {
@@ -294,7 +324,7 @@ __device__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* sh, uint32_t* tota
 __global__ void __launch_bounds__(256) sample_prep_kernel(
     DrawParams P, const float2* __restrict__ gws, const float* __restrict__ seg_max, int nseg_m,
     const int32_t* __restrict__ n_drafts, const int32_t* __restrict__ acc, const int* __restrict__ spec_row,
-    const int* __restrict__ spec_x, const unsigned int* __restrict__ spec_key, int force_exact) {
+    const int* __restrict__ spec_x, const unsigned long long* __restrict__ spec_key, int force_exact) {
     const int b = blockIdx.x;
     const int K = P.K, R = K + 1;
     int row, x = -1;
@@ -309,9 +339,9 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
         if (threadIdx.x == 0) P.state[b] = ST_NONE;
         return;
     }
-    // top-p alone with a hint of the cut's order key: the pass gathers that bin itself
-    const unsigned int hint = (P.use_p && !P.use_k && spec_key) ? spec_key[b] : 0u;
-    if (P.filtered && hint == 0)
+    // top-p alone with a hint of the cut element: the pass gathers its bin itself
+    const unsigned long long hint = P.hint_mode ? spec_key[b] : 0ull;
+    if (P.filtered && !P.hint_mode)
         for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
             P.hcnt[(size_t)b * kBins + i] = 0;
             P.hmass[(size_t)b * kBins + i] = 0.0;
@@ -343,6 +373,9 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             // the literal rule decides.
             if (!any || !(mx > -INFINITY && mx < INFINITY) || !(m > -INFINITY && m < INFINITY) || force_exact)
                 st |= ST_EXACT;
+            // Hint mode launches no select1 / gather: a row without a hint (the caller's
+            // nucleus kept every finite logit, or was not computed) takes the literal rule.
+            if (P.hint_mode && hint == 0) st |= ST_EXACT;
             RowInfo ri;
             ri.m = m;
             ri.cut = 0;
@@ -353,10 +386,12 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             ri.need = 0;
             ri.above = 0.0;
             ri.S = 0.0;
-            ri.kept_pass = 0;
+            // Without filters only a dense residual needs the kept launch's sums.
+            ri.kept_pass = !P.filtered && P.q && x >= 0;
             ri.pregather = hint != 0;
+            ri.hint = hint;
             if (hint != 0) {
-                ri.cbin = (int)(hint >> 20);
+                ri.cbin = (int)(hint >> 52);
                 P.ncand[b] = 0;
             }
             P.info[b] = ri;
@@ -382,6 +417,7 @@ __device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, con
     const double tau = P.tau;
     const double u = uniform_of(P, b);
     const int nseg = P.nseg;
+    const double inv_tot = 1.0 / ri.tot;
     if (threadIdx.x == 0) {
         double tot = 0.0;
         for (int s = 0; s < nseg; ++s) tot += sums[s];
@@ -419,13 +455,15 @@ __device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, con
     const int e0 = seg * kSeg + threadIdx.x * kPer;
     double ev[kPer];
     double loc = 0.0;
-    float xl[2][8];
+    float xl[2][8], ql[2][8];
     load8<DT>(row, P.V, e0, P.vec, xl[0]);
     load8<DT>(row, P.V, e0 + 8, P.vec, xl[1]);
+    load8q(qr, P.V, e0, P.vec_q, ql[0]);
+    load8q(qr, P.V, e0 + 8, P.vec_q, ql[1]);
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int e = e0 + q;
-        ev[q] = e < P.V ? draw_weight(P, ri, qr, xl[q >> 3][q & 7], e, s_tab) : 0.0;
+        ev[q] = e < P.V ? draw_weight(P, ri, ql[q >> 3][q & 7], xl[q >> 3][q & 7], e, s_tab, inv_tot) : 0.0;
         loc += ev[q];
     }
     double btot;
@@ -681,9 +719,49 @@ __device__ unsigned long long next_below(const unsigned long long* s_comp, int n
     return r;
 }
 
-// Select, first part (one block per sequence): from the coarse histograms, the bin the
-// gather launch collects — the top-k threshold bin, or without top-k the nucleus cut's bin
-// and the histogram mass above it. Without filters (a residual draw) only the row's total.
+// The caller's hinted cut among the gathered items: the lowest key with the hint's order key
+// that is >= the hint (the ties the hint keeps), i.e. the hint itself, or the last tie when
+// the hint keeps them all. If the rule's condition holds for it (the mass above it below
+// `target`, with it at least `target`), returns its position and, through before, the mass
+// above it; otherwise -1 and the radix descent decides.
+__device__ int hint_cut(const unsigned long long* s_comp, const double* s_e, int ng, unsigned long long h,
+                        double target, double* before, double* s_red, unsigned long long* s_u, int* s_i) {
+    unsigned long long best = ~0ull;
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+        const unsigned long long v = s_comp[i];
+        if ((v >> 32) == (h >> 32) && v >= h && v < best) best = v;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long v = __shfl_xor(best, o);
+        if (v < best) best = v;
+    }
+    if ((threadIdx.x & 63) == 0) s_u[threadIdx.x >> 6] = best;
+    if (threadIdx.x == 0) *s_i = -1;
+    __syncthreads();
+    unsigned long long c = ~0ull;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w)
+        if (s_u[w] < c) c = s_u[w];
+    if (c == ~0ull) {  // the same for every thread
+        __syncthreads();
+        return -1;
+    }
+    double a = 0.0;
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+        const unsigned long long v = s_comp[i];
+        if (v > c) a += s_e[i];
+        else if (v == c) *s_i = i;
+    }
+    const double A = block_sum(a, s_red);  // its barriers publish s_i
+    const int ci = *s_i;
+    __syncthreads();
+    if (ci < 0 || !(A < target && A + s_e[ci] >= target)) return -1;
+    *before = A;
+    return ci;
+}
+
+// Select, first part (one block per sequence, with filters and no hints): from the coarse
+// histograms, the bin the gather launch collects — the top-k threshold bin, or without
+// top-k the nucleus cut's bin and the histogram mass above it.
 __global__ void __launch_bounds__(kRowThreads) sample_select1_kernel(DrawParams P) {
     const int b = blockIdx.x;
     if (P.state[b] != ST_DRAW) return;
@@ -695,35 +773,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select1_kernel(DrawParams 
     const int per = kBins / kRowThreads;  // bins per thread, positions counted from the top bin
     const int nseg = P.nseg;
     RowInfo* info = P.info;
-    if (info[b].pregather) {  // the pass gathered the hinted bin and summed e above it
-        double sv = 0.0, av = 0.0;
-        for (int i = threadIdx.x; i < nseg; i += blockDim.x) {
-            sv += P.segsum[(size_t)b * nseg + i];
-            av += P.segabove[(size_t)b * nseg + i];
-        }
-        const double S = block_sum(sv, s_red);
-        const double A = block_sum(av, s_red);
-        if (threadIdx.x == 0) {
-            info[b].S = S;
-            info[b].above = A;
-        }
-        return;
-    }
     if (threadIdx.x == 0) P.ncand[b] = 0;
-    if (!P.filtered) {  // a residual draw without filters: the total of the pass
-        double sv = 0.0;
-        for (int i = threadIdx.x; i < nseg; i += blockDim.x) {
-            const double v = P.segsum[(size_t)b * nseg + i];
-            sv += v;
-            P.segkept[(size_t)b * nseg + i] = v;
-        }
-        const double S = block_sum(sv, s_red);
-        if (threadIdx.x == 0) {
-            info[b].tot = S;
-            info[b].kept_pass = P.q != nullptr;  // dense q: the residual needs its own sums
-        }
-        return;
-    }
     if (P.use_k) {
         // The bin where the count from the top first reaches k.
         uint32_t c = 0;
@@ -867,6 +917,15 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
     }
     if (threadIdx.x == 0) s_ok = 1;
     __syncthreads();
+    if (ri.pregather) {  // hint mode: the pass gathered the hinted bin and summed e above it
+        double sv = 0.0, av = 0.0;
+        for (int i = threadIdx.x; i < nseg; i += blockDim.x) {
+            sv += P.segsum[(size_t)b * nseg + i];
+            av += P.segabove[(size_t)b * nseg + i];
+        }
+        ri.S = block_sum(sv, s_red);
+        ri.above = block_sum(av, s_red);
+    }
 
     unsigned long long cut = 0, tk = 0;
     double tot = 0.0;
@@ -942,7 +1001,9 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
         const double S = ri.S, pS = P.top_p * S, above = ri.above;
         // The cut: the first item (value desc, index asc) whose running mass reaches p * S.
         double inbin = 0.0;
-        const int ci = select_desc(s_comp, s_e, ng, pS - above, true, &inbin, s_h, s_red, &s_i);
+        int ci = -1;
+        if (ri.hint != 0 && !P.use_k) ci = hint_cut(s_comp, s_e, ng, ri.hint, pS - above, &inbin, s_red, s_u, &s_i);
+        if (ci < 0) ci = select_desc(s_comp, s_e, ng, pS - above, true, &inbin, s_h, s_red, &s_i);
         if (ci < 0) {
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
             return;
@@ -1000,21 +1061,29 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
     const int b = blockIdx.y, seg = blockIdx.x;
     if (P.state[b] != ST_DRAW) return;
     __shared__ double s_red[16];
-    const RowInfo ri = P.info[b];
+    RowInfo ri = P.info[b];
     if (!ri.kept_pass) return;
+    if (!P.filtered) ri.tot = seg_total(P, b);  // a dense residual without filters
+    const double inv_tot = 1.0 / ri.tot;
     __shared__ double s_tab[64];
     load_exp_table(s_tab);
     const void* row = drawn_row(P, b, ri.row);
     const float* qr = q_row(P, b, ri);
     double acc = 0.0;
-    for (int c = threadIdx.x; c < kSeg / 8; c += blockDim.x) {
-        const int e0 = seg * kSeg + c * 8;
-        if (e0 >= P.V) break;
-        float x[8];
-        load8<DT>(row, P.V, e0, P.vec, x);
+    constexpr int kIt = kSeg / 8 / kSegThreads;  // both chunks' loads issued before the math
+    float x[kIt][8], y[kIt][8];
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+        const int e0 = seg * kSeg + (threadIdx.x + i * kSegThreads) * 8;
+        load8<DT>(row, P.V, e0, P.vec, x[i]);
+        load8q(qr, P.V, e0, P.vec_q, y[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+        const int e0 = seg * kSeg + (threadIdx.x + i * kSegThreads) * 8;
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-            if (e0 + k < P.V) acc += draw_weight(P, ri, qr, x[k], e0 + k, s_tab);
+            if (e0 + k < P.V) acc += draw_weight(P, ri, y[i][k], x[i][k], e0 + k, s_tab, inv_tot);
     }
     const double tot = block_sum(acc, s_red);
     if (threadIdx.x == 0) P.segkept[(size_t)b * P.nseg + seg] = tot;
@@ -1022,18 +1091,20 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
 
 // ------------------------------------------------------------------------ draw
 
-// One block per sequence: the draw over the segment sums of the pass (a plain draw without
-// filters) or of the kept e (select or the kept launch). A one-hot residual whose sums are
-// kept e takes them as (kept e - e of the rejected draft) / total, its weights r = e / total.
+// One block per sequence: the draw over the segment sums of the pass (no filters, unless a
+// dense residual) or of the kept e or residuals (select or the kept launch). A one-hot
+// residual whose sums are kept e takes them as (kept e - e of the rejected draft) / total,
+// its weights r = e / total.
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P, int use_segsum) {
+__global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P) {
     const int b = blockIdx.x;
     if (P.state[b] != ST_DRAW) return;
     __shared__ double s_sums[64];
     __shared__ double s_tab[64];
     load_exp_table(s_tab);
-    const RowInfo ri = P.info[b];
-    const double* src = (use_segsum ? P.segsum : P.segkept) + (size_t)b * P.nseg;
+    RowInfo ri = P.info[b];
+    if (!P.filtered) ri.tot = seg_total(P, b);
+    const double* src = (!P.filtered && !ri.kept_pass ? P.segsum : P.segkept) + (size_t)b * P.nseg;
     if (ri.x >= 0 && !ri.kept_pass) {
         if (threadIdx.x < P.nseg) {
             double v = src[threadIdx.x];
@@ -1337,9 +1408,11 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     P.use_k = d.top_k > 0 && d.top_k < V;
     P.use_p = d.top_p > 0 && d.top_p < 1.0;
     P.filtered = P.use_k || P.use_p;
+    P.hint_mode = d.spec_key && P.use_p && !P.use_k;
     {
         const size_t eb = dtype_bytes(d.dt);
         P.vec = ((size_t)V * eb % 16 == 0) && ((uintptr_t)d.logits % 16 == 0);
+        P.vec_q = (V % 4 == 0) && ((uintptr_t)d.draft_probs % 16 == 0);
     }
     // Bound on the rounding of a sequential or parallel float64 sum over the row (plus the
     // 4096 histogram bins), relative to the sum: 8 * (V + 4096) * 2^-53, plus twice the
@@ -1362,24 +1435,21 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     const int nseg_m = d.greedy_seg ? (V + kGreedySeg - 1) / kGreedySeg : d.nseg_max;
     sample_prep_kernel<<<B, 256, 0, s>>>(P, d.greedy_seg, d.seg_max, nseg_m, d.n_drafts, d.accepted, d.spec_row,
                                          d.spec_x, d.spec_key, force);
-    // A plain draw without filters draws from the pass's segment sums. With filters: the bin
-    // of the cut (select1), its elements and the sums above it (gather), the cut and the
-    // segment sums (select2); the kept launch only for dense residuals and for a nucleus cut
-    // above the top-k bin. A residual draw without filters takes the pass's total (select1).
-    const bool residual = d.spec_row != nullptr;
-    const bool two_pass = P.filtered || residual;
+    // Without filters the draw takes the pass's segment sums (a dense residual: the kept
+    // launch's). With filters: the bin of the cut (select1), its elements and the sums above
+    // it (gather) — both done by the pass when the caller hints the cut — then the cut and
+    // the segment sums (select2); the kept launch only for dense residuals and for a nucleus
+    // cut above the top-k bin.
+    const bool kept = P.q || (P.use_k && P.use_p);
 #define GG_DRAW(DTV)                                                                                 \
     sample_pass_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                              \
-    if (two_pass) {                                                                                  \
+    if (P.filtered && !P.hint_mode) {                                                                \
         sample_select1_kernel<<<B, kRowThreads, 0, s>>>(P);                                          \
-        if (P.filtered) {                                                                            \
-            sample_gather_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                    \
-            sample_select2_kernel<DTV><<<B, kRowThreads, 0, s>>>(P);                                 \
-        }                                                                                            \
-        if (P.filtered || P.q)                                                                       \
-            sample_kept_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                      \
+        sample_gather_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                        \
     }                                                                                                \
-    sample_draw_kernel<DTV><<<B, kSegThreads, 0, s>>>(P, two_pass ? 0 : 1);
+    if (P.filtered) sample_select2_kernel<DTV><<<B, kRowThreads, 0, s>>>(P);                         \
+    if (kept) sample_kept_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                    \
+    sample_draw_kernel<DTV><<<B, kSegThreads, 0, s>>>(P);
     switch (d.dt) {
         case GG_DTYPE_F32: GG_DRAW(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_DRAW(GG_DTYPE_BF16) break;

@@ -138,7 +138,8 @@ struct FinalDraw {
     const float2* greedy_seg;
     const int* spec_row;
     const int* spec_x;
-    const unsigned int* spec_key;  // given rows, top-p: an order key near the nucleus cut (0: none)
+    const unsigned long long* spec_key;  // given rows, top-p: (order key << 32 | ~index) of an element
+                                         // at or near the nucleus cut (0: none)
     const float* seg_max;
     int nseg_max;
     bool force_exact;

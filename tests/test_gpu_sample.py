@@ -205,3 +205,38 @@ def test_rejection_special_final_rows(gpu):
                                      torch.from_numpy(dq).cuda() if dq is not None else None)
         torch.cuda.synchronize()
         assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et)
+
+
+@pytest.mark.parametrize("ties,dense", [(False, False), (True, False), (False, True)])
+def test_rejection_nucleus_cut_on_float64_boundaries(gpu, ties, dense):
+    """top-p (a float32) placed on or next to the float64 rule's cumulative sums of the final
+    row: the acceptance's fixed-point nucleus, which the draw takes as its hint of the cut,
+    can then name a neighbour of the float64 cut, and the draw has to find the rule's own
+    cut. Rows with many equal logits put the cut inside a run of ties."""
+    B, K, V, T = 8, 2, 5003, 0.8
+    rng = np.random.default_rng(53 + 2 * int(ties) + int(dense))
+    row = rng.normal(0, 2, V).astype(np.float32)
+    if ties:
+        row = (np.round(row * 4) / 4).astype(np.float32)
+    host = np.broadcast_to(row, (B, K + 1, V)).copy()
+    drafts = np.full((B, K), int(np.argmin(row)), np.int32)  # outside any nucleus: rejected
+    n = np.full(B, K, np.int32)
+    q = rng.dirichlet(np.ones(V) * 0.3, (B, K)).astype(np.float32) if dense else None
+    p = ora.sampler_probs_f64(row, float(np.float32(T)), 0, 0.0)
+    order = sorted(range(V), key=lambda i: (-p[i], i))
+    c = np.cumsum(p[order])
+    ks = [int(k) for k in np.searchsorted(c, np.linspace(0.3, 0.97, 8))]
+    misses = 0
+    for k in ks:
+        for top_p in (np.float32(c[k]), np.nextafter(np.float32(c[k]), np.float32(0)),
+                      np.nextafter(np.float32(c[k]), np.float32(1))):
+            u = rng.random((B, K + 1)).astype(np.float32)
+            ea, et = ora.accept_rejection(host, drafts, n, u, T, float(top_p), q)
+            say(f"nucleus boundary ties={ties} dense={dense} k={k} top_p={float(top_p)!r}")
+            ga, gt = gv.accept_rejection(torch.from_numpy(host).cuda(), torch.from_numpy(drafts).cuda(),
+                                         torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda(), T, float(top_p),
+                                         torch.from_numpy(q).cuda() if dense else None)
+            torch.cuda.synchronize()
+            assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et), (k, top_p)
+            misses += int((ea == 0).all())
+    assert misses == len(ks) * 3  # every draft rejected, so every call drew from the nucleus
