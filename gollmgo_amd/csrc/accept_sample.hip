@@ -46,7 +46,7 @@ namespace {
 
 constexpr int kSeg = 8192;        // elements per block of the pass and kept launches
 constexpr int kSegThreads = 512;
-constexpr int kBins = 4096;       // coarse bins: the top 12 bits of the order key
+constexpr int kBins = 4096;       // coarse bins: 1/64-nat slices below the row max (bin_of)
 constexpr int kCap = 4096;        // items of one bin the select launch can gather
 constexpr int kRowThreads = 1024;
 constexpr int kChunk = 4096;      // exact path: bitonic sort entries held in LDS at once
@@ -147,6 +147,17 @@ __device__ __forceinline__ unsigned long long comp_key(uint32_t key, int idx) {
     return ((unsigned long long)key << 32) | (unsigned long long)(uint32_t)(~(uint32_t)idx);
 }
 __device__ __forceinline__ int comp_index(unsigned long long c) { return (int)(~(uint32_t)c); }
+
+// Coarse bin of a logit: 1/64-nat slices of its distance below the row max, x = (m - l/T)
+// * 64, the highest bin holding the max; everything more than (kBins - 1)/64 nats below
+// (and -inf, NaN) in bin 0. Monotone in the value, and a bin holds a few hundred of a
+// 128k-entry row where a nucleus cut falls (a 1/8-octave slice of the value holds thousands).
+// Elements below bin c have e <= gg_exp64(-(kBins - c) / 64) exactly: x is 64 * fl(m - v)
+// and e = gg_exp64(-fl(m - v)), with gg_exp64 monotone.
+__device__ __forceinline__ int bin_of(float l, double inv_t, double m) {
+    const double x = (m - (double)l * inv_t) * 64.0;
+    return x < (double)(kBins - 1) ? kBins - 1 - (int)x : 0;
+}
 
 __device__ __forceinline__ int clamp_n(const int32_t* n_drafts, int b, int K) {
     const int n = n_drafts[b];
@@ -391,7 +402,7 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             ri.pregather = hint != 0;
             ri.hint = hint;
             if (hint != 0) {
-                ri.cbin = (int)(hint >> 52);
+                ri.cbin = bin_of(key_value((uint32_t)(hint >> 32)), P.inv_t, m);
                 P.ncand[b] = 0;
             }
             P.info[b] = ri;
@@ -559,7 +570,7 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
             const double ev = (!in || l != l || l == INFINITY) ? 0.0 : fast_term(l, inv_t, m, s_tab);
             acc += ev;
             const uint32_t key = order_key(l);
-            const int bin = (int)(key >> 20);
+            const int bin = bin_of(l, inv_t, m);
             if (pre) {
                 if (in && bin > ri.cbin) above += ev;
                 stage_hit(in && bin == ri.cbin, comp_key(key, e0 + k), &s_hits, s_buf);
@@ -615,7 +626,7 @@ __device__ int gather_bin(const void* row, int V, bool vec, int bin, double inv_
             for (int k = 0; k < 8; ++k) {
                 const int e = c * 8 + k;
                 const uint32_t key = c < nch ? order_key(x[u][k]) : 0u;
-                const bool hit = c < nch && e < V && (int)(key >> 20) == bin;
+                const bool hit = c < nch && e < V && bin_of(x[u][k], inv_t, m) == bin;
                 // one LDS atomic per wave: the wave's hits take consecutive slots
                 const unsigned long long mask = __ballot(hit);
                 if (mask) {
@@ -643,17 +654,44 @@ __device__ int gather_bin(const void* row, int V, bool vec, int bin, double inv_
 
 // Among the ng gathered items (unique 64-bit keys, unordered), the first in descending key
 // order whose running total (of e with by_mass, else of 1) reaches `target`: a radix
-// descent over the low 52 key bits (the bin fixes the rest) in 8-bit digits, each a
-// 256-entry LDS histogram and a scan from the top digit. Returns the item's position in the
-// list (-1 if the total stays below target) and, through before, the total of the items
-// above it. The items are left in place.
+// descent in 8-bit digits over the key bits below the highest one in which the items
+// differ (from their minimum and maximum), each digit a 256-entry LDS histogram and a scan
+// from the top digit. Returns the item's position in the list (-1 if the total stays below
+// target) and, through before, the total of the items above it. The items are left in place.
 __device__ int select_desc(const unsigned long long* s_comp, const double* s_e, int ng, double target, bool by_mass,
                            double* before, double* s_h, double* s_red, int* s_i) {
-    unsigned long long prefix = 0, pmask = 0;
+    __shared__ unsigned long long s_lo[16], s_hi[16];
+    unsigned long long lo = ~0ull, hi = 0;
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+        const unsigned long long c = s_comp[i];
+        lo = c < lo ? c : lo;
+        hi = c > hi ? c : hi;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long a = __shfl_xor(lo, o), c = __shfl_xor(hi, o);
+        lo = a < lo ? a : lo;
+        hi = c > hi ? c : hi;
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_lo[threadIdx.x >> 6] = lo;
+        s_hi[threadIdx.x >> 6] = hi;
+    }
+    __syncthreads();
+    lo = ~0ull;
+    hi = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+        lo = s_lo[w] < lo ? s_lo[w] : lo;
+        hi = s_hi[w] > hi ? s_hi[w] : hi;
+    }
+    const unsigned long long diff = lo ^ hi;
+    int nbits = diff ? 64 - __clzll((long long)diff) : 0;  // the items share every bit above these
+    nbits = nbits < 8 ? 8 : nbits;
+    unsigned long long pmask = nbits >= 64 ? 0ull : ~((1ull << nbits) - 1ull);
+    unsigned long long prefix = hi & pmask;
     double above = 0.0;
-    for (int shift = 44; shift >= -4; shift -= 8) {
+    for (int shift = nbits - 8; shift > -8; shift -= 8) {
         const int sh = shift < 0 ? 0 : shift;
-        const int width = shift < 0 ? 4 : 8;
+        const int width = shift < 0 ? 8 + shift : 8;
         const unsigned long long dmask = ((1ull << width) - 1ull) << sh;
         for (int i = threadIdx.x; i < 256; i += blockDim.x) s_h[i] = 0.0;
         __syncthreads();
@@ -686,7 +724,7 @@ __device__ int select_desc(const unsigned long long* s_comp, const double* s_e, 
         pmask |= dmask;
         __syncthreads();
     }
-    // prefix now names exactly one item (the low 52 bits are unique within the bin)
+    // prefix now names exactly one item (the keys are unique)
     if (threadIdx.x == 0) *s_i = -1;
     __syncthreads();
     for (int i = threadIdx.x; i < ng; i += blockDim.x)
@@ -869,7 +907,7 @@ __global__ void __launch_bounds__(kSegThreads) sample_gather_kernel(DrawParams P
         for (int k = 0; k < 8; ++k) {
             const int e = e0 + k;
             const uint32_t key = order_key(x[k]);
-            const int bin = (int)(key >> 20);
+            const int bin = bin_of(x[k], P.inv_t, ri.m);
             const bool in = e < P.V;
             if (in && bin > ri.cbin) acc += fast_term(x[k], P.inv_t, ri.m, s_tab);
             stage_hit(in && bin == ri.cbin, comp_key(key, e), &s_cnt, s_buf);
@@ -1020,7 +1058,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
                 const double en = exp_term(key_value((uint32_t)(nb >> 32)), inv_t, m);
                 if (en == ec && (nb >> 32) != (cc >> 32)) ok = false;
             } else if (nb == 0 && !(P.use_k && cbin == ri.cbin) && cbin > 0) {
-                const double e_edge = exp_term(key_value(((uint32_t)cbin << 20) - 1u), inv_t, m);
+                const double e_edge = gg_exp64(-(double)(kBins - cbin) / 64.0);  // bound of the bins below
                 if (e_edge >= ec) ok = false;
             }
             if (!ok) {

@@ -240,3 +240,13 @@ def test_rejection_nucleus_cut_on_float64_boundaries(gpu, ties, dense):
             assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et), (k, top_p)
             misses += int((ea == 0).all())
     assert misses == len(ks) * 3  # every draft rejected, so every call drew from the nucleus
+
+
+@pytest.mark.parametrize("sd,top_k,top_p", [(4.0, 0, 0.95), (3.0, 2000, 0.9)])
+def test_sample_wide_logits_large_vocab(gpu, sd, top_k, top_p):
+    """Wide logits over a 2^18 vocab: where a top-p cut falls, a slice of the value's order
+    key (1/8 octave) would hold more elements than a gather can take; the draw's coarse bins
+    are 1/64-nat slices below the row max, so the parallel path resolves these rows."""
+    lg, host, drafts, n, u = case(8, 2, 1 << 18, "f32", seed=71 + int(sd), sd=sd, accept_all=1.0)
+    n[:] = 2
+    check(lg, host, drafts, n, u, 0.9, top_k, top_p, f"wide sd={sd} k={top_k} p={top_p}")
