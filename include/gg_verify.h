@@ -351,8 +351,9 @@ gg_status_t gg_ngram_draft(const int32_t* history, int hist_stride, const int32_
  * corrected or bonus token) followed by maybeDraft's NGramDrafter.Draft over the
  * whole history (serving.go:608-620, speculative.go:24-62). Sequence b:
  *   row       = hist_rows ? hist_rows[b] : b (history row of the sequence)
- *               rows must be distinct within one call: two sequences naming the
- *               same row race on its tokens and length
+ *               rows whose hist_len is >= 0 must be distinct within one call (two
+ *               sequences on one such row race on its tokens and length); rows of
+ *               length -1 may be shared, since they are only set to -1 again
  *   appends     drafts[b][0, accepted[b]) and then token[b] (if >= 0) at
  *               history[row][hist_len[row] ..]; hist_len[row] grows by that count
  *   then        out_drafts[b][0, out_n[b]) = gg_ngram_draft of the updated row
