@@ -1117,14 +1117,25 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
 // and, after a rejection, the rejected draft (the residual draw excludes it).
 // With top-p the row's fixed-point nucleus cut goes along as (boundary key << 32 | ~idx_cut)
 // (0: none): the float64 cut is almost always that element, and otherwise almost always in
-// its coarse bin, which the draw gathers in its first pass.
+// its coarse bin, which the draw gathers in its first pass. A residual draw against a dense
+// draft distribution without top-p gets the row's fixed-point total Z * 2^-70 as an
+// estimate of its float64 softmax sum (0: none), which lets the draw's first pass sum the
+// residual for all but the elements whose p and q nearly tie.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* __restrict__ out_acc,
                                                         int* __restrict__ spec_row, int* __restrict__ spec_x,
-                                                        unsigned long long* __restrict__ spec_key) {
+                                                        unsigned long long* __restrict__ spec_key,
+                                                        double* __restrict__ spec_s) {
     const int b = blockIdx.x;
     const SeqPlan p = decide_seq<DT>(din, b);
+    double sest = 0.0;
+    if (p.d.residual && din.dprobs && !din.use_topp) {  // uniform across the wave
+        const int row = b * (din.K + 1) + p.d.row;
+        const float m = row_max_wave(din.seg_max, row, din.nseg);
+        if (finite_f(m)) sest = gg_u128_to_double(row_z_wave(din.seg_max, din.seg_e, row, din.nseg, m, din.inv_t)) * 0x1p-70;
+    }
     if (threadIdx.x == 0) {
+        spec_s[b] = sest;
         out_acc[b] = p.d.accepted;
         spec_row[b] = p.d.row;
         spec_x[b] = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
@@ -1148,6 +1159,7 @@ struct RejWs {
     int* spec_row;     // the final draw's row per sequence
     int* spec_x;       // the rejected draft of a residual draw, -1 for a plain draw
     unsigned long long* spec_key;  // top-p: the final row's fixed-point nucleus cut element
+    double* spec_s;                // dense residual draws: the row's fixed-point total (0: none)
     void* draw;        // the final draw's own workspace (launch_final_draw)
     RowStats* stats;   // top-p: exact nucleus statistics of flagged rows
     u64* seg_hist;     // top-p: coarse histogram per (row, segment)
@@ -1179,6 +1191,7 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
     w.spec_row = (int*)take((size_t)num_seqs * sizeof(int));
     w.spec_x = (int*)take((size_t)num_seqs * sizeof(int));
     w.spec_key = (unsigned long long*)take((size_t)num_seqs * sizeof(unsigned long long));
+    w.spec_s = (double*)take((size_t)num_seqs * sizeof(double));
     w.draw = take(final_draw_workspace_bytes(num_seqs, vocab));
     if (topp) {
         w.stats = (RowStats*)take(rows * sizeof(RowStats));
@@ -1245,7 +1258,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                                                              inv_t, n_drafts, w.seg_max,     \
                                                                              w.seg_e, nullptr);              \
     }                                                                                                        \
-    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x, w.spec_key);
+    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x, w.spec_key, w.spec_s);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_REJ(GG_DTYPE_BF16) break;
@@ -1269,6 +1282,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     d.spec_row = w.spec_row;
     d.spec_x = w.spec_x;
     d.spec_key = w.spec_key;
+    d.spec_s = w.spec_s;
     d.seg_max = w.seg_max;
     d.nseg_max = nseg;
     d.out_tok = out_tok;

@@ -69,6 +69,8 @@ struct RowInfo {
     int kept_pass;            // the kept launch computes the draw's segment sums
     int pregather;            // cbin known before the pass (a hint), which gathers it
     unsigned long long hint;  // the hinted cut element's key (comp_key order), or 0
+    double Sest;              // dense residual without filters: the caller's estimate of the
+                              // row's e sum (0: none), see split_residual
 };
 
 struct Ent {                  // exact path sort entry, ordered by (hi, lo) descending
@@ -76,7 +78,7 @@ struct Ent {                  // exact path sort entry, ordered by (hi, lo) desc
 };
 
 struct Layout {
-    size_t state, info, hcnt, hmass, segsum, segkept, segabove, ncand, cand, exact, total;
+    size_t state, info, hcnt, hmass, segsum, segkept, segabove, segep, segqp, ncand, cand, exact, total;
     size_t slot_bytes, vpad, npow;
 };
 
@@ -103,6 +105,8 @@ struct DrawParams {
     double* segsum;
     double* segkept;
     double* segabove;         // per segment: e summed over the bins above cbin
+    double* segep;            // per segment (estimated residuals): e of the sure-positive elements
+    double* segqp;            //   and their q
     int* ncand;               // per sequence: elements of cbin gathered
     unsigned long long* cand; // per sequence: kCap gathered keys
     int32_t* out_tok;
@@ -121,6 +125,8 @@ Layout layout(int B, int V) {
     L.segsum = o;  o = align256(o + (size_t)B * nseg * sizeof(double));
     L.segkept = o; o = align256(o + (size_t)B * nseg * sizeof(double));
     L.segabove = o; o = align256(o + (size_t)B * nseg * sizeof(double));
+    L.segep = o;   o = align256(o + (size_t)B * nseg * sizeof(double));
+    L.segqp = o;   o = align256(o + (size_t)B * nseg * sizeof(double));
     L.ncand = o;   o = align256(o + (size_t)B * sizeof(int));
     L.cand = o;    o = align256(o + (size_t)B * kCap * sizeof(unsigned long long));
     L.vpad = ((size_t)V + 63) & ~(size_t)63;
@@ -256,6 +262,21 @@ __device__ __forceinline__ double draw_weight(const DrawParams& P, const RowInfo
     return p > qv ? p - qv : 0.0;
 }
 
+// A residual draw against a dense q without filters, with the caller's estimate S~ of the
+// row's e sum S: |S - S~| <= kSestTol * S~ (the fixed-point total of the rejection
+// acceptance; its exponential, the float32 arguments and the truncations stay within
+// about 1e-5). The residual of element i is max(0, e_i / S - q_i); it is e_i/S - q_i for
+// sure when e_i > q_i * S~ (1 + kSestTol) and 0 for sure when e_i < q_i * S~ (1 - kSestTol).
+// So the pass sums e and q of the sure-positive elements per segment, lists the few in
+// between (their p and q nearly tie), and the draw forms each segment's residual mass as
+// E+/S - Q+ plus the listed elements' own residuals, with S from the pass. More listed
+// elements than a list holds (a draft distribution close to p): the kept launch computes
+// the sums from S instead.
+constexpr double kSestTol = 1e-4;
+__device__ __forceinline__ bool split_residual(const DrawParams& P, const RowInfo& ri) {
+    return ri.x >= 0 && P.q && !P.filtered && ri.Sest > 0.0;
+}
+
 // The pass's segment sums added in segment order (the row's e total without filters); every
 // kernel that needs it adds them the same way.
 __device__ __forceinline__ double seg_total(const DrawParams& P, int b) {
@@ -335,7 +356,8 @@ __device__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* sh, uint32_t* tota
 __global__ void __launch_bounds__(256) sample_prep_kernel(
     DrawParams P, const float2* __restrict__ gws, const float* __restrict__ seg_max, int nseg_m,
     const int32_t* __restrict__ n_drafts, const int32_t* __restrict__ acc, const int* __restrict__ spec_row,
-    const int* __restrict__ spec_x, const unsigned long long* __restrict__ spec_key, int force_exact) {
+    const int* __restrict__ spec_x, const unsigned long long* __restrict__ spec_key,
+    const double* __restrict__ spec_s, int force_exact) {
     const int b = blockIdx.x;
     const int K = P.K, R = K + 1;
     int row, x = -1;
@@ -397,10 +419,13 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             ri.need = 0;
             ri.above = 0.0;
             ri.S = 0.0;
-            // Without filters only a dense residual needs the kept launch's sums.
-            ri.kept_pass = !P.filtered && P.q && x >= 0;
+            // Without filters only a dense residual needs the kept launch's sums, and with an
+            // estimate of S only when the pass lists too many near-ties.
+            ri.Sest = (spec_s && x >= 0) ? spec_s[b] : 0.0;
+            ri.kept_pass = !P.filtered && P.q && x >= 0 && !(ri.Sest > 0.0);
             ri.pregather = hint != 0;
             ri.hint = hint;
+            if (split_residual(P, ri)) P.ncand[b] = 0;
             if (hint != 0) {
                 ri.cbin = bin_of(key_value((uint32_t)(hint >> 32)), P.inv_t, m);
                 P.ncand[b] = 0;
@@ -530,20 +555,30 @@ __device__ __forceinline__ void flush_hits(const DrawParams& P, int b, int* s_cn
 // Per (segment, sequence): e of every element (the parallel exponential), the segment's
 // sum, the NaN / +inf check, and with top-k / top-p the coarse histograms — or, when the
 // cut's bin is known beforehand, that bin's elements and the sum of e above it.
-template <gg_dtype_t DT>
+// kHist: the launch builds histograms or gathers a hinted bin (with filters); without
+// filters it needs only the staging buffer of a split residual, and its smaller LDS lets
+// four blocks share a CU.
+template <gg_dtype_t DT, bool kHist>
 __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) {
     const int b = blockIdx.y, seg = blockIdx.x;
     if (P.state[b] != ST_DRAW) return;
-    __shared__ uint32_t s_cnt[kBins];
-    __shared__ double s_mass[kBins];
+    __shared__ uint32_t s_cnt[kHist ? kBins : 1];
+    __shared__ double s_mass[kHist ? kBins : 1];
+    __shared__ unsigned long long s_stage[kHist ? 1 : kBlockCap];
     __shared__ double s_red[16];
     __shared__ double s_tab[64];
     __shared__ int s_hits, s_base;
-    unsigned long long* s_buf = (unsigned long long*)s_mass;  // pregather: the staging buffer
+    // the staging buffer of a pregather or a split residual
+    unsigned long long* s_buf = kHist ? (unsigned long long*)s_mass : s_stage;
     load_exp_table(s_tab);
     const RowInfo ri = P.info[b];
-    const bool pre = ri.pregather;
-    const int want_cnt = P.use_k && !pre, want_mass = P.filtered && !pre;
+    const bool pre = kHist && ri.pregather;
+    const bool split = !kHist && split_residual(P, ri);
+    const float* qr = split ? q_row(P, b, ri) : nullptr;
+    // The bounds in float, widened by 1e-6 for the float rounding of e, q and the products.
+    const float shi = (float)(ri.Sest * (1.0 + kSestTol) * (1.0 + 1e-6));
+    const float slo = (float)(ri.Sest * (1.0 - kSestTol) * (1.0 - 1e-6));
+    const int want_cnt = kHist && P.use_k && !pre, want_mass = kHist && P.filtered && !pre;
     const int V = P.V;
     const double inv_t = P.inv_t;
     const void* row = drawn_row(P, b, ri.row);
@@ -556,12 +591,13 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
     }
     if (threadIdx.x == 0) s_hits = 0;
     __syncthreads();
-    double acc = 0.0, above = 0.0;
+    double acc = 0.0, above = 0.0, ep = 0.0, qp = 0.0;
     int bad = 0;
     for (int c0 = 0; c0 < kSeg / 8; c0 += blockDim.x) {
         const int e0 = seg * kSeg + (c0 + threadIdx.x) * 8;
-        float x[8];
+        float x[8], y[8];
         load8<DT>(row, V, e0, P.vec, x);
+        if (split) load8q(qr, V, e0, P.vec_q, y);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const float l = x[k];
@@ -574,6 +610,18 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
             if (pre) {
                 if (in && bin > ri.cbin) above += ev;
                 stage_hit(in && bin == ri.cbin, comp_key(key, e0 + k), &s_hits, s_buf);
+            } else if (split) {
+                const int e = e0 + k;
+                const bool cand = in && e != ri.x;
+                const float qf = (y[k] > 0.0f && y[k] <= 3.402823466e38f) ? fminf(y[k], 1.0f) : 0.0f;  // clean_q
+                const float ef = (float)ev;
+                const bool pos = cand && ef > qf * shi;
+                const bool amb = cand && !pos && ef != 0.0f && ef >= qf * slo;
+                if (pos) {
+                    ep += ev;
+                    qp += (double)qf;
+                }
+                if (__any(amb)) stage_hit(amb, (unsigned long long)e, &s_hits, s_buf);
             } else if ((want_cnt || want_mass) && in) {
                 if (want_cnt) atomicAdd(&s_cnt[bin], 1u);
                 if (want_mass && ev != 0.0) atomicAdd(&s_mass[bin], ev);
@@ -586,6 +634,15 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
     }
     const double tot = block_sum(acc, s_red);
     if (threadIdx.x == 0) P.segsum[(size_t)b * P.nseg + seg] = tot;
+    if (split) {
+        const double E = block_sum(ep, s_red), Q = block_sum(qp, s_red);
+        if (threadIdx.x == 0) {
+            P.segep[(size_t)b * P.nseg + seg] = E;
+            P.segqp[(size_t)b * P.nseg + seg] = Q;
+        }
+        flush_hits(P, b, &s_hits, &s_base, s_buf);
+        return;
+    }
     if (pre) {
         const double ab = block_sum(above, s_red);
         if (threadIdx.x == 0) P.segabove[(size_t)b * P.nseg + seg] = ab;
@@ -1100,7 +1157,8 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
     if (P.state[b] != ST_DRAW) return;
     __shared__ double s_red[16];
     RowInfo ri = P.info[b];
-    if (!ri.kept_pass) return;
+    // (a split residual only when its near-ties overflowed the list)
+    if (!ri.kept_pass && !(split_residual(P, ri) && P.ncand[b] > kCap)) return;
     if (!P.filtered) ri.tot = seg_total(P, b);  // a dense residual without filters
     const double inv_tot = 1.0 / ri.tot;
     __shared__ double s_tab[64];
@@ -1142,8 +1200,25 @@ __global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P) 
     load_exp_table(s_tab);
     RowInfo ri = P.info[b];
     if (!P.filtered) ri.tot = seg_total(P, b);
-    const double* src = (!P.filtered && !ri.kept_pass ? P.segsum : P.segkept) + (size_t)b * P.nseg;
-    if (ri.x >= 0 && !ri.kept_pass) {
+    const bool split = split_residual(P, ri);
+    const double* src = (!P.filtered && !ri.kept_pass && !split ? P.segsum : P.segkept) + (size_t)b * P.nseg;
+    if (split && P.ncand[b] <= kCap) {
+        // Segment residual masses: the sure-positive elements' E+/S - Q+, plus the listed
+        // near-ties' own residuals (the same weight the draw below gives each element).
+        const double inv = 1.0 / ri.tot;
+        if ((int)threadIdx.x < P.nseg)
+            s_sums[threadIdx.x] = P.segep[(size_t)b * P.nseg + threadIdx.x] * inv - P.segqp[(size_t)b * P.nseg + threadIdx.x];
+        __syncthreads();
+        const int n = P.ncand[b];
+        const float* qr = q_row(P, b, ri);
+        const void* row = drawn_row(P, b, ri.row);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const int e = (int)P.cand[(size_t)b * kCap + i];
+            atomicAdd(&s_sums[e / kSeg], draw_weight(P, ri, qr[e], load_as_f32(row, P.dt, e), e, s_tab, inv));
+        }
+        __syncthreads();
+        src = s_sums;
+    } else if (ri.x >= 0 && !ri.kept_pass && !split) {
         if (threadIdx.x < P.nseg) {
             double v = src[threadIdx.x];
             if (ri.x < P.V && ri.x / kSeg == (int)threadIdx.x) {
@@ -1466,13 +1541,15 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     P.segsum = (double*)(w + L.segsum);
     P.segkept = (double*)(w + L.segkept);
     P.segabove = (double*)(w + L.segabove);
+    P.segep = (double*)(w + L.segep);
+    P.segqp = (double*)(w + L.segqp);
     P.ncand = (int*)(w + L.ncand);
     P.cand = (unsigned long long*)(w + L.cand);
     P.out_tok = d.out_tok;
     const int force = d.force_exact ? 1 : 0;
     const int nseg_m = d.greedy_seg ? (V + kGreedySeg - 1) / kGreedySeg : d.nseg_max;
     sample_prep_kernel<<<B, 256, 0, s>>>(P, d.greedy_seg, d.seg_max, nseg_m, d.n_drafts, d.accepted, d.spec_row,
-                                         d.spec_x, d.spec_key, force);
+                                         d.spec_x, d.spec_key, d.spec_s, force);
     // Without filters the draw takes the pass's segment sums (a dense residual: the kept
     // launch's). With filters: the bin of the cut (select1), its elements and the sums above
     // it (gather) — both done by the pass when the caller hints the cut — then the cut and
@@ -1480,7 +1557,8 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     // cut above the top-k bin.
     const bool kept = P.q || (P.use_k && P.use_p);
 #define GG_DRAW(DTV)                                                                                 \
-    sample_pass_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                              \
+    if (P.filtered) sample_pass_kernel<DTV, true><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);        \
+    else sample_pass_kernel<DTV, false><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                  \
     if (P.filtered && !P.hint_mode) {                                                                \
         sample_select1_kernel<<<B, kRowThreads, 0, s>>>(P);                                          \
         sample_gather_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                        \

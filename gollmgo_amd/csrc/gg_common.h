@@ -140,6 +140,8 @@ struct FinalDraw {
     const int* spec_x;
     const unsigned long long* spec_key;  // given rows, top-p: (order key << 32 | ~index) of an element
                                          // at or near the nucleus cut (0: none)
+    const double* spec_s;                // given rows: an estimate of the drawn row's softmax sum
+                                         // within 1e-4 relative (0: none; dense residuals)
     const float* seg_max;
     int nseg_max;
     bool force_exact;

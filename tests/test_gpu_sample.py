@@ -250,3 +250,30 @@ def test_sample_wide_logits_large_vocab(gpu, sd, top_k, top_p):
     lg, host, drafts, n, u = case(8, 2, 1 << 18, "f32", seed=71 + int(sd), sd=sd, accept_all=1.0)
     n[:] = 2
     check(lg, host, drafts, n, u, 0.9, top_k, top_p, f"wide sd={sd} k={top_k} p={top_p}")
+
+
+def test_rejection_dense_draft_close_to_target(gpu):
+    """A dense draft distribution within 1e-6 of the target's own probabilities, with the
+    drafted token's q doubled so that u >= 0.6 rejects it. Every other element's p and q
+    then nearly tie: they are more than the residual draw's list of near-ties holds, so the
+    draw falls back to summing the residual from the row's total; the token is the oracle's."""
+    B, K, V, T = 16, 2, 20011, 0.8
+    rng = np.random.default_rng(61)
+    host = rng.normal(0, 2, (B, K + 1, V)).astype(np.float32)
+    drafts = rng.integers(0, V, (B, K)).astype(np.int32)
+    q = np.empty((B, K, V), np.float32)
+    for b in range(B):
+        for j in range(K):
+            p = ora.sampler_probs_f64(host[b, j], float(np.float32(T)), 0, 1.0)
+            q[b, j] = (p * (1.0 + 1e-6 * rng.standard_normal(V))).astype(np.float32)
+            q[b, j, drafts[b, j]] = np.float32(2.0 * p[drafts[b, j]])
+    n = np.full(B, K, np.int32)
+    u = rng.uniform(0.6, 1.0, (B, K + 1)).astype(np.float32)
+    ea, et = ora.accept_rejection(host, drafts, n, u, T, 1.0, q)
+    say("rejection dense draft close to target")
+    ga, gt = gv.accept_rejection(torch.from_numpy(host).cuda(), torch.from_numpy(drafts).cuda(),
+                                 torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda(), T, 1.0,
+                                 torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et)
+    assert (ea == 0).all()  # every sequence drew from the residual of its first row
