@@ -38,6 +38,7 @@
 
 #include "gg_common.h"
 #include "gg_fixed_exp.h"
+#include "gg_draw.h"
 
 namespace gg {
 namespace {
@@ -1120,20 +1121,20 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
 // its coarse bin, which the draw gathers in its first pass. A residual draw against a dense
 // draft distribution without top-p gets the row's fixed-point total Z * 2^-70 as an
 // estimate of its float64 softmax sum (0: none), which lets the draw's first pass sum the
-// residual for all but the elements whose p and q nearly tie.
+// residual for all but the elements whose p and q nearly tie. The kernel then sets the
+// sequence's draw up itself (fd::prep_row), so the draw needs no launch for it.
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* __restrict__ out_acc,
                                                         int* __restrict__ spec_row, int* __restrict__ spec_x,
                                                         unsigned long long* __restrict__ spec_key,
-                                                        double* __restrict__ spec_s) {
+                                                        double* __restrict__ spec_s, fd::DrawParams P) {
     const int b = blockIdx.x;
     const SeqPlan p = decide_seq<DT>(din, b);
     double sest = 0.0;
-    if (p.d.residual && din.dprobs && !din.use_topp) {  // uniform across the wave
-        const int row = b * (din.K + 1) + p.d.row;
-        const float m = row_max_wave(din.seg_max, row, din.nseg);
-        if (finite_f(m)) sest = gg_u128_to_double(row_z_wave(din.seg_max, din.seg_e, row, din.nseg, m, din.inv_t)) * 0x1p-70;
-    }
+    const int frow = b * (din.K + 1) + (p.d.row < 0 ? 0 : p.d.row);
+    const float fm = row_max_wave(din.seg_max, frow, din.nseg);  // the drawn row's finite max
+    if (p.d.residual && din.dprobs && !din.use_topp && finite_f(fm))  // uniform across the wave
+        sest = gg_u128_to_double(row_z_wave(din.seg_max, din.seg_e, frow, din.nseg, fm, din.inv_t)) * 0x1p-70;
     if (threadIdx.x == 0) {
         spec_s[b] = sest;
         out_acc[b] = p.d.accepted;
@@ -1146,6 +1147,8 @@ __global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* _
                 key = ((unsigned long long)st.lam << 32) | (unsigned long long)(~(unsigned int)st.idx_cut);
         }
         spec_key[b] = key;
+        const int x = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
+        fd::prep_row(P, b, p.d.row, x, fm, fm > -INFINITY, P.hint_mode ? key : 0ull, x >= 0 ? sest : 0.0, 0);
     }
 }
 
@@ -1232,6 +1235,26 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     // the draw launch (one-hot q), not as a launch of its own.
     const DecideIn din{logits, q, K, vocab, nseg, inv_t, use_topp, drafts, n_drafts, uniforms,
                        w.stats, w.status, w.flag, w.seg_max, w.seg_e};
+    FinalDraw d{};
+    d.logits = logits;
+    d.dt = dt;
+    d.num_seqs = num_seqs;
+    d.max_drafts = K;
+    d.vocab = vocab;
+    d.temperature = (double)temperature;
+    d.top_k = 0;
+    d.top_p = (double)top_p;
+    d.uniforms_f32 = uniforms;
+    d.draft_probs = q;
+    d.spec_row = w.spec_row;
+    d.spec_x = w.spec_x;
+    d.spec_key = w.spec_key;
+    d.spec_s = w.spec_s;
+    d.seg_max = w.seg_max;
+    d.nseg_max = nseg;
+    d.out_tok = out_tok;
+    d.prepped = true;  // rej_decide_kernel sets each sequence's draw up
+    const fd::DrawParams P = fd::final_draw_params(d, w.draw);
 #define GG_REJ(DTV)                                                                                          \
     if (use_topp) {                                                                                          \
         seg_pass_kernel<DTV, true><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,  \
@@ -1258,7 +1281,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
                                                                              inv_t, n_drafts, w.seg_max,     \
                                                                              w.seg_e, nullptr);              \
     }                                                                                                        \
-    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x, w.spec_key, w.spec_s);
+    rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x, w.spec_key, w.spec_s, P);
     switch (dt) {
         case GG_DTYPE_F32: GG_REJ(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_REJ(GG_DTYPE_BF16) break;
@@ -1268,24 +1291,6 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
 #undef GG_REJ
     const gg_status_t st = check_hip(hipGetLastError(), "accept_rejection launch");
     if (st != GG_OK) return st;
-    FinalDraw d{};
-    d.logits = logits;
-    d.dt = dt;
-    d.num_seqs = num_seqs;
-    d.max_drafts = K;
-    d.vocab = vocab;
-    d.temperature = (double)temperature;
-    d.top_k = 0;
-    d.top_p = (double)top_p;
-    d.uniforms_f32 = uniforms;
-    d.draft_probs = q;
-    d.spec_row = w.spec_row;
-    d.spec_x = w.spec_x;
-    d.spec_key = w.spec_key;
-    d.spec_s = w.spec_s;
-    d.seg_max = w.seg_max;
-    d.nseg_max = nseg;
-    d.out_tok = out_tok;
     return launch_final_draw(d, w.draw, s);
 }
 

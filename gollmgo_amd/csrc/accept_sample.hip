@@ -38,15 +38,17 @@
 //   exact  (a few blocks)   : the literal rule for the rows flagged on the way.
 #include "gg_common.h"
 #include "gg_exp64.h"
+#include "gg_draw.h"
 
 #pragma clang fp contract(off)
 
 namespace gg {
 namespace {
 
+using namespace fd;
+
 constexpr int kSeg = 8192;        // elements per block of the pass and kept launches
 constexpr int kSegThreads = 512;
-constexpr int kBins = 4096;       // coarse bins: 1/64-nat slices below the row max (bin_of)
 constexpr int kCap = 4096;        // items of one bin the select launch can gather
 constexpr int kRowThreads = 1024;
 constexpr int kChunk = 4096;      // exact path: bitonic sort entries held in LDS at once
@@ -54,24 +56,7 @@ constexpr int kExactSlots = 4;    // exact path: workgroups (each with its own s
 constexpr int kGreedySeg = 4096;  // accept_greedy.hip's segment length
 constexpr int kNone = 0x7fffffff; // accept_greedy.hip's "no element" index
 
-enum : int { ST_NONE = 0, ST_DRAW = 1, ST_EXACT = 2 };
 
-struct RowInfo {
-    double m;                 // max scaled logit of the drawn row
-    unsigned long long cut;   // kept <=> comp_key >= cut (0 keeps every element)
-    double tot;               // the kept e summed (the nucleus mass with top-p)
-    int row;                  // row of the sequence drawn from
-    int x;                    // residual draw: the rejected draft (excluded); -1: plain draw
-    int cbin;                 // the coarse bin the gather launch collects (-1: none)
-    int need;                 // top-k: how many of that bin's elements the filter keeps
-    double above;             // histogram mass of the bins above cbin (top-p without top-k)
-    double S;                 // top-p without top-k: the row's e summed
-    int kept_pass;            // the kept launch computes the draw's segment sums
-    int pregather;            // cbin known before the pass (a hint), which gathers it
-    unsigned long long hint;  // the hinted cut element's key (comp_key order), or 0
-    double Sest;              // dense residual without filters: the caller's estimate of the
-                              // row's e sum (0: none), see split_residual
-};
 
 struct Ent {                  // exact path sort entry, ordered by (hi, lo) descending
     unsigned long long hi, lo;
@@ -82,35 +67,6 @@ struct Layout {
     size_t slot_bytes, vpad, npow;
 };
 
-// Everything the draw launches share (passed by value).
-struct DrawParams {
-    const void* logits;       // [B][K+1][V]
-    gg_dtype_t dt;
-    int B, K, V, nseg;
-    double inv_t;
-    int top_k;
-    double top_p;
-    int use_k, use_p, filtered;
-    int hint_mode;            // top-p alone with the caller's cut hints: select1 / gather not launched
-    int vec;                  // rows allow 16-byte loads
-    int vec_q;                // so do the draft distributions' rows
-    double tau;
-    const double* ud;         // uniform of sequence b: ud[b], or else
-    const float* uf;          //   uf[b * (K + 1) + K]
-    const float* q;           // residual draws: dense draft distributions [B][K][V], or null
-    int* state;
-    RowInfo* info;
-    uint32_t* hcnt;
-    double* hmass;
-    double* segsum;
-    double* segkept;
-    double* segabove;         // per segment: e summed over the bins above cbin
-    double* segep;            // per segment (estimated residuals): e of the sure-positive elements
-    double* segqp;            //   and their q
-    int* ncand;               // per sequence: elements of cbin gathered
-    unsigned long long* cand; // per sequence: kCap gathered keys
-    int32_t* out_tok;
-};
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -145,25 +101,12 @@ __device__ __forceinline__ uint32_t order_key(float l) {
     const uint32_t u = __float_as_uint(l == 0.0f ? 0.0f : l);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-__device__ __forceinline__ float key_value(uint32_t k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
 // (value desc, index asc) as one descending 64-bit key; every element's key is > 0.
 __device__ __forceinline__ unsigned long long comp_key(uint32_t key, int idx) {
     return ((unsigned long long)key << 32) | (unsigned long long)(uint32_t)(~(uint32_t)idx);
 }
 __device__ __forceinline__ int comp_index(unsigned long long c) { return (int)(~(uint32_t)c); }
 
-// Coarse bin of a logit: 1/64-nat slices of its distance below the row max, x = (m - l/T)
-// * 64, the highest bin holding the max; everything more than (kBins - 1)/64 nats below
-// (and -inf, NaN) in bin 0. Monotone in the value, and a bin holds a few hundred of a
-// 128k-entry row where a nucleus cut falls (a 1/8-octave slice of the value holds thousands).
-// Elements below bin c have e <= gg_exp64(-(kBins - c) / 64) exactly: x is 64 * fl(m - v)
-// and e = gg_exp64(-fl(m - v)), with gg_exp64 monotone.
-__device__ __forceinline__ int bin_of(float l, double inv_t, double m) {
-    const double x = (m - (double)l * inv_t) * 64.0;
-    return x < (double)(kBins - 1) ? kBins - 1 - (int)x : 0;
-}
 
 __device__ __forceinline__ int clamp_n(const int32_t* n_drafts, int b, int K) {
     const int n = n_drafts[b];
@@ -262,20 +205,6 @@ __device__ __forceinline__ double draw_weight(const DrawParams& P, const RowInfo
     return p > qv ? p - qv : 0.0;
 }
 
-// A residual draw against a dense q without filters, with the caller's estimate S~ of the
-// row's e sum S: |S - S~| <= kSestTol * S~ (the fixed-point total of the rejection
-// acceptance; its exponential, the float32 arguments and the truncations stay within
-// about 1e-5). The residual of element i is max(0, e_i / S - q_i); it is e_i/S - q_i for
-// sure when e_i > q_i * S~ (1 + kSestTol) and 0 for sure when e_i < q_i * S~ (1 - kSestTol).
-// So the pass sums e and q of the sure-positive elements per segment, lists the few in
-// between (their p and q nearly tie), and the draw forms each segment's residual mass as
-// E+/S - Q+ plus the listed elements' own residuals, with S from the pass. More listed
-// elements than a list holds (a draft distribution close to p): the kept launch computes
-// the sums from S instead.
-constexpr double kSestTol = 1e-4;
-__device__ __forceinline__ bool split_residual(const DrawParams& P, const RowInfo& ri) {
-    return ri.x >= 0 && P.q && !P.filtered && ri.Sest > 0.0;
-}
 
 // The pass's segment sums added in segment order (the row's e total without filters); every
 // kernel that needs it adds them the same way.
@@ -399,40 +328,7 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
             mx = fmaxf(mx, __shfl_xor(mx, o));
             any |= __shfl_xor(any, o);
         }
-        if (threadIdx.x == 0) {
-            const double m = (double)mx * P.inv_t;
-            int st = ST_DRAW;
-            // No finite maximum (all -inf / NaN, or +inf present), or a non-finite scale:
-            // the literal rule decides.
-            if (!any || !(mx > -INFINITY && mx < INFINITY) || !(m > -INFINITY && m < INFINITY) || force_exact)
-                st |= ST_EXACT;
-            // Hint mode launches no select1 / gather: a row without a hint (the caller's
-            // nucleus kept every finite logit, or was not computed) takes the literal rule.
-            if (P.hint_mode && hint == 0) st |= ST_EXACT;
-            RowInfo ri;
-            ri.m = m;
-            ri.cut = 0;
-            ri.tot = 0.0;
-            ri.row = row;
-            ri.x = x;
-            ri.cbin = -1;
-            ri.need = 0;
-            ri.above = 0.0;
-            ri.S = 0.0;
-            // Without filters only a dense residual needs the kept launch's sums, and with an
-            // estimate of S only when the pass lists too many near-ties.
-            ri.Sest = (spec_s && x >= 0) ? spec_s[b] : 0.0;
-            ri.kept_pass = !P.filtered && P.q && x >= 0 && !(ri.Sest > 0.0);
-            ri.pregather = hint != 0;
-            ri.hint = hint;
-            if (split_residual(P, ri)) P.ncand[b] = 0;
-            if (hint != 0) {
-                ri.cbin = bin_of(key_value((uint32_t)(hint >> 32)), P.inv_t, m);
-                P.ncand[b] = 0;
-            }
-            P.info[b] = ri;
-            P.state[b] = st;
-        }
+        if (threadIdx.x == 0) prep_row(P, b, row, x, mx, any != 0, hint, spec_s && x >= 0 ? spec_s[b] : 0.0, force_exact);
     }
 }
 
@@ -1504,7 +1400,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_exact_kernel(DrawParams P,
 
 size_t final_draw_workspace_bytes(int num_seqs, int vocab) { return layout(num_seqs, vocab).total; }
 
-gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
+fd::DrawParams fd::final_draw_params(const FinalDraw& d, void* ws) {
     const int B = d.num_seqs, K = d.max_drafts, V = d.vocab;
     const Layout L = layout(B, V);
     uint8_t* w = (uint8_t*)ws;
@@ -1546,10 +1442,19 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     P.ncand = (int*)(w + L.ncand);
     P.cand = (unsigned long long*)(w + L.cand);
     P.out_tok = d.out_tok;
+    return P;
+}
+
+gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
+    const int B = d.num_seqs, V = d.vocab;
+    const Layout L = layout(B, V);
+    uint8_t* w = (uint8_t*)ws;
+    const DrawParams P = fd::final_draw_params(d, ws);
     const int force = d.force_exact ? 1 : 0;
     const int nseg_m = d.greedy_seg ? (V + kGreedySeg - 1) / kGreedySeg : d.nseg_max;
-    sample_prep_kernel<<<B, 256, 0, s>>>(P, d.greedy_seg, d.seg_max, nseg_m, d.n_drafts, d.accepted, d.spec_row,
-                                         d.spec_x, d.spec_key, d.spec_s, force);
+    if (!d.prepped)
+        sample_prep_kernel<<<B, 256, 0, s>>>(P, d.greedy_seg, d.seg_max, nseg_m, d.n_drafts, d.accepted, d.spec_row,
+                                             d.spec_x, d.spec_key, d.spec_s, force);
     // Without filters the draw takes the pass's segment sums (a dense residual: the kept
     // launch's). With filters: the bin of the cut (select1), its elements and the sums above
     // it (gather) — both done by the pass when the caller hints the cut — then the cut and

@@ -145,6 +145,7 @@ struct FinalDraw {
     const float* seg_max;
     int nseg_max;
     bool force_exact;
+    bool prepped;                        // the caller set every sequence's row up (fd::prep_row)
     int32_t* out_tok;
 };
 size_t final_draw_workspace_bytes(int num_seqs, int vocab);
