@@ -1053,8 +1053,7 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
     if (P.state[b] != ST_DRAW) return;
     __shared__ double s_red[16];
     RowInfo ri = P.info[b];
-    // (a split residual only when its near-ties overflowed the list)
-    if (!ri.kept_pass && !(split_residual(P, ri) && P.ncand[b] > kCap)) return;
+    if (!ri.kept_pass) return;
     if (!P.filtered) ri.tot = seg_total(P, b);  // a dense residual without filters
     const double inv_tot = 1.0 / ri.tot;
     __shared__ double s_tab[64];
@@ -1098,7 +1097,29 @@ __global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P) 
     if (!P.filtered) ri.tot = seg_total(P, b);
     const bool split = split_residual(P, ri);
     const double* src = (!P.filtered && !ri.kept_pass && !split ? P.segsum : P.segkept) + (size_t)b * P.nseg;
-    if (split && P.ncand[b] <= kCap) {
+    if (split && P.ncand[b] > kCap) {
+        // More near-ties than the list holds (q close to p): this block sums the row's
+        // residual by segment itself, 16 elements per thread and round.
+        const double inv = 1.0 / ri.tot;
+        if ((int)threadIdx.x < P.nseg) s_sums[threadIdx.x] = 0.0;
+        __syncthreads();
+        const float* qr = q_row(P, b, ri);
+        const void* row = drawn_row(P, b, ri.row);
+        for (int e0 = threadIdx.x * 16; e0 < P.V; e0 += blockDim.x * 16) {  // 16 | kSeg: one segment
+            float xl[2][8], ql[2][8];
+            load8<DT>(row, P.V, e0, P.vec, xl[0]);
+            load8<DT>(row, P.V, e0 + 8, P.vec, xl[1]);
+            load8q(qr, P.V, e0, P.vec_q, ql[0]);
+            load8q(qr, P.V, e0 + 8, P.vec_q, ql[1]);
+            double part = 0.0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q)
+                if (e0 + q < P.V) part += draw_weight(P, ri, ql[q >> 3][q & 7], xl[q >> 3][q & 7], e0 + q, s_tab, inv);
+            atomicAdd(&s_sums[e0 / kSeg], part);
+        }
+        __syncthreads();
+        src = s_sums;
+    } else if (split) {
         // Segment residual masses: the sure-positive elements' E+/S - Q+, plus the listed
         // near-ties' own residuals (the same weight the draw below gives each element).
         const double inv = 1.0 / ri.tot;
@@ -1418,6 +1439,7 @@ fd::DrawParams fd::final_draw_params(const FinalDraw& d, void* ws) {
     P.use_p = d.top_p > 0 && d.top_p < 1.0;
     P.filtered = P.use_k || P.use_p;
     P.hint_mode = d.spec_key && P.use_p && !P.use_k;
+    P.kept_launched = (d.draft_probs && (P.filtered || !d.spec_s)) || (P.use_k && P.use_p);
     {
         const size_t eb = dtype_bytes(d.dt);
         P.vec = ((size_t)V * eb % 16 == 0) && ((uintptr_t)d.logits % 16 == 0);
@@ -1460,7 +1482,9 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     // it (gather) — both done by the pass when the caller hints the cut — then the cut and
     // the segment sums (select2); the kept launch only for dense residuals and for a nucleus
     // cut above the top-k bin.
-    const bool kept = P.q || (P.use_k && P.use_p);
+    // (A dense residual without filters but with the caller's estimate of S needs none: the
+    // pass and the draw form its sums.)
+    const bool kept = P.kept_launched;
 #define GG_DRAW(DTV)                                                                                 \
     if (P.filtered) sample_pass_kernel<DTV, true><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);        \
     else sample_pass_kernel<DTV, false><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                  \

@@ -38,6 +38,7 @@ struct DrawParams {
     double top_p;
     int use_k, use_p, filtered;
     int hint_mode;            // top-p alone with the caller's cut hints: select1 / gather not launched
+    int kept_launched;        // the kept launch runs (a row that needs it otherwise goes exact)
     int vec;                  // rows allow 16-byte loads
     int vec_q;                // so do the draft distributions' rows
     double tau;
@@ -121,6 +122,7 @@ __device__ inline void prep_row(const DrawParams& P, int b, int row, int x, floa
     // estimate of S only when the pass lists too many near-ties.
     ri.Sest = sest;
     ri.kept_pass = !P.filtered && P.q && x >= 0 && !(ri.Sest > 0.0);
+    if (ri.kept_pass && !P.kept_launched) st |= ST_EXACT;
     ri.pregather = hint != 0;
     ri.hint = hint;
     if (split_residual(P, ri)) P.ncand[b] = 0;
