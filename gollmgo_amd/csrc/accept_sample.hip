@@ -128,8 +128,9 @@ __device__ __forceinline__ double fast_term(float l, double inv_t, double m, con
     return gg_fast_exp64_tab(v - m, tab);  // -inf logits give -inf, hence 0
 }
 // Each block's copy of the exponential's table (64 doubles in LDS).
+__constant__ double c_exp_tab[64] = {GG_EXP64_TAB64};
 __device__ __forceinline__ void load_exp_table(double* s_tab) {
-    if (threadIdx.x < 64) s_tab[threadIdx.x] = gg_exp64((double)threadIdx.x * (6.93147180559945286227e-01 / 64.0));
+    if (threadIdx.x < 64) s_tab[threadIdx.x] = c_exp_tab[threadIdx.x];
     __syncthreads();
 }
 

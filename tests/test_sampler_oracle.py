@@ -188,3 +188,34 @@ def test_sample_closed_forms(ora):
     t = np.array([10, 0, 0, 0], np.float32)
     assert all(ora.sample_f64(t, 0.01, 0.0, u) == 0 for u in (0.0, 0.5, 0.999))
     assert ora.sample_f64(t, 100.0, 0.0, 0.6) == 2
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_exp64_table_literals(ora, tmp_path):
+    """The fast exponential's table literals (GG_EXP64_TAB64) are gg_exp64(j ln2 / 64) bit
+    for bit, and equal the oracle's exp64 there."""
+    src = tmp_path / "t.c"
+    src.write_text(r"""
+#include <stdio.h>
+#include <string.h>
+#include "gg_exp64.h"
+int main(void) {
+    double t[64];
+    gg_exp64_table(t);
+    int bad = 0;
+    for (int j = 0; j < 64; ++j) {
+        const double v = gg_exp64((double)j * (6.93147180559945286227e-01 / 64.0));
+        if (memcmp(&v, &t[j], 8) != 0) ++bad;
+        printf("%a\n", t[j]);
+    }
+    return bad;
+}
+""")
+    exe = tmp_path / "t"
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-I", str(ROOT / "gollmgo_amd" / "csrc"), str(src), "-o",
+                    str(exe), "-lm"], check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert res.returncode == 0
+    got = np.array([float.fromhex(v) for v in res.stdout.split()])
+    want = ora.exp64(np.arange(64) * (0.693147180559945286227 / 64.0))
+    assert np.array_equal(got.view(np.int64), want.view(np.int64))
