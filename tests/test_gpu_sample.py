@@ -54,7 +54,7 @@ def check(lg, host, drafts, n, u, T, top_k, top_p, label):
 
 @pytest.mark.parametrize("T,top_k,top_p", [(0.8, 0, 0.0), (0.8, 50, 0.0), (0.8, 0, 0.95), (1.3, 50, 0.9),
                                            (0.6, 1, 0.5), (1.0, 4095, 0.99), (0.0, 50, 0.95)])
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 def test_sample_small_vocab(gpu, dt, T, top_k, top_p):
     lg, host, drafts, n, u = case(24, 3, 5003, dt, seed=int(T * 100) + top_k + int(top_p * 1000))
     check(lg, host, drafts, n, u, T, top_k, top_p, f"small dt={dt} T={T} k={top_k} p={top_p}")
@@ -277,3 +277,15 @@ def test_rejection_dense_draft_close_to_target(gpu):
     torch.cuda.synchronize()
     assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gt.cpu().numpy(), et)
     assert (ea == 0).all()  # every sequence drew from the residual of its first row
+
+
+@pytest.mark.parametrize("top_k,top_p", [(0, 0.0), (40, 0.0), (0, 0.9)])
+def test_sample_without_drafts_and_many_sequences(gpu, top_k, top_p):
+    """No drafts (max_drafts 0: every sequence draws its token from row 0, as a plain decode
+    step's Sampler.Sample) over 1000 sequences, and a batch of 600 with 2 drafts."""
+    for B, K, seed in ((1000, 0, 81), (600, 2, 82)):
+        lg, host, drafts, n, u = case(B, K, 3001, "bf16", seed=seed + top_k, accept_all=1.0)
+        if K == 0:
+            drafts = np.zeros((B, 0), np.int32)
+            n = np.zeros(B, np.int32)
+        check(lg, host, drafts, n, u, 0.8, top_k, top_p, f"B={B} K={K} k={top_k} p={top_p}")
