@@ -38,6 +38,8 @@ def test_sampled_bonus_sweep(gpu, T, top_k, top_p):
         torch.cuda.synchronize()
         bad += int(((acc.cpu().numpy() != ea) | (tok.cpu().numpy() != et)).sum())
         done += B
+        if done % 20000 == 0:
+            say(f"  {done} rows, {bad} disagreements")
     say(f"sampled bonus T={T} k={top_k} p={top_p}: {done} rows, {bad} disagreements")
     assert bad == 0
 
@@ -64,5 +66,7 @@ def test_rejection_residual_sweep(gpu, dense, top_p):
         bad += int(((ga.cpu().numpy() != ea) | (gt.cpu().numpy() != et)).sum())
         assert (ea == 0).all()
         done += B
+        if done % 10000 == 0:
+            say(f"  {done} rows, {bad} disagreements")
     say(f"rejection residual dense={dense} top_p={top_p}: {done} rows, {bad} disagreements")
     assert bad == 0
