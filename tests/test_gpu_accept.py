@@ -328,3 +328,24 @@ def test_acceptance_full_size_configs(gpu, cid):
     # The decision handed back as the engine's LogitsPerPosition (one-hot rows).
     T = cfg.temperature if cfg.accept != "greedy" else 0.0
     check_positions(drafts.cpu().numpy(), n.cpu().numpy(), a, t, V, T, cfg.top_p, cid)
+
+
+def test_greedy_ties_across_segment_boundaries(gpu):
+    """Ties and a NaN around the segment boundaries of a 2^17-entry row (every segment
+    length up to 2^16 that divides it has a boundary at 2^14): the first index wins."""
+    say("greedy ties across segments")
+    V = 1 << 17
+    rows = np.full((4, 2, V), -1.0, np.float32)
+    rows[0, 0, [16384, 16383]] = 5.0                          # tie straddling 2^14 -> 16383
+    rows[1, 0, [32768, 100000, 16384]] = 7.0                  # ties in later segments -> 16384
+    rows[2, 0, 16383] = np.nan; rows[2, 0, [16384, 65536]] = 2.0  # NaN skipped -> 16384
+    rows[3, 0, V - 1] = 3.0; rows[3, 0, 65535] = 3.0          # last element ties earlier -> 65535
+    drafts = np.array([[16383], [16384], [16384], [65535]], np.int32)
+    n = np.ones(4, np.int32)
+    for dt in ("f32", "bf16"):
+        lg = torch.from_numpy(rows).to(TD[dt])
+        acc, tok = gv.accept_greedy(lg.cuda(), torch.from_numpy(drafts).cuda(), torch.from_numpy(n).cuda())
+        torch.cuda.synchronize()
+        ea, et = ora.accept_greedy(lg.float().numpy(), drafts, n)
+        assert np.array_equal(acc.cpu().numpy(), ea) and np.array_equal(tok.cpu().numpy(), et), dt
+        assert acc.cpu().tolist() == [1, 1, 1, 1], dt
