@@ -452,11 +452,14 @@ __device__ __forceinline__ void flush_hits(const DrawParams& P, int b, int* s_cn
 // Per (segment, sequence): e of every element (the parallel exponential), the segment's
 // sum, the NaN / +inf check, and with top-k / top-p the coarse histograms — or, when the
 // cut's bin is known beforehand, that bin's elements and the sum of e above it.
-// kHist: the launch builds histograms or gathers a hinted bin (with filters); without
-// filters it needs only the staging buffer of a split residual, and its smaller LDS lets
-// four blocks share a CU.
-template <gg_dtype_t DT, bool kHist>
+// kMode: kPassPlain without filters (a split residual's staging at most); kPassHist builds
+// the histograms (filters without hints); kPassPre gathers the hinted bin (hint mode, where
+// every drawn row has its hint). Only kPassHist holds the 48 KB of histograms: the others
+// stage in 16 KB, so four blocks share a CU.
+constexpr int kPassPlain = 0, kPassHist = 1, kPassPre = 2;
+template <gg_dtype_t DT, int kMode>
 __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) {
+    constexpr bool kHist = kMode == kPassHist;
     const int b = blockIdx.y, seg = blockIdx.x;
     if (P.state[b] != ST_DRAW) return;
     __shared__ uint32_t s_cnt[kHist ? kBins : 1];
@@ -466,11 +469,15 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
     __shared__ double s_tab[64];
     __shared__ int s_hits, s_base;
     // the staging buffer of a pregather or a split residual
-    unsigned long long* s_buf = kHist ? (unsigned long long*)s_mass : s_stage;
+    unsigned long long* s_buf = s_stage;
     load_exp_table(s_tab);
     const RowInfo ri = P.info[b];
-    const bool pre = kHist && ri.pregather;
-    const bool split = !kHist && split_residual(P, ri);
+    if (kMode == kPassPre && !ri.pregather) {  // hint mode marks rows without a hint exact
+        if (threadIdx.x == 0) atomicOr(&P.state[b], ST_EXACT);
+        return;
+    }
+    const bool pre = kMode == kPassPre;
+    const bool split = kMode == kPassPlain && split_residual(P, ri);
     const float* qr = split ? q_row(P, b, ri) : nullptr;
     // The bounds in float, widened by 1e-6 for the float rounding of e, q and the products.
     const float shi = (float)(ri.Sest * (1.0 + kSestTol) * (1.0 + 1e-6));
@@ -1487,8 +1494,9 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
     // pass and the draw form its sums.)
     const bool kept = P.kept_launched;
 #define GG_DRAW(DTV)                                                                                 \
-    if (P.filtered) sample_pass_kernel<DTV, true><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);        \
-    else sample_pass_kernel<DTV, false><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                  \
+    if (P.hint_mode) sample_pass_kernel<DTV, kPassPre><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);   \
+    else if (P.filtered) sample_pass_kernel<DTV, kPassHist><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P); \
+    else sample_pass_kernel<DTV, kPassPlain><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);             \
     if (P.filtered && !P.hint_mode) {                                                                \
         sample_select1_kernel<<<B, kRowThreads, 0, s>>>(P);                                          \
         sample_gather_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                        \
