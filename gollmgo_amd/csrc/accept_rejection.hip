@@ -533,16 +533,30 @@ __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restric
         const unsigned long long rej = __ballot(lane > j0 && lane < n && st == kRowReject);
         jend = rej ? __ffsll((long long)rej) - 1 : n;
     }
-    // Rows 0 .. n (n <= 64): lane j writes row j, lane 0 also row 64.
+    // When the bounds settle the walk, row j0 is only drawn from: it is flagged 2 and not
+    // listed, and the draw gets its coarse boundary bin as a range hint instead of the exact
+    // cut (rej_decide_kernel), unless that bin is the last row bin, which holds everything
+    // below it. Rows 0 .. n (n <= 64): lane j writes row j, lane 0 also row 64.
+    const bool settled = !(j0 < n && __shfl(st, j0) == kRowUnsure);
     int mine = 0, mine64 = 0;
     if (lane <= n) {
         mine = lane >= j0 && lane <= jend;
+        if (mine && settled) {
+            const int cb = pick[b * R + lane].cbin;
+            if (cb >= 0 && cb < kRowBins - 1) mine = 2;
+        }
         flag[b * R + lane] = mine;
     }
     if (lane == 0 && n == 64) {
         mine64 = jend >= 64;
+        if (mine64 && settled) {
+            const int cb = pick[b * R + 64].cbin;
+            if (cb >= 0 && cb < kRowBins - 1) mine64 = 2;
+        }
         flag[b * R + 64] = mine64;
+        mine64 = mine64 == 1;
     }
+    mine = mine == 1;
     const unsigned long long fl = __ballot(mine);
     const int cnt = __popcll(fl) + __shfl(mine64, 0);
     int base = 0;
@@ -1039,6 +1053,7 @@ struct DecideIn {
     const int* flag;
     const float* seg_max;
     const u64* seg_e;
+    const RowPick* pick;
 };
 // F: per sequence, one wave: the acceptance walk and the view of the final row. Without
 // top-p every row's values come from the segment maxima and sums; with top-p a row the
@@ -1075,7 +1090,7 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
         const int row = b * R + (live ? j : 0);
         const int x = live ? drafts[(size_t)b * K + j] : -1;
         bool ok = true;
-        if (use_topp && !flag[row]) {
+        if (use_topp && flag[row] != 1) {  // decided by the bounds (flag 2: only drawn from)
             ok = status[row] == kRowAccept;
         } else {
             float m;
@@ -1118,7 +1133,9 @@ __device__ SeqPlan decide_seq(const DecideIn& in, int b) {
 // and, after a rejection, the rejected draft (the residual draw excludes it).
 // With top-p the row's fixed-point nucleus cut goes along as (boundary key << 32 | ~idx_cut)
 // (0: none): the float64 cut is almost always that element, and otherwise almost always in
-// its coarse bin, which the draw gathers in its first pass. A residual draw against a dense
+// its coarse bin, which the draw gathers in its first pass. A row only drawn from (flag 2)
+// has no exact cut: its boundary coarse bin goes along as a range of l / T instead, which
+// the draw's first pass gathers whole. A residual draw against a dense
 // draft distribution without top-p gets the row's fixed-point total Z * 2^-70 as an
 // estimate of its float64 softmax sum (0: none), which lets the draw's first pass sum the
 // residual for all but the elements whose p and q nearly tie. The kernel then sets the
@@ -1141,14 +1158,25 @@ __global__ void __launch_bounds__(64) rej_decide_kernel(DecideIn din, int32_t* _
         spec_row[b] = p.d.row;
         spec_x[b] = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
         unsigned long long key = 0;
+        double vlo = 0.0, vhi = 0.0;
         if (din.use_topp) {
-            const RowStats st = din.stats[(size_t)b * (din.K + 1) + p.d.row];
-            if (st.valid && st.lam != 0u)
-                key = ((unsigned long long)st.lam << 32) | (unsigned long long)(~(unsigned int)st.idx_cut);
+            if (din.flag[frow] == 2) {
+                // Only drawn from: the values l / T of its boundary coarse bin (cb_abs bin A
+                // holds l * (16 / T) in [A, A + 1)) as the draw's range hint.
+                const RowPick pk = din.pick[frow];
+                const int A = cb_abs(pk.m, din.inv_t) - pk.cbin;
+                vlo = (double)A / 16.0;
+                vhi = (double)(A + 1) / 16.0;
+            } else {
+                const RowStats st = din.stats[frow];
+                if (st.valid && st.lam != 0u)
+                    key = ((unsigned long long)st.lam << 32) | (unsigned long long)(~(unsigned int)st.idx_cut);
+            }
         }
         spec_key[b] = key;
         const int x = p.d.residual ? din.drafts[(size_t)b * din.K + p.d.row] : -1;
-        fd::prep_row(P, b, p.d.row, x, fm, fm > -INFINITY, P.hint_mode ? key : 0ull, x >= 0 ? sest : 0.0, 0);
+        fd::prep_row(P, b, p.d.row, x, fm, fm > -INFINITY, P.hint_mode ? key : 0ull, x >= 0 ? sest : 0.0, 0,
+                     P.hint_mode ? vlo : 0.0, P.hint_mode ? vhi : 0.0);
     }
 }
 
@@ -1234,7 +1262,7 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     // The acceptance walk of each sequence runs inside the residual launch (dense q) or
     // the draw launch (one-hot q), not as a launch of its own.
     const DecideIn din{logits, q, K, vocab, nseg, inv_t, use_topp, drafts, n_drafts, uniforms,
-                       w.stats, w.status, w.flag, w.seg_max, w.seg_e};
+                       w.stats, w.status, w.flag, w.seg_max, w.seg_e, w.pick};
     FinalDraw d{};
     d.logits = logits;
     d.dt = dt;

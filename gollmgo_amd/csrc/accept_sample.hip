@@ -513,7 +513,7 @@ __global__ void __launch_bounds__(kSegThreads) sample_pass_kernel(DrawParams P) 
             const int bin = bin_of(l, inv_t, m);
             if (pre) {
                 if (in && bin > ri.cbin) above += ev;
-                stage_hit(in && bin == ri.cbin, comp_key(key, e0 + k), &s_hits, s_buf);
+                stage_hit(in && bin <= ri.cbin && bin >= ri.cbin_lo, comp_key(key, e0 + k), &s_hits, s_buf);
             } else if (split) {
                 const int e = e0 + k;
                 const bool cand = in && e != ri.x;
@@ -650,15 +650,25 @@ __device__ int select_desc(const unsigned long long* s_comp, const double* s_e, 
     unsigned long long pmask = nbits >= 64 ? 0ull : ~((1ull << nbits) - 1ull);
     unsigned long long prefix = hi & pmask;
     double above = 0.0;
+    // items per digit: once the chosen digit holds one item, that item is the answer
+    __shared__ int s_hc[256];
+    __shared__ int s_one;
     for (int shift = nbits - 8; shift > -8; shift -= 8) {
         const int sh = shift < 0 ? 0 : shift;
         const int width = shift < 0 ? 8 + shift : 8;
         const unsigned long long dmask = ((1ull << width) - 1ull) << sh;
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) s_h[i] = 0.0;
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+            s_h[i] = 0.0;
+            s_hc[i] = 0;
+        }
         __syncthreads();
         for (int i = threadIdx.x; i < ng; i += blockDim.x) {
             const unsigned long long c = s_comp[i];
-            if ((c & pmask) == prefix) atomicAdd(&s_h[(int)((c & dmask) >> sh)], by_mass ? s_e[i] : 1.0);
+            if ((c & pmask) == prefix) {
+                const int d = (int)((c & dmask) >> sh);
+                atomicAdd(&s_h[d], by_mass ? s_e[i] : 1.0);
+                atomicAdd(&s_hc[d], 1);
+            }
         }
         __syncthreads();
         // digits from the top: thread t < 256 holds digit 255 - t
@@ -673,7 +683,10 @@ __device__ int select_desc(const unsigned long long* s_comp, const double* s_e, 
         const bool claim = t < 256 && hv > 0.0 && above + ex < target && above + ex + hv >= target;
         if (claim) atomicMax(s_i, 255 - t);
         __syncthreads();
-        if (claim && *s_i == 255 - t) s_h[256] = above + ex;
+        if (claim && *s_i == 255 - t) {
+            s_h[256] = above + ex;
+            s_one = s_hc[255 - t] == 1;
+        }
         __syncthreads();
         const int dgt = *s_i;
         if (dgt < 0) {  // rounding between the histogram and the target: the caller's margin fails
@@ -683,9 +696,11 @@ __device__ int select_desc(const unsigned long long* s_comp, const double* s_e, 
         above = s_h[256];
         prefix |= (unsigned long long)dgt << sh;
         pmask |= dmask;
+        const bool one = s_one;
         __syncthreads();
+        if (one) break;
     }
-    // prefix now names exactly one item (the keys are unique)
+    // prefix now names exactly one item (the keys are unique; or the digit held one)
     if (threadIdx.x == 0) *s_i = -1;
     __syncthreads();
     for (int i = threadIdx.x; i < ng; i += blockDim.x)
@@ -797,7 +812,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select1_kernel(DrawParams 
         __syncthreads();
         if (threadIdx.x == 0) {
             if (s_bin < 0) atomicOr(&P.state[b], ST_EXACT);  // fewer counted elements than k
-            info[b].cbin = s_bin;
+            info[b].cbin = info[b].cbin_lo = s_bin;
             info[b].need = P.top_k - (int)s_cabove;
         }
         return;
@@ -836,7 +851,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select1_kernel(DrawParams 
     __syncthreads();
     if (threadIdx.x == 0) {
         if (s_bin < 0) atomicOr(&P.state[b], ST_EXACT);  // p * S at the very end: rounding decides
-        info[b].cbin = s_bin;
+        info[b].cbin = info[b].cbin_lo = s_bin;
         info[b].above = s_above;
         info[b].S = S;
     }
@@ -1018,8 +1033,9 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
             if (nb != 0 && !(P.use_k && nb < tk)) {
                 const double en = exp_term(key_value((uint32_t)(nb >> 32)), inv_t, m);
                 if (en == ec && (nb >> 32) != (cc >> 32)) ok = false;
-            } else if (nb == 0 && !(P.use_k && cbin == ri.cbin) && cbin > 0) {
-                const double e_edge = gg_exp64(-(double)(kBins - cbin) / 64.0);  // bound of the bins below
+            } else if (nb == 0 && !(P.use_k && cbin == ri.cbin) && (ri.pregather ? ri.cbin_lo : cbin) > 0) {
+                // bound of the bins below the gathered ones
+                const double e_edge = gg_exp64(-(double)(kBins - (ri.pregather ? ri.cbin_lo : cbin)) / 64.0);
                 if (e_edge >= ec) ok = false;
             }
             if (!ok) {

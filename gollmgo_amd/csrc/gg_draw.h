@@ -17,7 +17,9 @@ struct RowInfo {
     double tot;               // the kept e summed (the nucleus mass with top-p)
     int row;                  // row of the sequence drawn from
     int x;                    // residual draw: the rejected draft (excluded); -1: plain draw
-    int cbin;                 // the coarse bin the gather launch collects (-1: none)
+    int cbin;                 // the coarse bin the gather launch collects (-1: none); with a
+                              // range hint the highest bin of the range
+    int cbin_lo;              // the lowest bin gathered (cbin but for a range hint)
     int need;                 // top-k: how many of that bin's elements the filter keeps
     double above;             // histogram mass of the bins above cbin (top-p without top-k)
     double S;                 // top-p without top-k: the row's e summed
@@ -69,6 +71,12 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 // 128k-entry row where a nucleus cut falls (a 1/8-octave slice of the value holds thousands).
 // Elements below bin c have e <= gg_exp64(-(kBins - c) / 64) exactly: x is 64 * fl(m - v)
 // and e = gg_exp64(-fl(m - v)), with gg_exp64 monotone.
+// bin_of_scaled takes the scaled value v = l / T itself (clamped to the top bin above m).
+__device__ __forceinline__ int bin_of_scaled(double v, double m) {
+    const double x = (m - v) * 64.0;
+    if (!(x >= 0.0)) return x < 0.0 ? kBins - 1 : 0;
+    return x < (double)(kBins - 1) ? kBins - 1 - (int)x : 0;
+}
 __device__ __forceinline__ int bin_of(float l, double inv_t, double m) {
     const double x = (m - (double)l * inv_t) * 64.0;
     return x < (double)(kBins - 1) ? kBins - 1 - (int)x : 0;
@@ -92,9 +100,14 @@ __device__ __forceinline__ bool split_residual(const DrawParams& P, const RowInf
 // One sequence's draw set up (by one thread, after the acceptance decided it): row `row` of
 // sequence b (-1: no draw), residual after draft x (-1: plain), mx the row's max logit and
 // any whether it has a finite one, hint the caller's cut element (0: none), sest the
-// caller's estimate of the row's e sum (0: none).
+// caller's estimate of the row's e sum (0: none). Without a cut element, vlo < vhi hints
+// the cut by a range of scaled values l / T instead: the pass gathers the bins from
+// bin_of_scaled(vlo) to bin_of_scaled(vhi). Either hint only steers where the draw looks:
+// when the cut is not among the gathered elements, the select finds no cut that clears
+// its margins and the row takes the literal rule.
 __device__ inline void prep_row(const DrawParams& P, int b, int row, int x, float mx, bool any,
-                                unsigned long long hint, double sest, int force_exact) {
+                                unsigned long long hint, double sest, int force_exact, double vlo = 0.0,
+                                double vhi = 0.0) {
     if (row < 0) {
         P.state[b] = ST_NONE;
         return;
@@ -107,7 +120,8 @@ __device__ inline void prep_row(const DrawParams& P, int b, int row, int x, floa
         st |= ST_EXACT;
     // Hint mode launches no select1 / gather: a row without a hint (the caller's
     // nucleus kept every finite logit, or was not computed) takes the literal rule.
-    if (P.hint_mode && hint == 0) st |= ST_EXACT;
+    const bool range = hint == 0 && vhi > vlo;
+    if (P.hint_mode && hint == 0 && !range) st |= ST_EXACT;
     RowInfo ri;
     ri.m = m;
     ri.cut = 0;
@@ -115,6 +129,7 @@ __device__ inline void prep_row(const DrawParams& P, int b, int row, int x, floa
     ri.row = row;
     ri.x = x;
     ri.cbin = -1;
+    ri.cbin_lo = -1;
     ri.need = 0;
     ri.above = 0.0;
     ri.S = 0.0;
@@ -123,11 +138,15 @@ __device__ inline void prep_row(const DrawParams& P, int b, int row, int x, floa
     ri.Sest = sest;
     ri.kept_pass = !P.filtered && P.q && x >= 0 && !(ri.Sest > 0.0);
     if (ri.kept_pass && !P.kept_launched) st |= ST_EXACT;
-    ri.pregather = hint != 0;
+    ri.pregather = hint != 0 || range;
     ri.hint = hint;
     if (split_residual(P, ri)) P.ncand[b] = 0;
     if (hint != 0) {
-        ri.cbin = bin_of(key_value((uint32_t)(hint >> 32)), P.inv_t, m);
+        ri.cbin = ri.cbin_lo = bin_of(key_value((uint32_t)(hint >> 32)), P.inv_t, m);
+        P.ncand[b] = 0;
+    } else if (range) {
+        ri.cbin = bin_of_scaled(vhi, m);
+        ri.cbin_lo = bin_of_scaled(vlo, m);
         P.ncand[b] = 0;
     }
     P.info[b] = ri;
