@@ -335,13 +335,13 @@ __global__ void __launch_bounds__(256) sample_prep_kernel(
 
 // ------------------------------------------------------------------------ pass
 
-// The draw itself, by one block of kSegThreads: the segment where u * total falls (sums
-// per segment of the draw's weights), then the element inside it (16 per thread). A plain
+// The draw itself, by one block of NT threads: the segment where u * total falls (sums
+// per segment of the draw's weights), then the element inside it (kSeg / NT per thread). A plain
 // draw's margins are tau * total (e units); a residual's tau * (1 + total) (probability
 // units: the parallel p carries up to tau of error summed over the row, whatever q is). A
 // residual total within a few margins of 0 may be 0 in the rule, whose fallbacks then
 // apply. Undecided: the row is left to the literal rule.
-template <gg_dtype_t DT>
+template <gg_dtype_t DT, int NT>
 __device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, const double* sums,
                               const double* s_tab) {
     __shared__ double s_red[16];
@@ -383,16 +383,17 @@ __device__ void draw_in_block(const DrawParams& P, int b, const RowInfo& ri, con
     const double marg = ri.x < 0 ? tau * tot : tau * (1.0 + tot);
     const void* row = drawn_row(P, b, ri.row);
     const float* qr = q_row(P, b, ri);
-    constexpr int kPer = kSeg / kSegThreads;
-    static_assert(kPer == 16, "sixteen elements per thread");
+    constexpr int kPer = kSeg / NT;
+    static_assert(kPer == 8 || kPer == 16, "eight or sixteen elements per thread");
     const int e0 = seg * kSeg + threadIdx.x * kPer;
     double ev[kPer];
     double loc = 0.0;
-    float xl[2][8], ql[2][8];
-    load8<DT>(row, P.V, e0, P.vec, xl[0]);
-    load8<DT>(row, P.V, e0 + 8, P.vec, xl[1]);
-    load8q(qr, P.V, e0, P.vec_q, ql[0]);
-    load8q(qr, P.V, e0 + 8, P.vec_q, ql[1]);
+    float xl[kPer / 8][8], ql[kPer / 8][8];
+#pragma unroll
+    for (int h = 0; h < kPer / 8; ++h) {
+        load8<DT>(row, P.V, e0 + 8 * h, P.vec, xl[h]);
+        load8q(qr, P.V, e0 + 8 * h, P.vec_q, ql[h]);
+    }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int e = e0 + q;
@@ -898,13 +899,12 @@ __global__ void __launch_bounds__(kSegThreads) sample_gather_kernel(DrawParams P
 // top-k threshold and/or the nucleus cut — with the margins, then the draw's segment sums
 // (the mass above the bin plus the bin's kept elements), unless the kept launch has to
 // compute them.
+// Returns whether the row is still drawn (ri then holds its cut, total and kept_pass, and
+// s_segk its segment sums unless the kept launch computes them); every return is uniform
+// across the block.
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams P) {
-    const int b = blockIdx.x;
+__device__ bool select2_row(const DrawParams& P, int b, RowInfo& ri, double* s_segk, double* s_tab) {
     int* __restrict__ state = P.state;
-    if (state[b] != ST_DRAW) return;
-    RowInfo ri = P.info[b];
-    if (ri.cbin < 0) return;
     const int V = P.V, nseg = P.nseg;
     const double inv_t = P.inv_t, tau = P.tau, m = ri.m;
     __shared__ double s_mass[kBins];
@@ -913,17 +913,14 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
     __shared__ double s_h[257];
     __shared__ double s_red[16];
     __shared__ unsigned long long s_u[16];
-    __shared__ double s_segk[64];
-    __shared__ double s_tab[64];
     __shared__ int s_n, s_bin, s_i, s_ok;
-    load_exp_table(s_tab);
     __shared__ double s_above;
     const void* row = drawn_row(P, b, ri.row);
     const int per = kBins / kRowThreads;
     int ng = P.ncand[b];
     if (ng > kCap) {  // a crowded bin: the literal rule decides
         if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-        return;
+        return false;
     }
     for (int i = threadIdx.x; i < ng; i += blockDim.x) {
         s_comp[i] = P.cand[(size_t)b * kCap + i];
@@ -949,7 +946,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
         const int ck = ng < ri.need ? -1 : select_desc(s_comp, s_e, ng, (double)ri.need, false, &dummy, s_h, s_red, &s_i);
         if (ck < 0) {
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-            return;
+            return false;
         }
         tk = s_comp[ck];
         cut = tk;
@@ -994,7 +991,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
             const int pbin = s_bin;
             if (pbin < 0) {
                 if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-                return;
+                return false;
             }
             if (pbin != ri.cbin) {
                 // The cut lies above the threshold bin: that bin's elements (one block gathers
@@ -1002,7 +999,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
                 ng = gather_bin<DT>(row, V, P.vec, pbin, inv_t, m, s_comp, s_e, &s_n);
                 if (ng < 0) {
                     if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-                    return;
+                    return false;
                 }
                 ri.kept_pass = 1;
                 cbin = pbin;
@@ -1020,7 +1017,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
         if (ci < 0) ci = select_desc(s_comp, s_e, ng, pS - above, true, &inbin, s_h, s_red, &s_i);
         if (ci < 0) {
             if (threadIdx.x == 0) atomicOr(&state[b], ST_EXACT);
-            return;
+            return false;
         }
         const unsigned long long cc = s_comp[ci];
         const unsigned long long nb = next_below(s_comp, ng, cc, s_u);
@@ -1048,7 +1045,7 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
         cut = cc;
         tot = s_above;
     }
-    if (!s_ok) return;
+    if (!s_ok) return false;
     if (P.q && ri.x >= 0) ri.kept_pass = 1;  // dense residual weights need the kept launch
     if (!ri.kept_pass) {
         // segment sums: the bins above cbin (gather launch) plus cbin's kept elements
@@ -1065,6 +1062,36 @@ __global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams 
         P.info[b].cut = cut;
         P.info[b].tot = tot;
         P.info[b].kept_pass = ri.kept_pass;
+    }
+    ri.cut = cut;
+    ri.tot = tot;
+    return true;
+}
+
+template <gg_dtype_t DT, int NT>
+__device__ void draw_seq(const DrawParams& P, int b, RowInfo ri, const double* kept, const double* s_tab);
+
+// kFuse: no kept launch follows, so the block draws right after its select, from the
+// segment sums in its LDS, and the draw launch is not made.
+template <gg_dtype_t DT, bool kFuse>
+__global__ void __launch_bounds__(kRowThreads) sample_select2_kernel(DrawParams P) {
+    const int b = blockIdx.x;
+    if (P.state[b] != ST_DRAW) return;
+    RowInfo ri = P.info[b];
+    if (ri.cbin < 0) {  // (select1 marks such a row exact)
+        if (kFuse && threadIdx.x == 0) atomicOr(&P.state[b], ST_EXACT);
+        return;
+    }
+    __shared__ double s_segk[64];
+    __shared__ double s_tab[64];
+    load_exp_table(s_tab);
+    if (!select2_row<DT>(P, b, ri, s_segk, s_tab)) return;
+    if constexpr (kFuse) {
+        if (ri.kept_pass) {  // (needs the kept launch, which a fused select rules out)
+            if (threadIdx.x == 0) atomicOr(&P.state[b], ST_EXACT);
+            return;
+        }
+        draw_seq<DT, kRowThreads>(P, b, ri, s_segk, s_tab);
     }
 }
 
@@ -1106,21 +1133,18 @@ __global__ void __launch_bounds__(kSegThreads) sample_kept_kernel(DrawParams P) 
 
 // ------------------------------------------------------------------------ draw
 
-// One block per sequence: the draw over the segment sums of the pass (no filters, unless a
-// dense residual) or of the kept e or residuals (select or the kept launch). A one-hot
+// The draw of sequence b by one block of NT threads, from its row's state ri: over the
+// segment sums of the pass (no filters, unless a dense residual) or of the kept e or
+// residuals (select or the kept launch; `kept`: a fused select's own, in LDS). A one-hot
 // residual whose sums are kept e takes them as (kept e - e of the rejected draft) / total,
 // its weights r = e / total.
-template <gg_dtype_t DT>
-__global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P) {
-    const int b = blockIdx.x;
-    if (P.state[b] != ST_DRAW) return;
+template <gg_dtype_t DT, int NT>
+__device__ void draw_seq(const DrawParams& P, int b, RowInfo ri, const double* kept, const double* s_tab) {
     __shared__ double s_sums[64];
-    __shared__ double s_tab[64];
-    load_exp_table(s_tab);
-    RowInfo ri = P.info[b];
     if (!P.filtered) ri.tot = seg_total(P, b);
     const bool split = split_residual(P, ri);
-    const double* src = (!P.filtered && !ri.kept_pass && !split ? P.segsum : P.segkept) + (size_t)b * P.nseg;
+    const double* src = kept ? kept
+                             : (!P.filtered && !ri.kept_pass && !split ? P.segsum : P.segkept) + (size_t)b * P.nseg;
     if (split && P.ncand[b] > kCap) {
         // More near-ties than the list holds (q close to p): this block sums the row's
         // residual by segment itself, 16 elements per thread and round.
@@ -1171,7 +1195,16 @@ __global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P) 
         __syncthreads();
         src = s_sums;
     }
-    draw_in_block<DT>(P, b, ri, src, s_tab);
+    draw_in_block<DT, NT>(P, b, ri, src, s_tab);
+}
+
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) sample_draw_kernel(DrawParams P) {
+    const int b = blockIdx.x;
+    if (P.state[b] != ST_DRAW) return;
+    __shared__ double s_tab[64];
+    load_exp_table(s_tab);
+    draw_seq<DT, kSegThreads>(P, b, P.info[b], nullptr, s_tab);
 }
 
 // ----------------------------------------------------------------------- exact
@@ -1517,9 +1550,10 @@ gg_status_t launch_final_draw(const FinalDraw& d, void* ws, hipStream_t s) {
         sample_select1_kernel<<<B, kRowThreads, 0, s>>>(P);                                          \
         sample_gather_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                        \
     }                                                                                                \
-    if (P.filtered) sample_select2_kernel<DTV><<<B, kRowThreads, 0, s>>>(P);                         \
+    if (P.filtered && !kept) sample_select2_kernel<DTV, true><<<B, kRowThreads, 0, s>>>(P);           \
+    if (P.filtered && kept) sample_select2_kernel<DTV, false><<<B, kRowThreads, 0, s>>>(P);           \
     if (kept) sample_kept_kernel<DTV><<<dim3(P.nseg, B), kSegThreads, 0, s>>>(P);                    \
-    sample_draw_kernel<DTV><<<B, kSegThreads, 0, s>>>(P);
+    if (!(P.filtered && !kept)) sample_draw_kernel<DTV><<<B, kSegThreads, 0, s>>>(P);
     switch (d.dt) {
         case GG_DTYPE_F32: GG_DRAW(GG_DTYPE_F32) break;
         case GG_DTYPE_BF16: GG_DRAW(GG_DTYPE_BF16) break;
