@@ -71,6 +71,42 @@ struct RowPick {
     int n_cand;      // elements of that bin gathered so far
 };
 
+// A RowPick written and read across workgroups of one launch: device-scope relaxed stores
+// and loads (the ordering argument is at row_pick_kernel).
+__device__ __forceinline__ void store_pick(RowPick* p, const RowPick& v) {
+    u64* d = (u64*)p;
+    const u64* w = (const u64*)&v;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(RowPick) / 8); ++i) __hip_atomic_store(d + i, w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ RowPick load_pick(const RowPick* p) {
+    RowPick v;
+    u64* w = (u64*)&v;
+    const u64* d = (const u64*)p;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(RowPick) / 8); ++i) w[i] = __hip_atomic_load(d + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+}
+static_assert(sizeof(RowPick) % 8 == 0, "RowPick moves as 64-bit words");
+
+// What the bounds walk (run by row_pick_kernel's last row block of a sequence) takes.
+struct DecideBoundsIn {
+    const void* logits;
+    const float* dprobs;
+    int K, V, nseg;
+    float inv_t;
+    const int32_t* drafts;
+    const int32_t* n_drafts;
+    const float* uniforms;
+    const float* seg_max;
+    const u64* seg_e;
+    RowPick* pick;
+    int* status;
+    int* flag;
+    int* n_flagged;
+    int* flagged;
+};
+
 __device__ __forceinline__ u64 shfl_xor_u64(u64 v, int o) {
     unsigned int lo = (unsigned int)v, hi = (unsigned int)(v >> 32);
     lo = __shfl_xor(lo, o);
@@ -311,16 +347,23 @@ __device__ __forceinline__ void load8(const void* row, int V, int e0, bool vec_o
 
 // A: per (row, segment): the segment max m_s and E_s = sum of weight(l, m_s); with top-p
 // also the segment's coarse histogram of e over bins cb(m_s) - cb(l) (written out: the
-// row max, needed to merge, is not known yet). The only full read of the logits.
+// row max, needed to merge, is not known yet), and the counters the next launch counts
+// in cleared: each sequence's row count, and the flagged-row and crowded-row list lengths.
+// The only full read of the logits.
 template <gg_dtype_t DT, bool kTopP>
 __global__ void __launch_bounds__(kSegThreads) seg_pass_kernel(const void* __restrict__ logits, int K, int V,
                                                                int nseg, int vec_ok, float inv_t,
                                                                const int32_t* __restrict__ n_drafts,
                                                                float* __restrict__ seg_max, u64* __restrict__ seg_e,
-                                                               u64* __restrict__ seg_hist) {
+                                                               u64* __restrict__ seg_hist, int* __restrict__ seq_cnt,
+                                                               int* __restrict__ n_flagged) {
     const int seg = blockIdx.x, row = blockIdx.y;
     const int R = K + 1;
     const int b = row / R, j = row % R;
+    if constexpr (kTopP) {
+        if (seg == 0 && j == 0 && threadIdx.x == 0) seq_cnt[b] = 0;
+        if (seg == 0 && row == 0 && threadIdx.x < 2) n_flagged[threadIdx.x] = 0;
+    }
     if (j > live_rows(n_drafts, b, K)) return;
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
     float x[32];
@@ -376,44 +419,75 @@ __device__ __forceinline__ int row_bin(float l, int cbm, float inv_t) {
 // The boundary is the last element, in (logit desc, index asc) order, whose mass before
 // it is below Tp = ceil(p*Z) (or zero). (B) A block per row merges the segments'
 // histograms into the row's (bins shifted by cb(m) - cb(m_s), masses scaled by f_s:
-// exact) and finds the boundary bin and the mass above it. (C) One wave per sequence
-// decides every draft whose outcome the bounds already fix: the nucleus mass lies in
-// [C, C + M] (C the mass above the boundary bin, M its mass), a draft in a bin above the
-// boundary bin is in the nucleus and one below is out. The rows left open, and the row
-// of the final draw, are flagged. (D) For flagged rows only, the boundary bin's
-// elements are gathered (usually a few hundred to a few thousand) together with each
-// segment's sum of e above the boundary bin; (E) a block per flagged row sorts them by
-// (key desc, index asc) and walks the weights to the exact cut. A boundary bin with more
-// than kCandCap elements falls back to the exact single-block row kernel.
+// exact) and finds the boundary bin and the mass above it. (C) In the same launch, the
+// last of a sequence's row blocks to finish decides with one wave every draft whose
+// outcome the bounds already fix: the nucleus mass lies in [C, C + M] (C the mass above
+// the boundary bin, M its mass), a draft in a bin above the boundary bin is in the nucleus
+// and one below is out. The rows left open are flagged for the exact nucleus; the row of
+// the final draw, when the bounds settle the walk, only for the draw's range hint. (D) For
+// the rows flagged exact, the boundary bin's elements are gathered (usually a few hundred
+// to a few thousand); (E) a block per such row sorts them by (key desc, index asc) and
+// walks the weights to the exact cut. A boundary bin with more than kCandCap elements
+// falls back to the exact single-block row kernel.
 
 // B: per row, merge the segment histograms; the boundary bin, the mass above it and its
 // own mass. Thread t owns row bins t, t + 256, ...: row bin r gathers f_s * H_s[r - shift_s]
 // over the segments (the last row bin everything from there down), no atomics. A thread's
-// loads for a batch of segments are issued together. Block 0 also clears the counts of
-// the flagged-row list (decide_bounds_kernel) and the crowded-row list (row_select_kernel).
+// loads for a batch of segments are issued together. The row's RowPick goes out with
+// device-scope stores; then the block counts itself in its sequence's counter (cleared by
+// seg_pass_kernel), and the last of the sequence's rows runs the bounds walk (C) for it.
 constexpr int kPickBatch = 8;
-__global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, float inv_t, float top_p,
-                                                               const int32_t* __restrict__ n_drafts,
-                                                               const float* __restrict__ seg_max,
-                                                               const u64* __restrict__ seg_e,
-                                                               const u64* __restrict__ seg_hist,
-                                                               RowPick* __restrict__ pick, int* __restrict__ n_flagged) {
+template <gg_dtype_t DT>
+__device__ void bounds_walk(const DecideBoundsIn& in, int b);
+__device__ __forceinline__ void row_pick_merge(int nseg, float inv_t, float top_p, const float* __restrict__ seg_max,
+                               const u64* __restrict__ seg_hist, RowPick* __restrict__ pick, int row, float m,
+                               u128 z, u64* hlo, u64* hhi, int* s_shift, u64* s_f, int* p_bin, u128* p_c);
+template <gg_dtype_t DT>
+__global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int nseg, float top_p, const u64* __restrict__ seg_hist,
+                                                               int* __restrict__ seq_cnt, DecideBoundsIn in) {
     const int row = blockIdx.x;
-    if (row == 0 && threadIdx.x < 2) n_flagged[threadIdx.x] = 0;  // (flagged and crowded counts)
+    const int K = in.K;
+    const float inv_t = in.inv_t;
+    const float* __restrict__ seg_max = in.seg_max;
+    const u64* __restrict__ seg_e = in.seg_e;
     const int R = K + 1;
     const int b = row / R, j = row % R;
-    if (j > live_rows(n_drafts, b, K)) return;
+    const int n = live_rows(in.n_drafts, b, K);
+    if (j > n) return;
     __shared__ u64 hlo[kRowBins], hhi[kRowBins];
     __shared__ int s_shift[64];
     __shared__ u64 s_f[64];
     __shared__ int s_bin;
     __shared__ u128 s_c;
+    __shared__ int s_last;
     const float m = row_max_wave(seg_max, row, nseg);
     const u128 z = row_z_wave(seg_max, seg_e, row, nseg, m, inv_t);
     if (!finite_f(m) || z == 0) {
-        if (threadIdx.x == 0) pick[row] = RowPick{0, 0, 0, m, -1, 0};
-        return;
+        if (threadIdx.x == 0) store_pick(&in.pick[row], RowPick{0, 0, 0, m, -1, 0});
+    } else {
+        row_pick_merge(nseg, inv_t, top_p, seg_max, seg_hist, in.pick, row, m, z, hlo, hhi, s_shift, s_f, &s_bin,
+                       &s_c);
     }
+    // Ordering (gfx950; the library has no code object for other devices): a device-scope
+    // relaxed store is written through the XCD's L2 to the coherence point and counts in
+    // vmcnt until acknowledged, so after `s_waitcnt vmcnt(0)` the row's RowPick is visible
+    // there. The barrier puts that before thread 0's counter add (performed at the coherence
+    // point); the last row sees the full count in the add's return value and only then
+    // reads the sequence's RowPicks, with device-scope loads (served from the coherence
+    // point, never from a stale line of its own L2).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&seq_cnt[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n;
+    __syncthreads();
+    if (!s_last || threadIdx.x >= 64) return;
+    bounds_walk<DT>(in, b);
+}
+
+// B's merge for one row with a finite max m and Z > 0.
+__device__ __forceinline__ void row_pick_merge(int nseg, float inv_t, float top_p, const float* __restrict__ seg_max,
+                               const u64* __restrict__ seg_hist, RowPick* __restrict__ pick, int row, float m,
+                               u128 z, u64* hlo, u64* hhi, int* s_shift, u64* s_f, int* p_bin, u128* p_c) {
     const int cbm = cb_abs(m, inv_t);
     if (threadIdx.x < 64) {
         int sh = kRowBins;
@@ -465,13 +539,13 @@ __global__ void __launch_bounds__(kSegThreads) row_pick_kernel(int K, int nseg, 
         hhi[r] = (u64)(acc[k] >> 64);
     }
     const u128 tp = gg_u128_floor(ceil((double)top_p * gg_u128_to_double(z)));
-    if (threadIdx.x == 0) s_bin = -1;
+    if (threadIdx.x == 0) *p_bin = -1;
     __syncthreads();
-    pick_bin(hlo, hhi, nullptr, kRowBins, false, 0, tp, &s_bin, &s_c);
+    pick_bin(hlo, hhi, nullptr, kRowBins, false, 0, tp, p_bin, p_c);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int cb = s_bin;
-        pick[row] = RowPick{s_c, ((u128)hhi[cb] << 64) | hlo[cb], tp, m, cb, 0};
+        const int cb = *p_bin;
+        store_pick(&pick[row], RowPick{*p_c, ((u128)hhi[cb] << 64) | hlo[cb], tp, m, cb, 0});
     }
 }
 
@@ -494,24 +568,29 @@ __device__ __forceinline__ int bounds_test(const void* lp, const float* rsm, con
     return kRowUnsure;
 }
 
-// C: per sequence, one wave: the rows' bound outcomes; flags the rows that need the exact
-// nucleus (an open row and every row after it through the first certain rejection, or
-// just the row of the final draw when the bounds settle the walk) and appends them to the
-// flagged-row list (order free: each listed row is processed on its own). Lane j tests
-// draft j (max_drafts <= 64), so the rows' loads overlap.
+// C: per sequence, one wave (threads 0..63 of the block): the rows' bound outcomes; flags
+// the rows that need the exact nucleus (an open row and every row after it through the
+// first certain rejection) and appends them to the flagged-row list (order free: each
+// listed row is processed on its own), or flags just the row of the final draw when the
+// bounds settle the walk. Lane j tests draft j (max_drafts <= 64), so the rows' loads
+// overlap. The sequence's RowPicks come from other blocks of the same launch: device-scope
+// loads.
 template <gg_dtype_t DT>
-__global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restrict__ logits,
-                                                           const float* __restrict__ dprobs, int K, int V, int nseg,
-                                                           float inv_t, const int32_t* __restrict__ drafts,
-                                                           const int32_t* __restrict__ n_drafts,
-                                                           const float* __restrict__ uniforms,
-                                                           const float* __restrict__ seg_max,
-                                                           const RowPick* __restrict__ pick,
-                                                           int* __restrict__ status, int* __restrict__ flag,
-                                                           int* __restrict__ n_flagged, int* __restrict__ flagged) {
-    const int b = blockIdx.x;
+__device__ void bounds_walk(const DecideBoundsIn& in, int b) {
+    const void* __restrict__ logits = in.logits;
+    const float* __restrict__ dprobs = in.dprobs;
+    const int K = in.K, V = in.V, nseg = in.nseg;
+    const float inv_t = in.inv_t;
+    const int32_t* __restrict__ drafts = in.drafts;
+    const float* __restrict__ uniforms = in.uniforms;
+    const float* __restrict__ seg_max = in.seg_max;
+    const RowPick* __restrict__ pick = in.pick;
+    int* __restrict__ status = in.status;
+    int* __restrict__ flag = in.flag;
+    int* __restrict__ n_flagged = in.n_flagged;
+    int* __restrict__ flagged = in.flagged;
     const int R = K + 1;
-    const int n = live_rows(n_drafts, b, K);
+    const int n = live_rows(in.n_drafts, b, K);
     const int lane = threadIdx.x;
     int st = kRowAccept;
     if (lane < n) {
@@ -520,7 +599,7 @@ __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restric
         const int x = drafts[(size_t)b * K + lane];
         const double q = (dprobs && x >= 0 && x < V) ? gg_clean_q(dprobs[((size_t)b * K + lane) * V + x]) : 1.0;
         const double u = (double)uniforms[(size_t)b * R + lane];
-        const RowPick pk = pick[row];
+        const RowPick pk = load_pick(&pick[row]);
         st = bounds_test<DT>(lp, seg_max + (size_t)row * nseg, pk, pk.m, inv_t, x, V, u, q);
         status[row] = st;
     }
@@ -542,7 +621,7 @@ __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restric
     if (lane <= n) {
         mine = lane >= j0 && lane <= jend;
         if (mine && settled) {
-            const int cb = pick[b * R + lane].cbin;
+            const int cb = load_pick(&pick[b * R + lane]).cbin;
             if (cb >= 0 && cb < kRowBins - 1) mine = 2;
         }
         flag[b * R + lane] = mine;
@@ -550,7 +629,7 @@ __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restric
     if (lane == 0 && n == 64) {
         mine64 = jend >= 64;
         if (mine64 && settled) {
-            const int cb = pick[b * R + 64].cbin;
+            const int cb = load_pick(&pick[b * R + 64]).cbin;
             if (cb >= 0 && cb < kRowBins - 1) mine64 = 2;
         }
         flag[b * R + 64] = mine64;
@@ -566,15 +645,13 @@ __global__ void __launch_bounds__(64) decide_bounds_kernel(const void* __restric
     if (mine64) flagged[base + cnt - 1] = b * R + 64;
 }
 
-// D: per (flagged row, segment): the sum of e over the elements above the boundary bin
-// (all in the nucleus), and the boundary bin's elements gathered for the cut. Block
+// D: per (flagged row, segment): the boundary bin's elements gathered for the cut. Block
 // (seg, y) takes the listed rows y, y + gridDim.y, ... (the grid is sized for about one
 // flagged row per sequence, so no block is launched for an unflagged row).
 template <gg_dtype_t DT>
 __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, int V, int nseg, int vec_ok,
                                                float inv_t, int seg, int row, const float* __restrict__ seg_max,
-                                               RowPick* __restrict__ pick, uint2* __restrict__ cand,
-                                               u64* __restrict__ seg_keep);
+                                               RowPick* __restrict__ pick, uint2* __restrict__ cand);
 template <gg_dtype_t DT>
 __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __restrict__ logits, int V,
                                                                  int nseg, int vec_ok, float inv_t,
@@ -582,29 +659,25 @@ __global__ void __launch_bounds__(kSegThreads) seg_gather_kernel(const void* __r
                                                                  const int* __restrict__ flagged,
                                                                  const float* __restrict__ seg_max,
                                                                  RowPick* __restrict__ pick,
-                                                                 uint2* __restrict__ cand, u64* __restrict__ seg_keep) {
+                                                                 uint2* __restrict__ cand) {
     const int nf = *n_flagged;
     for (int li = blockIdx.y; li < nf; li += gridDim.y)
-        seg_gather_row<DT>(logits, V, nseg, vec_ok, inv_t, blockIdx.x, flagged[li], seg_max, pick, cand, seg_keep);
+        seg_gather_row<DT>(logits, V, nseg, vec_ok, inv_t, blockIdx.x, flagged[li], seg_max, pick, cand);
 }
 template <gg_dtype_t DT>
 __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, int V, int nseg, int vec_ok,
                                                float inv_t, int seg, int row, const float* __restrict__ seg_max,
-                                               RowPick* __restrict__ pick, uint2* __restrict__ cand,
-                                               u64* __restrict__ seg_keep) {
+                                               RowPick* __restrict__ pick, uint2* __restrict__ cand) {
     const void* lp = (const uint8_t*)logits + (size_t)row * V * dtype_bytes(DT);
-    __shared__ u64 red[kSegThreads / 64];
     __shared__ int s_hits[kSegThreads / 64];
     __shared__ int s_base;
     const int cbin = pick[row].cbin;
     const float m = pick[row].m;
     const float ms = seg_max[(size_t)row * nseg + seg];
     const int cbm = cb_abs(m, inv_t);
-    // Above the boundary bin: kept (weights summed exactly in a double); in it: gathered
-    // (a bit mask per thread, bit k for load_seg's element k). No per-element branch: the
-    // weight is computed for every element and selected. The thread's 32 logits are taken
-    // in two halves of 16, so fewer registers are live and more waves fit per SIMD.
-    double kd = 0.0;
+    // The boundary bin's elements: a bit mask per thread, bit k for load_seg's element k.
+    // The thread's 32 logits are taken in two halves of 16, so fewer registers are live and
+    // more waves fit per SIMD.
     uint32_t hits = 0;
     if (cbin >= 0 && finite_f(ms)) {
 #pragma unroll 1
@@ -619,13 +692,10 @@ __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, 
                 const bool fin = finite_f(xk);
                 const float xv = fin ? xk : -INFINITY;
                 const int rb = row_bin(xv, cbm, inv_t);
-                const float w = gg_weight_f(xv, ms, inv_t);
-                kd += rb < cbin ? (double)w : 0.0;
                 hits |= (uint32_t)(fin && rb == cbin) << (16 * half + k);
             }
         }
     }
-    u64 keep = (u64)kd;
     // The candidates' slots: an exclusive scan of the per-thread counts within the block
     // and one counter update per block.
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -636,9 +706,8 @@ __device__ __forceinline__ void seg_gather_row(const void* __restrict__ logits, 
         if (lane >= o) incl += t;
     }
     if (lane == 63) s_hits[wv] = incl;
-    keep = seg_block_sum(keep, red);  // (its barriers also publish s_hits)
+    __syncthreads();
     if (threadIdx.x == 0) {
-        seg_keep[(size_t)row * nseg + seg] = keep;
         int tot = 0;
         for (int i = 0; i < kSegThreads / 64; ++i) tot += s_hits[i];
         s_base = tot ? atomicAdd(&pick[row].n_cand, tot) : 0;
@@ -665,15 +734,14 @@ __device__ __forceinline__ float logit_of_key(unsigned int key) {
     return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
-// Exact per-row nucleus statistics by one 1024-thread block (passes over the whole row),
-// for a row whose boundary bin is crowded (more than kCandCap elements); also rewrites the
-// row's per-segment sums of kept e. Uses the segment maxima and sums of seg_pass_kernel.
+// Exact per-row nucleus statistics by one block of kThreads (passes over the whole row),
+// for a row whose boundary bin is crowded (more than kCandCap elements). Uses the segment
+// maxima and sums of seg_pass_kernel.
 template <gg_dtype_t DT>
 __device__ void row_stats_exact(const void* __restrict__ logits, int K, int V, int nseg,
                                 const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
                                 float inv_t, float top_p, const float* __restrict__ seg_max,
-                                const u64* __restrict__ seg_e, RowStats* __restrict__ stats,
-                                u64* __restrict__ seg_keep, int row) {
+                                const u64* __restrict__ seg_e, RowStats* __restrict__ stats, int row) {
     const int R = K + 1;
     const int b = row / R, j = row % R;
     const int n = live_rows(n_drafts, b, K);
@@ -789,20 +857,7 @@ __device__ void row_stats_exact(const void* __restrict__ logits, int K, int V, i
         idx_cut = (int)iprefix;
         zp = base + w_of(logit_of_key(lam), idx_cut);
     }
-    // The kept elements' e per segment.
     const Nucleus nu{m, inv_t, lam, idx_cut};
-    __shared__ u64 s_segk[64];
-    __syncthreads();
-    if (threadIdx.x < 64) s_segk[threadIdx.x] = 0;
-    __syncthreads();
-    for (int i = threadIdx.x; i < V; i += kThreads) {
-        const float l = ld<DT>(lp, i);
-        if (!nu.kept(l, i)) continue;
-        const u64 e = gg_weight(l, rms[i / kSegElems], inv_t);
-        if (e) atomicAdd(&s_segk[i / kSegElems], e);
-    }
-    __syncthreads();
-    if (threadIdx.x < nseg) seg_keep[(size_t)row * nseg + threadIdx.x] = s_segk[threadIdx.x];
     if (threadIdx.x == 0) {
         RowStats st{zp, 0, m, idx_cut, lam, 1};
         if (j < n) {
@@ -873,22 +928,21 @@ __device__ __forceinline__ void sort_desc_1024(u64* s, int np2) {
     __syncthreads();
 }
 
-// E: per flagged row, sort the boundary bin's elements by (key desc, index asc) and cut;
-// the row's exact statistics, and the kept elements' e added to their segments' sums.
+// E: per flagged row, sort the boundary bin's elements by (key desc, index asc) and cut:
+// the row's exact statistics.
 // A crowded bin (more than kCandCap elements) is left to rejection_row_stats_kernel.
 template <gg_dtype_t DT>
 __device__ void row_select_row(const void* __restrict__ logits, int K, int V, int nseg, float inv_t, float top_p,
                                const int32_t* __restrict__ drafts, const int32_t* __restrict__ n_drafts,
                                const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
                                const RowPick* __restrict__ pick, const uint2* __restrict__ cand,
-                               RowStats* __restrict__ stats, u64* __restrict__ seg_keep, int* __restrict__ n_crowded,
+                               RowStats* __restrict__ stats, int* __restrict__ n_crowded,
                                int* __restrict__ crowded, int row) {
     const int R = K + 1;
     const int b = row / R, j = row % R;
     const int n = live_rows(n_drafts, b, K);
     __shared__ u64 s_key[kCandCap];    // order key << 32 | (~index): descending = the nucleus order
     __shared__ u128 red[1024 / 64];
-    __shared__ u64 s_segk[64];
     __shared__ int s_last;
     const RowPick pk = pick[row];
     const float m = pk.m;
@@ -911,7 +965,6 @@ __device__ void row_select_row(const void* __restrict__ logits, int K, int V, in
             s_key[i] = 0;  // sorts last
         }
     }
-    if (threadIdx.x < 64) s_segk[threadIdx.x] = 0;
     __syncthreads();
     sort_desc_1024(s_key, np2);
     // Weights in that order (logit from the order key, segment max from the index).
@@ -956,7 +1009,6 @@ __device__ void row_select_row(const void* __restrict__ logits, int K, int V, in
         if (p0 + k < nc && (before < pk.tp || before == 0)) {
             last = p0 + k;
             zp = before + w[k];
-            if (ev[k]) atomicAdd(&s_segk[sv[k]], ev[k]);
         }
         before += w[k];
     }
@@ -964,9 +1016,6 @@ __device__ void row_select_row(const void* __restrict__ logits, int K, int V, in
     __syncthreads();
     if (last >= 0) atomicMax(&s_last, last);
     __syncthreads();
-    // The kept candidates' e into their segments' sums (seg_gather_kernel wrote the part
-    // above the boundary bin).
-    if (threadIdx.x < nseg && s_segk[threadIdx.x]) seg_keep[(size_t)row * nseg + threadIdx.x] += s_segk[threadIdx.x];
     if (last >= 0 && last == s_last) {  // the owner of the cut (position 0 always qualifies)
         const unsigned int lam = (unsigned int)(s_key[last] >> 32);
         // Ties at the boundary key kept for index <= idx_cut; every index when all are.
@@ -996,12 +1045,12 @@ __global__ void __launch_bounds__(1024) row_select_kernel(const void* __restrict
                                                           const u64* __restrict__ seg_e,
                                                           const RowPick* __restrict__ pick,
                                                           const uint2* __restrict__ cand,
-                                                          RowStats* __restrict__ stats, u64* __restrict__ seg_keep,
+                                                          RowStats* __restrict__ stats,
                                                           int* __restrict__ n_crowded, int* __restrict__ crowded) {
     const int nf = *n_flagged;
     for (int li = blockIdx.x; li < nf; li += gridDim.x) {
         row_select_row<DT>(logits, K, V, nseg, inv_t, top_p, drafts, n_drafts, seg_max, seg_e, pick, cand, stats,
-                           seg_keep, n_crowded, crowded, flagged[li]);
+                           n_crowded, crowded, flagged[li]);
         __syncthreads();  // (the next row reuses the shared arrays)
     }
 }
@@ -1014,12 +1063,11 @@ __global__ void __launch_bounds__(kThreads) rejection_row_stats_kernel(
     const void* __restrict__ logits, int K, int V, int nseg, const int32_t* __restrict__ drafts,
     const int32_t* __restrict__ n_drafts, float inv_t, float top_p, const int* __restrict__ n_crowded,
     const int* __restrict__ crowded, const float* __restrict__ seg_max, const u64* __restrict__ seg_e,
-    RowStats* __restrict__ stats, u64* __restrict__ seg_keep) {
+    RowStats* __restrict__ stats) {
     const int nc = *n_crowded;
     for (int li = blockIdx.x; li < nc; li += gridDim.x) {
         const int row = crowded[li];
-        row_stats_exact<DT>(logits, K, V, nseg, drafts, n_drafts, inv_t, top_p, seg_max, seg_e, stats, seg_keep,
-                            row);
+        row_stats_exact<DT>(logits, K, V, nseg, drafts, n_drafts, inv_t, top_p, seg_max, seg_e, stats, row);
         __syncthreads();
     }
 }
@@ -1201,7 +1249,7 @@ struct RejWs {
     int* crowded;      // top-p: flagged rows whose boundary bin is crowded
     int* flagged;      // top-p: the rows that need the exact nucleus
     uint2* cand;       // top-p: boundary-bin elements per row (logit bits, index)
-    u64* seg_keep;     // top-p: per (row, segment) sum of kept e
+    int* seq_cnt;      // top-p: rows of each sequence whose RowPick is out (row_pick_kernel)
     size_t bytes;
 };
 
@@ -1234,7 +1282,7 @@ static RejWs rej_layout(void* base, int num_seqs, int max_drafts, int vocab, boo
         w.crowded = (int*)take(rows * sizeof(int));
         w.flagged = (int*)take(rows * sizeof(int));
         w.cand = (uint2*)take(rows * kCandCap * sizeof(uint2));
-        w.seg_keep = (u64*)take(rows * nseg * sizeof(u64));
+        w.seq_cnt = (int*)take((size_t)num_seqs * sizeof(int));
     }
     w.bytes = off;
     return w;
@@ -1263,6 +1311,8 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     // the draw launch (one-hot q), not as a launch of its own.
     const DecideIn din{logits, q, K, vocab, nseg, inv_t, use_topp, drafts, n_drafts, uniforms,
                        w.stats, w.status, w.flag, w.seg_max, w.seg_e, w.pick};
+    const DecideBoundsIn dbin{logits, q, K, vocab, nseg, inv_t, drafts, n_drafts, uniforms, w.seg_max, w.seg_e,
+                              w.pick, w.status, w.flag, w.n_flagged, w.flagged};
     FinalDraw d{};
     d.logits = logits;
     d.dt = dt;
@@ -1285,29 +1335,25 @@ gg_status_t launch_accept_rejection(const void* logits, gg_dtype_t dt, const flo
     const fd::DrawParams P = fd::final_draw_params(d, w.draw);
 #define GG_REJ(DTV)                                                                                          \
     if (use_topp) {                                                                                          \
-        seg_pass_kernel<DTV, true><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok,  \
-                                                                            inv_t, n_drafts, w.seg_max,      \
-                                                                            w.seg_e, w.seg_hist);            \
-        row_pick_kernel<<<rows, kSegThreads, 0, s>>>(K, nseg, inv_t, top_p, n_drafts, w.seg_max, w.seg_e,    \
-                                                     w.seg_hist, w.pick, w.n_flagged);                       \
-        decide_bounds_kernel<DTV><<<num_seqs, 64, 0, s>>>(logits, q, K, vocab, nseg, inv_t, drafts,          \
-                                                          n_drafts, uniforms, w.seg_max, w.pick, w.status,   \
-                                                          w.flag, w.n_flagged, w.flagged);                   \
+        seg_pass_kernel<DTV, true><<<dim3(nseg, rows), kSegThreads, 0, s>>>(                                 \
+            logits, K, vocab, nseg, vec_ok, inv_t, n_drafts, w.seg_max, w.seg_e, w.seg_hist, w.seq_cnt,       \
+            w.n_flagged);                                                                                    \
+        row_pick_kernel<DTV><<<rows, kSegThreads, 0, s>>>(nseg, top_p, w.seg_hist, w.seq_cnt, dbin);         \
         seg_gather_kernel<DTV><<<dim3(nseg, num_seqs), kSegThreads, 0, s>>>(logits, vocab, nseg, vec_ok,     \
                                                                             inv_t, w.n_flagged, w.flagged,   \
-                                                                            w.seg_max, w.pick, w.cand,       \
-                                                                            w.seg_keep);                     \
+                                                                            w.seg_max, w.pick, w.cand);      \
         row_select_kernel<DTV><<<num_seqs, 1024, 0, s>>>(logits, K, vocab, nseg, inv_t, top_p, drafts,       \
                                                          n_drafts, w.n_flagged, w.flagged, w.seg_max,        \
-                                                         w.seg_e, w.pick, w.cand, w.stats, w.seg_keep,       \
-                                                         w.n_flagged + 1, w.crowded);                        \
+                                                         w.seg_e, w.pick, w.cand, w.stats, w.n_flagged + 1,  \
+                                                         w.crowded);                                         \
         rejection_row_stats_kernel<DTV><<<kRowStatsBlocks, kThreads, 0, s>>>(                                \
             logits, K, vocab, nseg, drafts, n_drafts, inv_t, top_p, w.n_flagged + 1, w.crowded, w.seg_max,   \
-            w.seg_e, w.stats, w.seg_keep);                                                                   \
+            w.seg_e, w.stats);                                                                               \
     } else {                                                                                                 \
         seg_pass_kernel<DTV, false><<<dim3(nseg, rows), kSegThreads, 0, s>>>(logits, K, vocab, nseg, vec_ok, \
                                                                              inv_t, n_drafts, w.seg_max,     \
-                                                                             w.seg_e, nullptr);              \
+                                                                             w.seg_e, nullptr, nullptr,      \
+                                                                             nullptr);                       \
     }                                                                                                        \
     rej_decide_kernel<DTV><<<num_seqs, 64, 0, s>>>(din, out_acc, w.spec_row, w.spec_x, w.spec_key, w.spec_s, P);
     switch (dt) {
