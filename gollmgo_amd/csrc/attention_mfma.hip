@@ -32,8 +32,8 @@
 namespace gg {
 #ifdef GG_TRACE
 // Debug builds (-DGG_TRACE) only: the LPT kernel's per-workgroup timeline in wall-clock
-// ticks (100 MHz): [4p] start, [4p+1] end, [4p+2] CU id (__smid), [4p+3] when wave 0's
-// first chunk had arrived. gg_debug_trace_ptr gives its device address.
+// ticks (100 MHz): [4p] start, [4p+1] end, [4p+2] CU id (__smid) | 1 << 32 | XCC << 40 |
+// keys << 44, [4p+3] when wave 0's first chunk had arrived. gg_debug_trace_ptr gives its device address.
 __device__ long long g_trace[65536 * 4];
 #endif
 namespace {
@@ -1261,7 +1261,9 @@ __global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) 
     if (threadIdx.x == 0) {
         g_trace[4 * p + 0] = tr_t0;
         g_trace[4 * p + 1] = wall_clock64();
-        g_trace[4 * p + 2] = (long long)__smid() | (1LL << 32);
+        // CU id, a valid bit, the XCC (hardware register XCC_ID) and the piece's key count
+        const long long xcc = (long long)(__builtin_amdgcn_s_getreg(20 | (15 << 11)) & 0xf);
+        g_trace[4 * p + 2] = (long long)__smid() | (1LL << 32) | (xcc << 40) | ((long long)(e.w - e.z) << 44);
     }
 #endif
 }

@@ -32,7 +32,7 @@ def main():
     from gollmgo_amd._lib import lib
 
     t = gv.device_bytes(lib().gg_debug_trace_ptr(), 65536 * 4 * 8).view(torch.int64).cpu().numpy().reshape(-1, 4)
-    t = t[(t[:, 2] >> 32) == 1]
+    t = t[((t[:, 2] >> 32) & 1) == 1]
     st, en = t[:, 0].astype(np.float64), t[:, 1].astype(np.float64)
     t0 = st.min()
     st, en = (st - t0) / 100.0, (en - t0) / 100.0
