@@ -119,20 +119,24 @@ struct AttnPlan {
 
 // LPT schedule: most sequences the plan kernel ranks (one per thread).
 constexpr int kLptMaxSeqs = 1024;
-// LPT piece length: at most T = ceil(C * num / (slots * den)) chunks for C chunks of work
-// over `slots` resident workgroups, num/den = 8/5 of the mean slot load when the
-// (sequence, kv head) items fill the slots and 4/3 when they are fewer. Measured on MI355X
-// with the merge inside the launch, attention µs (the call with its append, one layer,
-// mean over eight seeded layouts of each config's context distribution):
-//   config-3 layouts (items = slots), f = 3/2 / 8/5 / 13/8 / 5/3 / 17/10:
-//     131.0 / 128.4 / 129.1 / 130.3 / 130.8 (8/5 the fastest on 7 of the 8 layouts);
-//   config-2 layouts (items = slots / 2), f = 6/5 / 5/4 / 4/3 / 7/5:
-//     70.6 / 67.3 / 64.3 / 64.1;
-//   config 5 (items = 2 slots) within 0.3 µs at every factor.
-// Longer pieces split fewer items; with fewer items than slots the long items must be cut
-// finer to occupy every slot. The factor is a tuned constant; the time moves in steps as
-// items cross piece boundaries.
-constexpr int kLptPieceNum = 8, kLptPieceDen = 5;            // items >= slots
+// LPT piece length: T = ceil(C * num / (slots * den)) chunks for C chunks of work over
+// `slots` resident workgroups, num/den = 2 of the mean slot load when the (sequence, kv
+// head) items fill the slots and 4/3 when they are fewer.
+//   - Items that fill the slots are cut into pieces of T chunks and a shorter last piece,
+//     which the longest-first order then runs at the end. Measured on MI355X (the call with
+//     its append, one layer, mean over eight seeded config-3 layouts, same box): equal
+//     pieces at 8/5 (the earlier rule) 127.1 µs; T pieces and a remainder at 8/5 / 9/5 / 2:
+//     124.1 / 123.9 / 123.3 (bench layout 123.7 -> 118.5 at 9/5 and 2); at 7/5, 6/5 and 1
+//     slower than equal pieces on the bench layout (123.7, 129.2, 132.7). With equal
+//     pieces the factors had measured 3/2 / 8/5 / 13/8 / 5/3 / 17/10: 131.0 / 128.4 /
+//     129.1 / 130.3 / 130.8 over eight layouts (an older build).
+//   - Fewer items than slots: every long item has to be cut to fill the slots, and equal
+//     pieces balance them (config 2 with remainder pieces: 71 -> 79 µs). Config-2 layouts
+//     (items = slots / 2), f = 6/5 / 5/4 / 4/3 / 7/5: 70.6 / 67.3 / 64.3 / 64.1.
+//   - Config 5 (items = 2 slots) cuts nothing at any of these factors.
+// The factors are tuned constants; the time moves in steps as items cross piece
+// boundaries.
+constexpr int kLptPieceNum = 2, kLptPieceDen = 1;            // items >= slots
 constexpr int kLptPieceNumFew = 4, kLptPieceDenFew = 3;      // items < slots
 __host__ __device__ constexpr bool lpt_few_items(int slots, int num_seqs, int num_kv_heads) {
     return num_seqs * num_kv_heads < slots;

@@ -1069,11 +1069,13 @@ __global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) 
     }
 }
 
-// ---- LPT schedule: pieces of at most about the mean slot load, longest first ----
+// ---- LPT schedule: pieces of a few mean slot loads at most, longest first ----
 //
-// Items longer than T = ceil(f * total chunks / resident slots) are cut into equal pieces
-// of at most T chunks. attn_lpt_plan_kernel orders the pieces by size, descending (ties:
-// sequence, then piece, then kv head), and the main launch runs them in that order (with
+// Items longer than T = ceil(f * total chunks / resident slots) are cut: while the items
+// fill the slots, into pieces of T chunks and a shorter last piece; with fewer items, into
+// equal pieces of at most T chunks. attn_lpt_plan_kernel orders the pieces by size,
+// descending (ties: sequence, then piece, then kv head), and the main launch runs them in
+// that order (with
 // few items the first round pairs long and shorter pieces per CU, lpt_slot): dispatched in
 // order, the longest pieces start first and the shortest fill the tail.
 // The last piece of a split item to finish merges the item's partial records
@@ -1083,11 +1085,15 @@ __global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) 
 //
 // Plan layout (ints, in the workspace after the records), R = record bound, B = sequences:
 //   [0]                       number of pieces
+//   [1]                       1: T-chunk pieces and a remainder, 0: equal pieces
+//   [2]                       T (with remainder pieces)
 //   [16 + 4p ..]              piece p: (sequence, kv head | pieces per kv head << 16,
 //                             first token, end token); sequence -1 past the last piece
-//   [16 + 4R + 2b ..]         sequence b: (first piece, pieces per kv head)
+//   [16 + 4R + 2b ..]         sequence b: (first record, pieces per kv head)
 //   [16 + 4R + 2B + b*Hkv + h]  merge counter of (sequence b, kv head h)
-// Pieces of sequence b are first + j*Hkv + kvh.
+// The records of sequence b are first + j*Hkv + kvh for its piece j: with equal pieces the
+// records follow the ranks (a sequence's pieces have consecutive ranks); with remainder
+// pieces (whose ranks are not consecutive) the plan numbers them by sequence.
 __device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
 // Workgroup of the piece of rank r (and, as an involution, rank of workgroup r). While the
 // (sequence, kv head) items do not outnumber the S slots: over the first W = min(S,
@@ -1119,12 +1125,34 @@ __device__ __forceinline__ long long block_sum_1024(long long v, long long* s_w)
     return t;
 }
 
+// Exclusive prefix sum over a 1024-thread workgroup, and the total.
+__device__ __forceinline__ int block_excl_scan_1024(int v, int* s_w, int* total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    __syncthreads();
+    if (lane == 63) s_w[w] = inc;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        before += i < w ? s_w[i] : 0;
+        all += s_w[i];
+    }
+    *total = all;
+    return before + inc - v;
+}
+
 // One 1024-thread workgroup (one sequence per thread): sizes, ranks and lays out the
 // pieces.
 __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv, int tok, int slots, int recs) {
     __shared__ __align__(16) int s_key[kLptMaxSeqs];  // piece size in chunks (0: no work)
     __shared__ __align__(16) int s_cnt[kLptMaxSeqs];  // pieces of the sequence over all kv heads
     __shared__ long long s_w[16];
+    __shared__ int s_wi[16];
     const int B = a.num_seqs;
     const int b = threadIdx.x;
     const int nch = b < B ? seq_chunks(a, b, tok) : 0;
@@ -1134,6 +1162,59 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     const long long den = (long long)slots * (few ? kLptPieceDenFew : kLptPieceDen);
     const long long num = few ? kLptPieceNumFew : kLptPieceNum;
     const int T = (int)max((C * num + den - 1) / den, (long long)kStreamKMinChunks);
+    if (!few) {
+        // Items that fill the slots: pieces of T chunks and the remainder last. The full
+        // pieces come first (by sequence), then the last pieces by size, descending (ties:
+        // sequence). Records by (sequence, piece, kv head): a sequence's first record is the
+        // count of the pieces of the sequences before it.
+        const int np = nch ? (nch + T - 1) / T : 0;
+        const int rem = np ? nch - (np - 1) * T : 0;
+        const int nfull = np > 1 ? (np - 1) * Hkv : 0;
+        const int cnt = np * Hkv;
+        if (b < ((B + 7) & ~7)) {
+            s_key[b] = b < B ? rem : 0;
+            s_cnt[b] = (b < B && np) ? Hkv : 0;
+        }
+        int F, total;
+        const int full_pos = block_excl_scan_1024(nfull, s_wi, &F);
+        const int rec_first = block_excl_scan_1024(cnt, s_wi, &total);  // (barriers publish s_key)
+        int* plan = a.plan;
+        if (b == 0) {
+            plan[0] = total;
+            plan[1] = 1;
+            plan[2] = T;
+        }
+        if (b >= B) return;
+        int pos = F;
+        for (int t0 = 0; t0 < B; t0 += 8) {
+            const int4 k0 = *(const int4*)&s_key[t0], k1 = *(const int4*)&s_key[t0 + 4];
+            const int4 n0 = *(const int4*)&s_cnt[t0], n1 = *(const int4*)&s_cnt[t0 + 4];
+            const int kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const int nn[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = t0 + e;
+                pos += (kk[e] > rem || (kk[e] == rem && t < b)) ? nn[e] : 0;
+            }
+        }
+        int* seq = lpt_seq(plan, recs) + 2 * b;
+        seq[0] = rec_first;
+        seq[1] = np;
+        for (int h = 0; h < Hkv; ++h) lpt_count(plan, recs, B)[b * Hkv + h] = 0;
+        int4* table = (int4*)lpt_table(plan);
+        for (int j = 0; j < np; ++j) {
+            const int c0 = j * T, c1 = j == np - 1 ? nch : (j + 1) * T;
+            const int t0 = c0 * tok, t1 = min(c1 * tok, ctx);
+            for (int h = 0; h < Hkv; ++h) {
+                const int r = j < np - 1 ? full_pos + j * Hkv + h : pos + h;
+                table[lpt_slot(r, slots, total, B * Hkv <= slots)] = make_int4(b, h | (np << 16), t0, t1);
+            }
+        }
+        for (int q = total + b; q < recs; q += B) table[q] = make_int4(-1, 0, 0, 0);
+        return;
+    }
+    // Fewer items than slots: every long item has to be cut to fill the slots, and equal
+    // pieces balance them. Records by rank.
     const int np = nch ? (nch + T - 1) / T : 0;
     const int key = np ? (nch + np - 1) / np : 0;
     const int cnt = np * Hkv;
@@ -1144,7 +1225,10 @@ __global__ void __launch_bounds__(1024) attn_lpt_plan_kernel(AttnArgs a, int Hkv
     }
     const long long total = block_sum_1024(cnt, s_w);  // (its barriers also publish s_key / s_cnt)
     int* plan = a.plan;
-    if (b == 0) plan[0] = (int)total;
+    if (b == 0) {
+        plan[0] = (int)total;
+        plan[1] = 0;
+    }
     if (b >= B) return;
     // Pieces ahead of this sequence's: larger pieces, then equal pieces of lower sequences.
     // Eight sequences per step from 16-byte LDS reads (independent adds, no serial chain).
@@ -1250,8 +1334,16 @@ __global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) 
     const int b = e.x;
     if (b < 0) return;  // past the last piece
     const int kvh = e.y & 0xffff, np = e.y >> 16;
-    const PieceDesc d{b, kvh, e.z, e.w, -1,
-                      np > 1 ? lpt_slot(p, a.sk_grid, a.plan[0], a.num_seqs * kv.Hkv <= a.sk_grid) : -1};
+    // The piece's record: with remainder pieces (plan[1]) the sequence's first record plus
+    // (piece j = first chunk / T) * Hkv + kv head; with equal pieces its rank.
+    int rec = -1;
+    if (np > 1) {
+        constexpr int kTokC = attn_chunk_tokens(PoolTraits<DT>::kEB, NT);
+        rec = a.plan[1] ? lpt_seq(a.plan, lpt_records(a.sk_grid, a.num_seqs, kv.Hkv))[2 * b] +
+                              (e.z / kTokC / a.plan[2]) * kv.Hkv + kvh
+                        : lpt_slot(p, a.sk_grid, a.plan[0], a.num_seqs * kv.Hkv <= a.sk_grid);
+    }
+    const PieceDesc d{b, kvh, e.z, e.w, -1, rec};
     PieceIn<DT, attn_chunk_tokens(PoolTraits<DT>::kEB, NT)> in;
     DeferredRows ap;
     start_piece(a, kv, d, in, &ap);
