@@ -190,6 +190,31 @@ def test_rejection_more_listed_rows_than_workgroups(gpu):
             assert np.array_equal(tok.cpu().numpy(), et), (seed, top_p)
 
 
+@pytest.mark.parametrize("top_p", [0.95, 0.6])
+def test_rejection_sixty_four_drafts_with_top_p(gpu, top_p):
+    """The most drafts a call takes (64), with top-p: a sequence accepting all of them draws
+    its bonus from row 64 (the row the bounds walk marks through its own branch), one is
+    rejected at draft 30 (certainly, outside the nucleus), one has 10 drafts; the rows only
+    drawn from get the range hint."""
+    say(f"rejection 64 drafts top_p={top_p}")
+    rng = np.random.default_rng(64 + int(top_p * 100))
+    B, K, V = 3, 64, 32000
+    host = rng.normal(0, 2.0, (B, K + 1, V)).astype(np.float32)
+    for b in range(B):  # a clear mode per row, so its draft is surely accepted at a small u
+        host[b, np.arange(K + 1), rng.integers(0, V, K + 1)] += 8.0
+    drafts = np.argmax(host[:, :K], axis=-1).astype(np.int32)
+    drafts[1, 30] = int(np.argmin(host[1, 30]))
+    n = np.array([K, K, 10], np.int32)
+    u = (rng.random((B, K + 1)) * 1e-3).astype(np.float32)
+    acc, tok = gv.accept_rejection(torch.from_numpy(host).cuda(), torch.from_numpy(drafts).cuda(),
+                                   torch.from_numpy(n).cuda(), torch.from_numpy(u).cuda(), 0.8, top_p)
+    torch.cuda.synchronize()
+    ea, et = ora.accept_rejection(host, drafts, n, u, 0.8, top_p)
+    assert ea.tolist() == [K, 30, 10]
+    assert np.array_equal(acc.cpu().numpy(), ea)
+    assert np.array_equal(tok.cpu().numpy(), et)
+
+
 def test_rejection_small_temperature_is_greedy(gpu):
     say("rejection T->0")
     lg, host, drafts, n = logits_case(5, 3, 3000, "f32", seed=5)
