@@ -15,25 +15,27 @@
 // floor(exp_gg((l - a)/T) * 2^35)); sums are exact 128-bit integers. The nucleus order
 // is (logit desc, index asc). Launches:
 //   seg_pass, one block per (row, segment): the segment max m_s and E_s = sum of e_i (with
-//     top-p also the segment's coarse histogram of e on an absolute 1/16-nat grid). The
-//     only read of the whole logits: m and Z = sum f_s * E_s follow from the segments.
-//   top-p only: row_pick (per row, the segment histograms merged exactly into the row's
-//     and its boundary bin), decide_bounds (per sequence, every draft the bounds of the
-//     nucleus mass already decide, and the rows left open or holding the final draw
-//     flagged and listed), seg_gather (listed rows: each segment's kept sum above the
-//     boundary bin and that bin's elements), row_select (listed rows: a sort of those
-//     elements to the exact cut). The later kernels are sized for about one listed row
-//     per sequence and loop over the list, so no block is launched for a row that needs
-//     nothing. A row whose boundary bin is crowded falls back to the exact single-block
-//     row passes (three 11/11/10-bit radix levels on the order key and a 9+9-bit index
-//     select of a tied cut).
-//   decide, one wave per sequence: the acceptance walk (accept iff u*q(x)*Zp < W(x)) and
-//     the view of the final row.
-//   seg_residual (dense draft distributions only), one block per (sequence, segment):
-//     the final row's residual sums, W - min(W, floor(q*Zp)) in the segment's units.
-//   draw find, one block per sequence: the segment holding floor(u*total) (segment masses
-//     from the sums above), then the element inside it.
-// The draft distributions are read only at drafted tokens and on the final row.
+//     top-p also the segment's coarse histogram of e on an absolute 1/16-nat grid, and the
+//     counters of the next launch cleared). The only read of the whole logits: m and
+//     Z = sum f_s * E_s follow from the segments.
+//   top-p only:
+//     row_pick (per row, the segment histograms merged exactly into the row's, and its
+//       boundary bin); the last row block of each sequence then runs the bounds walk:
+//       every draft the bounds of the nucleus mass already decide; the rows left open are
+//       flagged and listed for the exact nucleus, or, when the bounds settle the walk,
+//       the row of the final draw is marked as only drawn from;
+//     seg_gather (listed rows: the boundary bin's elements), row_select (listed rows: a
+//       sort of those elements to the exact cut). The later kernels are sized for about
+//       one listed row per sequence and loop over the list, so no block is launched for a
+//       row that needs nothing. A row whose boundary bin is crowded falls back to the
+//       exact single-block row passes (three 11/11/10-bit radix levels on the order key
+//       and a 9+9-bit index select of a tied cut).
+//   rej_decide, one wave per sequence: the acceptance walk (accept iff u*q(x)*Zp < W(x))
+//     and the set-up of the sequence's final draw (its row, the rejected draft, and with
+//     top-p the exact cut element of a listed row, or the range of l/T of a marked row's
+//     boundary bin, as the draw's hint).
+//   The float64 draw's launches (accept_sample.hip) draw the token.
+// The draft distributions are read only at drafted tokens and, by the draw, on the drawn row.
 #pragma clang fp contract(off)
 
 #include "gg_common.h"
