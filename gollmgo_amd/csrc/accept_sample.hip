@@ -20,19 +20,25 @@
 //           row goes to the exact path.
 //   exact : one workgroup replays the rule literally: the same float64 operations in the
 //           same order (sorted orders by a bitonic sort), every sequential sum in one wave.
-//           About 3 ms per row; a row lands here with probability ~1e-4 (rows with NaN or
+//           6-17 ms per row; a row lands here with probability ~1e-4 (rows with NaN or
 //           +inf logits always do).
 // Orders the reference leaves open (sort.Slice is not stable) are fixed as value desc,
 // then index asc, NaN last; exp is gg_exp64 (gg_exp64.h), identical on host and device.
 //
 // Launches after the acceptance has decided which row of each sequence is drawn from:
 //   prep   (B blocks)       : which sequences draw, from which row; the row max from the
-//                             acceptance's segment maxima.
+//                             acceptance's segment maxima (the rejection acceptance's
+//                             decide kernel does this itself, fd::prep_row).
 //   pass   (segments x B)   : e_i = exp(l_i/T - m) per element, segment sums, NaN/+inf
-//                             check, coarse histograms (count and mass per 4096 bins of
-//                             the value's order key) when top-k or top-p is on.
-//   select (B, top-k/p only): top-k threshold and nucleus cut from the histograms, the
-//                             crossing bin's items gathered and sorted in LDS.
+//                             check; with top-k or top-p the coarse histograms (count and
+//                             mass per 1/64-nat slice below the row max), or, with the
+//                             caller's hint of the nucleus cut, the hinted bins' elements
+//                             and the mass above them; for a dense residual with an
+//                             estimate of its total, the residual's sums.
+//   select (B, top-k/p only): from the histograms, the crossing bin (select1) and its
+//                             elements (gather), unless hinted; then the top-k threshold
+//                             and the nucleus cut in LDS (select2), which draws itself
+//                             when no kept launch follows.
 //   kept   (segments x B)   : the draw's weight per segment (kept e, or the residual).
 //   draw   (B)              : the segment and then the element where u * total falls.
 //   exact  (a few blocks)   : the literal rule for the rows flagged on the way.
