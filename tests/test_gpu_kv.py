@@ -501,6 +501,22 @@ def test_attention_random_lpt_cases(gpu, seed):
     assert err <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt,long_ctx", [("fp8", 3000), ("bf16", 9000), ("int8", 5000)])
+def test_attention_lpt_remainder_pieces(gpu, dt, long_ctx):
+    """LPT with more items than slots (72 sequences x 8 kv heads): an item longer than T
+    is cut into pieces of T chunks and a shorter last piece, which runs at the end; the
+    records are numbered by (sequence, piece, kv head) and the piece that finishes last
+    merges them. Every sequence against the oracle."""
+    r = np.random.default_rng(3300 + long_ctx)
+    B = 72
+    ctx = [int(x) for x in r.integers(32, 300, B)]
+    ctx[int(r.integers(0, B))] = long_ctx
+    c = dict(dt=dt, B=B, R=6, Hq=32, H=8, D=128, bs=16, ctx=ctx, src="bf16", seed=long_ctx, q_dt="bf16")
+    say(f"attention LPT remainder pieces: dt={dt} long context {long_ctx}")
+    err = run_attention_case(**c)
+    print(f"  rel err {err:.2e}")
+    assert err <= TOL[dt]
+
 @pytest.mark.parametrize("dt,long_ctx", [("fp8", 24000), ("bf16", 9000), ("int8", 16000)])
 def test_attention_lpt_item_split_many_ways(gpu, dt, long_ctx):
     """LPT with one long sequence among short ones: its items are cut into many pieces
