@@ -121,7 +121,7 @@ struct AttnPlan {
 constexpr int kLptMaxSeqs = 1024;
 // LPT piece length: T = ceil(C * num / (slots * den)) chunks for C chunks of work over
 // `slots` resident workgroups, num/den = 2 of the mean slot load when the (sequence, kv
-// head) items fill the slots and 4/3 when they are fewer.
+// head) items fill the slots and 7/5 when they are fewer.
 //   - Items that fill the slots are cut into pieces of T chunks and a shorter last piece,
 //     which the longest-first order then runs at the end. Measured on MI355X (the call with
 //     its append, one layer, mean over eight seeded config-3 layouts, same box): equal
@@ -131,19 +131,21 @@ constexpr int kLptMaxSeqs = 1024;
 //     pieces the factors had measured 3/2 / 8/5 / 13/8 / 5/3 / 17/10: 131.0 / 128.4 /
 //     129.1 / 130.3 / 130.8 over eight layouts (an older build).
 //   - Fewer items than slots: every long item has to be cut to fill the slots, and equal
-//     pieces balance them (config 2 with remainder pieces: 71 -> 79 µs). Config-2 layouts
-//     (items = slots / 2), f = 6/5 / 5/4 / 4/3 / 7/5: 70.6 / 67.3 / 64.3 / 64.1.
+//     pieces balance them (config 2 with remainder pieces: 71 -> 79 µs). Mean over eight
+//     seeded config-2 layouts (items = slots / 2), f = 6/5 / 5/4 / 11/8 / 4/3 / 10/7 / 7/5
+//     / 13/9 / 3/2: 69.9 / 67.9 / 61.5 / 63.1 / 61.4 / 60.7 / 61.4 / 62.8 µs (bench layout:
+//     7/5 70.4, 4/3 70.8).
 //   - Config 5 (items = 2 slots) cuts nothing at any of these factors.
 // The factors are tuned constants; the time moves in steps as items cross piece
 // boundaries.
 constexpr int kLptPieceNum = 2, kLptPieceDen = 1;            // items >= slots
-constexpr int kLptPieceNumFew = 4, kLptPieceDenFew = 3;      // items < slots
+constexpr int kLptPieceNumFew = 7, kLptPieceDenFew = 5;      // items < slots
 __host__ __device__ constexpr bool lpt_few_items(int slots, int num_seqs, int num_kv_heads) {
     return num_seqs * num_kv_heads < slots;
 }
 // Bound on the number of LPT pieces (= main-grid workgroups and partial records): the
 // cuts of every item at T chunks give at most C/T + items pieces, C/T <= slots * den / num
-// (the smaller factor, 4/3, gives the larger bound). (Stream-K needs grid + items records,
+// (the smaller factor, 7/5, gives the larger bound). (Stream-K needs grid + items records,
 // which is more: the workspace holds the larger of the two.)
 __host__ __device__ constexpr int lpt_records(int slots, int num_seqs, int num_kv_heads) {
     return (slots * kLptPieceDenFew + kLptPieceNumFew - 1) / kLptPieceNumFew + num_seqs * num_kv_heads;
