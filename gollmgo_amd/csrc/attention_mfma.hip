@@ -1097,16 +1097,32 @@ __global__ void __launch_bounds__(256, attn_occupancy(PoolTraits<DT>::kEB, NT)) 
 __device__ __forceinline__ int* lpt_table(int* plan) { return plan + 16; }
 // Workgroup of the piece of rank r (and, as an involution, rank of workgroup r). While the
 // (sequence, kv head) items do not outnumber the S slots: over the first W = min(S,
-// pieces) ranks, ranks [W/2, W) are reversed, so workgroups w and w + W/2 get ranks w and
-// W - 1 - w. Dispatched round-robin, those two land on one CU as its first two slots,
-// which then hold a long and a shorter piece instead of two long ones. Measured, same box:
-// config 2 (items = S/2) 73.3 -> 71.1 µs; over eight seeded config-3 layouts (items = S)
-// the mean 127.2 -> 126.1 µs and the worst layout 136.8 -> 129.4 µs; config 5 (items =
+// pieces) ranks, the groups of eight ranks in [H, W), H = W/2, are taken in reverse order,
+// so workgroup w + H gets a rank near W - 1 - w. Dispatched round-robin, workgroups w and
+// w + H land on one CU as its first two slots, which then hold a long and a shorter piece
+// instead of two long ones. Measured, same box (with the ranks of [H, W) reversed one by
+// one): config 2 (items = S/2) 73.3 -> 71.1 µs; over eight seeded config-3 layouts (items =
+// S) the mean 127.2 -> 126.1 µs and the worst layout 136.8 -> 129.4 µs; config 5 (items =
 // 2S) 128.3 -> 129.2 µs, so more items than slots keep the plain order. Records stay
 // indexed by rank.
+// Reversing whole groups of eight keeps every workgroup's index congruent to its rank
+// modulo 8, and workgroup w runs on XCD w mod 8. A sequence's kv-head items have
+// consecutive ranks from a multiple of Hkv, so with Hkv = 8 item (b, h) runs on XCD
+// (first rank of b + h) mod 8 = h mod 8 whether b's items are long or short, and two
+// sequences that share prefix blocks read each shared block of a head on one XCD, the
+// second read mostly from that XCD's L2. (Reversed one by one, a short sequence's head h
+// ran on XCD 7 - h, and a shared block's second read went to another XCD's L2.) Config 3
+// (20 % of the blocks shared by pairs of sequences), same box: attention reads 291,491 ->
+// 282,994 KiB per call (FETCH_SIZE; 597.0 -> 579.6 MB, the unique pool bytes are 579.2 MB),
+// 117.5 -> 116.9 µs per call; configs 2 and 5 unchanged.
 __device__ __forceinline__ int lpt_slot(int r, int S, int total, bool pair) {
     const int W = min(S, total);
-    return (pair && r >= W / 2 && r < W) ? W / 2 + (W - 1 - r) : r;
+    const int H = W / 2;
+    if (pair && r >= H && r < W) {
+        const int q = r - H, G = (W - H) / 8;
+        return q < 8 * G ? H + 8 * (G - 1 - q / 8) + (q & 7) : r;
+    }
+    return r;
 }
 __device__ __forceinline__ int* lpt_seq(int* plan, int recs) { return plan + 16 + 4 * recs; }
 // Merge counters, one per (sequence, kv head): pieces of a split item that have written
